@@ -1,0 +1,132 @@
+/*
+ * rwkv6_amd.h — C ABI of the MI355X (gfx950) RWKV-6 time-mix hot path.
+ *
+ * One shared library, librwkv6_amd.so, built from the .hip sources in rwkv-megatron_amd/csrc.
+ * Plain pointers and sizes only: no torch or C++ types cross this boundary.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers, owned by the caller (the library never
+ *     allocates, frees or synchronises the host).  Work is enqueued on `stream`
+ *     (a hipStream_t; NULL = the default stream).
+ *   - Tensors are dense, row-major, and 16-byte aligned.
+ *   - Return value: RWKV6_OK or an rwkv6_status code; rwkv6_strerror() maps it
+ *     to text.  Validation failures never launch anything.
+ *   - Calls are re-entrant: no mutable global state; the same inputs give
+ *     bit-identical outputs (no floating-point atomics anywhere).
+ *
+ * Reference interface each group replaces (TimeMobius/RWKV-Megatron):
+ *   WKV6      fla `fused_recurrent_rwkv6` / `chunk_rwkv6` as called at
+ *             rwkv_megatron/rwkv6_layer_specs.py:339 (layout glue :330-341)
+ *   mix       token shift + lerp + data-dependent lerp of RWKV6TimeMix.forward,
+ *             rwkv6_layer_specs.py:290-300 and :440-452 (bias of :195 folded in)
+ *   gn_gate   GroupNorm (rwkv6_layer_specs.py:90-97) applied at :461-465, times
+ *             the silu gate of :458, the product formed at :466
+ */
+#ifndef RWKV6_AMD_H
+#define RWKV6_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RWKV6_ABI_VERSION 1
+
+enum rwkv6_status {
+    RWKV6_OK = 0,
+    RWKV6_ERR_INVALID_ARG = 1, /* null pointer, bad size, bad dtype code */
+    RWKV6_ERR_UNSUPPORTED = 2, /* e.g. head size other than 64 */
+    RWKV6_ERR_LAUNCH = 3,      /* hipGetLastError() after a launch */
+    RWKV6_ERR_ALIGNMENT = 4    /* a tensor pointer is not 16-byte aligned */
+};
+
+enum rwkv6_dtype { RWKV6_F32 = 0, RWKV6_BF16 = 1 };
+
+int rwkv6_abi_version(void);
+const char* rwkv6_strerror(int code);
+
+/* ------------------------------------------------------------------------
+ * WKV6.  Replaces fla.ops.rwkv6.fused_recurrent_rwkv6 / chunk_rwkv6
+ * (call site rwkv_megatron/rwkv6_layer_specs.py:339).
+ *   r, k, w : [B,H,T,K] bf16 (w = log-space decay, as the caller passes -exp(decay), :336)
+ *   v, o    : [B,H,T,V] bf16
+ *   u       : [H,K] in u_dtype (f32 or bf16; time_first viewed per head, :337)
+ *   h0, hT  : [B,H,K,V] f32, each nullable (initial_state / output_final_state)
+ *   scale   : multiplies r (the reference passes 1.0)
+ * Only K == V == 64 (RWKV-6 head size) is supported; T >= 0 arbitrary.
+ * `saved` (rwkv6_wkv_saved_bytes) receives the per-chunk states and decays that
+ * the backward consumes; keep it alive until rwkv6_wkv_bwd.  `workspace`
+ * (rwkv6_wkv_workspace_bytes) is scratch for the duration of one call.
+ * ---------------------------------------------------------------------- */
+size_t rwkv6_wkv_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V);
+size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                                 int for_bwd);
+
+int rwkv6_wkv_fwd(const void* r, const void* k, const void* v, const void* w, const void* u,
+                  int u_dtype, const float* h0, void* o, float* hT, void* saved,
+                  void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                  float scale, void* stream);
+
+/* Gradients of rwkv6_wkv_fwd for loss terms on o (dO, bf16 [B,H,T,V]) and on the
+ * final state (dhT, f32 [B,H,K,V], nullable = zero).  dr, dk, dw: [B,H,T,K] bf16;
+ * dv: [B,H,T,V] bf16; du: [H,K] in u_dtype; dh0: [B,H,K,V] f32, nullable. */
+int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, const void* u,
+                  int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                  void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
+                  int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
+ * Token shift and lerps of RWKV6TimeMix.forward, sequence-first [T,B,C] bf16.
+ *   shift(x)[t] = x[t-1], shift(x)[0] = 0              (rwkv6_layer_specs.py:294-300)
+ *   xxx         = x + (shift(x) - x) * maa              (:443-444), maa [C]
+ *   mixed[e]    = x + (shift(x) - x) * (mexp[e] + bias[e])   (:446-452)
+ *                 mexp [5,T,B,C] is the LoRA up-projection before its bias (:195),
+ *                 bias [5,C]; mixed is [5,T,B,C] in the order w,k,v,r,g.
+ * maa and bias are in param_dtype (f32 or bf16).  C must be a multiple of 8.
+ * ---------------------------------------------------------------------- */
+int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* xxx,
+                         int64_t T, int64_t B, int64_t C, void* stream);
+int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int param_dtype,
+                     void* mixed, int64_t T, int64_t B, int64_t C, void* stream);
+/* Backward of the data-dependent lerp w.r.t. its LoRA input: d_mixed [5,T,B,C] ->
+ * d_mexp [5,T,B,C] = d_mixed * (shift(x) - x) and d_bias [5,C] (param_dtype). */
+size_t rwkv6_ddlerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
+int rwkv6_ddlerp_bwd(const void* x, const void* d_mixed, int param_dtype, void* d_mexp,
+                     void* d_bias, void* workspace, int64_t T, int64_t B, int64_t C,
+                     void* stream);
+/* Input gradient of both lerps (they share x): d_mixed [5,T,B,C] and d_xxx [T,B,C]
+ * (nullable = 0) -> dx [T,B,C] and d_maa [C] (param_dtype). */
+size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
+int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
+                  int param_dtype, const void* d_mixed, const void* d_xxx, void* dx,
+                  void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
+ * GroupNorm(per head) * silu(gate), fused with the head-first -> sequence-first
+ * layout change of rwkv6_layer_specs.py:341 and :461-465.
+ *   o      : WKV output, [B,H,T,K] bf16 (head_first=1) or [T,B,H*K] (head_first=0)
+ *   g_pre  : [T,B,H*K] bf16, linear_gate output before silu (:458)
+ *   gamma, beta : [H*K] in param_dtype; eps = config.layernorm_epsilon (:68)
+ *   y      : [T,B,H*K] bf16 = GN(o) * silu(g_pre)
+ *   mean, rstd : [T*B*H] f32 statistics saved for the backward
+ * ---------------------------------------------------------------------- */
+int rwkv6_gn_gate_fwd(const void* o, int head_first, const void* g_pre, const void* gamma,
+                      const void* beta, int param_dtype, float eps, void* y, float* mean,
+                      float* rstd, int64_t T, int64_t B, int64_t H, int64_t K, void* stream);
+size_t rwkv6_gn_gate_bwd_workspace_bytes(int64_t T, int64_t B, int64_t H, int64_t K);
+/* dy [T,B,H*K] -> d_o (layout of o), d_g_pre [T,B,H*K], dgamma, dbeta [H*K] (param_dtype). */
+int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const void* gamma,
+                      const void* beta, int param_dtype, const float* mean, const float* rstd,
+                      const void* dy, void* d_o, void* d_g_pre, void* dgamma, void* dbeta,
+                      void* workspace, int64_t T, int64_t B, int64_t H, int64_t K,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV6_AMD_H */

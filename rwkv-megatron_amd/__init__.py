@@ -1,0 +1,12 @@
+"""MI355X-native RWKV-6 time-mix hot path (drop-in for RWKV-Megatron's fla call).
+
+The package directory name carries a dash, so load it with
+``importlib.import_module("rwkv-megatron_amd")``.
+
+Exports
+  chunk_rwkv6, fused_recurrent_rwkv6   fla-compatible WKV6 ops (HIP kernels)
+"""
+from .wkv import chunk_rwkv6, fused_recurrent_rwkv6  # noqa: F401
+from . import _lib  # noqa: F401
+
+__all__ = ["chunk_rwkv6", "fused_recurrent_rwkv6"]

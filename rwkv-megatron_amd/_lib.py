@@ -1,0 +1,81 @@
+"""ctypes binding of librwkv6_amd.so (C ABI declared in include/rwkv6_amd.h).
+
+The library is the only compute path: if it is missing this module raises, it
+never falls back to another implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librwkv6_amd.so")
+
+RWKV6_OK = 0
+RWKV6_ERR_INVALID_ARG = 1
+RWKV6_ERR_UNSUPPORTED = 2
+RWKV6_ERR_LAUNCH = 3
+RWKV6_ERR_ALIGNMENT = 4
+RWKV6_F32 = 0
+RWKV6_BF16 = 1
+
+_vp = ctypes.c_void_p
+_fp = ctypes.c_void_p          # float* passed as an address
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/rwkv6_amd.h
+SIGNATURES = {
+    "rwkv6_abi_version": (_int, []),
+    "rwkv6_strerror": (ctypes.c_char_p, [_int]),
+    "rwkv6_wkv_saved_bytes": (ctypes.c_size_t, [_i64] * 5),
+    "rwkv6_wkv_workspace_bytes": (ctypes.c_size_t, [_i64] * 5 + [_int]),
+    "rwkv6_wkv_fwd": (_int, [_vp] * 5 + [_int] + [_fp, _vp, _fp, _vp, _vp] + [_i64] * 5 + [_f32, _vp]),
+    "rwkv6_wkv_bwd": (_int, [_vp] * 5 + [_int] + [_vp, _fp, _vp] + [_vp] * 5 + [_fp, _vp]
+                      + [_i64] * 5 + [_f32, _vp]),
+    "rwkv6_shift_lerp_fwd": (_int, [_vp, _vp, _int, _vp] + [_i64] * 3 + [_vp]),
+    "rwkv6_ddlerp_fwd": (_int, [_vp, _vp, _vp, _int, _vp] + [_i64] * 3 + [_vp]),
+    "rwkv6_ddlerp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
+    "rwkv6_ddlerp_bwd": (_int, [_vp, _vp, _int, _vp, _vp, _vp] + [_i64] * 3 + [_vp]),
+    "rwkv6_mix_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
+    "rwkv6_mix_bwd": (_int, [_vp] * 4 + [_int] + [_vp] * 5 + [_i64] * 3 + [_vp]),
+    "rwkv6_gn_gate_fwd": (_int, [_vp, _int, _vp, _vp, _vp, _int, _f32, _vp, _fp, _fp] + [_i64] * 4 + [_vp]),
+    "rwkv6_gn_gate_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
+    "rwkv6_gn_gate_bwd": (_int, [_vp, _int, _vp, _vp, _vp, _int, _fp, _fp] + [_vp] * 5 + [_vp]
+                          + [_i64] * 4 + [_vp]),
+}
+
+_lib = None
+
+
+class Rwkv6Error(RuntimeError):
+    pass
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} not found: build it with `python rwkv-megatron_amd/build.py` "
+                "(or __graft_entry__.build()); there is no fallback implementation")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == RWKV6_OK:
+        return
+    msg = load().rwkv6_strerror(status).decode()
+    if status == RWKV6_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    if status in (RWKV6_ERR_INVALID_ARG, RWKV6_ERR_ALIGNMENT):
+        raise ValueError(f"{what}: {msg}")
+    raise Rwkv6Error(f"{what}: {msg} (status {status})")

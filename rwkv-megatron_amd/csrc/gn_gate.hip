@@ -1,0 +1,243 @@
+// Fused per-head GroupNorm * silu(gate) for MI355X (gfx950), forward and backward.
+//
+// Reference (/root/reference/rwkv_megatron/rwkv6_layer_specs.py):
+//   o = rearrange(wkv_out, "b h t n -> t b (h n)")                     :341
+//   y = group_norm(o as [(t b), c], groups = heads, weight, bias, eps)  :90-97, :461-465
+//   y = y * silu(linear_gate(mixed_gate))                               :458, :466
+// eps is config.layernorm_epsilon (:68).  One group is the 64 channels of one
+// (token, batch, head); 8 lanes own a group, 8 channels (16 bytes) each, and
+// reduce with cross-lane shuffles.  The WKV output may be read head-first, which
+// fuses away the layout copy of :341.  Parameter-gradient sums are two-stage
+// with a fixed order (deterministic).
+#include "common.h"
+#include "../../include/rwkv6_amd.h"
+
+#define GN_D 64           // channels per group (head size)
+#define GN_THR 256        // 32 groups per block pass
+#define GN_TT 64          // tokens per block (one (b,h) per block row)
+
+namespace {
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
+    unpack8(*reinterpret_cast<const uint4*>(p), f);
+}
+__device__ __forceinline__ void store8(uint16_t* p, const float* f) {
+    uint4 q;
+    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+    *reinterpret_cast<uint4*>(p) = q;
+}
+__device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {
+    if (dtype == RWKV6_BF16) {
+        load8(reinterpret_cast<const uint16_t*>(p) + off, f);
+    } else {
+        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
+        float4 a = q[0], b = q[1];
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    }
+}
+__device__ __forceinline__ float sum8lanes(float v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    return v;
+}
+__device__ __forceinline__ float sigmoidf_(float z) { return 1.f / (1.f + __expf(-z)); }
+
+// element offset of (t, b, h, channel c0) in o
+__device__ __forceinline__ int64_t o_off(int head_first, int64_t t, int64_t b, int64_t h,
+                                         int64_t c0, int64_t T, int64_t B, int64_t H) {
+    return head_first ? ((b * H + h) * T + t) * GN_D + c0 : ((t * B + b) * H + h) * GN_D + c0;
+}
+
+}  // namespace
+
+// grid: (ceil(T / GN_TT), B*H); thread = (group slot gs = tid/8, lane8 = tid%8)
+__global__ void __launch_bounds__(GN_THR)
+rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
+                         const uint16_t* __restrict__ g_pre, const void* __restrict__ gamma,
+                         const void* __restrict__ beta, int pdt, float eps,
+                         uint16_t* __restrict__ y, float* __restrict__ mean_out,
+                         float* __restrict__ rstd_out, int64_t T, int64_t B, int64_t H) {
+    const int64_t bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int gs = threadIdx.x >> 3, l8 = threadIdx.x & 7;
+    const int64_t c0 = 8 * l8;
+    float ga[8], be[8];
+    load_param8(gamma, pdt, h * GN_D + c0, ga);
+    load_param8(beta, pdt, h * GN_D + c0, be);
+    const int64_t C = H * GN_D;
+    for (int p = 0; p < GN_TT / 32; ++p) {
+        const int64_t t = (int64_t)blockIdx.x * GN_TT + p * 32 + gs;
+        if (t >= T) break;
+        float x[8], z[8], out[8];
+        load8(o + o_off(head_first, t, b, h, c0, T, B, H), x);
+        const int64_t yo = (t * B + b) * C + h * GN_D + c0;
+        load8(g_pre + yo, z);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += x[i];
+        const float mean = sum8lanes(s) * (1.f / GN_D);
+        float v = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v += (x[i] - mean) * (x[i] - mean);
+        const float rstd = rsqrtf(sum8lanes(v) * (1.f / GN_D) + eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            out[i] = ((x[i] - mean) * rstd * ga[i] + be[i]) * (z[i] * sigmoidf_(z[i]));
+        store8(y + yo, out);
+        if (l8 == 0) {
+            mean_out[(t * B + b) * H + h] = mean;
+            rstd_out[(t * B + b) * H + h] = rstd;
+        }
+    }
+}
+
+// Backward.  Partial sums of dgamma/dbeta per block: part[((b*nTB + tb)*H + h)][2][64].
+__global__ void __launch_bounds__(GN_THR)
+rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
+                         const uint16_t* __restrict__ g_pre, const void* __restrict__ gamma,
+                         const void* __restrict__ beta, int pdt,
+                         const float* __restrict__ mean_in, const float* __restrict__ rstd_in,
+                         const uint16_t* __restrict__ dy, uint16_t* __restrict__ d_o,
+                         uint16_t* __restrict__ d_g, float* __restrict__ part, int64_t T,
+                         int64_t B, int64_t H) {
+    __shared__ float red[2][32][GN_D + 1];
+    const int64_t bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int gs = threadIdx.x >> 3, l8 = threadIdx.x & 7;
+    const int64_t c0 = 8 * l8;
+    const int64_t C = H * GN_D;
+    float ga[8], be[8], accg[8], accb[8];
+    load_param8(gamma, pdt, h * GN_D + c0, ga);
+    load_param8(beta, pdt, h * GN_D + c0, be);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) accg[i] = accb[i] = 0.f;
+    for (int p = 0; p < GN_TT / 32; ++p) {
+        const int64_t t = (int64_t)blockIdx.x * GN_TT + p * 32 + gs;
+        if (t >= T) break;
+        float x[8], z[8], g[8], xh[8], dxh[8], outo[8], outg[8];
+        const int64_t oo = o_off(head_first, t, b, h, c0, T, B, H);
+        const int64_t yo = (t * B + b) * C + h * GN_D + c0;
+        load8(o + oo, x);
+        load8(g_pre + yo, z);
+        load8(dy + yo, g);
+        const float mean = mean_in[(t * B + b) * H + h], rstd = rstd_in[(t * B + b) * H + h];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xh[i] = (x[i] - mean) * rstd;
+            const float sg = sigmoidf_(z[i]);
+            const float gate = z[i] * sg;
+            const float n = xh[i] * ga[i] + be[i];
+            outg[i] = g[i] * n * sg * (1.f + z[i] * (1.f - sg));
+            const float dn = g[i] * gate;
+            accg[i] += dn * xh[i];
+            accb[i] += dn;
+            dxh[i] = dn * ga[i];
+            s1 += dxh[i];
+            s2 += dxh[i] * xh[i];
+        }
+        s1 = sum8lanes(s1) * (1.f / GN_D);
+        s2 = sum8lanes(s2) * (1.f / GN_D);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) outo[i] = rstd * (dxh[i] - s1 - xh[i] * s2);
+        store8(d_o + oo, outo);
+        store8(d_g + yo, outg);
+    }
+    // reduce the 32 group slots of this block (fixed order)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        red[0][gs][c0 + i] = accg[i];
+        red[1][gs][c0 + i] = accb[i];
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * GN_D) {
+        const int which = threadIdx.x / GN_D, c = threadIdx.x % GN_D;
+        float acc = 0.f;
+        for (int j = 0; j < 32; ++j) acc += red[which][j][c];
+        const int64_t nTB = gridDim.x;
+        part[(((b * nTB + blockIdx.x) * H + h) * 2 + which) * GN_D + c] = acc;
+    }
+}
+
+// dgamma[h*64+c] = sum_{b,tb} part[b][tb][h][0][c]; dbeta likewise (fixed order).
+__global__ void rwkv6_gn_param_reduce(const float* __restrict__ part, int64_t B, int64_t nTB,
+                                      int64_t H, int pdt, void* __restrict__ dgamma,
+                                      void* __restrict__ dbeta) {
+    const int64_t h = blockIdx.x;
+    const int which = threadIdx.x / GN_D, c = threadIdx.x % GN_D;
+    float acc = 0.f;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t tb = 0; tb < nTB; ++tb) acc += part[(((b * nTB + tb) * H + h) * 2 + which) * GN_D + c];
+    void* dst = which == 0 ? dgamma : dbeta;
+    if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(dst)[h * GN_D + c] = f2bf(acc);
+    else reinterpret_cast<float*>(dst)[h * GN_D + c] = acc;
+}
+
+namespace {
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int gn_check(int64_t T, int64_t B, int64_t H, int64_t K, int pdt) {
+    if (T < 0 || B < 1 || H < 1 || K < 1) return RWKV6_ERR_INVALID_ARG;
+    if (K != GN_D) return RWKV6_ERR_UNSUPPORTED;
+    if (B * H > 65535) return RWKV6_ERR_UNSUPPORTED;
+    if (pdt != RWKV6_F32 && pdt != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
+    return RWKV6_OK;
+}
+inline int launch_status() { return hipGetLastError() == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH; }
+}  // namespace
+
+extern "C" {
+
+int rwkv6_gn_gate_fwd(const void* o, int head_first, const void* g_pre, const void* gamma,
+                      const void* beta, int param_dtype, float eps, void* y, float* mean,
+                      float* rstd, int64_t T, int64_t B, int64_t H, int64_t K, void* stream) {
+    int st = gn_check(T, B, H, K, param_dtype);
+    if (st) return st;
+    if (T == 0) return RWKV6_OK;
+    if (!o || !g_pre || !gamma || !beta || !y || !mean || !rstd) return RWKV6_ERR_INVALID_ARG;
+    if (!al16(o) || !al16(g_pre) || !al16(gamma) || !al16(beta) || !al16(y))
+        return RWKV6_ERR_ALIGNMENT;
+    dim3 grid((unsigned)((T + GN_TT - 1) / GN_TT), (unsigned)(B * H));
+    hipLaunchKernelGGL(rwkv6_gn_gate_fwd_kernel, grid, dim3(GN_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)o, head_first,
+                       (const uint16_t*)g_pre, gamma, beta, param_dtype, eps, (uint16_t*)y, mean,
+                       rstd, T, B, H);
+    return launch_status();
+}
+
+size_t rwkv6_gn_gate_bwd_workspace_bytes(int64_t T, int64_t B, int64_t H, int64_t K) {
+    if (T < 0 || B < 1 || H < 1 || K != GN_D) return 0;
+    const int64_t nTB = (T + GN_TT - 1) / GN_TT;
+    return (size_t)((nTB > 0 ? nTB : 1) * B * H * 2 * GN_D) * sizeof(float);
+}
+
+int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const void* gamma,
+                      const void* beta, int param_dtype, const float* mean, const float* rstd,
+                      const void* dy, void* d_o, void* d_g_pre, void* dgamma, void* dbeta,
+                      void* workspace, int64_t T, int64_t B, int64_t H, int64_t K,
+                      void* stream) {
+    int st = gn_check(T, B, H, K, param_dtype);
+    if (st) return st;
+    if (!gamma || !beta || !dgamma || !dbeta || !workspace ||
+        (T > 0 && (!o || !g_pre || !mean || !rstd || !dy || !d_o || !d_g_pre)))
+        return RWKV6_ERR_INVALID_ARG;
+    if (!al16(o) || !al16(g_pre) || !al16(gamma) || !al16(beta) || !al16(dy) || !al16(d_o) ||
+        !al16(d_g_pre) || !al16(workspace))
+        return RWKV6_ERR_ALIGNMENT;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t nTB = (T + GN_TT - 1) / GN_TT;
+    if (T > 0) {
+        dim3 grid((unsigned)nTB, (unsigned)(B * H));
+        hipLaunchKernelGGL(rwkv6_gn_gate_bwd_kernel, grid, dim3(GN_THR), 0, s, (const uint16_t*)o,
+                           head_first, (const uint16_t*)g_pre, gamma, beta, param_dtype, mean, rstd,
+                           (const uint16_t*)dy, (uint16_t*)d_o, (uint16_t*)d_g_pre,
+                           (float*)workspace, T, B, H);
+    }
+    hipLaunchKernelGGL(rwkv6_gn_param_reduce, dim3((unsigned)H), dim3(2 * GN_D), 0, s,
+                       (const float*)workspace, B, nTB, H, param_dtype, dgamma, dbeta);
+    return launch_status();
+}
+
+}  // extern "C"

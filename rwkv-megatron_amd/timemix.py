@@ -1,0 +1,234 @@
+"""Fused time-mix building blocks (HIP kernels) as autograd Functions.
+
+* ``token_shift_mix``: token shift + static lerp + LoRA bottleneck + data-dependent
+  lerp of RWKV6TimeMix.forward (/root/reference/rwkv_megatron/rwkv6_layer_specs.py
+  :440-452, bottleneck :177-195).  The two elementwise stages are HIP kernels; the
+  LoRA GEMMs run on hipBLASLt through torch.matmul / torch.bmm.
+* ``group_norm_gate``: GroupNorm over heads (:90-97, applied at :461-465) times
+  silu(gate) (:458, :466), reading the WKV output head-first so the layout copy
+  of :341 disappears.
+
+Every function raises if the HIP library is missing; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+NE = 5  # data-dependent mixes, order w, k, v, r, g (rwkv6_layer_specs.py:450)
+
+
+def _p(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _c(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t.clone() if t.data_ptr() % 16 else t
+
+
+def _param(t: torch.Tensor):
+    """Parameters may be fp32 or bf16; anything else is computed as fp32."""
+    if t.dtype == torch.bfloat16:
+        return _c(t), _lib.RWKV6_BF16
+    return _c(t.float()), _lib.RWKV6_F32
+
+
+def _check_act(name, x, ndim):
+    if x.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {x.dtype}")
+    if x.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got shape {tuple(x.shape)}")
+
+
+# ---------------------------------------------------------------------------
+# raw kernel calls
+# ---------------------------------------------------------------------------
+
+def shift_lerp(x: torch.Tensor, maa: torch.Tensor) -> torch.Tensor:
+    """xxx = x + (shift(x) - x) * maa, x [T,B,C] bf16 (rwkv6_layer_specs.py:440-444)."""
+    _check_act("x", x, 3)
+    T, B, C = x.shape
+    x = _c(x)
+    m, pdt = _param(maa)
+    out = torch.empty_like(x)
+    _lib.check(_lib.load().rwkv6_shift_lerp_fwd(_p(x), _p(m), pdt, _p(out), T, B, C,
+                                                _stream(x.device)), "rwkv6_shift_lerp_fwd")
+    return out
+
+
+def ddlerp(x: torch.Tensor, mexp: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]); mexp [5,T,B,C] -> [5,T,B,C]."""
+    _check_act("x", x, 3)
+    T, B, C = x.shape
+    if tuple(mexp.shape) != (NE, T, B, C):
+        raise ValueError(f"mexp must be [5,T,B,C] = {(NE, T, B, C)}, got {tuple(mexp.shape)}")
+    x, mexp = _c(x), _c(mexp.to(torch.bfloat16))
+    b, pdt = _param(bias)
+    out = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().rwkv6_ddlerp_fwd(_p(x), _p(mexp), _p(b), pdt, _p(out), T, B, C,
+                                            _stream(x.device)), "rwkv6_ddlerp_fwd")
+    return out
+
+
+def ddlerp_bwd(x, d_mixed, param_dtype):
+    T, B, C = x.shape
+    L = _lib.load()
+    d_mexp = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
+    pdt = _lib.RWKV6_BF16 if param_dtype == torch.bfloat16 else _lib.RWKV6_F32
+    d_bias = torch.empty(NE, C, dtype=torch.bfloat16 if pdt == _lib.RWKV6_BF16 else torch.float32,
+                         device=x.device)
+    ws = torch.empty(L.rwkv6_ddlerp_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
+    _lib.check(L.rwkv6_ddlerp_bwd(_p(x), _p(d_mixed), pdt, _p(d_mexp), _p(d_bias), _p(ws), T, B, C,
+                                  _stream(x.device)), "rwkv6_ddlerp_bwd")
+    return d_mexp, d_bias
+
+
+def mix_bwd(x, maa, mexp, bias, d_mixed, d_xxx):
+    T, B, C = x.shape
+    L = _lib.load()
+    m, pdt = _param(maa)
+    b, pdt_b = _param(bias)
+    if pdt_b != pdt:
+        b = _c(b.to(m.dtype))
+    dx = torch.empty_like(x)
+    d_maa = torch.empty(C, dtype=m.dtype, device=x.device)
+    ws = torch.empty(L.rwkv6_mix_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
+    _lib.check(L.rwkv6_mix_bwd(_p(x), _p(m), _p(mexp), _p(b), pdt, _p(d_mixed), _p(d_xxx), _p(dx),
+                               _p(d_maa), _p(ws), T, B, C, _stream(x.device)), "rwkv6_mix_bwd")
+    return dx, d_maa
+
+
+def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
+    if head_first:
+        B, H, T, K = o.shape
+    else:
+        T, B, C = o.shape
+        K = 64
+        H = C // K
+    o, g_pre = _c(o), _c(g_pre)
+    ga, pdt = _param(gamma)
+    be, pdt_b = _param(beta)
+    if pdt_b != pdt:
+        be = _c(be.to(ga.dtype))
+    y = torch.empty(T, B, H * K, dtype=torch.bfloat16, device=o.device)
+    mean = torch.empty(T * B * H, dtype=torch.float32, device=o.device)
+    rstd = torch.empty_like(mean)
+    _lib.check(_lib.load().rwkv6_gn_gate_fwd(_p(o), int(head_first), _p(g_pre), _p(ga), _p(be), pdt,
+                                             float(eps), _p(y), _p(mean), _p(rstd), T, B, H, K,
+                                             _stream(o.device)), "rwkv6_gn_gate_fwd")
+    return y, mean, rstd
+
+
+# ---------------------------------------------------------------------------
+# autograd Functions
+# ---------------------------------------------------------------------------
+
+class _TokenShiftMix(torch.autograd.Function):
+    """x [T,B,C] -> mixed [5,T,B,C] (w,k,v,r,g); params maa [C], w_down [C,5,R],
+    w_up [5,R,C], bias [5,C] with the shapes of rwkv6_layer_specs.py:126-170, :377-385."""
+
+    @staticmethod
+    def forward(ctx, x, maa, w_down, w_up, bias):
+        T, B, C = x.shape
+        R = w_down.shape[-1]
+        N = T * B
+        x = _c(x)
+        wd = w_down.to(torch.bfloat16).reshape(C, NE * R)
+        wu = _c(w_up.to(torch.bfloat16))
+        xxx = shift_lerp(x, maa)
+        neck = torch.tanh(xxx.view(N, C) @ wd)                                  # [N, 5R]
+        neck_t = neck.view(N, NE, R).transpose(0, 1).contiguous()              # [5, N, R]
+        mexp = torch.bmm(neck_t, wu)                                             # [5, N, C]
+        mixed = ddlerp(x, mexp.view(NE, T, B, C), bias)
+        ctx.save_for_backward(x, maa, w_down, w_up, bias, xxx, neck_t, mexp)
+        return mixed
+
+    @staticmethod
+    def backward(ctx, d_mixed):
+        x, maa, w_down, w_up, bias, xxx, neck_t, mexp = ctx.saved_tensors
+        T, B, C = x.shape
+        R = w_down.shape[-1]
+        N = T * B
+        d_mixed = _c(d_mixed.to(torch.bfloat16))
+        d_mexp, d_bias = ddlerp_bwd(x, d_mixed, bias.dtype)
+        d_mexp = d_mexp.view(NE, N, C)
+        wu = w_up.to(torch.bfloat16)
+        d_w_up = torch.bmm(neck_t.transpose(1, 2).contiguous(), d_mexp)         # [5, R, C]
+        d_neck_t = torch.bmm(d_mexp, wu.transpose(1, 2).contiguous())           # [5, N, R]
+        d_pre = (d_neck_t.float() * (1.0 - neck_t.float() ** 2)).to(torch.bfloat16)
+        d_pre = d_pre.transpose(0, 1).reshape(N, NE * R)
+        wd = w_down.to(torch.bfloat16).reshape(C, NE * R)
+        d_w_down = (xxx.view(N, C).t() @ d_pre).view(C, NE, R)
+        d_xxx = _c(d_pre @ wd.t())
+        dx, d_maa = mix_bwd(x, maa, mexp.view(NE, T, B, C), bias, d_mixed, d_xxx.view(T, B, C))
+        return (dx, d_maa.to(maa.dtype), d_w_down.to(w_down.dtype), d_w_up.to(w_up.dtype),
+                d_bias.to(bias.dtype))
+
+
+def token_shift_mix(x, maa, w_down, w_up, bias):
+    """Returns mixed [5,T,B,C] = (w, k, v, r, g) inputs of RWKV6TimeMix (:440-452)."""
+    _check_act("x", x, 3)
+    return _TokenShiftMix.apply(x, maa, w_down, w_up, bias)
+
+
+class _GroupNormGate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, o, head_first, g_pre, gamma, beta, eps):
+        y, mean, rstd = gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps)
+        ctx.save_for_backward(o, g_pre, gamma, beta, mean, rstd)
+        ctx.head_first = head_first
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        o, g_pre, gamma, beta, mean, rstd = ctx.saved_tensors
+        head_first = ctx.head_first
+        if head_first:
+            B, H, T, K = o.shape
+        else:
+            T, B, C = o.shape
+            K = 64
+            H = C // K
+        L = _lib.load()
+        o, g_pre, dy = _c(o), _c(g_pre), _c(dy.to(torch.bfloat16))
+        ga, pdt = _param(gamma)
+        be, pdt_b = _param(beta)
+        if pdt_b != pdt:
+            be = _c(be.to(ga.dtype))
+        d_o = torch.empty_like(o)
+        d_g = torch.empty_like(g_pre)
+        dgamma = torch.empty(H * K, dtype=ga.dtype, device=o.device)
+        dbeta = torch.empty_like(dgamma)
+        ws = torch.empty(L.rwkv6_gn_gate_bwd_workspace_bytes(T, B, H, K), dtype=torch.uint8,
+                         device=o.device)
+        _lib.check(L.rwkv6_gn_gate_bwd(_p(o), int(head_first), _p(g_pre), _p(ga), _p(be), pdt,
+                                       _p(mean), _p(rstd), _p(dy), _p(d_o), _p(d_g), _p(dgamma),
+                                       _p(dbeta), _p(ws), T, B, H, K, _stream(o.device)),
+                   "rwkv6_gn_gate_bwd")
+        return d_o, None, d_g, dgamma.to(gamma.dtype), dbeta.to(beta.dtype), None
+
+
+def group_norm_gate(o, g_pre, gamma, beta, eps, head_first=True):
+    """y [T,B,C] = GroupNorm_heads(o) * silu(g_pre); o is [B,H,T,64] (head_first) or [T,B,C]."""
+    _check_act("o", o, 4 if head_first else 3)
+    _check_act("g_pre", g_pre, 3)
+    if head_first:
+        B, H, T, K = o.shape
+    else:
+        T, B, C = o.shape
+        K, H = 64, o.shape[-1] // 64
+    if K != 64 or (not head_first and o.shape[-1] % 64):
+        raise NotImplementedError("GroupNorm gate supports head size 64 only")
+    if tuple(g_pre.shape) != (T, B, H * K):
+        raise ValueError(f"g_pre must be [T,B,C] = {(T, B, H * K)}, got {tuple(g_pre.shape)}")
+    return _GroupNormGate.apply(o, bool(head_first), g_pre, gamma, beta, float(eps))

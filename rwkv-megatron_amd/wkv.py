@@ -1,0 +1,157 @@
+"""Drop-in for fla's RWKV-6 ops, backed by the HIP kernels of librwkv6_amd.so.
+
+The reference calls ``fused_recurrent_rwkv6(r, k, v, w, u, scale=1.)[0]`` at
+/root/reference/rwkv_megatron/rwkv6_layer_specs.py:339 after laying its
+tensors out head-first (:333-337).  fla also exports ``chunk_rwkv6`` with the
+same contract (4th argument named ``g``).  Both names are provided here:
+
+    o, final_state = chunk_rwkv6(r, k, v, g, u, scale=None, initial_state=None,
+                                 output_final_state=False)
+
+* r, k, g(=w): [B,H,T,K]; v: [B,H,T,V]; u: [H,K]; K == V == 64.
+* g / w is LOG-space decay (the caller passes ``-exp(decay)``, :336).
+* scale None or -1 means K**-0.5 (fla's convention); any other float is used as is.
+* initial_state: [B,H,K,V] (computed in fp32); final_state is fp32 or None.
+* o has r's dtype.  Arithmetic: bf16 operands on MFMA, fp32 accumulation and fp32
+  carried state; fp32 / fp16 inputs are rounded to bf16 on entry.
+* Backward returns gradients for r, k, v, g, u and initial_state, and accepts a
+  gradient on final_state.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_HEAD = 64
+
+
+def _stream_ptr(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return _aligned(t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16))
+
+
+def _u_arg(u: torch.Tensor):
+    if u.dtype == torch.bfloat16:
+        return _aligned(u), _lib.RWKV6_BF16
+    return _aligned(u.float()), _lib.RWKV6_F32
+
+
+class _WKV6(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, r, k, v, w, u, scale, h0, output_final_state):
+        B, H, T, K = r.shape
+        V = v.shape[-1]
+        dev = r.device
+        out_dtype = r.dtype
+        rb, kb, vb, wb = _bf16(r), _bf16(k), _bf16(v), _bf16(w)
+        ua, u_code = _u_arg(u)
+        h0f = None if h0 is None else _aligned(h0.float())
+        L = _lib.load()
+        saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, K, V), dtype=torch.uint8, device=dev)
+        work = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, V, 0), dtype=torch.uint8, device=dev)
+        o = torch.empty(B, H, T, V, dtype=torch.bfloat16, device=dev)
+        hT = torch.empty(B, H, K, V, dtype=torch.float32, device=dev) if output_final_state else None
+        _lib.check(L.rwkv6_wkv_fwd(_p(rb), _p(kb), _p(vb), _p(wb), _p(ua), u_code, _p(h0f), _p(o),
+                                   _p(hT), _p(saved), _p(work), B, H, T, K, V, float(scale),
+                                   _stream_ptr(dev)), "rwkv6_wkv_fwd")
+        ctx.save_for_backward(rb, kb, vb, wb, ua, saved)
+        ctx.meta = (scale, u_code, h0 is not None, u.dtype, out_dtype, r.dtype, k.dtype, v.dtype,
+                    w.dtype, None if h0 is None else h0.dtype)
+        if out_dtype != torch.bfloat16:
+            o = o.to(out_dtype)
+        return o, hT
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        rb, kb, vb, wb, ua, saved = ctx.saved_tensors
+        scale, u_code, has_h0, u_dtype, _, r_dt, k_dt, v_dt, w_dt, h0_dt = ctx.meta
+        B, H, T, K = rb.shape
+        V = vb.shape[-1]
+        dev = rb.device
+        L = _lib.load()
+        dob = _bf16(do) if do is not None else torch.zeros(B, H, T, V, dtype=torch.bfloat16, device=dev)
+        dhtf = None if dht is None else _aligned(dht.float())
+        dr = torch.empty_like(rb)
+        dk = torch.empty_like(kb)
+        dv = torch.empty_like(vb)
+        dw = torch.empty_like(wb)
+        du = torch.empty(H, K, dtype=ua.dtype, device=dev)
+        need_h0 = has_h0 and ctx.needs_input_grad[6]
+        dh0 = torch.empty(B, H, K, V, dtype=torch.float32, device=dev) if need_h0 else None
+        work = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, V, 1), dtype=torch.uint8, device=dev)
+        _lib.check(L.rwkv6_wkv_bwd(_p(rb), _p(kb), _p(vb), _p(wb), _p(ua), u_code, _p(dob), _p(dhtf),
+                                   _p(saved), _p(dr), _p(dk), _p(dv), _p(dw), _p(du), _p(dh0), _p(work),
+                                   B, H, T, K, V, float(scale), _stream_ptr(dev)), "rwkv6_wkv_bwd")
+        cast = lambda t, dt: t if t.dtype == dt else t.to(dt)
+        return (cast(dr, r_dt), cast(dk, k_dt), cast(dv, v_dt), cast(dw, w_dt), cast(du, u_dtype),
+                None, None if dh0 is None else cast(dh0, h0_dt), None)
+
+
+def _validate(r, k, v, w, u, initial_state):
+    for name, t in (("r", r), ("k", k), ("v", v), ("w", w), ("u", u)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must live on the GPU (got {t.device})")
+        if t.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise TypeError(f"{name}: unsupported dtype {t.dtype}")
+    if r.dim() != 4:
+        raise ValueError(f"r must be [B,H,T,K], got shape {tuple(r.shape)}")
+    B, H, T, K = r.shape
+    if k.shape != r.shape or w.shape != r.shape:
+        raise ValueError(f"k and w must match r's shape {tuple(r.shape)}")
+    if v.dim() != 4 or v.shape[:3] != r.shape[:3]:
+        raise ValueError(f"v must be [B,H,T,V] with B,H,T of r, got {tuple(v.shape)}")
+    V = v.shape[-1]
+    if u.shape != (H, K):
+        raise ValueError(f"u must be [H,K] = {(H, K)}, got {tuple(u.shape)}")
+    if K != _HEAD or V != _HEAD:
+        raise NotImplementedError(f"head size must be K == V == {_HEAD}, got K={K}, V={V}")
+    if initial_state is not None and tuple(initial_state.shape) != (B, H, K, V):
+        raise ValueError(f"initial_state must be [B,H,K,V] = {(B, H, K, V)}")
+    devs = {t.device for t in (r, k, v, w, u)}
+    if initial_state is not None:
+        devs.add(initial_state.device)
+    if len(devs) != 1:
+        raise ValueError("all tensors must be on the same device")
+
+
+def chunk_rwkv6(r, k, v, g, u, scale=None, initial_state=None, output_final_state=False,
+                checkpoint_level=None, cu_seqlens=None, head_first=True):
+    """RWKV-6 WKV, fla ``chunk_rwkv6`` contract.  Returns ``(o, final_state or None)``."""
+    if cu_seqlens is not None:
+        raise NotImplementedError("variable-length batches (cu_seqlens) are not supported")
+    if not head_first:
+        raise NotImplementedError("only the head-first [B,H,T,K] layout is supported")
+    _validate(r, k, v, g, u, initial_state)
+    if scale is None or scale == -1:
+        scale = r.shape[-1] ** -0.5
+    return _WKV6.apply(r, k, v, g, u, float(scale), initial_state, bool(output_final_state))
+
+
+def fused_recurrent_rwkv6(r, k, v, w, u, scale=-1, initial_state=None, output_final_state=False,
+                          causal=True, cu_seqlens=None, head_first=True):
+    """RWKV-6 WKV, fla ``fused_recurrent_rwkv6`` contract (the name the reference imports at
+    rwkv6_layer_specs.py:47 and calls at :339).  Same kernels as ``chunk_rwkv6``."""
+    if not causal:
+        raise NotImplementedError("only causal RWKV-6 is defined")
+    return chunk_rwkv6(r, k, v, w, u, scale=scale, initial_state=initial_state,
+                       output_final_state=output_final_state, cu_seqlens=cu_seqlens,
+                       head_first=head_first)

@@ -1,0 +1,91 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol the header
+declares, and its argument validation rejects bad calls before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rwkv6_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(rwkv6_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("rwkv6_wkv_fwd", "rwkv6_wkv_bwd", "rwkv6_shift_lerp_fwd", "rwkv6_ddlerp_fwd",
+                 "rwkv6_mix_bwd", "rwkv6_gn_gate_fwd", "rwkv6_gn_gate_bwd", "rwkv6_strerror"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = ctypes.CDLL(pkg._lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the ctypes signature table covers exactly the header
+    assert sorted(pkg._lib.SIGNATURES) == _declared()
+
+
+def test_version_and_strerror(pkg):
+    L = pkg._lib.load()
+    assert L.rwkv6_abi_version() == 1
+    assert L.rwkv6_strerror(0) == b"ok"
+    assert b"64" in L.rwkv6_strerror(2)
+    assert L.rwkv6_strerror(12345) == b"unknown rwkv6 status code"
+
+
+def test_workspace_sizes(pkg):
+    L = pkg._lib.load()
+    B, H, T = 8, 32, 4096
+    NT = T // 64
+    saved = L.rwkv6_wkv_saved_bytes(B, H, T, 64, 64)
+    assert saved >= B * H * (NT + 1) * 64 * 64 * 2 + B * H * NT * 64 * 4
+    assert L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 0) >= B * H * NT * 64 * 64 * 4
+    assert L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 1) > L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 0)
+    assert L.rwkv6_wkv_saved_bytes(B, H, T, 32, 64) == 0          # unsupported head size
+
+
+def _fake(addr):
+    return ctypes.c_void_p(addr)
+
+
+def test_validation_rejects_before_launch(pkg):
+    """Bad calls return an error code without dereferencing anything (the pointers are fake)."""
+    L = pkg._lib.load()
+    p = _fake(0x100000)
+    args = lambda K=64, u_dt=1, r=p, saved=p: (r, p, p, p, p, u_dt, None, p, None, saved, p,
+                                               2, 2, 64, K, 64, 1.0, None)
+    assert L.rwkv6_wkv_fwd(*args(K=32)) == pkg._lib.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_wkv_fwd(*args(u_dt=7)) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_wkv_fwd(*args(r=None)) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_wkv_fwd(*args(saved=None)) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_wkv_fwd(*args(r=_fake(0x100002))) == pkg._lib.RWKV6_ERR_ALIGNMENT
+    assert L.rwkv6_shift_lerp_fwd(p, p, 1, p, 4, 2, 12, None) == pkg._lib.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_ddlerp_fwd(p, p, p, 3, p, 4, 2, 16, None) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_gn_gate_fwd(p, 1, p, p, p, 0, 1e-5, p, p, p, 4, 2, 2, 32, None) == \
+        pkg._lib.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_gn_gate_fwd(None, 1, p, p, p, 0, 1e-5, p, p, p, 4, 2, 2, 64, None) == \
+        pkg._lib.RWKV6_ERR_INVALID_ARG
+
+
+def test_python_checker_maps_codes(pkg):
+    with pytest.raises(NotImplementedError):
+        pkg._lib.check(2, "x")
+    with pytest.raises(ValueError):
+        pkg._lib.check(1, "x")
+    with pytest.raises(pkg._lib.Rwkv6Error):
+        pkg._lib.check(3, "x")
+    pkg._lib.check(0, "x")
+
+
+def test_wrapper_rejects_cpu_tensors(pkg):
+    import torch
+    x = torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.chunk_rwkv6(x, x, x, x, torch.zeros(1, 64))
+    with pytest.raises(NotImplementedError):
+        pkg.chunk_rwkv6(x, x, x, x, torch.zeros(1, 64), cu_seqlens=torch.tensor([0, 4]))

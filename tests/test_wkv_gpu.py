@@ -1,0 +1,155 @@
+"""GPU parity of the HIP WKV6 path (through the C ABI via the autograd drop-in)
+against the CPU oracle on identical bf16 inputs.
+
+Tolerance (bf16 I/O, fp32 accumulate): for every output tensor,
+    max|gpu - oracle| / max|oracle|  <= TOL_MAX (1e-2)  and
+    ||gpu - oracle||_2 / ||oracle||_2 <= TOL_L2 (1e-2).
+The oracle runs in fp64 on the same bf16-rounded inputs, so the error is the
+kernels' own (bf16 MFMA operands, bf16 outputs).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL_MAX = 1e-2
+TOL_L2 = 1e-2
+
+
+def _inputs(B, H, T, seed, w_lo=-6.0, w_hi=-0.5, u_bf16=False):
+    g = torch.Generator().manual_seed(seed)
+    bf = lambda t: t.to(torch.bfloat16)
+    K = V = 64
+    r = bf(torch.randn(B, H, T, K, generator=g))
+    k = bf(torch.randn(B, H, T, K, generator=g))
+    v = bf(torch.randn(B, H, T, V, generator=g))
+    w = bf(-torch.exp(torch.rand(B, H, T, K, generator=g) * (w_hi - w_lo) + w_lo))
+    u = 0.1 * torch.randn(H, K, generator=g)
+    if u_bf16:
+        u = bf(u)
+    h0 = 0.5 * torch.randn(B, H, K, V, generator=g)
+    do = bf(torch.randn(B, H, T, V, generator=g))
+    dht = torch.randn(B, H, K, V, generator=g)
+    return dict(r=r, k=k, v=v, w=w, u=u, h0=h0, do=do, dht=dht)
+
+
+def _n(t):
+    return None if t is None else t.detach().float().cpu().numpy()
+
+
+def _errs(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale_max = max(np.abs(ref).max(), 1e-30)
+    scale_l2 = max(np.linalg.norm(ref), 1e-30)
+    return np.abs(got - ref).max() / scale_max, np.linalg.norm(got - ref) / scale_l2
+
+
+def run_gpu(pkg, x, scale, with_h0, with_dht, fn="chunk_rwkv6"):
+    dev = torch.device("cuda:0")
+    leaves = {n: x[n].to(dev).requires_grad_(True) for n in ("r", "k", "v", "w", "u")}
+    h0 = x["h0"].to(dev).requires_grad_(True) if with_h0 else None
+    op = getattr(pkg, fn)
+    o, hT = op(leaves["r"], leaves["k"], leaves["v"], leaves["w"], leaves["u"], scale=scale,
+               initial_state=h0, output_final_state=True)
+    loss = (o.float() * x["do"].to(dev).float()).sum()
+    if with_dht:
+        loss = loss + (hT * x["dht"].to(dev)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    out = dict(o=_n(o), hT=_n(hT))
+    for n in ("r", "k", "v", "w", "u"):
+        out["d" + n] = _n(leaves[n].grad)
+    if with_h0:
+        out["dh0"] = _n(h0.grad)
+    return out
+
+
+def run_oracle(x, scale, with_h0, with_dht):
+    a = {n: _n(t) for n, t in x.items()}
+    h0 = a["h0"] if with_h0 else None
+    dht = a["dht"] if with_dht else None
+    o, hT = orc.wkv6_fwd(a["r"], a["k"], a["v"], a["w"], a["u"], h0, scale)
+    g = orc.wkv6_bwd(a["r"], a["k"], a["v"], a["w"], a["u"], a["do"], h0, dht, scale)
+    out = dict(o=o, hT=hT)
+    out.update(g)
+    return out
+
+
+def _compare(got, ref, names, tol_max=TOL_MAX, tol_l2=TOL_L2):
+    report = {}
+    for n in names:
+        report[n] = _errs(got[n], ref[n])
+    bad = {n: e for n, e in report.items() if not (e[0] <= tol_max and e[1] <= tol_l2)}
+    print(" ".join(f"{n}:{e[0]:.1e}/{e[1]:.1e}" for n, e in report.items()))
+    assert not bad, f"parity failed (max-rel, l2-rel): {bad}"
+
+
+SHAPES = [(1, 1, 1), (2, 2, 63), (2, 2, 64), (2, 3, 130), (1, 2, 257)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("state", [False, True])
+def test_wkv_parity_small(pkg, shape, state):
+    B, H, T = shape
+    x = _inputs(B, H, T, seed=B * 1000 + H * 100 + T)
+    scale = 1.0 if not state else 0.5
+    got = run_gpu(pkg, x, scale, state, state)
+    ref = run_oracle(x, scale, state, state)
+    names = ["o", "hT", "dr", "dk", "dv", "dw", "du"] + (["dh0"] if state else [])
+    _compare(got, ref, names)
+
+
+def test_wkv_parity_bf16_u_and_fused_recurrent_name(pkg):
+    x = _inputs(2, 2, 96, seed=7, u_bf16=True)
+    got = run_gpu(pkg, x, 1.0, False, False, fn="fused_recurrent_rwkv6")
+    assert got["du"] is not None
+    ref = run_oracle(x, 1.0, False, False)
+    _compare(got, ref, ["o", "dr", "dk", "dv", "dw", "du"])
+
+
+def test_wkv_strong_decay(pkg):
+    """Log-decay down to -exp(2.3) per token (much faster forgetting than the default init)."""
+    x = _inputs(1, 2, 192, seed=9, w_lo=-3.0, w_hi=2.3)
+    got = run_gpu(pkg, x, 1.0, True, True)
+    ref = run_oracle(x, 1.0, True, True)
+    _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
+
+
+def test_wkv_deterministic(pkg):
+    x = _inputs(2, 2, 200, seed=3)
+    a = run_gpu(pkg, x, 1.0, True, True)
+    b = run_gpu(pkg, x, 1.0, True, True)
+    for n in a:
+        assert np.array_equal(a[n], b[n]), n
+
+
+def test_wkv_empty_sequence(pkg):
+    dev = torch.device("cuda:0")
+    B, H, K = 2, 2, 64
+    r = torch.zeros(B, H, 0, K, dtype=torch.bfloat16, device=dev)
+    u = torch.zeros(H, K, device=dev)
+    h0 = torch.randn(B, H, K, K, device=dev)
+    o, hT = pkg.chunk_rwkv6(r, r, r, r, u, scale=1.0, initial_state=h0, output_final_state=True)
+    torch.cuda.synchronize()
+    assert o.shape == (B, H, 0, K)
+    assert torch.equal(hT, h0)
+
+
+@pytest.mark.parametrize("cfg", ["config2", "config5"])
+def test_wkv_baseline_configs(pkg, cfg):
+    """BASELINE.json configs 2 and 5 at full size (B=8,H=32,T=4096 / B=1,H=32,T=32768 with
+    h0 and a final-state gradient)."""
+    if cfg == "config2":
+        x = _inputs(8, 32, 4096, seed=2)
+        args = (1.0, False, False)
+    else:
+        x = _inputs(1, 32, 32768, seed=5)
+        args = (1.0, True, True)
+    got = run_gpu(pkg, x, *args)
+    ref = run_oracle(x, *args)
+    names = ["o", "hT", "dr", "dk", "dv", "dw", "du"] + (["dh0"] if args[1] else [])
+    _compare(got, ref, names)
