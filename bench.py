@@ -1,0 +1,192 @@
+"""Benchmark of the RWKV-6 WKV6 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload ("config 2"): WKV6 forward + backward at
+B=8, H=32, T=4096, K=V=64, bf16 r/k/v/w, fp32 u, h0 = 0, final state returned,
+dO ~ N(0,1).  One step = one forward and one backward of chunk_rwkv6 through
+the C ABI, inputs already resident in HBM.  value = tokens (B*T) per second.
+
+Also reported:
+  * per-phase kernel times, measured live with HIP events recorded by the
+    library on the stream the kernels run on (rwkv6_wkv_*_ex);
+  * roofline of the dominant kernel (HBM-bound): algorithmic bytes per launch
+    (reads r,k,v,w,dO + writes dr,dk,dv,dw = 1152 B per token-head) over its
+    average event-timed duration, against 8 TB/s;
+  * TFLOP/s of the whole op (fwd 32768 + bwd 65536 FLOP per token-head) and the
+    fraction of the 2.5 PFLOP/s dense bf16 MFMA peak;
+  * cpu_baseline: the CPU oracle (fp64 naive recurrence, C + OpenMP, a port of
+    fla's naive recurrent RWKV-6) timed on this host on the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "WKV6 fwd+bwd ms & % MFMA peak; RWKV6-1.6B-shape train tokens/s, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FLOP_FWD = 32768          # per token-head, chunk 64, full tiles (2*64*(K+V) + 4*K*V)
+FLOP_BWD = 65536
+BYTES_BWD_GRADS = 1152    # per token-head: read r,k,v,w,dO, write dr,dk,dv,dw (bf16, K=V=64)
+BYTES_FWD = 640           # per token-head: read r,k,v,w, write o
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--B", type=int, default=8)
+    ap.add_argument("--H", type=int, default=32)
+    ap.add_argument("--T", type=int, default=4096)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-heads", type=int, default=0,
+                    help="(b,h) sequences in the CPU sample (0 = the whole workload)")
+    return ap.parse_args()
+
+
+def cpu_baseline(B, H, T, sample_heads):
+    """Time the CPU oracle (fwd + bwd) on this host; returns the reported dict."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    n = B * H if sample_heads <= 0 else min(sample_heads, B * H)
+    Hs = min(H, n)
+    Bs = max(1, n // Hs)
+    rng = np.random.default_rng(0)
+    K = 64
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    r, k, v, dO = f(Bs, Hs, T, K), f(Bs, Hs, T, K), f(Bs, Hs, T, K), f(Bs, Hs, T, K)
+    w = -np.exp(rng.uniform(-6, -0.5, (Bs, Hs, T, K))).astype(np.float32)
+    u = (0.1 * f(Hs, K)).astype(np.float32)
+    threads = orc.max_threads()
+    # warm up on a short prefix, then one timed run
+    orc.wkv6_fwd(r[:, :, :64], k[:, :, :64], v[:, :, :64], w[:, :, :64], u)
+    t0 = time.perf_counter()
+    orc.wkv6_fwd(r, k, v, w, u)
+    orc.wkv6_bwd(r, k, v, w, u, dO)
+    dt = time.perf_counter() - t0
+    frac = (Bs * Hs) / (B * H)
+    tokens_per_s = (B * T) * frac / dt
+    return {
+        "value": tokens_per_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": f"oracle fp64 naive recurrence fwd+bwd over {Bs*Hs} of {B*H} (b,h) sequences "
+                  f"at T={T} ({dt:.2f} s), scaled to the whole B={B},H={H} job",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the WKV6 path shards over B and H "
+              "with no exchange; multi-GPU runs are out of scope).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    pkg = importlib.import_module("rwkv-megatron_amd")
+    L = pkg._lib.load()
+    dev = torch.device("cuda:0")
+    B, H, T, K = args.B, args.H, args.T, 64
+    N_th = B * H * T
+
+    g = torch.Generator().manual_seed(0)
+    bf = lambda t: t.to(torch.bfloat16).to(dev)
+    r, k, v = (bf(torch.randn(B, H, T, K, generator=g)) for _ in range(3))
+    w = bf(-torch.exp(torch.rand(B, H, T, K, generator=g) * 5.5 - 6.0))
+    u = (0.1 * torch.randn(H, K, generator=g)).to(dev)
+    do = bf(torch.randn(B, H, T, K, generator=g))
+
+    NT = (T + 63) // 64
+    saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, K, K), dtype=torch.uint8, device=dev)
+    ws_f = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 0), dtype=torch.uint8, device=dev)
+    ws_b = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    hT = torch.empty(B, H, K, K, dtype=torch.float32, device=dev)
+    dr, dk, dv, dw = (torch.empty_like(r) for _ in range(4))
+    du = torch.empty(H, K, dtype=torch.float32, device=dev)
+    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def step(fev=None, bev=None):
+        fa = (ctypes.c_void_p * 6)(*[e.cuda_event for e in fev]) if fev else None
+        ba = (ctypes.c_void_p * 8)(*[e.cuda_event for e in bev]) if bev else None
+        pkg._lib.check(L.rwkv6_wkv_fwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, None, P(o),
+                                          P(hT), P(saved), P(ws_f), B, H, T, K, K, 1.0, sp, fa), "fwd")
+        pkg._lib.check(L.rwkv6_wkv_bwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, P(do), None,
+                                          P(saved), P(dr), P(dk), P(dv), P(dw), P(du), None, P(ws_b),
+                                          B, H, T, K, K, 1.0, sp, ba), "bwd")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    fevs = [[ev() for _ in range(6)] for _ in range(args.steps)]
+    bevs = [[ev() for _ in range(8)] for _ in range(args.steps)]
+    t0 = ev()
+    t1 = ev()
+    for e in [x for evs in fevs + bevs for x in evs]:
+        e.record(stream)               # torch creates the hipEvent_t on first record
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(args.steps):
+        step(fevs[i], bevs[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+    avg = lambda evs, a, b: sum(e[a].elapsed_time(e[b]) for e in evs) / len(evs)
+    fwd_ph = [avg(fevs, 2 * p, 2 * p + 1) for p in range(3)]
+    bwd_ph = [avg(bevs, 2 * p, 2 * p + 1) for p in range(4)]
+    fwd_ms = avg(fevs, 0, 5)
+    bwd_ms = avg(bevs, 0, 7)
+
+    grads_ms = bwd_ph[2]
+    achieved = N_th * BYTES_BWD_GRADS / (grads_ms * 1e-3) / 1e9
+    flops = N_th * (FLOP_FWD + FLOP_BWD)
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    alg_bytes = N_th * (BYTES_FWD + BYTES_BWD_GRADS)
+    out = {
+        "metric": METRIC,
+        "value": B * T / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "WKV6 fwd+bwd, BASELINE config 2 (chunk_rwkv6 via C ABI)",
+                   "B": B, "H": H, "T": T, "K": K, "V": K, "h0": None, "output_final_state": True,
+                   "parallelism": "single GPU"},
+        "wkv6_fwd_ms": fwd_ms,
+        "wkv6_bwd_ms": bwd_ms,
+        "wkv6_tflops": tflops,
+        "wkv6_pct_bf16_mfma_peak": 100.0 * tflops / BF16_PEAK_TFLOPS,
+        "wkv6_alg_hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "phase_ms": {"fwd_chunk_state": fwd_ph[0], "fwd_state_scan": fwd_ph[1],
+                     "fwd_chunk_output": fwd_ph[2], "bwd_chunk_dstate": bwd_ph[0],
+                     "bwd_dstate_scan": bwd_ph[1], "bwd_chunk_grads": bwd_ph[2],
+                     "bwd_du_reduce": bwd_ph[3]},
+        "roofline": {"kernel": "wkv6_bwd_chunk_grads", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, H, T, args.cpu_sample_heads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

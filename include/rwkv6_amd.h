@@ -125,6 +125,24 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
                       void* workspace, int64_t T, int64_t B, int64_t H, int64_t K,
                       void* stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement variants (no counterpart in the reference): identical to
+ * rwkv6_wkv_fwd / rwkv6_wkv_bwd, and additionally record caller-created timing
+ * hipEvent_t objects around each kernel phase on `stream` (phase_events may be
+ * NULL, and so may any entry).  Index pairs (2p, 2p+1) bracket phase p:
+ *   fwd: 0 chunk-local states, 1 state scan, 2 chunk outputs
+ *   bwd: 0 chunk-local dstates, 1 dstate scan, 2 chunk gradients, 3 du reduction
+ * ---------------------------------------------------------------------- */
+int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const float* h0, void* o, float* hT, void* saved,
+                     void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                     float scale, void* stream, void* const* phase_events);
+int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                     void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
+                     int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                     void* stream, void* const* phase_events);
+
 #ifdef __cplusplus
 }
 #endif

@@ -231,6 +231,24 @@ def gn_gate_bwd(o, g_pre, groups, gamma, beta, eps, dy):
     return do.reshape(N, C), dg_pre, dgamma, dbeta
 
 
+def bottleneck_bwd(x, w_down, w_up, dm):
+    """Backward of ``bottleneck_fwd`` for dm = dL/d(output) [T,B,E,C].
+
+    Returns (dx [T,B,C], d_w_down [C,E,R], d_w_up [E,R,C], d_bias [E,C]).
+    """
+    x = np.asarray(x, np.float64)
+    wd = np.asarray(w_down, np.float64)
+    wu = np.asarray(w_up, np.float64)
+    dm = np.asarray(dm, np.float64)
+    neck = np.tanh(np.einsum("tbd,der->tber", x, wd))
+    d_bias = dm.sum(axis=(0, 1))
+    d_wu = np.einsum("tber,tbed->erd", neck, dm)
+    d_pre = np.einsum("tbed,erd->tber", dm, wu) * (1.0 - neck ** 2)
+    d_wd = np.einsum("tbd,tber->der", x, d_pre)
+    dx = np.einsum("tber,der->tbd", d_pre, wd)
+    return dx, d_wd, d_wu, d_bias
+
+
 def bottleneck_fwd(x, w_down, w_up, bias):
     """tanh(x . W_down) . W_up + bias  (rwkv6_layer_specs.py:177-195, TP=1).
 

@@ -4,9 +4,12 @@ The package directory name carries a dash, so load it with
 ``importlib.import_module("rwkv-megatron_amd")``.
 
 Exports
-  chunk_rwkv6, fused_recurrent_rwkv6   fla-compatible WKV6 ops (HIP kernels)
+  chunk_rwkv6, fused_recurrent_rwkv6   fla-compatible WKV6 ops (wkv.py, HIP kernels)
+  timemix                              fused token-shift/ddlerp and GroupNorm*gate ops
+  modules                              RWKV6TimeMix / RWKV6ChannelMix / ... mirrors of
+                                       rwkv_megatron/rwkv6_layer_specs.py
 """
 from .wkv import chunk_rwkv6, fused_recurrent_rwkv6  # noqa: F401
-from . import _lib  # noqa: F401
+from . import _lib, timemix, modules  # noqa: F401
 
-__all__ = ["chunk_rwkv6", "fused_recurrent_rwkv6"]
+__all__ = ["chunk_rwkv6", "fused_recurrent_rwkv6", "timemix", "modules"]

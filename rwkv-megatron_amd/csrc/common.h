@@ -41,6 +41,19 @@ __device__ __forceinline__ void unpack4(uint2 q, float* f) {
     f[2] = __uint_as_float(q.y << 16); f[3] = __uint_as_float(q.y & 0xffff0000u);
 }
 
+// Splits fp32 values into bf16 hi + lo parts (hi + lo carries ~16 mantissa bits):
+// an MFMA against both parts keeps operand rounding out of cancelling sums.
+template <int N>
+__device__ __forceinline__ void split_bf16(const float* f,
+                                           __bf16 __attribute__((ext_vector_type(N))) & hi,
+                                           __bf16 __attribute__((ext_vector_type(N))) & lo) {
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+        hi[s] = (__bf16)f[s];
+        lo[s] = (__bf16)(f[s] - (float)hi[s]);
+    }
+}
+
 __device__ __forceinline__ float warp_sum4(float v) {
     // sum over groups of 4 consecutive lanes
     v += __shfl_xor(v, 1);

@@ -19,7 +19,10 @@
 //   so both factors are <= 1; diagonal blocks use the block midpoint, so each
 //   factor is bounded by the decay of 8 tokens (finite while 8 consecutive
 //   log-decays sum to > -88, i.e. |w| < ~11 per token).
-// Every MFMA accumulates in fp32; the carried states are fp32.
+// Every MFMA accumulates in fp32; the carried states are fp32.  In the dr / dk
+// contractions the decay-scaled operand is split into bf16 hi + lo parts: dw is a
+// cancelling suffix sum of r*dr - k*dk, and single-bf16 operands there would
+// dominate its error.
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
@@ -479,10 +482,12 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float sc = bW ? ex2(bW[i]) : 1.f;
             float sf[8];
             unpack8(*reinterpret_cast<const uint4*>(&sm.Sm[i][j0]), sf);
-            bf16x8 b;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) b[s] = (__bf16)(sf[s] * sc);
-            accR[ti] = mfma32(a, b, accR[ti]);
+            for (int s = 0; s < 8; ++s) sf[s] *= sc;
+            bf16x8 bh, bl;
+            split_bf16<8>(sf, bh, bl);
+            accR[ti] = mfma32(a, bh, accR[ti]);
+            accR[ti] = mfma32(a, bl, accR[ti]);
         }
     }
     for (int J = 0; J <= W; ++J) {
@@ -508,11 +513,17 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const int i = 16 * ti + lr;
             float kf[4];
             unpack4(*reinterpret_cast<const uint2*>(&sm.Kt[i][tau0]), kf);
-            bf16x4 b;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) b[s] = (__bf16)(kf[s] * ex2(ref[i] - sm.GtX[i][tau0 + s + 1]));
-            if (diag) accRd[ti] = mfma16(aop, b, accRd[ti]);
-            else accR[ti] = mfma16(aop, b, accR[ti]);
+            for (int s = 0; s < 4; ++s) kf[s] *= ex2(ref[i] - sm.GtX[i][tau0 + s + 1]);
+            bf16x4 bh, bl;
+            split_bf16<4>(kf, bh, bl);
+            if (diag) {
+                accRd[ti] = mfma16(aop, bh, accRd[ti]);
+                accRd[ti] = mfma16(aop, bl, accRd[ti]);
+            } else {
+                accR[ti] = mfma16(aop, bh, accR[ti]);
+                accR[ti] = mfma16(aop, bl, accR[ti]);
+            }
         }
     }
     // ---------------- dk (source rows tau in W) ----------------
@@ -527,10 +538,12 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float sc = ex2(g63[i] - eW[i]);
             float sf[8];
             unpack8(*reinterpret_cast<const uint4*>(&sm.dSm[i][j0]), sf);
-            bf16x8 b;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) b[s] = (__bf16)(sf[s] * sc);
-            accK[ti] = mfma32(a, b, accK[ti]);
+            for (int s = 0; s < 8; ++s) sf[s] *= sc;
+            bf16x8 bh, bl;
+            split_bf16<8>(sf, bh, bl);
+            accK[ti] = mfma32(a, bh, accK[ti]);
+            accK[ti] = mfma32(a, bl, accK[ti]);
         }
     }
     for (int I = W; I < 4; ++I) {
@@ -556,11 +569,17 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const int i = 16 * ti + lr;
             float rf[4];
             unpack4(*reinterpret_cast<const uint2*>(&sm.Rt[i][tt0]), rf);
-            bf16x4 b;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) b[s] = (__bf16)(rf[s] * ex2(sm.GtX[i][tt0 + s] - ref[i]));
-            if (diag) accKd[ti] = mfma16(aop, b, accKd[ti]);
-            else accK[ti] = mfma16(aop, b, accK[ti]);
+            for (int s = 0; s < 4; ++s) rf[s] *= ex2(sm.GtX[i][tt0 + s] - ref[i]);
+            bf16x4 bh, bl;
+            split_bf16<4>(rf, bh, bl);
+            if (diag) {
+                accKd[ti] = mfma16(aop, bh, accKd[ti]);
+                accKd[ti] = mfma16(aop, bl, accKd[ti]);
+            } else {
+                accK[ti] = mfma16(aop, bh, accK[ti]);
+                accK[ti] = mfma16(aop, bl, accK[ti]);
+            }
         }
     }
     // ---------------- dv (source rows tau in W) ----------------
@@ -675,17 +694,26 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     store_tile(dw + base, sm.Dt, nvalid);
 }
 
-// du[h][i] = sum_b sum_c du_part[b,h,c,i]   (fixed order: deterministic)
-__global__ void wkv6_du_reduce(const float* __restrict__ du_part, void* __restrict__ du,
-                               int u_dtype, int B, int H, int NT) {
-    const int h = blockIdx.x, i = threadIdx.x;
+// du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q): strided partial sum over the
+// B*NT (b, c) pairs with p = q mod 4, then a fixed-order combine (deterministic).
+__global__ void __launch_bounds__(NTHR)
+wkv6_du_reduce(const float* __restrict__ du_part, void* __restrict__ du, int u_dtype, int B,
+               int H, int NT) {
+    __shared__ float part[4][KD];
+    const int h = blockIdx.x, i = threadIdx.x & 63, q = threadIdx.x >> 6;
     float acc = 0.f;
-    for (int b = 0; b < B; ++b) {
-        const float* p = du_part + ((size_t)(b * H + h) * NT) * KD + i;
-        for (int c = 0; c < NT; ++c) acc += p[(size_t)c * KD];
+    const int P = B * NT;
+    for (int p = q; p < P; p += 4) {
+        const int b = p / NT, c = p - b * NT;
+        acc += du_part[((size_t)(b * H + h) * NT + c) * KD + i];
     }
-    if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[h * KD + i] = f2bf(acc);
-    else reinterpret_cast<float*>(du)[h * KD + i] = acc;
+    part[q][i] = acc;
+    __syncthreads();
+    if (q == 0) {
+        const float tot = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+        if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[h * KD + i] = f2bf(tot);
+        else reinterpret_cast<float*>(du)[h * KD + i] = tot;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -710,6 +738,11 @@ int launch_status() {
     return e == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH;
 }
 
+// Records phase_events[i] (a hipEvent_t) on the stream when the caller asked for timing.
+inline void mark(void* const* ev, int i, hipStream_t s) {
+    if (ev && ev[i]) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -730,10 +763,10 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
     return sz;
 }
 
-int rwkv6_wkv_fwd(const void* r, const void* k, const void* v, const void* w, const void* u,
-                  int u_dtype, const float* h0, void* o, float* hT, void* saved,
-                  void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
-                  float scale, void* stream) {
+int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const float* h0, void* o, float* hT, void* saved,
+                     void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                     float scale, void* stream, void* const* phase_events) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
@@ -749,28 +782,34 @@ int rwkv6_wkv_fwd(const void* r, const void* k, const void* v, const void* w, co
     float* decay = reinterpret_cast<float*>(reinterpret_cast<char*>(saved) +
                                             round_up((size_t)BH * (NT + 1) * KD * KD * 2));
     float* Sloc = reinterpret_cast<float*>(workspace);
+    mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
         hipLaunchKernelGGL(wkv6_fwd_chunk_state, grid, dim3(NTHR), 0, s,
                            (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, Sloc, decay,
                            (int)T, (int)NT);
     }
+    mark(phase_events, 1, s);
+    mark(phase_events, 2, s);
     hipLaunchKernelGGL(wkv6_state_scan_fwd, dim3((unsigned)BH * 16), dim3(NTHR), 0, s, Sloc, decay,
                        h0, Hs, hT, (int)NT);
+    mark(phase_events, 3, s);
+    mark(phase_events, 4, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
         hipLaunchKernelGGL(wkv6_fwd_chunk_output, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
                            (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, u, u_dtype,
                            (const uint16_t*)Hs, (uint16_t*)o, scale, (int)H, (int)T, (int)NT);
     }
+    mark(phase_events, 5, s);
     return launch_status();
 }
 
-int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, const void* u,
-                  int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
-                  void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
-                  int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
-                  void* stream) {
+int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                     void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
+                     int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                     void* stream, void* const* phase_events) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
@@ -793,31 +832,56 @@ int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, co
                                                 round_up((size_t)BH * NTa * KD * KD * 4));
     float* du_part = reinterpret_cast<float*>(reinterpret_cast<char*>(dHs) +
                                               round_up((size_t)BH * NTa * KD * KD * 2));
+    mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
         hipLaunchKernelGGL(wkv6_bwd_chunk_dstate, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
                            (const uint16_t*)w, (const uint16_t*)dO, dSloc, scale, (int)T, (int)NT);
     }
+    mark(phase_events, 1, s);
+    mark(phase_events, 2, s);
     hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * 16), dim3(NTHR), 0, s, dSloc,
                        decay, dhT, dHs, dh0, (int)NT);
+    mark(phase_events, 3, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)sizeof(BwdSmem)) != hipSuccess)
             return RWKV6_ERR_LAUNCH;
+        mark(phase_events, 4, s);
         hipLaunchKernelGGL(wkv6_bwd_chunk_grads, grid, dim3(NTHR), sizeof(BwdSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, Hs,
                            (const uint16_t*)dHs, (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv,
                            (uint16_t*)dw, du_part, scale, (int)H, (int)T, (int)NT);
-        hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(KD), 0, s, du_part, du, u_dtype,
+        mark(phase_events, 5, s);
+        mark(phase_events, 6, s);
+        hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(NTHR), 0, s, du_part, du, u_dtype,
                            (int)B, (int)H, (int)NT);
+        mark(phase_events, 7, s);
     } else {
         if (hipMemsetAsync(du, 0, (size_t)H * KD * (u_dtype == RWKV6_BF16 ? 2 : 4), s) != hipSuccess)
             return RWKV6_ERR_LAUNCH;
     }
     return launch_status();
+}
+
+int rwkv6_wkv_fwd(const void* r, const void* k, const void* v, const void* w, const void* u,
+                  int u_dtype, const float* h0, void* o, float* hT, void* saved,
+                  void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                  float scale, void* stream) {
+    return rwkv6_wkv_fwd_ex(r, k, v, w, u, u_dtype, h0, o, hT, saved, workspace, B, H, T, K, V,
+                            scale, stream, nullptr);
+}
+
+int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, const void* u,
+                  int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                  void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
+                  int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                  void* stream) {
+    return rwkv6_wkv_bwd_ex(r, k, v, w, u, u_dtype, dO, dhT, saved, dr, dk, dv, dw, du, dh0,
+                            workspace, B, H, T, K, V, scale, stream, nullptr);
 }
 
 }  // extern "C"

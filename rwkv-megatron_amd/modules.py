@@ -1,0 +1,269 @@
+"""Host-side mirror of the reference's RWKV-6 layer modules (TP = 1, one GPU).
+
+Same class names, constructor/forward contracts and parameter names/shapes as
+/root/reference/rwkv_megatron/rwkv6_layer_specs.py, so state_dicts load either
+way (Megatron's module prefix aside).  The hot path runs on the HIP kernels:
+
+  RWKV6TimeMix.forward  (:431-468)
+    token shift + lerp + LoRA + ddlerp   -> timemix.token_shift_mix   (HIP + hipBLASLt)
+    decay LoRA, r/k/v/gate projections   -> torch.matmul (hipBLASLt)
+    WKV6                                 -> wkv.chunk_rwkv6           (HIP)
+    GroupNorm * silu(gate)               -> timemix.group_norm_gate   (HIP, head-first read)
+    output projection                    -> torch.matmul
+
+Deliberate differences, all documented in the reference's own terms:
+  * ``mix_coeff_input`` and ``RWKV6ChannelMix.mix_coeffs`` are left uninitialised by
+    the reference (torch.empty, :377-385, :475-477); here they get the RWKV-6 ramp
+    ``1 - (c / C) ** (1 - l / L)`` so a freshly built model is finite.
+  * Biases on the linear layers are absent (config ``add_bias_linear = False``,
+    the reference's example config), matching ``bias=...add_bias_linear`` (:393, :416).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import timemix
+from .wkv import chunk_rwkv6
+
+
+@dataclass
+class TransformerConfig:
+    """The fields of Megatron's TransformerConfig that the RWKV-6 layers read."""
+    hidden_size: int = 2048
+    num_attention_heads: int = 32
+    ffn_hidden_size: int = 7168
+    num_layers: int = 24
+    layernorm_epsilon: float = 1e-5              # example_config.yaml:18, used by GroupNorm (:68)
+    token_shift_bottleneck_size: int = 32        # example_config.yaml:8
+    decay_bottleneck_size: int = 64              # example_config.yaml:9
+    init_method_std: float = 0.02                # example_config.yaml:31
+    params_dtype: torch.dtype = torch.bfloat16
+    perform_initialization: bool = True
+
+
+def _ramp(C, layer_id, n_layers, device):
+    ratio = 1.0 - layer_id / max(n_layers, 1)
+    ddd = torch.arange(C, dtype=torch.float32, device=device) / C
+    return 1.0 - torch.pow(ddd, ratio)
+
+
+class _Linear(nn.Module):
+    """Column/RowParallelLinear at TP=1: weight [out, in], y = x @ W^T (no bias)."""
+
+    def __init__(self, cfg, n_in, n_out, std, device):
+        super().__init__()
+        self.weight = nn.Parameter(torch.empty(n_out, n_in, device=device, dtype=cfg.params_dtype))
+        if cfg.perform_initialization:
+            nn.init.normal_(self.weight, 0.0, std)
+
+    def forward(self, x):
+        return F.linear(x, self.weight.to(x.dtype)), None
+
+
+class GroupNorm(nn.Module):
+    """rwkv6_layer_specs.py:50-109 (eps taken from config.layernorm_epsilon, :68)."""
+
+    def __init__(self, config, num_groups, num_channels, eps=1e-5, device=None):
+        super().__init__()
+        self.num_groups = num_groups
+        self.num_channels = num_channels
+        self.eps = config.layernorm_epsilon
+        self.weight = nn.Parameter(torch.ones(num_channels, device=device, dtype=config.params_dtype))
+        self.bias = nn.Parameter(torch.zeros(num_channels, device=device, dtype=config.params_dtype))
+
+    def forward(self, hidden_states):
+        """Plain GroupNorm over [N, C] (the reference's forward)."""
+        return F.group_norm(hidden_states, self.num_groups, self.weight.to(hidden_states.dtype),
+                            self.bias.to(hidden_states.dtype), eps=self.eps)
+
+
+class RWKV6Bottleneck(nn.Module):
+    """rwkv6_layer_specs.py:112-210 (TP = 1): tanh(x W_down) W_up + bias."""
+
+    def __init__(self, config, bottleneck_size, expansion, to_tensor_parallel, device=None):
+        super().__init__()
+        C = config.hidden_size
+        self.bottleneck_size = bottleneck_size
+        self.expansion = expansion
+        self.to_tensor_parallel = to_tensor_parallel
+        dt = config.params_dtype
+        self.weight_down = nn.Parameter(torch.empty(C, expansion, bottleneck_size, device=device, dtype=dt))
+        self.weight_up = nn.Parameter(torch.empty(expansion, bottleneck_size, C, device=device, dtype=dt))
+        self.bias = nn.Parameter(torch.empty(expansion, C, device=device, dtype=dt))
+        if config.perform_initialization:
+            nn.init.uniform_(self.weight_down, -1e-4, 1e-4)
+            nn.init.uniform_(self.weight_up, -1e-4, 1e-4)
+            nn.init.uniform_(self.bias, -1, 1)
+
+    def forward(self, x):
+        """[T,B,C] -> [T,B,E,C] (reference layout, :177-195)."""
+        T, B, C = x.shape
+        neck = torch.tanh(x.reshape(T * B, C) @ self.weight_down.to(x.dtype).reshape(C, -1))
+        neck = neck.view(T * B, self.expansion, self.bottleneck_size).transpose(0, 1).contiguous()
+        up = torch.bmm(neck, self.weight_up.to(x.dtype).contiguous())          # [E, N, C]
+        return up.transpose(0, 1).reshape(T, B, self.expansion, C) + self.bias.to(x.dtype)
+
+
+class WKV6(nn.Module):
+    """rwkv6_layer_specs.py:303-353: time_first [C] (N(1, 0.02)), forward over [T,B,C]."""
+
+    def __init__(self, config, layer_number=1, device=None):
+        super().__init__()
+        self.num_heads_local = config.num_attention_heads
+        self.time_first = nn.Parameter(torch.empty(config.hidden_size, device=device,
+                                                   dtype=config.params_dtype))
+        if config.perform_initialization:
+            nn.init.normal_(self.time_first, mean=1.0, std=0.02)
+
+    def head_first(self, r, k, v, decay):
+        """Layout glue of :333-337: [T,B,(h n)] -> [B,h,T,n]; w = -exp(decay)."""
+        H = self.num_heads_local
+        T, B, C = r.shape
+        hf = lambda t: t.view(T, B, H, C // H).permute(1, 2, 0, 3).contiguous()
+        w = hf(-torch.exp(decay.float())).to(torch.bfloat16)
+        u = self.time_first.view(H, C // H)
+        return hf(r), hf(k), hf(v), w, u
+
+    def forward(self, r, k, v, w):
+        """Reference contract: returns [T,B,C]."""
+        rr, kk, vv, ww, u = self.head_first(r, k, v, w)
+        o, _ = chunk_rwkv6(rr, kk, vv, ww, u, scale=1.0)
+        T, B, C = r.shape
+        return o.permute(2, 0, 1, 3).reshape(T, B, C)
+
+
+class RWKV6TimeMix(nn.Module):
+    """rwkv6_layer_specs.py:356-468 with the hot path on HIP kernels."""
+
+    def __init__(self, config, layer_number=1, device=None):
+        super().__init__()
+        self.config = config
+        C = config.hidden_size
+        self.layer_number = layer_number
+        self.bottleneck_token_shift = RWKV6Bottleneck(config, config.token_shift_bottleneck_size, 5,
+                                                      False, device)
+        self.bottleneck_decay = RWKV6Bottleneck(config, config.decay_bottleneck_size, 1, True, device)
+        self.mix_coeff_input = nn.Parameter(torch.empty(C, device=device, dtype=config.params_dtype))
+        std = config.init_method_std
+        out_std = std / math.sqrt(2.0 * config.num_layers)
+        self.linear_receptance = _Linear(config, C, C, std, device)
+        self.linear_key = _Linear(config, C, C, std, device)
+        self.linear_value = _Linear(config, C, C, std, device)
+        self.linear_gate = _Linear(config, C, C, std, device)
+        self.core_attention = WKV6(config, layer_number, device)
+        self.group_norm = GroupNorm(config, config.num_attention_heads, C, config.layernorm_epsilon, device)
+        self.linear_proj = _Linear(config, C, C, out_std, device)
+        self.num_heads_per_partition = config.num_attention_heads
+        self.head_size = C // config.num_attention_heads
+        if config.perform_initialization:
+            with torch.no_grad():
+                self.mix_coeff_input.copy_(_ramp(C, layer_number - 1, config.num_layers, device))
+                # decay bias: RWKV-6 ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1))
+                L = max(config.num_layers - 1, 1)
+                c = torch.arange(C, dtype=torch.float32, device=device) / max(C - 1, 1)
+                self.bottleneck_decay.bias.copy_((-6 + 5 * c ** (0.7 + 1.3 * (layer_number - 1) / L))[None])
+
+    def forward(self, hidden_states, attention_mask=None, key_value_states=None,
+                inference_params=None, rotary_pos_emb=None, packed_seq_params=None):
+        x = hidden_states
+        T, B, C = x.shape
+        ts = self.bottleneck_token_shift
+        mixed = timemix.token_shift_mix(x, self.mix_coeff_input, ts.weight_down, ts.weight_up, ts.bias)
+        mixed_decay, mixed_key, mixed_value, mixed_receptance, mixed_gate = mixed.unbind(0)
+        decay = self.bottleneck_decay(mixed_decay).squeeze(-2)
+        key = self.linear_key(mixed_key)[0]
+        value = self.linear_value(mixed_value)[0]
+        receptance = self.linear_receptance(mixed_receptance)[0]
+        gate_pre = self.linear_gate(mixed_gate)[0]
+        r, k, v, w, u = self.core_attention.head_first(receptance, key, value, decay)
+        o, _ = chunk_rwkv6(r, k, v, w, u, scale=1.0)
+        y = timemix.group_norm_gate(o, gate_pre, self.group_norm.weight, self.group_norm.bias,
+                                    self.group_norm.eps, head_first=True)
+        output, bias = self.linear_proj(y)
+        return output, bias
+
+
+class RWKV6ChannelMix(nn.Module):
+    """rwkv6_layer_specs.py:471-536 (TP = 1)."""
+
+    def __init__(self, config, layer_number=1, device=None):
+        super().__init__()
+        self.config = config
+        C, Fh = config.hidden_size, config.ffn_hidden_size
+        self.mix_coeffs = nn.Parameter(torch.empty(2, C, device=device, dtype=config.params_dtype))
+        std = config.init_method_std
+        self.linear_up = _Linear(config, C, Fh, std, device)
+        self.linear_gate = _Linear(config, C, C, std, device)
+        self.linear_down = _Linear(config, Fh, C, std / math.sqrt(2.0 * config.num_layers), device)
+        if config.perform_initialization:
+            with torch.no_grad():
+                ramp = _ramp(C, layer_number - 1, config.num_layers, device)
+                self.mix_coeffs.copy_(torch.stack([ramp, ramp]))
+
+    def forward(self, hidden_states):
+        x = hidden_states
+        shifted = torch.cat([torch.zeros_like(x[:1]), x[:-1]], 0)
+        delta = shifted - x
+        mixed = x.unsqueeze(-2) + delta.unsqueeze(-2) * self.mix_coeffs.to(x.dtype)
+        mixed_up, mixed_gate = mixed.unbind(-2)
+        h = torch.square(torch.relu(self.linear_up(mixed_up.contiguous())[0]))
+        out = self.linear_down(h)[0]
+        gate = torch.sigmoid(self.linear_gate(mixed_gate.contiguous())[0])
+        return out * gate, None
+
+
+class RWKV6Layer(nn.Module):
+    """The TransformerLayer that get_rwkv6_layer_spec() builds (:539-550):
+    LN -> time mix -> residual -> LN -> channel mix -> residual (dropout 0)."""
+
+    def __init__(self, config, layer_number=1, device=None):
+        super().__init__()
+        C = config.hidden_size
+        self.input_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device,
+                                            dtype=config.params_dtype)
+        self.self_attention = RWKV6TimeMix(config, layer_number, device)
+        self.pre_mlp_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device,
+                                              dtype=config.params_dtype)
+        self.mlp = RWKV6ChannelMix(config, layer_number, device)
+
+    def forward(self, x):
+        a, _ = self.self_attention(self.input_layernorm(x), None)
+        x = x + a
+        m, _ = self.mlp(self.pre_mlp_layernorm(x))
+        return x + m
+
+
+def get_rwkv6_layer_spec():
+    """Mirror of rwkv6_layer_specs.py:539-550 as a plain description (no Megatron here)."""
+    return dict(module=RWKV6Layer,
+                submodules=dict(input_layernorm=nn.LayerNorm, self_attention=RWKV6TimeMix,
+                                pre_mlp_layernorm=nn.LayerNorm, mlp=RWKV6ChannelMix))
+
+
+class RWKV6Model(nn.Module):
+    """One-GPU RWKV-6 LM mirroring RWKV6Model (rwkv6_model.py:28-184): embedding ->
+    pre_norm (ln0, :34-37, :108-112) -> layers -> final LayerNorm -> untied output head."""
+
+    def __init__(self, config, vocab_size, device=None):
+        super().__init__()
+        C = config.hidden_size
+        dt = config.params_dtype
+        self.embedding = nn.Embedding(vocab_size, C, device=device, dtype=dt)
+        nn.init.normal_(self.embedding.weight, 0.0, config.init_method_std)
+        self.pre_norm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
+        self.layers = nn.ModuleList(RWKV6Layer(config, i + 1, device) for i in range(config.num_layers))
+        self.final_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
+        self.output_layer = nn.Linear(C, vocab_size, bias=False, device=device, dtype=dt)
+        nn.init.normal_(self.output_layer.weight, 0.0, config.init_method_std)
+
+    def forward(self, tokens):
+        """tokens [B,T] -> logits [T,B,V] (sequence-first inside, as Megatron)."""
+        x = self.pre_norm(self.embedding(tokens.t()))
+        for layer in self.layers:
+            x = layer(x)
+        return self.output_layer(self.final_layernorm(x))

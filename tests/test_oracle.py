@@ -251,3 +251,20 @@ def test_bottleneck_matches_einops_pattern():
     ref = torch.stack([neck[:, :, e] @ wu[e] for e in range(E)], dim=2) + b
     got = orc.bottleneck_fwd(x.numpy(), wd.numpy(), wu.numpy(), b.numpy())
     assert _rel(got, ref) < 1e-12
+
+
+def test_bottleneck_backward_matches_autograd():
+    T, B, C, E, R = 4, 3, 10, 5, 3
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(T, B, C, generator=g, dtype=torch.float64, requires_grad=True)
+    wd = torch.randn(C, E, R, generator=g, dtype=torch.float64, requires_grad=True)
+    wu = torch.randn(E, R, C, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(E, C, generator=g, dtype=torch.float64, requires_grad=True)
+    neck = torch.tanh(torch.einsum("tbd,der->tber", x, wd))
+    m = torch.einsum("tber,erd->tbed", neck, wu) + b
+    dm = torch.randn_like(m)
+    (m * dm).sum().backward()
+    n = lambda t: t.detach().numpy()
+    dx, dwd, dwu, db = orc.bottleneck_bwd(n(x), n(wd), n(wu), n(dm))
+    for got, ref in ((dx, x.grad), (dwd, wd.grad), (dwu, wu.grad), (db, b.grad)):
+        assert _rel(got, ref) < 1e-12

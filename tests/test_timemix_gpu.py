@@ -1,0 +1,140 @@
+"""GPU parity of the fused time-mix kernels (token shift / lerp / ddlerp, GroupNorm*gate)
+against the numpy oracle on identical bf16 inputs.
+
+Tolerance: max|gpu - oracle| / max|oracle| <= 1e-2 and relative L2 <= 1e-2 for the
+elementwise kernels (their only rounding is the bf16 store); the LoRA weight
+gradients go through bf16 hipBLASLt GEMMs and use 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _n(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return (np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30),
+            np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def _check(name, got, ref, tol=1e-2):
+    e = _err(got, ref)
+    print(f"{name}: {e[0]:.1e}/{e[1]:.1e}")
+    assert e[0] <= tol and e[1] <= tol, (name, e)
+
+
+def _bf(t):
+    return t.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 8), (7, 3, 64), (130, 2, 512)])
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+def test_shift_lerp_and_ddlerp(pkg, shape, pdt):
+    T, B, C = shape
+    g = torch.Generator().manual_seed(T + C)
+    x = _bf(torch.randn(T, B, C, generator=g))
+    maa = torch.rand(C, generator=g).to(pdt)
+    mexp = _bf(torch.randn(5, T, B, C, generator=g))
+    bias = torch.randn(5, C, generator=g).to(pdt)
+    xxx = pkg.timemix.shift_lerp(x.to(DEV), maa.to(DEV))
+    mixed = pkg.timemix.ddlerp(x.to(DEV), mexp.to(DEV), bias.to(DEV))
+    torch.cuda.synchronize()
+    _check("xxx", _n(xxx), orc.shift_lerp_fwd(_n(x), _n(maa)))
+    _check("mixed", _n(mixed), orc.ddlerp_fwd(_n(x), np.moveaxis(_n(mexp), 0, 2), _n(bias)))
+
+
+@pytest.mark.parametrize("T,B,C", [(5, 2, 64), (70, 3, 256)])
+def test_token_shift_mix_forward_backward(pkg, T, B, C):
+    R = 32
+    g = torch.Generator().manual_seed(C)
+    x = _bf(torch.randn(T, B, C, generator=g))
+    maa = torch.rand(C, generator=g)
+    wd = torch.empty(C, 5, R).uniform_(-0.1, 0.1, generator=g)
+    wu = torch.empty(5, R, C).uniform_(-0.1, 0.1, generator=g)
+    bias = torch.empty(5, C).uniform_(-1, 1, generator=g)
+    dmix = _bf(torch.randn(5, T, B, C, generator=g))
+    # the GEMMs run in bf16: give the oracle the same bf16-rounded weights
+    wd_b, wu_b = _bf(wd), _bf(wu)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x, maa, wd_b, wu_b, bias)]
+    mixed = pkg.timemix.token_shift_mix(*leaves)
+    (mixed.float() * dmix.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    xn, maan, wdn, wun, bn = (_n(t) for t in (x, maa, wd_b, wu_b, bias))
+    xxx = orc.shift_lerp_fwd(xn, maan)
+    m = orc.bottleneck_fwd(xxx, wdn, wun, np.zeros_like(bn))           # [T,B,5,C] without bias
+    ref_mixed = orc.ddlerp_fwd(xn, m, bn)
+    _check("mixed", _n(mixed), ref_mixed)
+    dmn = _n(dmix)
+    _, d_m, _, _ = orc.mix_bwd(xn, maan, m, bn, dmn, np.zeros_like(xn))
+    d_xxx, d_wd, d_wu, _ = orc.bottleneck_bwd(xxx, wdn, wun, d_m)
+    dx, _, d_bias, d_maa = orc.mix_bwd(xn, maan, m, bn, dmn, d_xxx)
+    _check("dx", _n(leaves[0].grad), dx)
+    _check("d_maa", _n(leaves[1].grad), d_maa)
+    _check("d_w_down", _n(leaves[2].grad), d_wd, 2e-2)
+    _check("d_w_up", _n(leaves[3].grad), d_wu, 2e-2)
+    _check("d_bias", _n(leaves[4].grad), d_bias)
+
+
+@pytest.mark.parametrize("head_first", [True, False])
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,B,H", [(1, 1, 1), (70, 3, 4), (129, 2, 8)])
+def test_group_norm_gate(pkg, head_first, pdt, T, B, H):
+    K, eps = 64, 1e-5
+    C = H * K
+    g = torch.Generator().manual_seed(T * 10 + H)
+    o_hf = _bf(torch.randn(B, H, T, K, generator=g) * 2 + 0.5)
+    gp = _bf(torch.randn(T, B, C, generator=g))
+    gamma = (1 + 0.3 * torch.randn(C, generator=g)).to(pdt)
+    beta = (0.2 * torch.randn(C, generator=g)).to(pdt)
+    dy = _bf(torch.randn(T, B, C, generator=g))
+    o_tb = o_hf.permute(2, 0, 1, 3).reshape(T, B, C).contiguous()
+    o_in = o_hf if head_first else o_tb
+    leaves = [t.to(DEV).requires_grad_(True) for t in (o_in, gp, gamma, beta)]
+    y = pkg.timemix.group_norm_gate(leaves[0], leaves[1], leaves[2], leaves[3], eps, head_first=head_first)
+    (y.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    on = _n(o_tb).reshape(T * B, C)
+    y_ref, _, _ = orc.gn_gate_fwd(on, _n(gp).reshape(T * B, C), H, _n(gamma), _n(beta), eps)
+    _check("y", _n(y).reshape(T * B, C), y_ref)
+    do, dz, dgam, dbet = orc.gn_gate_bwd(on, _n(gp).reshape(T * B, C), H, _n(gamma), _n(beta), eps,
+                                         _n(dy).reshape(T * B, C))
+    d_o = _n(leaves[0].grad)
+    if head_first:
+        d_o = np.transpose(d_o, (2, 0, 1, 3))
+    _check("d_o", d_o.reshape(T * B, C), do)
+    _check("d_g", _n(leaves[1].grad).reshape(T * B, C), dz)
+    _check("dgamma", _n(leaves[2].grad), dgam)
+    _check("dbeta", _n(leaves[3].grad), dbet)
+
+
+def test_mix_and_gn_deterministic(pkg):
+    T, B, C, H = 200, 3, 256, 4
+    g = torch.Generator().manual_seed(1)
+    x = _bf(torch.randn(T, B, C, generator=g)).to(DEV)
+    params = [torch.rand(C, generator=g), torch.empty(C, 5, 32).uniform_(-0.1, 0.1, generator=g),
+              torch.empty(5, 32, C).uniform_(-0.1, 0.1, generator=g), torch.randn(5, C, generator=g)]
+    o = _bf(torch.randn(B, H, T, 64, generator=g)).to(DEV)
+    gp = _bf(torch.randn(T, B, C, generator=g)).to(DEV)
+
+    def run():
+        ps = [p.to(DEV).requires_grad_(True) for p in params]
+        xi = x.clone().requires_grad_(True)
+        mixed = pkg.timemix.token_shift_mix(xi, *ps)
+        gam = torch.ones(C, device=DEV, requires_grad=True)
+        bet = torch.zeros(C, device=DEV, requires_grad=True)
+        y = pkg.timemix.group_norm_gate(o, gp, gam, bet, 1e-5)
+        (mixed.float().sum() + y.float().square().sum()).backward()
+        return [mixed, y, xi.grad, gam.grad, bet.grad] + [p.grad for p in ps]
+
+    a, b = run(), run()
+    for ta, tb in zip(a, b):
+        assert torch.equal(ta, tb)
