@@ -12,62 +12,126 @@
 //   state_scan_bwd   per (b,h,elem) : dS_out(c-1) = e^{G_63(c)} dS_out(c) + dS_loc(c)
 //   bwd_chunk_grads  per (b,h,chunk): dr, dk, dv, dw, du-partials                        [MFMA]
 //
-// Inside a 64-token chunk G is the inclusive cumulative log-decay (kept in base-2
-// units).  The intra-chunk attention A[t,tau] = sum_i r_t k_tau e^{G_{t-1}-G_tau}
-// is evaluated per 16x16 sub-block with bf16 MFMA on factorised operands:
-//   off-diagonal blocks use a reference point between source and target block,
-//   so both factors are <= 1; diagonal blocks use the block midpoint, so each
-//   factor is bounded by the decay of 8 tokens (finite while 8 consecutive
-//   log-decays sum to > -88, i.e. |w| < ~11 per token).
-// Every MFMA accumulates in fp32; the carried states are fp32.  In the dr / dk
-// contractions the decay-scaled operand is split into bf16 hi + lo parts: dw is a
-// cancelling suffix sum of r*dr - k*dk, and single-bf16 operands there would
-// dominate its error.
+// Inside a 64-token chunk G is the inclusive cumulative log-decay (base-2 units, so
+// every exponential is one v_exp_f32) and a chunk is four 16-token sub-blocks with
+// midpoints mu_I = G[16I+7].  Each chunk kernel first builds, once, the operand tiles
+//   Rm[t] = r_t e^{G_{t-1} - mu_I(t)},      Km[tau] = k_tau e^{mu_J(tau) - G_tau}
+// (bounded by the decay of 8 tokens either way; finite while 8 consecutive log-decays
+// sum to > -88, i.e. |w| < ~11 per token).  The intra-chunk attention is then
+//   A[t][tau] = sum_i Rm[t][i] f_IJ[i] Km[tau][i],   f_IJ = e^{mu_I - mu_J} <= 1 (I > J)
+// on bf16 MFMA; every cross-block factor is a per-channel scalar applied to one
+// operand or to accumulator columns, never a per-element exponential.
+//
+// Operands that reduce over tokens are read from the same token-major LDS tile with
+// the gfx950 LDS transpose read (ds_read_b64_tr_b16), so no tile is stored twice.
+// Every MFMA accumulates in fp32 and the carried states are fp32.  In the dr / dk
+// contractions Rm / Km are bf16 hi + lo pairs: dw is a cancelling suffix sum of
+// r*dr - k*dk, and single-bf16 operands there would dominate its error.
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
 #define KD 64            // head size (K == V)
 #define CL 64            // chunk length (tokens)
 #define TS 72            // LDS row stride of a bf16 64x64 tile (elements): 144 B rows
-#define GS 68            // LDS row stride of a token-major fp32 tile
-#define GXS 68           // LDS row stride of a channel-major fp32 tile (65 used)
+#define GS 72            // LDS row stride of an fp32 64x64 tile (elements)
 #define NTHR 256
+#define NTHR_G 512       // threads of the gradient kernel (8 waves)
 
 typedef uint16_t tile_t[CL][TS];
-typedef float gtile_t[CL][GS];
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // ---------------------------------------------------------------------------
-// tile movement
+// operand fragments
 // ---------------------------------------------------------------------------
+// Fragment convention (16x16 MFMA tiles): lane = 16*q + L.  An A operand supplies
+// row L, a B operand column L; the k-slot s of the operand maps to one reduction
+// index, identically for both operands of a product.
 
-// Global [64 rows][64] bf16 (rows contiguous, 128 B each) -> LDS, optionally also
-// transposed.  Rows >= nvalid read as zero.
-__device__ __forceinline__ void load_tile(uint16_t (*tok)[TS], uint16_t (*tr)[TS],
-                                          const uint16_t* __restrict__ src, int nvalid) {
+// Transposed read of a token-major tile X (row stride TS): the lane receives
+// X[r0 + 4q + s][c0 + L], s = 0..3 -- one column, four consecutive rows.
+__device__ __forceinline__ bf16x4 ld_tr4(const uint16_t* X, int r0, int c0) {
+    const int lane = threadIdx.x & 63;
+    const int L = lane & 15, q = lane >> 4;
+    const uint16_t* p = X + (r0 + 4 * q + (L >> 2)) * TS + c0 + 4 * (L & 3);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
+// 32-row version for the 16x16x32 MFMA: slots 0-3 rows r0+4q+s, slots 4-7 rows r0+16+4q+s.
+__device__ __forceinline__ bf16x8 ld_tr8(const uint16_t* X, int r0, int c0) {
+    const bf16x4 a = ld_tr4(X, r0, c0), b = ld_tr4(X, r0 + 16, c0);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+// Direct read of row `row` with the slot order of ld_tr8: columns c0+4q+(0..3), c0+16+4q+(0..3).
+__device__ __forceinline__ bf16x8 ld_dir8(const uint16_t* X, int row, int c0) {
+    const int q = (threadIdx.x & 63) >> 4;
+    const uint2 a = *reinterpret_cast<const uint2*>(X + row * TS + c0 + 4 * q);
+    const uint2 b = *reinterpret_cast<const uint2*>(X + row * TS + c0 + 16 + 4 * q);
+    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+// Direct 16-byte read of row `row`, columns c0 + 8q .. +7 (products whose operands are both direct).
+__device__ __forceinline__ bf16x8 ld_row8(const uint16_t* X, int row, int c0) {
+    const int q = (threadIdx.x & 63) >> 4;
+    return ld_bf16x8(X + row * TS + c0 + 8 * q);
+}
+// Per-slot fp32 factors in ld_dir8 order from a 64-vector.
+__device__ __forceinline__ void dir8_vec(const float* v, int c0, float* f) {
+    const int q = (threadIdx.x & 63) >> 4;
+    const float4 a = *reinterpret_cast<const float4*>(v + c0 + 4 * q);
+    const float4 b = *reinterpret_cast<const float4*>(v + c0 + 16 + 4 * q);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void row8_vec(const float* v, int c0, float* f) {
+    const int q = (threadIdx.x & 63) >> 4;
+    const float4 a = *reinterpret_cast<const float4*>(v + c0 + 8 * q);
+    const float4 b = *reinterpret_cast<const float4*>(v + c0 + 8 * q + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ bf16x8 scale8(bf16x8 x, const float* f) {
+    bf16x8 y;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        int idx = p * NTHR + threadIdx.x;
-        int row = idx >> 3, c8 = (idx & 7) * 8;
-        uint4 val = make_uint4(0u, 0u, 0u, 0u);
-        if (row < nvalid) val = *reinterpret_cast<const uint4*>(src + (size_t)row * KD + c8);
-        if (tok) *reinterpret_cast<uint4*>(&tok[row][c8]) = val;
-        if (tr) {
-            uint32_t wv[4] = {val.x, val.y, val.z, val.w};
+    for (int s = 0; s < 8; ++s) y[s] = (__bf16)((float)x[s] * f[s]);
+    return y;
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+    uint4 q;
+    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+    return q;
+}
+// hi / lo split of 8 fp32 values, packed
+__device__ __forceinline__ void pack8_split(const float* f, uint4& hi, uint4& lo) {
+    float h[8], l[8];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                tr[c8 + 2 * s][row] = (uint16_t)(wv[s] & 0xffffu);
-                tr[c8 + 2 * s + 1][row] = (uint16_t)(wv[s] >> 16);
-            }
-        }
+    for (int s = 0; s < 8; ++s) {
+        h[s] = bf2f(f2bf(f[s]));
+        l[s] = f[s] - h[s];
     }
+    hi = pack8(h);
+    lo = pack8(l);
 }
 
-// Token-major LDS tile -> global (rows < nvalid).
+// ---------------------------------------------------------------------------
+// tile movement and the chunk cumulative decay
+// ---------------------------------------------------------------------------
+
+// One 16-byte piece per thread per pass: row = idx >> 3, columns 8*(idx & 7) .. +7.
+__device__ __forceinline__ uint4 gload16(const uint16_t* __restrict__ src, int row, int c8,
+                                         int nvalid) {
+    if (row < nvalid) return *reinterpret_cast<const uint4*>(src + (size_t)row * KD + c8);
+    return make_uint4(0u, 0u, 0u, 0u);
+}
+__device__ __forceinline__ void sstore16(uint16_t (*X)[TS], int row, int c8, uint4 v) {
+    *reinterpret_cast<uint4*>(&X[row][c8]) = v;
+}
+
+// Token-major LDS tile -> global (rows < nvalid), nthr threads.
+template <int NT_>
 __device__ __forceinline__ void store_tile(uint16_t* __restrict__ dst, uint16_t (*tok)[TS],
                                            int nvalid) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        int idx = p * NTHR + threadIdx.x;
+    for (int p = 0; p < 512 / NT_; ++p) {
+        int idx = p * NT_ + threadIdx.x;
         int row = idx >> 3, c8 = (idx & 7) * 8;
         if (row < nvalid)
             *reinterpret_cast<uint4*>(dst + (size_t)row * KD + c8) =
@@ -75,18 +139,18 @@ __device__ __forceinline__ void store_tile(uint16_t* __restrict__ dst, uint16_t 
     }
 }
 
-// Inclusive cumulative log2-decay over the 64 tokens of a chunk, from a
-// token-major bf16 w tile.  Writes token-major Gm[t][i] and/or channel-major
-// shifted GtX[i][t+1] = G[t] with GtX[i][0] = 0 (so GtX[i][t] = G[t-1]).
-// `tot` is 256 floats of scratch.  Ends with a barrier.
-__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GS],
-                                        float (*GtX)[GXS], float* tot) {
-    int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-    float loc[16];
+// Inclusive cumulative log2-decay over the 64 tokens of a chunk (token-major fp32
+// Gm[t][i]) from a token-major bf16 w tile, NT_ threads (NT_/64 token parts).
+// `tot` holds NT_ floats.  Ends with a barrier.
+template <int NT_>
+__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GS], float* tot) {
+    constexpr int NP = NT_ / 64, PL = CL / NP;
+    const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+    float loc[PL];
     float run = 0.f;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-        run += bf2f(Wm[16 * part + s][i]) * RW_L2E;
+    for (int s = 0; s < PL; ++s) {
+        run += bf2f(Wm[PL * part + s][i]) * RW_L2E;
         loc[s] = run;
     }
     tot[part * 64 + i] = run;
@@ -94,12 +158,7 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GS],
     float off = 0.f;
     for (int p = 0; p < part; ++p) off += tot[p * 64 + i];
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-        float g = loc[s] + off;
-        if (Gm) Gm[16 * part + s][i] = g;
-        if (GtX) GtX[i][16 * part + s + 1] = g;
-    }
-    if (GtX && part == 0) GtX[i][0] = 0.f;
+    for (int s = 0; s < PL; ++s) Gm[PL * part + s][i] = loc[s] + off;
     __syncthreads();
 }
 
@@ -107,66 +166,76 @@ __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
     return u_dtype == RWKV6_BF16 ? bf2f(reinterpret_cast<const uint16_t*>(u)[idx])
                                  : reinterpret_cast<const float*>(u)[idx];
 }
-
-// sum_i a[t][i] * b[t][i] * (u ? u[i] : 1) for each token t (256 threads, 4 per token).
-__device__ __forceinline__ float row_dot(uint16_t (*A)[TS], uint16_t (*Bm)[TS], const float* u,
-                                         int t, int q) {
-    float f[8], g[8], acc = 0.f;
+// 8 consecutive u values as fp32
+__device__ __forceinline__ void load_u8(const void* u, int u_dtype, int idx, float* f) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        int c0 = 16 * q + 8 * h;
-        unpack8(*reinterpret_cast<const uint4*>(&A[t][c0]), f);
-        unpack8(*reinterpret_cast<const uint4*>(&Bm[t][c0]), g);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) acc += f[s] * g[s] * (u ? u[c0 + s] : 1.f);
-    }
-    return warp_sum4(acc);
+    for (int s = 0; s < 8; ++s) f[s] = load_u(u, u_dtype, idx + s);
+}
+__device__ __forceinline__ float sum8lanes(float v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    return v;
 }
 
 // ---------------------------------------------------------------------------
-// phase A (forward): chunk-local state and chunk decay
+// phase A: chunk-local state (forward) / dstate (backward)
 // ---------------------------------------------------------------------------
-// S_loc[i][j] = sum_tau k[tau][i] e^{G_63[i]-G_tau[i]} v[tau][j]   (fp32 out)
-// decay[i]    = e^{G_63[i]}
+// out[i][j] = scale * sum_t X[t][i] e^{E[t][i]} Y[t][j] with
+//   forward : X = k, E = G_63 - G_t,   Y = v      (S_loc)
+//   backward: X = r, E = G_{t-1},      Y = dO     (dS_loc)
+// and, forward only, decay[i] = e^{G_63[i]}.
+template <bool FWD>
 __global__ void __launch_bounds__(NTHR)
-wkv6_fwd_chunk_state(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                     const uint16_t* __restrict__ w, float* __restrict__ Sloc,
-                     float* __restrict__ decay, int T, int NT) {
-    __shared__ __attribute__((aligned(16))) tile_t Kt, Vt, Wm;
-    __shared__ __attribute__((aligned(16))) float GtX[KD][GXS];
-    __shared__ float tot[256];
+wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
+                 const uint16_t* __restrict__ w, float* __restrict__ out,
+                 float* __restrict__ decay, float scale, int T, int NT) {
+    __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
+    __shared__ __attribute__((aligned(16))) float Gm[CL][GS];
+    __shared__ float tot[NTHR];
     const int c = blockIdx.x, bh = blockIdx.y;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
-    load_tile(nullptr, Kt, k + base, nvalid);
-    load_tile(nullptr, Vt, v + base, nvalid);
-    load_tile(Wm, nullptr, w + base, nvalid);
+    uint4 xr[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        xr[p] = gload16(X + base, row, c8, nvalid);
+        sstore16(Ys, row, c8, gload16(Y + base, row, c8, nvalid));
+        sstore16(Wm, row, c8, gload16(w + base, row, c8, nvalid));
+    }
     __syncthreads();
-    build_G(Wm, nullptr, GtX, tot);
-
+    build_G<NTHR>(Wm, Gm, tot);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        float xf[8], e[8];
+        unpack8(xr[p], xf);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float ex = FWD ? Gm[CL - 1][c8 + s] - Gm[row][c8 + s]
+                                 : (row > 0 ? Gm[row - 1][c8 + s] : 0.f);
+            e[s] = xf[s] * ex2(ex);
+        }
+        sstore16(Xs, row, c8, pack8(e));
+    }
+    __syncthreads();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int lr = lane & 15, lq = lane >> 4;
-    const int i = 16 * wv + lr;
-    const float g63 = GtX[i][64];
     f32x4 acc[4] = {};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        const int tau0 = 32 * ks + 8 * lq;
-        float kf[8];
-        unpack8(*reinterpret_cast<const uint4*>(&Kt[i][tau0]), kf);
-        bf16x8 a;
+        const bf16x8 a = ld_tr8(&Xs[0][0], 32 * ks, 16 * wv);          // row i = 16wv+lr
 #pragma unroll
-        for (int s = 0; s < 8; ++s) a[s] = (__bf16)(kf[s] * ex2(g63 - GtX[i][tau0 + s + 1]));
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_bf16x8(&Vt[16 * tj + lr][tau0]), acc[tj]);
+        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Ys[0][0], 32 * ks, 16 * tj), acc[tj]);
     }
-    float* out = Sloc + ((size_t)bh * NT + c) * KD * KD;
+    float* o = out + ((size_t)bh * NT + c) * KD * KD;
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) out[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = acc[tj][rr];
-    if (threadIdx.x < KD)
-        decay[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(GtX[threadIdx.x][64]);
+        for (int rr = 0; rr < 4; ++rr) o[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = scale * acc[tj][rr];
+    if (FWD && threadIdx.x < KD)
+        decay[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
 }
 
 // ---------------------------------------------------------------------------
@@ -234,163 +303,145 @@ wkv6_state_scan_bwd(const float* __restrict__ dSloc, const float* __restrict__ d
 // ---------------------------------------------------------------------------
 // phase C (forward): chunk output
 // ---------------------------------------------------------------------------
-// Wave W owns target tokens t in [16W, 16W+16) and all 64 value columns.
-//   o_t = s [ (r_t e^{G_{t-1}}) S_in + sum_{J<W} A_WJ v_J + A_WW v_W ]
-// A_WJ (J<W): factors r_t e^{G_{t-1}-b_W} and k_tau e^{b_W-G_tau}, b_W = G_{16W-1}
-// A_WW      : factors around mu_W = G_{16W+7}, strictly causal, u-bonus on the diagonal.
+// Wave W owns target tokens [16W, 16W+16) and all 64 value columns:
+//   o_t = s [ (Rm_t e^{mu_W}) S_in + sum_{J<W} A_WJ v_J + A_WW v_W ],
+//   A_WJ[t][tau] = sum_i Rm[t][i] f_WJ[i] Km[tau][i]; A_WW strictly causal + u-bonus diagonal.
+__device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }   // I > J
+
 __global__ void __launch_bounds__(NTHR)
 wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                       const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
                       const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ Hs,
                       uint16_t* __restrict__ o, float scale, int H, int T, int NT) {
-    __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vt, Wm, St;
-    __shared__ __attribute__((aligned(16))) gtile_t Gm;
-    __shared__ float tot[256];
-    __shared__ float us[KD], bonus[CL];
+    __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vm;
+    __shared__ __attribute__((aligned(16))) float RegA[CL][GS];   // G, then the S_in tile
+    __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD];
+    __shared__ float tot[NTHR], bonus[CL];
+    uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&RegA[0][0]);
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
-    load_tile(Rm, nullptr, r + base, nvalid);
-    load_tile(Km, nullptr, k + base, nvalid);
-    load_tile(nullptr, Vt, v + base, nvalid);
-    load_tile(Wm, nullptr, w + base, nvalid);
-    load_tile(nullptr, St, Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, KD);   // St[j][i] = S_in[i][j]
-    if (threadIdx.x < KD) us[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
-    __syncthreads();
-    {
-        float bsum = row_dot(Rm, Km, us, threadIdx.x >> 2, threadIdx.x & 3);
-        if ((threadIdx.x & 3) == 0) bonus[threadIdx.x >> 2] = bsum;
+    uint4 rq[2], kq[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        rq[p] = gload16(r + base, row, c8, nvalid);
+        kq[p] = gload16(k + base, row, c8, nvalid);
+        sstore16(Vm, row, c8, gload16(v + base, row, c8, nvalid));
+        sstore16(Rm, row, c8, gload16(w + base, row, c8, nvalid));          // w scratch
+        float rf[8], kf[8], uf[8], b = 0.f;
+        unpack8(rq[p], rf);
+        unpack8(kq[p], kf);
+        load_u8(u, u_dtype, h * KD + c8, uf);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) b += rf[s] * uf[s] * kf[s];
+        b = sum8lanes(b);
+        if ((threadIdx.x & 7) == 0) bonus[row] = b;
     }
-    build_G(Wm, Gm, nullptr, tot);
+    __syncthreads();
+    build_G<NTHR>(Rm, RegA, tot);
+    {
+        const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+        emu[part][i] = ex2(RegA[16 * part + 7][i]);
+        for (int pi = part; pi < 6; pi += 4) {
+            const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
+            fp[pi][i] = ex2(RegA[16 * I + 7][i] - RegA[16 * J + 7][i]);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        const int mrow = 16 * (row >> 4) + 7;
+        float rf[8], kf[8], a[8], b[8];
+        unpack8(rq[p], rf);
+        unpack8(kq[p], kf);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float m = RegA[mrow][c8 + s];
+            const float gm1 = row > 0 ? RegA[row - 1][c8 + s] : 0.f;
+            a[s] = rf[s] * ex2(gm1 - m);
+            b[s] = kf[s] * ex2(m - RegA[row][c8 + s]);
+        }
+        sstore16(Rm, row, c8, pack8(a));
+        sstore16(Km, row, c8, pack8(b));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        sstore16(Sin, row, c8, gload16(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, row, c8, KD));
+    }
+    __syncthreads();
 
     const int lane = threadIdx.x & 63, W = threadIdx.x >> 6;
     const int lr = lane & 15, lq = lane >> 4;
-    const int t = 16 * W + lr;                    // this lane's target row for A/B fragments
+    const int t = 16 * W + lr;
     f32x4 acc[4] = {};
-    // inter-chunk: (r_t e^{G_{t-1}}) S_in
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        const int i0 = 32 * ks + 8 * lq;
-        float rf[8];
-        unpack8(*reinterpret_cast<const uint4*>(&Rm[t][i0]), rf);
-        bf16x8 a;
+        float f[8];
+        dir8_vec(emu[W], 32 * ks, f);
+        const bf16x8 a = scale8(ld_dir8(&Rm[0][0], t, 32 * ks), f);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) a[s] = (__bf16)(rf[s] * (t > 0 ? ex2(Gm[t - 1][i0 + s]) : 1.f));
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_bf16x8(&St[16 * tj + lr][i0]), acc[tj]);
+        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Sin[0][0], 32 * ks, 16 * tj), acc[tj]);
     }
-    // intra-chunk sub-blocks J <= W
     for (int J = 0; J <= W; ++J) {
         const bool diag = (J == W);
-        const int refrow = diag ? 16 * W + 7 : 16 * W - 1;     // b_W or mu_W (W>0 when !diag)
-        const int tau = 16 * J + lr;
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int i0 = 32 * ks + 8 * lq;
-            float kf[8], rf[8];
-            unpack8(*reinterpret_cast<const uint4*>(&Km[tau][i0]), kf);
-            unpack8(*reinterpret_cast<const uint4*>(&Rm[t][i0]), rf);
-            bf16x8 ka, rb;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float ref = Gm[refrow][i0 + s];
-                ka[s] = (__bf16)(kf[s] * ex2(ref - Gm[tau][i0 + s]));
-                const float gm1 = t > 0 ? Gm[t - 1][i0 + s] : 0.f;
-                rb[s] = (__bf16)(rf[s] * ex2(gm1 - ref));
+            bf16x8 rb = ld_row8(&Rm[0][0], t, 32 * ks);
+            if (!diag) {
+                float f[8];
+                row8_vec(fp[pair_index(W, J)], 32 * ks, f);
+                rb = scale8(rb, f);
             }
-            at = mfma32(ka, rb, at);      // at[rr] = A^T[tau = 16J+4lq+rr][t = 16W+lr]
+            at = mfma32(ld_row8(&Km[0][0], 16 * J + lr, 32 * ks), rb, at);   // A^T[tau][t]
         }
         bf16x4 aop;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             float x = at[rr];
             if (diag) {
-                const int tl = 4 * lq + rr;              // source index within the block
+                const int tl = 4 * lq + rr;
                 x = tl < lr ? x : (tl == lr ? bonus[t] : 0.f);
             }
             aop[rr] = (__bf16)x;
         }
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-            acc[tj] = mfma16(aop, ld_bf16x4(&Vt[16 * tj + lr][16 * J + 4 * lq]), acc[tj]);
+        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma16(aop, ld_tr4(&Vm[0][0], 16 * J, 16 * tj), acc[tj]);
     }
-    // stage this wave's 16 rows through its own rows of Rm, then coalesced store
     __syncthreads();
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) Rm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
     __syncthreads();
-    store_tile(o + base, Rm, nvalid);
-}
-
-// ---------------------------------------------------------------------------
-// phase A (backward): chunk-local dstate
-// ---------------------------------------------------------------------------
-// dS_loc[i][j] = s * sum_t r[t][i] e^{G_{t-1}[i]} dO[t][j]
-__global__ void __launch_bounds__(NTHR)
-wkv6_bwd_chunk_dstate(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
-                      const uint16_t* __restrict__ dO, float* __restrict__ dSloc, float scale,
-                      int T, int NT) {
-    __shared__ __attribute__((aligned(16))) tile_t Rt, Dt, Wm;
-    __shared__ __attribute__((aligned(16))) float GtX[KD][GXS];
-    __shared__ float tot[256];
-    const int c = blockIdx.x, bh = blockIdx.y;
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = ((size_t)bh * T + t0) * KD;
-    load_tile(nullptr, Rt, r + base, nvalid);
-    load_tile(nullptr, Dt, dO + base, nvalid);
-    load_tile(Wm, nullptr, w + base, nvalid);
-    __syncthreads();
-    build_G(Wm, nullptr, GtX, tot);
-
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int lr = lane & 15, lq = lane >> 4;
-    const int i = 16 * wv + lr;
-    f32x4 acc[4] = {};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int tt0 = 32 * ks + 8 * lq;
-        float rf[8];
-        unpack8(*reinterpret_cast<const uint4*>(&Rt[i][tt0]), rf);
-        bf16x8 a;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) a[s] = (__bf16)(rf[s] * ex2(GtX[i][tt0 + s]));   // G_{t-1}
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_bf16x8(&Dt[16 * tj + lr][tt0]), acc[tj]);
-    }
-    float* out = dSloc + ((size_t)bh * NT + c) * KD * KD;
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-            out[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = scale * acc[tj][rr];
+    store_tile<NTHR>(o + base, Rm, nvalid);
 }
 
 // ---------------------------------------------------------------------------
 // phase C (backward): gradients of one chunk
 // ---------------------------------------------------------------------------
-// Wave W owns tokens [16W, 16W+16): as target (dr) and as source (dk, dv).
-// With dA[t][tau] = dO_t . v_tau, s = scale, S_in / S_out the states before / after
-// the chunk and dS_out the gradient of S_out:
-//   dr_h[t] = s e^{G_{t-1}-b_W} (S_in e^{b_W} dO_t + sum_{J<W} dA k e^{b_W-G})
-//           + s e^{G_{t-1}-mu_W} sum_{tau in W, tau<t} dA k e^{mu_W-G}
-//   dk_h[tau] = e^{e_W-G_tau} (dS_out e^{G_63-e_W} v_tau + s sum_{I>W} dA r e^{G_{t-1}-e_W})
-//             + e^{mu_W-G_tau} s sum_{t in W, t>tau} dA r e^{G_{t-1}-mu_W}
-//   dv[tau] = (k_tau e^{G_63-G_tau}) dS_out + s sum_{t>=tau} A[t][tau] dO_t
-//   dr = dr_h + s u k dd,  dk = dk_h + s u r dd,  dd_t = dO_t . v_t
-//   dw[t] = sum_{m>t} (r dr_h - k dk_h)[m] - k_t dk_h[t] + D,  D = rowsum(S_out * dS_out)
-//   du_part = s sum_t r_t k_t dd_t
-struct BwdSmem {
-    tile_t Rm, Km, Vm, Dm, Rt, Kt, Dt, Sm, dSm, dSt;
-    gtile_t Gm;
-    float GtX[KD][GXS];
-    float tot[256];
-    float us[KD], bonus[CL], dd[CL], Dv[KD];
+// 8 waves: wave (W, h) owns tokens [16W, 16W+16) (as target for dr, as source for
+// dk and dv) and the 32 output columns 32h .. 32h+31.  With dA[t][tau] = dO_t . v_tau,
+// Fm = e^{G_{t-1} - mu}, Fk = e^{mu - G}, s = scale, S_in / S_out the states before /
+// after the chunk and dS the gradient of S_out:
+//   dr = s Fm (e^{mu_W} dO S_in^T + sum_{J<W} f_WJ dA Km + tril(dA) Km)     + s u k dd
+//   dk = Fk (e^{G_63-mu_W} v dS^T + s sum_{I>W} f_IW dA^T Rm + s tril(dA)^T Rm) + s u r dd
+//   dv = (Km e^{G_63-mu_W}) dS + s sum_{I>=W} A_IW^T dO
+//   dw[t] = sum_{m>t} (Rm acc_r - Km acc_k)[m] - Km acc_k[t] + D,  D = rowsum(S_out * dS)
+// where acc_r = dr_h / Fm and acc_k = dk_h / Fk are the bracketed accumulators.
+struct GradSmem {
+    tile_t Vm, Dm;                  // raw v, dO (adjacent: the fp32 y tile in the epilogue)
+    tile_t RmH, RmL, KmH, KmL;      // operand tiles (hi/lo); output staging in the epilogue
+    float A[CL][GS];                // G -> S_in | dS bf16 tiles -> the fp32 x tile
+    float emu[4][KD], eg[4][KD], fp[6][KD];
+    float bonus[CL], dd[CL], Dv[KD];
+    float red[8][KD];               // build_G scratch, du partials, dw block totals
 };
 
-__global__ void __launch_bounds__(NTHR)
+__global__ void __launch_bounds__(NTHR_G)
 wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                      const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
                      const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ dO,
@@ -399,221 +450,221 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
                      uint16_t* __restrict__ dv, uint16_t* __restrict__ dw,
                      float* __restrict__ du_part, float scale, int H, int T, int NT) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    BwdSmem& sm = *reinterpret_cast<BwdSmem*>(smem_raw);
+    GradSmem& sm = *reinterpret_cast<GradSmem*>(smem_raw);
+    uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&sm.A[0][0]);
+    uint16_t (*dSm)[TS] = Sin + CL;
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
-    load_tile(sm.Rm, sm.Rt, r + base, nvalid);
-    load_tile(sm.Km, sm.Kt, k + base, nvalid);
-    load_tile(sm.Vm, nullptr, v + base, nvalid);
-    load_tile(sm.Dm, sm.Dt, dO + base, nvalid);
-    // w goes through the dS^T tile as scratch before the states are loaded
-    load_tile(sm.dSt, nullptr, w + base, nvalid);
-    load_tile(sm.Sm, nullptr, Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, KD);
-    if (threadIdx.x < KD) sm.us[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
-    __syncthreads();
+    const size_t st_in = ((size_t)bh * (NT + 1) + c) * KD * KD;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+
+    // ---- prologue: one 16-byte piece of every tile per thread ----
+    const uint4 rq = gload16(r + base, row, c8, nvalid), kq = gload16(k + base, row, c8, nvalid);
     {
-        const int tq = threadIdx.x >> 2, q = threadIdx.x & 3;
-        float bsum = row_dot(sm.Rm, sm.Km, sm.us, tq, q);
-        float dsum = row_dot(sm.Dm, sm.Vm, nullptr, tq, q);
-        if (q == 0) {
-            sm.bonus[tq] = bsum;
-            sm.dd[tq] = dsum;
+        const uint4 vq = gload16(v + base, row, c8, nvalid), dq = gload16(dO + base, row, c8, nvalid);
+        sstore16(sm.Vm, row, c8, vq);
+        sstore16(sm.Dm, row, c8, dq);
+        sstore16(sm.RmL, row, c8, gload16(w + base, row, c8, nvalid));     // w scratch
+        float rf[8], kf[8], uf[8], vf[8], df[8], b = 0.f, d = 0.f;
+        unpack8(rq, rf);
+        unpack8(kq, kf);
+        unpack8(vq, vf);
+        unpack8(dq, df);
+        load_u8(u, u_dtype, h * KD + c8, uf);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            b += rf[s] * uf[s] * kf[s];
+            d += df[s] * vf[s];
+        }
+        b = sum8lanes(b);
+        d = sum8lanes(d);
+        if ((threadIdx.x & 7) == 0) {
+            sm.bonus[row] = b;
+            sm.dd[row] = d;
         }
     }
-    // G in both layouts (build_G ends with a barrier; it also publishes bonus/dd)
+    // states: S_in and dS rows (thread row = channel i), kept in registers until G is consumed;
+    // D[i] = sum_j S_out[i][j] dS[i][j]
+    const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
+    const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
     {
-        // build_G reads w from the scratch tile
-        build_G(sm.dSt, sm.Gm, sm.GtX, sm.tot);
+        const uint4 soq = *reinterpret_cast<const uint4*>(Hs + st_in + KD * KD + row * KD + c8);
+        float a8[8], b8[8], d = 0.f;
+        unpack8(soq, a8);
+        unpack8(dsq, b8);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) d += a8[s] * b8[s];
+        d = sum8lanes(d);
+        if ((threadIdx.x & 7) == 0) sm.Dv[row] = d;
     }
-    // now the states: dS_out in both layouts (overwrites the w scratch)
-    load_tile(sm.dSm, sm.dSt, dHs + ((size_t)bh * NT + c) * KD * KD, KD);
-    // du partial: s * sum_t r k dd  (thread: channel i, 16 tokens)
+    __syncthreads();
+    build_G<NTHR_G>(sm.RmL, sm.A, &sm.red[0][0]);
+
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;
+    const int lr = lane & 15, lq = lane >> 4;
     {
+        // du partial: sum over the wave's 8 rows of r k dd, then over waves in fixed order
+        float rf[8], kf[8], du8[8];
+        unpack8(rq, rf);
+        unpack8(kq, kf);
+        const float ddr = sm.dd[row];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            float x = rf[s] * kf[s] * ddr;
+            x += __shfl_xor(x, 8);
+            x += __shfl_xor(x, 16);
+            x += __shfl_xor(x, 32);
+            du8[s] = x;
+        }
+        if (lane < 8) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) sm.red[wv][8 * lane + s] = du8[s];
+        }
+        // tables
         const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+        if (part < 4) {
+            const float m = sm.A[16 * part + 7][i];
+            sm.emu[part][i] = ex2(m);
+            sm.eg[part][i] = ex2(sm.A[CL - 1][i] - m);
+        } else {
+            for (int pi = part - 4; pi < 6; pi += 4) {
+                const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
+                sm.fp[pi][i] = ex2(sm.A[16 * I + 7][i] - sm.A[16 * J + 7][i]);
+            }
+        }
+        // operand tiles Rm, Km (hi/lo); the w scratch in RmL was consumed by build_G
+        const int mrow = 16 * (row >> 4) + 7;
+        float a[8], b[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float m = sm.A[mrow][c8 + s];
+            const float gm1 = row > 0 ? sm.A[row - 1][c8 + s] : 0.f;
+            a[s] = rf[s] * ex2(gm1 - m);
+            b[s] = kf[s] * ex2(m - sm.A[row][c8 + s]);
+        }
+        uint4 hi, lo;
+        pack8_split(a, hi, lo);
+        sstore16(sm.RmH, row, c8, hi);
+        sstore16(sm.RmL, row, c8, lo);
+        pack8_split(b, hi, lo);
+        sstore16(sm.KmH, row, c8, hi);
+        sstore16(sm.KmL, row, c8, lo);
+    }
+    // epilogue factors at this lane's accumulator positions (token 16W+4lq+rr, channel cb+lr)
+    float Fm[2][4], Fk[2][4];
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+        const int i = 16 * (2 * hh + tp) + lr;
+        const float m = sm.A[16 * W + 7][i];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int tt = 16 * W + 4 * lq + rr;
+            Fm[tp][rr] = ex2((tt > 0 ? sm.A[tt - 1][i] : 0.f) - m);
+            Fk[tp][rr] = ex2(m - sm.A[tt][i]);
+        }
+    }
+    __syncthreads();                       // G fully consumed
+    if (threadIdx.x < KD) {
         float acc = 0.f;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int tt = 16 * part + s;
-            acc += bf2f(sm.Rt[i][tt]) * bf2f(sm.Kt[i][tt]) * sm.dd[tt];
-        }
-        sm.tot[part * 64 + i] = acc;
+        for (int p = 0; p < 8; ++p) acc += sm.red[p][threadIdx.x];
+        du_part[((size_t)bh * NT + c) * KD + threadIdx.x] = scale * acc;
     }
+    sstore16(Sin, row, c8, sq);
+    sstore16(dSm, row, c8, dsq);
     __syncthreads();
-    if (threadIdx.x < KD) {
-        const int i = threadIdx.x;
-        du_part[((size_t)bh * NT + c) * KD + i] =
-            scale * (sm.tot[i] + sm.tot[64 + i] + sm.tot[128 + i] + sm.tot[192 + i]);
-    }
-    // D[i] = sum_j S_out[i][j] dS_out[i][j], S_out = Hs[c+1]
+
+    const uint16_t* Vp = &sm.Vm[0][0];
+    const uint16_t* Dp = &sm.Dm[0][0];
+    const uint16_t* RH = &sm.RmH[0][0];
+    const uint16_t* RL = &sm.RmL[0][0];
+    const uint16_t* KH = &sm.KmH[0][0];
+    const uint16_t* KL = &sm.KmL[0][0];
+    const int rowW = 16 * W + lr;
+    f32x4 ar[2], ak[2], av[2] = {};
+    // ---------------- dr (target rows in W, channels 32hh..) ----------------
     {
-        const int i = threadIdx.x >> 2, q = threadIdx.x & 3;
-        const uint16_t* so = Hs + ((size_t)bh * (NT + 1) + c + 1) * KD * KD + i * KD + 16 * q;
-        float f[8], g[8], acc = 0.f;
+        f32x4 tmp[2] = {};
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            unpack8(*reinterpret_cast<const uint4*>(so + 8 * hh), f);
-            unpack8(*reinterpret_cast<const uint4*>(&sm.dSm[i][16 * q + 8 * hh]), g);
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_row8(Dp, rowW, 32 * ks);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) acc += f[s] * g[s];
+            for (int tp = 0; tp < 2; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&Sin[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
         }
-        acc = warp_sum4(acc);
-        if (q == 0) sm.Dv[i] = acc;
-    }
-    __syncthreads();
-
-    const int lane = threadIdx.x & 63, W = threadIdx.x >> 6;
-    const int lr = lane & 15, lq = lane >> 4;
-    const int rowW = 16 * W + lr;              // this lane's fragment row in block W
-    const float* bW = W > 0 ? sm.Gm[16 * W - 1] : nullptr;
-    const float* muW = sm.Gm[16 * W + 7];
-    const float* eW = sm.Gm[16 * W + 15];
-    const float* g63 = sm.Gm[63];
-
-    // ---------------- dr (target rows t in W) ----------------
-    f32x4 accR[4] = {}, accRd[4] = {};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int j0 = 32 * ks + 8 * lq;
-        const bf16x8 a = ld_bf16x8(&sm.Dm[rowW][j0]);
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-            const int i = 16 * ti + lr;
-            const float sc = bW ? ex2(bW[i]) : 1.f;
-            float sf[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Sm[i][j0]), sf);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) sf[s] *= sc;
-            bf16x8 bh, bl;
-            split_bf16<8>(sf, bh, bl);
-            accR[ti] = mfma32(a, bh, accR[ti]);
-            accR[ti] = mfma32(a, bl, accR[ti]);
-        }
+        for (int tp = 0; tp < 2; ++tp) ar[tp] = tmp[tp] * sm.emu[W][16 * (2 * hh + tp) + lr];
     }
     for (int J = 0; J <= W; ++J) {
         const bool diag = (J == W);
         f32x4 at = {};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int j0 = 32 * ks + 8 * lq;
-            at = mfma32(ld_bf16x8(&sm.Vm[16 * J + lr][j0]), ld_bf16x8(&sm.Dm[rowW][j0]), at);
-        }
-        // at[rr] = dA[t = 16W+lr][tau = 16J+4lq+rr]
-        bf16x4 aop;
+        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+        bf16x4 aop;                                      // dA[t = 16W+lr][tau = 16J+4lq+rr]
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            float x = at[rr];
-            if (diag && 4 * lq + rr >= lr) x = 0.f;
-            aop[rr] = (__bf16)x;
-        }
-        const float* ref = diag ? muW : bW;
-        const int tau0 = 16 * J + 4 * lq;
+        for (int rr = 0; rr < 4; ++rr) aop[rr] = (__bf16)((diag && 4 * lq + rr >= lr) ? 0.f : at[rr]);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-            const int i = 16 * ti + lr;
-            float kf[4];
-            unpack4(*reinterpret_cast<const uint2*>(&sm.Kt[i][tau0]), kf);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) kf[s] *= ex2(ref[i] - sm.GtX[i][tau0 + s + 1]);
-            bf16x4 bh, bl;
-            split_bf16<4>(kf, bh, bl);
-            if (diag) {
-                accRd[ti] = mfma16(aop, bh, accRd[ti]);
-                accRd[ti] = mfma16(aop, bl, accRd[ti]);
-            } else {
-                accR[ti] = mfma16(aop, bh, accR[ti]);
-                accR[ti] = mfma16(aop, bl, accR[ti]);
-            }
+        for (int tp = 0; tp < 2; ++tp) {
+            const int cb = 16 * (2 * hh + tp);
+            f32x4 tmp = {};
+            tmp = mfma16(aop, ld_tr4(KH, 16 * J, cb), tmp);
+            tmp = mfma16(aop, ld_tr4(KL, 16 * J, cb), tmp);
+            ar[tp] += diag ? tmp : tmp * sm.fp[pair_index(W, J)][cb + lr];
         }
     }
-    // ---------------- dk (source rows tau in W) ----------------
-    f32x4 accK[4] = {}, accKd[4] = {};
+    // ---------------- dk (source rows in W) ----------------
+    {
+        f32x4 tmp[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_row8(Vp, rowW, 32 * ks);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&dSm[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
+        }
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) ak[tp] = tmp[tp] * sm.eg[W][16 * (2 * hh + tp) + lr];
+    }
+    for (int I = W; I < 4; ++I) {
+        const bool diag = (I == W);
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+        bf16x4 aop;                                      // dA[t = 16I+4lq+rr][tau = 16W+lr]
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) aop[rr] = (__bf16)((diag && 4 * lq + rr <= lr) ? 0.f : at[rr] * scale);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) {
+            const int cb = 16 * (2 * hh + tp);
+            f32x4 tmp = {};
+            tmp = mfma16(aop, ld_tr4(RH, 16 * I, cb), tmp);
+            tmp = mfma16(aop, ld_tr4(RL, 16 * I, cb), tmp);
+            ak[tp] += diag ? tmp : tmp * sm.fp[pair_index(I, W)][cb + lr];
+        }
+    }
+    // ---------------- dv (source rows in W, value columns 32hh..) ----------------
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        const int j0 = 32 * ks + 8 * lq;
-        const bf16x8 a = ld_bf16x8(&sm.Vm[rowW][j0]);
+        float f[8];
+        dir8_vec(sm.eg[W], 32 * ks, f);
+        const bf16x8 a = scale8(ld_dir8(KH, rowW, 32 * ks), f);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-            const int i = 16 * ti + lr;
-            const float sc = ex2(g63[i] - eW[i]);
-            float sf[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.dSm[i][j0]), sf);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) sf[s] *= sc;
-            bf16x8 bh, bl;
-            split_bf16<8>(sf, bh, bl);
-            accK[ti] = mfma32(a, bh, accK[ti]);
-            accK[ti] = mfma32(a, bl, accK[ti]);
-        }
+        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma32(a, ld_tr8(&dSm[0][0], 32 * ks, 16 * (2 * hh + tp)), av[tp]);
     }
     for (int I = W; I < 4; ++I) {
         const bool diag = (I == W);
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int j0 = 32 * ks + 8 * lq;
-            at = mfma32(ld_bf16x8(&sm.Dm[16 * I + lr][j0]), ld_bf16x8(&sm.Vm[rowW][j0]), at);
-        }
-        // at[rr] = dA[t = 16I+4lq+rr][tau = 16W+lr]
-        bf16x4 aop;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            float x = at[rr] * scale;
-            if (diag && 4 * lq + rr <= lr) x = 0.f;
-            aop[rr] = (__bf16)x;
-        }
-        const float* ref = diag ? muW : eW;
-        const int tt0 = 16 * I + 4 * lq;
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti) {
-            const int i = 16 * ti + lr;
-            float rf[4];
-            unpack4(*reinterpret_cast<const uint2*>(&sm.Rt[i][tt0]), rf);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) rf[s] *= ex2(sm.GtX[i][tt0 + s] - ref[i]);
-            bf16x4 bh, bl;
-            split_bf16<4>(rf, bh, bl);
-            if (diag) {
-                accKd[ti] = mfma16(aop, bh, accKd[ti]);
-                accKd[ti] = mfma16(aop, bl, accKd[ti]);
-            } else {
-                accK[ti] = mfma16(aop, bh, accK[ti]);
-                accK[ti] = mfma16(aop, bl, accK[ti]);
+            bf16x8 ra = ld_row8(RH, 16 * I + lr, 32 * ks);
+            if (!diag) {
+                float f[8];
+                row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
+                ra = scale8(ra, f);
             }
-        }
-    }
-    // ---------------- dv (source rows tau in W) ----------------
-    f32x4 accV[4] = {};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int i0 = 32 * ks + 8 * lq;
-        float kf[8];
-        unpack8(*reinterpret_cast<const uint4*>(&sm.Km[rowW][i0]), kf);
-        bf16x8 a;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) a[s] = (__bf16)(kf[s] * ex2(g63[i0 + s] - sm.Gm[rowW][i0 + s]));
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) accV[tj] = mfma32(a, ld_bf16x8(&sm.dSt[16 * tj + lr][i0]), accV[tj]);
-    }
-    for (int I = W; I < 4; ++I) {
-        const bool diag = (I == W);
-        const float* ref = diag ? muW : eW;
-        const int trow = 16 * I + lr;
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int i0 = 32 * ks + 8 * lq;
-            float rf[8], kf[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[trow][i0]), rf);
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[rowW][i0]), kf);
-            bf16x8 ra, kb;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float gm1 = trow > 0 ? sm.Gm[trow - 1][i0 + s] : 0.f;
-                ra[s] = (__bf16)(rf[s] * ex2(gm1 - ref[i0 + s]));
-                kb[s] = (__bf16)(kf[s] * ex2(ref[i0 + s] - sm.Gm[rowW][i0 + s]));
-            }
-            at = mfma32(ra, kb, at);       // at[rr] = A[t = 16I+4lq+rr][tau = 16W+lr]
+            at = mfma32(ra, ld_row8(KH, rowW, 32 * ks), at);     // A[t = 16I+4lq+rr][tau = 16W+lr]
         }
         bf16x4 aop;
 #pragma unroll
@@ -621,77 +672,75 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             float x = at[rr];
             if (diag) {
                 const int tl = 4 * lq + rr;
-                x = tl > lr ? x : (tl == lr ? sm.bonus[16 * W + lr] : 0.f);
+                x = tl > lr ? x : (tl == lr ? sm.bonus[rowW] : 0.f);
             }
             aop[rr] = (__bf16)(x * scale);
         }
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-            accV[tj] = mfma16(aop, ld_bf16x4(&sm.Dt[16 * tj + lr][16 * I + 4 * lq]), accV[tj]);
+        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 16 * (2 * hh + tp)), av[tp]);
     }
 
     // ---------------- epilogue ----------------
-    // Accumulator element (lq, rr) of tile ti sits at token 16W+4lq+rr, channel 16ti+lr.
-    float drh[4][4], dkh[4][4], xv[4][4], yv[4][4];
+    float drv[2][4], dkv[2][4], xv[2][4], yv[2][4];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-        const int i = 16 * ti + lr;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int tt = 16 * W + 4 * lq + rr;
-            const float gm1 = sm.GtX[i][tt], g = sm.GtX[i][tt + 1];
-            const float fR = bW ? ex2(gm1 - bW[i]) : ex2(gm1);
-            drh[ti][rr] = scale * (fR * accR[ti][rr] + ex2(gm1 - muW[i]) * accRd[ti][rr]);
-            dkh[ti][rr] = ex2(eW[i] - g) * accK[ti][rr] + ex2(muW[i] - g) * accKd[ti][rr];
-            const float rv = bf2f(sm.Rt[i][tt]), kv = bf2f(sm.Kt[i][tt]);
-            xv[ti][rr] = rv * drh[ti][rr] - kv * dkh[ti][rr];
-            yv[ti][rr] = sm.Dv[i] - kv * dkh[ti][rr];
-        }
-    }
-    __syncthreads();     // every wave is done with the MFMA operand tiles
-    float (*Xs)[GS] = sm.Gm;                                            // x  (fp32)
-    float (*Ys)[GXS] = sm.GtX;                                          // y  (fp32)
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-        const int i = 16 * ti + lr;
+    for (int tp = 0; tp < 2; ++tp) {
+        const int cb = 16 * (2 * hh + tp), i = cb + lr;
+        const bf16x4 rh = ld_tr4(RH, 16 * W, cb), rl = ld_tr4(RL, 16 * W, cb);
+        const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
+        const float ui = scale * load_u(u, u_dtype, h * KD + i);
+        const float Di = sm.Dv[i];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
-            const float rv = bf2f(sm.Rm[tt][i]), kv = bf2f(sm.Km[tt][i]);
-            const float sdd = scale * sm.dd[tt] * sm.us[i];
-            Xs[tt][i] = xv[ti][rr];
-            Ys[tt][i] = yv[ti][rr];
-            sm.Rt[tt][i] = f2bf(drh[ti][rr] + sdd * kv);              // dr staging
-            sm.Kt[tt][i] = f2bf(dkh[ti][rr] + sdd * rv);              // dk staging
+            const float rmv = (float)rh[rr] + (float)rl[rr];
+            const float kmv = (float)kh[rr] + (float)kl[rr];
+            const float accr = scale * ar[tp][rr], acck = ak[tp][rr];
+            const float udd = ui * sm.dd[tt];
+            drv[tp][rr] = Fm[tp][rr] * accr + udd * (kmv / Fk[tp][rr]);
+            dkv[tp][rr] = Fk[tp][rr] * acck + udd * (rmv / Fm[tp][rr]);
+            xv[tp][rr] = rmv * accr - kmv * acck;
+            yv[tp][rr] = Di - kmv * acck;
         }
     }
+    __syncthreads();                       // all waves are done with the operand tiles
+    float (*Xs)[GS] = sm.A;
+    float (*Ys)[GS] = reinterpret_cast<float (*)[GS]>(&sm.Vm[0][0]);
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
+    for (int tp = 0; tp < 2; ++tp) {
+        const int i = 16 * (2 * hh + tp) + lr;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sm.Sm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(accV[tj][rr]);
+        for (int rr = 0; rr < 4; ++rr) {
+            const int tt = 16 * W + 4 * lq + rr;
+            Xs[tt][i] = xv[tp][rr];
+            Ys[tt][i] = yv[tp][rr];
+            sm.RmH[tt][i] = f2bf(drv[tp][rr]);
+            sm.RmL[tt][i] = f2bf(dkv[tp][rr]);
+            sm.KmH[tt][i] = f2bf(av[tp][rr]);
+        }
+    }
     __syncthreads();
-    // dw: suffix sums over tokens, thread = (channel i, 16-token part)
     {
+        // dw: suffix sums over tokens; thread = (channel i, 8-token part)
         const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
         float tsum = 0.f;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) tsum += Xs[16 * part + s][i];
-        sm.tot[part * 64 + i] = tsum;
+        for (int s = 0; s < 8; ++s) tsum += Xs[8 * part + s][i];
+        sm.red[part][i] = tsum;
         __syncthreads();
-        float run = 0.f;          // sum_{m > t} x[m]
-        for (int p = part + 1; p < 4; ++p) run += sm.tot[p * 64 + i];
+        float run = 0.f;                   // sum_{m > t} x[m]
+        for (int p = part + 1; p < 8; ++p) run += sm.red[p][i];
 #pragma unroll
-        for (int s = 15; s >= 0; --s) {
-            const int tt = 16 * part + s;
-            sm.Dt[tt][i] = f2bf(run + Ys[tt][i]);
+        for (int s = 7; s >= 0; --s) {
+            const int tt = 8 * part + s;
+            sm.KmL[tt][i] = f2bf(run + Ys[tt][i]);
             run += Xs[tt][i];
         }
     }
     __syncthreads();
-    store_tile(dr + base, sm.Rt, nvalid);
-    store_tile(dk + base, sm.Kt, nvalid);
-    store_tile(dv + base, sm.Sm, nvalid);
-    store_tile(dw + base, sm.Dt, nvalid);
+    store_tile<NTHR_G>(dr + base, sm.RmH, nvalid);
+    store_tile<NTHR_G>(dk + base, sm.RmL, nvalid);
+    store_tile<NTHR_G>(dv + base, sm.KmH, nvalid);
+    store_tile<NTHR_G>(dw + base, sm.KmL, nvalid);
 }
 
 // du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q): strided partial sum over the
@@ -785,9 +834,9 @@ int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL(wkv6_fwd_chunk_state, grid, dim3(NTHR), 0, s,
+        hipLaunchKernelGGL(wkv6_chunk_local<true>, grid, dim3(NTHR), 0, s,
                            (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, Sloc, decay,
-                           (int)T, (int)NT);
+                           1.0f, (int)T, (int)NT);
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
@@ -835,8 +884,9 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL(wkv6_bwd_chunk_dstate, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
-                           (const uint16_t*)w, (const uint16_t*)dO, dSloc, scale, (int)T, (int)NT);
+        hipLaunchKernelGGL(wkv6_chunk_local<false>, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
+                           (const uint16_t*)dO, (const uint16_t*)w, dSloc, (float*)nullptr, scale,
+                           (int)T, (int)NT);
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
@@ -847,10 +897,10 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
         dim3 grid((unsigned)NT, (unsigned)BH);
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)sizeof(BwdSmem)) != hipSuccess)
+                                (int)sizeof(GradSmem)) != hipSuccess)
             return RWKV6_ERR_LAUNCH;
         mark(phase_events, 4, s);
-        hipLaunchKernelGGL(wkv6_bwd_chunk_grads, grid, dim3(NTHR), sizeof(BwdSmem), s,
+        hipLaunchKernelGGL(wkv6_bwd_chunk_grads, grid, dim3(NTHR_G), sizeof(GradSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, Hs,
                            (const uint16_t*)dHs, (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv,

@@ -56,3 +56,16 @@ def test_chunk_model_strong_decay():
     gm = cm.bwd(r, k, v, w, u, dO, h0, dhT)
     for name in ("dr", "dk", "dv", "dw", "du", "dh0"):
         assert _rel(gm[name], g[name]) < 1e-5, name
+
+
+@pytest.mark.parametrize("T", [1, 64, 130])
+@pytest.mark.parametrize("strong", [False, True])
+def test_midpoint_form_matches_recurrence(T, strong):
+    lo, hi = (-3.0, 2.3) if strong else (-6.0, -0.5)
+    r, k, v, w, u, h0, dO, dhT = _inputs(1, 2, T, 16, 8, seed=T + 7, w_lo=lo, w_hi=hi)
+    o, _ = orc.wkv6_fwd(r, k, v, w, u, h0, 0.8)
+    assert _rel(cm.fwd_mid(r, k, v, w, u, h0, 0.8), o) < 1e-5
+    g = orc.wkv6_bwd(r, k, v, w, u, dO, h0, dhT, 0.8)
+    gm = cm.bwd_mid(r, k, v, w, u, dO, h0, dhT, 0.8)
+    for name in ("dr", "dk", "dv", "dw", "du", "dh0"):
+        assert _rel(gm[name], g[name]) < 1e-5, name

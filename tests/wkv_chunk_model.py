@@ -156,3 +156,117 @@ def bwd(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
     du = np.einsum("bhcti,bhcti,bhct->hi", rc, kc, dd)
     cut = lambda a: a.reshape(B, H, NT * L, -1)[:, :, :T]
     return dict(dr=cut(dr), dk=cut(dk), dv=cut(dv), dw=cut(dw), du=du, dh0=dh0)
+
+
+# ---------------------------------------------------------------------------
+# Midpoint-referenced form (the form of the current kernels).  Per sub-block I,
+# mu_I = G[16I+7]; stored operand tiles
+#   Rm[t] = r_t e^{G_{t-1} - mu_I(t)},   Km[tau] = k_tau e^{mu_J(tau) - G_tau}
+# are bounded by the decay of 8 tokens either way; every cross-block factor is a
+# per-channel scalar f_IJ = e^{mu_I - mu_J} <= 1 (I > J) applied to accumulator
+# columns (dr, dk) or to one operand (A blocks).
+# ---------------------------------------------------------------------------
+
+def _mid(G, Gm1):
+    NB = L // SUB
+    mu = np.stack([G[..., SUB * I + 7, :] for I in range(NB)], axis=-2)      # [...,4,K]
+    blk = np.arange(L) // SUB
+    mu_t = mu[..., blk, :]                                                      # [...,64,K]
+    return mu, mu_t
+
+
+def fwd_mid(r, k, v, w, u, h0=None, scale=1.0):
+    r, k, v, w = (np.asarray(a, np.float64) for a in (r, k, v, w))
+    u = np.asarray(u, np.float64)
+    B, H, T, K = r.shape
+    V = v.shape[-1]
+    NT = (T + L - 1) // L
+    _, _, S_in = fwd(r, k, v, w, u, h0, scale)          # scan phases are unchanged
+    rc, kc, vc, wc = (_chunks(a, T, NT) for a in (r, k, v, w))
+    G, Gm1 = _chunk_cumsum(wc)
+    mu, mu_t = _mid(G, Gm1)
+    Rm = rc * np.exp(Gm1 - mu_t)
+    Km = kc * np.exp(mu_t - G)
+    bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
+    O = np.zeros((B, H, NT, L, V))
+    tril = np.tril(np.ones((SUB, SUB)), -1)
+    for I in range(L // SUB):
+        ti = slice(SUB * I, SUB * I + SUB)
+        O[..., ti, :] += np.einsum("bhcti,bhcij->bhctj", Rm[..., ti, :] * np.exp(mu[..., I, None, :]),
+                                   S_in[:, :, :NT])
+        for J in range(I + 1):
+            tj = slice(SUB * J, SUB * J + SUB)
+            f = np.exp(mu[..., I, :] - mu[..., J, :])[..., None, :]
+            A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * f, Km[..., tj, :])
+            if I == J:
+                A = A * tril + np.einsum("bhct,ts->bhcts", bonus[..., ti], np.eye(SUB))
+            O[..., ti, :] += np.einsum("bhcts,bhcsj->bhctj", A, vc[..., tj, :])
+    return scale * O.reshape(B, H, NT * L, V)[:, :, :T]
+
+
+def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
+    r, k, v, w, dO = (np.asarray(a, np.float64) for a in (r, k, v, w, dO))
+    u = np.asarray(u, np.float64)
+    B, H, T, K = r.shape
+    V = v.shape[-1]
+    NT = (T + L - 1) // L
+    _, _, S_in = fwd(r, k, v, w, u, h0, scale)
+    rc, kc, vc, wc, dc = (_chunks(a, T, NT) for a in (r, k, v, w, dO))
+    dc = scale * dc
+    G, Gm1 = _chunk_cumsum(wc)
+    GL = G[..., -1, :]
+    mu, mu_t = _mid(G, Gm1)
+    dSloc = np.einsum("bhcti,bhctj->bhcij", rc * np.exp(Gm1), dc)
+    dS = np.zeros((B, H, K, V)) if dhT is None else np.asarray(dhT, np.float64).copy()
+    dS_out = np.empty((B, H, NT, K, V))
+    for c in range(NT - 1, -1, -1):
+        dS_out[:, :, c] = dS
+        dS = np.exp(GL[:, :, c])[..., None] * dS + dSloc[:, :, c]
+    dh0 = dS
+    Rm = rc * np.exp(Gm1 - mu_t)
+    Km = kc * np.exp(mu_t - G)
+    Fm = np.exp(Gm1 - mu_t)
+    Fk = np.exp(mu_t - G)
+    dA = np.einsum("bhctj,bhcsj->bhcts", dc, vc)
+    dd = np.einsum("bhctt->bhct", dA)
+    bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
+    D = np.einsum("bhcij,bhcij->bhci", S_in[:, :, 1:], dS_out)
+    tril = np.tril(np.ones((SUB, SUB)), -1)
+    acc_r = np.zeros_like(rc)
+    acc_k = np.zeros_like(kc)
+    dv = np.zeros_like(vc)
+    NB = L // SUB
+    for W in range(NB):
+        tw = slice(SUB * W, SUB * W + SUB)
+        f = lambda I, J: np.exp(mu[..., I, :] - mu[..., J, :])
+        # dr accumulator (columns i): inter, off-diagonal, diagonal
+        a = np.exp(mu[..., W, :])[..., None, :] * np.einsum("bhctj,bhcij->bhcti", dc[..., tw, :], S_in[:, :, :NT])
+        for J in range(W):
+            tj = slice(SUB * J, SUB * J + SUB)
+            a += f(W, J)[..., None, :] * np.einsum("bhcts,bhcsi->bhcti", dA[..., tw, tj], Km[..., tj, :])
+        a += np.einsum("bhcts,bhcsi->bhcti", dA[..., tw, tw] * tril, Km[..., tw, :])
+        acc_r[..., tw, :] = a
+        # dk accumulator
+        a = np.exp(GL - mu[..., W, :])[..., None, :] * np.einsum("bhcsj,bhcij->bhcsi", vc[..., tw, :], dS_out)
+        for I in range(W + 1, NB):
+            ti = slice(SUB * I, SUB * I + SUB)
+            a += f(I, W)[..., None, :] * np.einsum("bhcts,bhcti->bhcsi", dA[..., ti, tw], Rm[..., ti, :])
+        a += np.einsum("bhcts,bhcti->bhcsi", dA[..., tw, tw] * tril, Rm[..., tw, :])
+        acc_k[..., tw, :] = a
+        # dv
+        dv[..., tw, :] = np.einsum("bhcsi,bhcij->bhcsj", Km[..., tw, :] * np.exp(GL - mu[..., W, :])[..., None, :],
+                                   dS_out)
+        for I in range(W, NB):
+            ti = slice(SUB * I, SUB * I + SUB)
+            A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * f(I, W)[..., None, :], Km[..., tw, :])
+            if I == W:
+                A = A * tril + np.einsum("bhct,ts->bhcts", bonus[..., ti], np.eye(SUB))
+            dv[..., tw, :] += np.einsum("bhcts,bhctj->bhcsj", A, dc[..., ti, :])
+    dr = Fm * acc_r + u[None, :, None, None, :] * kc * dd[..., None]
+    dk = Fk * acc_k + u[None, :, None, None, :] * rc * dd[..., None]
+    x = Rm * acc_r - Km * acc_k
+    suffix = np.cumsum(x[..., ::-1, :], axis=-2)[..., ::-1, :] - x
+    dw = suffix - Km * acc_k + D[..., None, :]
+    du = np.einsum("bhcti,bhcti,bhct->hi", rc, kc, dd)
+    cut = lambda a: a.reshape(B, H, NT * L, -1)[:, :, :T]
+    return dict(dr=cut(dr), dk=cut(dk), dv=cut(dv), dw=cut(dw), du=du, dh0=dh0)
