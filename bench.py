@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-heads", type=int, default=0,
                     help="(b,h) sequences in the CPU sample (0 = the whole workload)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="after timing, run a plain device copy of this many MiB 3 times (reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -82,6 +85,22 @@ def cpu_baseline(B, H, T, sample_heads):
         "sample": f"oracle fp64 naive recurrence fwd+bwd over {Bs*Hs} of {B*H} (b,h) sequences "
                   f"at T={T} ({dt:.2f} s), scaled to the whole B={B},H={H} job",
     }
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "wkv6_bwd_chunk_grads_traffic.json")
+
+
+def measured_traffic(B, H, T):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter runs
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter on a copy of known size)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if (d.get("B"), d.get("H"), d.get("T")) != (B, H, T):
+        return None
+    return d.get("traffic_bytes")
 
 
 def main():
@@ -181,8 +200,17 @@ def main():
                      "bwd_du_reduce": bwd_ph[3]},
         "roofline": {"kernel": "wkv6_bwd_chunk_grads", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None},
+                     "traffic": measured_traffic(B, H, T)},
     }
+    if args.copy_calibration_mb > 0:
+        n = args.copy_calibration_mb * (1 << 20) // 2
+        src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_calibration_bytes"] = 2 * n
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, H, T, args.cpu_sample_heads)
     print(json.dumps(out), flush=True)

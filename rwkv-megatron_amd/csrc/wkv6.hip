@@ -321,10 +321,11 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
-    uint4 rq[2], kq[2];
+    uint4 rq[2], kq[2], sq[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        sq[p] = gload16(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, row, c8, KD);
         rq[p] = gload16(r + base, row, c8, nvalid);
         kq[p] = gload16(k + base, row, c8, nvalid);
         sstore16(Vm, row, c8, gload16(v + base, row, c8, nvalid));
@@ -369,7 +370,7 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        sstore16(Sin, row, c8, gload16(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, row, c8, KD));
+        sstore16(Sin, row, c8, sq[p]);
     }
     __syncthreads();
 
@@ -553,7 +554,8 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         sstore16(sm.KmL, row, c8, lo);
     }
     // epilogue factors at this lane's accumulator positions (token 16W+4lq+rr, channel cb+lr)
-    float Fm[2][4], Fk[2][4];
+    // Fm, Fk and the factors r / Rm = 1 / Fm, k / Km = 1 / Fk (as exponentials, not divisions)
+    float Fm[2][4], Fk[2][4], iFm[2][4], iFk[2][4];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
@@ -561,8 +563,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
-            Fm[tp][rr] = ex2((tt > 0 ? sm.A[tt - 1][i] : 0.f) - m);
-            Fk[tp][rr] = ex2(m - sm.A[tt][i]);
+            const float em = (tt > 0 ? sm.A[tt - 1][i] : 0.f) - m, ek = m - sm.A[tt][i];
+            Fm[tp][rr] = ex2(em);
+            iFm[tp][rr] = ex2(-em);
+            Fk[tp][rr] = ex2(ek);
+            iFk[tp][rr] = ex2(-ek);
         }
     }
     __syncthreads();                       // G fully consumed
@@ -696,8 +701,8 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float kmv = (float)kh[rr] + (float)kl[rr];
             const float accr = scale * ar[tp][rr], acck = ak[tp][rr];
             const float udd = ui * sm.dd[tt];
-            drv[tp][rr] = Fm[tp][rr] * accr + udd * (kmv / Fk[tp][rr]);
-            dkv[tp][rr] = Fk[tp][rr] * acck + udd * (rmv / Fm[tp][rr]);
+            drv[tp][rr] = Fm[tp][rr] * accr + udd * (kmv * iFk[tp][rr]);
+            dkv[tp][rr] = Fk[tp][rr] * acck + udd * (rmv * iFm[tp][rr]);
             xv[tp][rr] = rmv * accr - kmv * acck;
             yv[tp][rr] = Di - kmv * acck;
         }
@@ -743,23 +748,28 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     store_tile<NTHR_G>(dw + base, sm.KmL, nvalid);
 }
 
-// du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q): strided partial sum over the
-// B*NT (b, c) pairs with p = q mod 4, then a fixed-order combine (deterministic).
-__global__ void __launch_bounds__(NTHR)
+// du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q), q < 16: strided partial sum over
+// the B*NT (b, c) pairs with p = q mod 16, then a fixed-order combine (deterministic).
+#define DU_THR 1024
+__global__ void __launch_bounds__(DU_THR)
 wkv6_du_reduce(const float* __restrict__ du_part, void* __restrict__ du, int u_dtype, int B,
                int H, int NT) {
-    __shared__ float part[4][KD];
+    __shared__ float part[DU_THR / KD][KD];
     const int h = blockIdx.x, i = threadIdx.x & 63, q = threadIdx.x >> 6;
+    constexpr int NQ = DU_THR / KD;
     float acc = 0.f;
     const int P = B * NT;
-    for (int p = q; p < P; p += 4) {
+#pragma unroll 4
+    for (int p = q; p < P; p += NQ) {
         const int b = p / NT, c = p - b * NT;
         acc += du_part[((size_t)(b * H + h) * NT + c) * KD + i];
     }
     part[q][i] = acc;
     __syncthreads();
     if (q == 0) {
-        const float tot = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) tot += part[j][i];
         if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[h * KD + i] = f2bf(tot);
         else reinterpret_cast<float*>(du)[h * KD + i] = tot;
     }
@@ -907,7 +917,7 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
                            (uint16_t*)dw, du_part, scale, (int)H, (int)T, (int)NT);
         mark(phase_events, 5, s);
         mark(phase_events, 6, s);
-        hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(NTHR), 0, s, du_part, du, u_dtype,
+        hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(DU_THR), 0, s, du_part, du, u_dtype,
                            (int)B, (int)H, (int)NT);
         mark(phase_events, 7, s);
     } else {
