@@ -51,6 +51,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-heads", type=int, default=0,
                     help="(b,h) sequences in the CPU sample (0 = the whole workload)")
+    ap.add_argument("--no-train", action="store_true",
+                    help="skip the config-3 training step (RWKV6 1.6B shape) measurement")
+    ap.add_argument("--train-steps", type=int, default=3)
+    ap.add_argument("--train-warmup", type=int, default=2)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after timing, run a plain device copy of this many MiB 3 times (reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -101,6 +105,58 @@ def measured_traffic(B, H, T):
     if (d.get("B"), d.get("H"), d.get("T")) != (B, H, T):
         return None
     return d.get("traffic_bytes")
+
+
+def train_step_bench(pkg, steps, warmup):
+    """RWKV-6 1.6B shape (24 layers, C=2048, 32 heads, ffn 7168, vocab 65536),
+    batch 4 x 4096 random tokens, bf16 weights, full forward + backward + grad clip + AdamW.
+    Returns tokens/s and the model-FLOP utilisation against 2.5 PFLOP/s dense bf16."""
+    import torch
+
+    M = pkg.modules
+    cfg = M.TransformerConfig(hidden_size=2048, num_attention_heads=32, ffn_hidden_size=7168,
+                              num_layers=24, params_dtype=torch.bfloat16)
+    B, T, V = 4, 4096, 65536
+    torch.manual_seed(0)
+    model = M.RWKV6Model(cfg, V, device="cuda:0")
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=2.5e-4, betas=(0.9, 0.995), eps=1e-8,
+                            weight_decay=0.1, fused=True)
+    g = torch.Generator(device="cuda:0").manual_seed(1)
+    tokens = torch.randint(0, V, (B, T + 1), device="cuda:0", generator=g)
+    inp, tgt = tokens[:, :-1], tokens[:, 1:]
+
+    def step():
+        logits = model(inp)                                      # [T, B, V]
+        loss = torch.nn.functional.cross_entropy(logits.float().view(-1, V), tgt.t().reshape(-1))
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        loss = step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # 6 * (matmul parameters incl. the output head) per token, + the WKV op (fwd+bwd per token-head)
+    emb = model.embedding.weight.numel()
+    flop_tok = 6 * (n_params - emb) + cfg.num_layers * cfg.num_attention_heads * (FLOP_FWD + FLOP_BWD)
+    tps = B * T / (ms * 1e-3)
+    out = {"workload": "RWKV-6 1.6B-shape train step (BASELINE config 3): 24 layers, d_model 2048, "
+                       "32 heads, ffn 7168, vocab 65536, batch 4 x 4096, bf16, fwd+bwd+clip+AdamW",
+           "tokens_per_s": tps, "ms_per_step": ms, "params": n_params, "steps": steps, "warmup": warmup,
+           "model_tflops": flop_tok * tps / 1e12, "mfu": flop_tok * tps / 1e12 / BF16_PEAK_TFLOPS,
+           "final_loss": float(loss.item())}
+    del model, opt
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -211,6 +267,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         out["copy_calibration_bytes"] = 2 * n
+    if not args.no_train:
+        out["train_step"] = train_step_bench(pkg, args.train_steps, args.train_warmup)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, H, T, args.cpu_sample_heads)
     print(json.dumps(out), flush=True)

@@ -27,6 +27,8 @@
 // Every MFMA accumulates in fp32 and the carried states are fp32.  In the dr / dk
 // contractions Rm / Km are bf16 hi + lo pairs: dw is a cancelling suffix sum of
 // r*dr - k*dk, and single-bf16 operands there would dominate its error.
+#include <algorithm>
+
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
@@ -34,6 +36,8 @@
 #define CL 64            // chunk length (tokens)
 #define TS 72            // LDS row stride of a bf16 64x64 tile (elements): 144 B rows
 #define GS 72            // LDS row stride of an fp32 64x64 tile (elements)
+#define GSG 69           // row stride of the fp32 cumulative-decay view: 69 = 5 (mod 64) banks keeps
+                         // the row-wise reads of 8 consecutive rows by 8 lanes each conflict-free
 #define NTHR 256
 #define NTHR_G 512       // threads of the gradient kernel (8 waves)
 
@@ -143,7 +147,7 @@ __device__ __forceinline__ void store_tile(uint16_t* __restrict__ dst, uint16_t 
 // Gm[t][i]) from a token-major bf16 w tile, NT_ threads (NT_/64 token parts).
 // `tot` holds NT_ floats.  Ends with a barrier.
 template <int NT_>
-__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GS], float* tot) {
+__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], float* tot) {
     constexpr int NP = NT_ / 64, PL = CL / NP;
     const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
     float loc[PL];
@@ -191,8 +195,9 @@ wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
                  const uint16_t* __restrict__ w, float* __restrict__ out,
                  float* __restrict__ decay, float scale, int T, int NT) {
     __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
-    __shared__ __attribute__((aligned(16))) float Gm[CL][GS];
+    __shared__ __attribute__((aligned(16))) float Gstore[CL * GSG];
     __shared__ float tot[NTHR];
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(Gstore);
     const int c = blockIdx.x, bh = blockIdx.y;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
@@ -308,117 +313,151 @@ wkv6_state_scan_bwd(const float* __restrict__ dSloc, const float* __restrict__ d
 //   A_WJ[t][tau] = sum_i Rm[t][i] f_WJ[i] Km[tau][i]; A_WW strictly causal + u-bonus diagonal.
 __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }   // I > J
 
-__global__ void __launch_bounds__(NTHR)
+// Persistent: each workgroup walks jobs (b*h, chunk) with a grid stride and prefetches the
+// next job's tiles into registers while it computes the current one.
+struct FwdPrefetch {
+    uint4 r[2], k[2], v[2], w[2], s[2];
+};
+
+__device__ __forceinline__ void fwd_issue(FwdPrefetch& f, const uint16_t* __restrict__ r,
+                                          const uint16_t* __restrict__ k,
+                                          const uint16_t* __restrict__ v,
+                                          const uint16_t* __restrict__ w,
+                                          const uint16_t* __restrict__ Hs, int job, int T, int NT) {
+    const int bh = job / NT, c = job - bh * NT;
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    const size_t base = ((size_t)bh * T + t0) * KD;
+    const uint16_t* sp = Hs + ((size_t)bh * (NT + 1) + c) * KD * KD;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        f.r[p] = gload16(r + base, row, c8, nvalid);
+        f.k[p] = gload16(k + base, row, c8, nvalid);
+        f.v[p] = gload16(v + base, row, c8, nvalid);
+        f.w[p] = gload16(w + base, row, c8, nvalid);
+        f.s[p] = gload16(sp, row, c8, KD);
+    }
+}
+
+__global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3, 3)))
 wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                       const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
                       const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ Hs,
-                      uint16_t* __restrict__ o, float scale, int H, int T, int NT) {
+                      uint16_t* __restrict__ o, float scale, int H, int T, int NT, int njobs) {
     __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vm;
     __shared__ __attribute__((aligned(16))) float RegA[CL][GS];   // G, then the S_in tile
     __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD];
     __shared__ float tot[NTHR], bonus[CL];
     uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&RegA[0][0]);
-    const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = ((size_t)bh * T + t0) * KD;
-    uint4 rq[2], kq[2], sq[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        sq[p] = gload16(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, row, c8, KD);
-        rq[p] = gload16(r + base, row, c8, nvalid);
-        kq[p] = gload16(k + base, row, c8, nvalid);
-        sstore16(Vm, row, c8, gload16(v + base, row, c8, nvalid));
-        sstore16(Rm, row, c8, gload16(w + base, row, c8, nvalid));          // w scratch
-        float rf[8], kf[8], uf[8], b = 0.f;
-        unpack8(rq[p], rf);
-        unpack8(kq[p], kf);
-        load_u8(u, u_dtype, h * KD + c8, uf);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) b += rf[s] * uf[s] * kf[s];
-        b = sum8lanes(b);
-        if ((threadIdx.x & 7) == 0) bonus[row] = b;
-    }
-    __syncthreads();
-    build_G<NTHR>(Rm, RegA, tot);
-    {
-        const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-        emu[part][i] = ex2(RegA[16 * part + 7][i]);
-        for (int pi = part; pi < 6; pi += 4) {
-            const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-            fp[pi][i] = ex2(RegA[16 * I + 7][i] - RegA[16 * J + 7][i]);
-        }
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        const int mrow = 16 * (row >> 4) + 7;
-        float rf[8], kf[8], a[8], b[8];
-        unpack8(rq[p], rf);
-        unpack8(kq[p], kf);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float m = RegA[mrow][c8 + s];
-            const float gm1 = row > 0 ? RegA[row - 1][c8 + s] : 0.f;
-            a[s] = rf[s] * ex2(gm1 - m);
-            b[s] = kf[s] * ex2(m - RegA[row][c8 + s]);
-        }
-        sstore16(Rm, row, c8, pack8(a));
-        sstore16(Km, row, c8, pack8(b));
-    }
-    __syncthreads();
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        sstore16(Sin, row, c8, sq[p]);
-    }
-    __syncthreads();
-
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(&RegA[0][0]);
     const int lane = threadIdx.x & 63, W = threadIdx.x >> 6;
     const int lr = lane & 15, lq = lane >> 4;
     const int t = 16 * W + lr;
-    f32x4 acc[4] = {};
+
+    FwdPrefetch nx;
+    if ((int)blockIdx.x < njobs) fwd_issue(nx, r, k, v, w, Hs, blockIdx.x, T, NT);
+    for (int job = blockIdx.x; job < njobs; job += gridDim.x) {
+        const int bh = job / NT, c = job - bh * NT, h = bh % H;
+        const int t0 = c * CL, nvalid = min(CL, T - t0);
+        const size_t base = ((size_t)bh * T + t0) * KD;
+        uint4 kc[2], sc[2];                    // k and S_in of this job stay in registers
+        __syncthreads();                       // the previous job is done with every tile
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        float f[8];
-        dir8_vec(emu[W], 32 * ks, f);
-        const bf16x8 a = scale8(ld_dir8(&Rm[0][0], t, 32 * ks), f);
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+            sstore16(Vm, row, c8, nx.v[p]);
+            sstore16(Rm, row, c8, nx.r[p]);                  // raw r, scaled in place below
+            sstore16(Km, row, c8, nx.w[p]);                  // w scratch
+            float rf[8], kf[8], uf[8], bsum = 0.f;
+            unpack8(nx.r[p], rf);
+            unpack8(nx.k[p], kf);
+            load_u8(u, u_dtype, h * KD + c8, uf);
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Sin[0][0], 32 * ks, 16 * tj), acc[tj]);
-    }
-    for (int J = 0; J <= W; ++J) {
-        const bool diag = (J == W);
-        f32x4 at = {};
+            for (int s8 = 0; s8 < 8; ++s8) bsum += rf[s8] * uf[s8] * kf[s8];
+            bsum = sum8lanes(bsum);
+            if ((threadIdx.x & 7) == 0) bonus[row] = bsum;
+            kc[p] = nx.k[p];
+            sc[p] = nx.s[p];
+        }
+        if (job + (int)gridDim.x < njobs) fwd_issue(nx, r, k, v, w, Hs, job + gridDim.x, T, NT);
+        __syncthreads();
+        build_G<NTHR>(Km, Gm, tot);
+        {
+            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+            emu[part][i] = ex2(Gm[16 * part + 7][i]);
+            for (int pi = part; pi < 6; pi += 4) {
+                const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
+                fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 7][i]);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+            const int mrow = 16 * (row >> 4) + 7;
+            float rf[8], kf[8], a[8], b[8];
+            unpack8(*reinterpret_cast<const uint4*>(&Rm[row][c8]), rf);
+            unpack8(kc[p], kf);
+#pragma unroll
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const float m = Gm[mrow][c8 + s8];
+                const float gm1 = row > 0 ? Gm[row - 1][c8 + s8] : 0.f;
+                a[s8] = rf[s8] * ex2(gm1 - m);
+                b[s8] = kf[s8] * ex2(m - Gm[row][c8 + s8]);
+            }
+            sstore16(Rm, row, c8, pack8(a));
+            sstore16(Km, row, c8, pack8(b));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+            sstore16(Sin, row, c8, sc[p]);
+        }
+        __syncthreads();
+
+        f32x4 acc[4] = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 rb = ld_row8(&Rm[0][0], t, 32 * ks);
-            if (!diag) {
-                float f[8];
-                row8_vec(fp[pair_index(W, J)], 32 * ks, f);
-                rb = scale8(rb, f);
-            }
-            at = mfma32(ld_row8(&Km[0][0], 16 * J + lr, 32 * ks), rb, at);   // A^T[tau][t]
-        }
-        bf16x4 aop;
+            float f[8];
+            dir8_vec(emu[W], 32 * ks, f);
+            const bf16x8 a = scale8(ld_dir8(&Rm[0][0], t, 32 * ks), f);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            float x = at[rr];
-            if (diag) {
-                const int tl = 4 * lq + rr;
-                x = tl < lr ? x : (tl == lr ? bonus[t] : 0.f);
-            }
-            aop[rr] = (__bf16)x;
+            for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Sin[0][0], 32 * ks, 16 * tj), acc[tj]);
         }
+        for (int J = 0; J <= W; ++J) {
+            const bool diag = (J == W);
+            f32x4 at = {};
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma16(aop, ld_tr4(&Vm[0][0], 16 * J, 16 * tj), acc[tj]);
+            for (int ks = 0; ks < 2; ++ks) {
+                bf16x8 rb = ld_row8(&Rm[0][0], t, 32 * ks);
+                if (!diag) {
+                    float f[8];
+                    row8_vec(fp[pair_index(W, J)], 32 * ks, f);
+                    rb = scale8(rb, f);
+                }
+                at = mfma32(ld_row8(&Km[0][0], 16 * J + lr, 32 * ks), rb, at);   // A^T[tau][t]
+            }
+            bf16x4 aop;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                float x = at[rr];
+                if (diag) {
+                    const int tl = 4 * lq + rr;
+                    x = tl < lr ? x : (tl == lr ? bonus[t] : 0.f);
+                }
+                aop[rr] = (__bf16)x;
+            }
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma16(aop, ld_tr4(&Vm[0][0], 16 * J, 16 * tj), acc[tj]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) Rm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
+        __syncthreads();
+        store_tile<NTHR>(o + base, Rm, nvalid);
     }
-    __syncthreads();
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Rm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
-    __syncthreads();
-    store_tile<NTHR>(o + base, Rm, nvalid);
 }
 
 // ---------------------------------------------------------------------------
@@ -454,6 +493,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     GradSmem& sm = *reinterpret_cast<GradSmem*>(smem_raw);
     uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&sm.A[0][0]);
     uint16_t (*dSm)[TS] = Sin + CL;
+    float (*Gv)[GSG] = reinterpret_cast<float (*)[GSG]>(&sm.A[0][0]);   // G view of the same region
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = ((size_t)bh * T + t0) * KD;
@@ -500,7 +540,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         if ((threadIdx.x & 7) == 0) sm.Dv[row] = d;
     }
     __syncthreads();
-    build_G<NTHR_G>(sm.RmL, sm.A, &sm.red[0][0]);
+    build_G<NTHR_G>(sm.RmL, Gv, &sm.red[0][0]);
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int W = wv >> 1, hh = wv & 1;
@@ -526,13 +566,13 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         // tables
         const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
         if (part < 4) {
-            const float m = sm.A[16 * part + 7][i];
+            const float m = Gv[16 * part + 7][i];
             sm.emu[part][i] = ex2(m);
-            sm.eg[part][i] = ex2(sm.A[CL - 1][i] - m);
+            sm.eg[part][i] = ex2(Gv[CL - 1][i] - m);
         } else {
             for (int pi = part - 4; pi < 6; pi += 4) {
                 const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                sm.fp[pi][i] = ex2(sm.A[16 * I + 7][i] - sm.A[16 * J + 7][i]);
+                sm.fp[pi][i] = ex2(Gv[16 * I + 7][i] - Gv[16 * J + 7][i]);
             }
         }
         // operand tiles Rm, Km (hi/lo); the w scratch in RmL was consumed by build_G
@@ -540,10 +580,10 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         float a[8], b[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const float m = sm.A[mrow][c8 + s];
-            const float gm1 = row > 0 ? sm.A[row - 1][c8 + s] : 0.f;
+            const float m = Gv[mrow][c8 + s];
+            const float gm1 = row > 0 ? Gv[row - 1][c8 + s] : 0.f;
             a[s] = rf[s] * ex2(gm1 - m);
-            b[s] = kf[s] * ex2(m - sm.A[row][c8 + s]);
+            b[s] = kf[s] * ex2(m - Gv[row][c8 + s]);
         }
         uint4 hi, lo;
         pack8_split(a, hi, lo);
@@ -559,11 +599,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
-        const float m = sm.A[16 * W + 7][i];
+        const float m = Gv[16 * W + 7][i];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
-            const float em = (tt > 0 ? sm.A[tt - 1][i] : 0.f) - m, ek = m - sm.A[tt][i];
+            const float em = (tt > 0 ? Gv[tt - 1][i] : 0.f) - m, ek = m - Gv[tt][i];
             Fm[tp][rr] = ex2(em);
             iFm[tp][rr] = ex2(-em);
             Fk[tp][rr] = ex2(ek);
@@ -797,6 +837,19 @@ int launch_status() {
     return e == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH;
 }
 
+// Number of workgroups of `kernel` that fit on the current device at once (for persistent
+// grid-stride kernels; correctness does not depend on all of them being resident).
+inline int resident_groups(const void* kernel, int threads, size_t dyn_lds) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, dyn_lds) != hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    return cus * per_cu;
+}
+
 // Records phase_events[i] (a hipEvent_t) on the stream when the caller asked for timing.
 inline void mark(void* const* ev, int i, hipStream_t s) {
     if (ev && ev[i]) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
@@ -856,9 +909,12 @@ int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 4, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL(wkv6_fwd_chunk_output, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
+        const int njobs = (int)(NT * BH);
+        const int nwg = std::min(njobs, resident_groups(reinterpret_cast<const void*>(wkv6_fwd_chunk_output),
+                                                        NTHR, 0));
+        hipLaunchKernelGGL(wkv6_fwd_chunk_output, dim3((unsigned)nwg), dim3(NTHR), 0, s, (const uint16_t*)r,
                            (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, u, u_dtype,
-                           (const uint16_t*)Hs, (uint16_t*)o, scale, (int)H, (int)T, (int)NT);
+                           (const uint16_t*)Hs, (uint16_t*)o, scale, (int)H, (int)T, (int)NT, njobs);
     }
     mark(phase_events, 5, s);
     return launch_status();
