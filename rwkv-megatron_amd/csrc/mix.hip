@@ -16,7 +16,6 @@
 #include "../../include/rwkv6_amd.h"
 
 #define MIX_NE 5          // number of data-dependent mixes (w,k,v,r,g)
-#define MIX_SEG 64        // tokens walked per thread in the backward
 #define MIX_THR 256
 
 namespace {
@@ -96,63 +95,78 @@ rwkv6_ddlerp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
     }
 }
 
-// d_mexp[e][t] = d_mixed[e][t] * delta[t]; part[(seg*B + b)][e][C] = sum over the
-// segment's tokens (thread = (segment of MIX_SEG tokens, batch b, 8 channels)).
+// Backward kernels: block = 8 token sub-segments x 32 channel groups (256 threads); the
+// block covers tokens [64*blockIdx.x, +64) of batch blockIdx.z and channels
+// [256*blockIdx.y, +256).  Thread (ss, cgl) walks 8 tokens of 8 channels.  Parameter
+// partial sums are reduced over the 8 sub-segments in LDS (fixed order) and written
+// per (token block, batch): part[(tblk*B + b)][rows][C].
+#define MIX_TB 64          // tokens per block
+#define MIX_SS 8           // tokens per thread
+
+// d_mexp[e][t] = d_mixed[e][t] * delta[t];  part rows e = 0..4 (d_bias)
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dmix,
                         uint16_t* __restrict__ dmexp, float* __restrict__ part, int64_t T,
                         int64_t B, int64_t C) {
-    const int64_t C8 = C / 8;
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
-    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    if (idx >= nseg * B * C8) return;
-    const int64_t cg = idx % C8, rest = idx / C8;
-    const int64_t b = rest % B, seg = rest / B;
-    const int64_t N = T * B;
-    const int64_t t_lo = seg * MIX_SEG, t_hi = min(T, t_lo + MIX_SEG);
+    __shared__ float red[MIX_SS][MIX_NE][32 * 8 + 4];
+    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
+    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
+    const int64_t b = blockIdx.z, N = T * B;
+    const int64_t t_lo = (int64_t)blockIdx.x * MIX_TB + MIX_SS * ss;
+    const int64_t t_hi = min(T, t_lo + MIX_SS);
     float acc[MIX_NE][8];
 #pragma unroll
     for (int e = 0; e < MIX_NE; ++e)
 #pragma unroll
         for (int s = 0; s < 8; ++s) acc[e][s] = 0.f;
-    float xprev[8];
-    if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
-    else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
-    for (int64_t t = t_lo; t < t_hi; ++t) {
-        const int64_t off = (t * B + b) * C + 8 * cg;
-        float xv[8], delta[8];
-        load8(x + off, xv);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            delta[s] = xprev[s] - xv[s];
-            xprev[s] = xv[s];
-        }
-#pragma unroll
-        for (int e = 0; e < MIX_NE; ++e) {
-            float g[8], out[8];
-            load8(dmix + e * N * C + off, g);
+    if (cg < C8 && t_lo < T) {
+        float xprev[8];
+        if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
+        else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
+        for (int64_t t = t_lo; t < t_hi; ++t) {
+            const int64_t off = (t * B + b) * C + 8 * cg;
+            float xv[8], delta[8];
+            load8(x + off, xv);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                out[s] = g[s] * delta[s];
-                acc[e][s] += out[s];
+                delta[s] = xprev[s] - xv[s];
+                xprev[s] = xv[s];
             }
-            store8(dmexp + e * N * C + off, out);
+#pragma unroll
+            for (int e = 0; e < MIX_NE; ++e) {
+                float g[8], out[8];
+                load8(dmix + e * N * C + off, g);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    out[s] = g[s] * delta[s];
+                    acc[e][s] += out[s];
+                }
+                store8(dmexp + e * N * C + off, out);
+            }
         }
     }
-    float* pp = part + (seg * B + b) * MIX_NE * C + 8 * cg;
 #pragma unroll
-    for (int e = 0; e < MIX_NE; ++e) {
-        float4* q = reinterpret_cast<float4*>(pp + e * C);
-        q[0] = make_float4(acc[e][0], acc[e][1], acc[e][2], acc[e][3]);
-        q[1] = make_float4(acc[e][4], acc[e][5], acc[e][6], acc[e][7]);
+    for (int e = 0; e < MIX_NE; ++e)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) red[ss][e][8 * cgl + s] = acc[e][s];
+    __syncthreads();
+    const int64_t P_row = (int64_t)blockIdx.x * B + b;
+    for (int j = threadIdx.x; j < MIX_NE * 256; j += MIX_THR) {
+        const int e = j >> 8, c = j & 255;
+        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
+        if (ch >= C) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < MIX_SS; ++q) sum += red[q][e][c];
+        part[(P_row * MIX_NE + e) * C + ch] = sum;
     }
 }
 
-// Input gradient of both lerps.  Thread = (segment, batch b, 8 channels), walking
-// its tokens from last to first and carrying d_delta[t+1]:
+// Input gradient of both lerps, d_maa partial (part row 0):
 //   d_delta[t] = sum_e dmix_e[t] m_e[t] + dxxx[t] maa,   m_e = mexp_e + bias_e
 //   dx[t]      = sum_e dmix_e[t] + dxxx[t] - d_delta[t] + d_delta[t+1]
-//   part[(seg*B + b)][C] = sum over the segment of dxxx[t] delta[t]   (d_maa)
+// Walked forward with dx[t] emitted one token late; d_delta of each sub-segment's first
+// token is handed to the previous sub-segment through LDS.
 __device__ __forceinline__ void mix_token(const uint16_t* __restrict__ mexp, const float* bb,
                                           const float* mv, const uint16_t* __restrict__ dmix,
                                           const uint16_t* __restrict__ dxxx, int64_t off,
@@ -183,60 +197,101 @@ rwkv6_mix_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ ma
                      const uint16_t* __restrict__ dmix, const uint16_t* __restrict__ dxxx,
                      uint16_t* __restrict__ dx, float* __restrict__ part, int64_t T, int64_t B,
                      int64_t C) {
-    const int64_t C8 = C / 8;
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
-    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    if (idx >= nseg * B * C8) return;
-    const int64_t cg = idx % C8, rest = idx / C8;
-    const int64_t b = rest % B, seg = rest / B;
-    const int64_t NC = T * B * C;
-    const int64_t t_lo = seg * MIX_SEG, t_hi = min(T, t_lo + MIX_SEG);
-    float mv[8], bb[MIX_NE * 8];
-    load_param8(maa, pdt, 8 * cg, mv);
-#pragma unroll
-    for (int e = 0; e < MIX_NE; ++e) load_param8(bias, pdt, e * C + 8 * cg, bb + 8 * e);
-    float dnext[8], acc[8];
+    __shared__ float first_dd[MIX_SS][32][8];
+    __shared__ float red[MIX_SS][32 * 8 + 4];
+    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
+    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
+    const int64_t b = blockIdx.z, NC = T * B * C;
+    const int64_t tb0 = (int64_t)blockIdx.x * MIX_TB;
+    const int64_t t_lo = tb0 + MIX_SS * ss, t_hi = min(T, t_lo + MIX_SS);
+    const bool active = cg < C8 && t_lo < T;
+    float acc[8], pend[8], mv[8], bb[MIX_NE * 8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc[s] = 0.f;
-    if (t_hi < T) {
-        float dsum[8], dxv[8];
-        mix_token(mexp, bb, mv, dmix, dxxx, (t_hi * B + b) * C + 8 * cg, NC, dnext, dsum, dxv);
-    } else {
+    if (active) {
+        load_param8(maa, pdt, 8 * cg, mv);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) dnext[s] = 0.f;
-    }
-    float xcur[8];
-    load8(x + ((t_hi - 1) * B + b) * C + 8 * cg, xcur);
-    for (int64_t t = t_hi - 1; t >= t_lo; --t) {
-        const int64_t off = (t * B + b) * C + 8 * cg;
-        float xprev[8], dd[8], dsum[8], dxv[8], out[8];
-        if (t > 0) load8(x + off - B * C, xprev);
+        for (int e = 0; e < MIX_NE; ++e) load_param8(bias, pdt, e * C + 8 * cg, bb + 8 * e);
+        float xprev[8];
+        if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
         else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
-        mix_token(mexp, bb, mv, dmix, dxxx, off, NC, dd, dsum, dxv);
+        for (int64_t t = t_lo; t < t_hi; ++t) {
+            const int64_t off = (t * B + b) * C + 8 * cg;
+            float xv[8], dd[8], dsum[8], dxv[8], out[8];
+            load8(x + off, xv);
+            mix_token(mexp, bb, mv, dmix, dxxx, off, NC, dd, dsum, dxv);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            out[s] = dsum[s] - dd[s] + dnext[s];
-            acc[s] += dxv[s] * (xprev[s] - xcur[s]);
-            dnext[s] = dd[s];
-            xcur[s] = xprev[s];
+            for (int s = 0; s < 8; ++s) {
+                acc[s] += dxv[s] * (xprev[s] - xv[s]);
+                xprev[s] = xv[s];
+            }
+            if (t > t_lo) {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) out[s] = pend[s] + dd[s];
+                store8(dx + off - B * C, out);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) first_dd[ss][cgl][s] = dd[s];
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) pend[s] = dsum[s] - dd[s];
         }
-        store8(dx + off, out);
     }
-    float4* q = reinterpret_cast<float4*>(part + (seg * B + b) * C + 8 * cg);
-    q[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    q[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    __syncthreads();
+    if (active) {
+        // d_delta of the token after this sub-segment
+        float nd[8];
+        if (t_hi >= T) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = 0.f;
+        } else if (ss + 1 < MIX_SS) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = first_dd[ss + 1][cgl][s];
+        } else {
+            float dsum[8], dxv[8];
+            mix_token(mexp, bb, mv, dmix, dxxx, (t_hi * B + b) * C + 8 * cg, NC, nd, dsum, dxv);
+        }
+        float out[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) out[s] = pend[s] + nd[s];
+        store8(dx + ((t_hi - 1) * B + b) * C + 8 * cg, out);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) red[ss][8 * cgl + s] = acc[s];
+    __syncthreads();
+    const int64_t P_row = (int64_t)blockIdx.x * B + b;
+    for (int c = threadIdx.x; c < 256; c += MIX_THR) {
+        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
+        if (ch >= C) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < MIX_SS; ++q) sum += red[q][c];
+        part[P_row * C + ch] = sum;
+    }
 }
 
-// out[n] = sum_p part[p][n] for n < Nn, in param dtype; fixed order.
+// out[n] = sum_p part[p][n] for n < Nn, in param dtype; thread (n, q): strided partial over
+// p = q mod 8, then a fixed-order combine (deterministic).
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
                  void* __restrict__ out) {
-    const int64_t n = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    if (n >= Nn) return;
+    __shared__ float acc8[8][32];
+    const int q = threadIdx.x >> 5, nl = threadIdx.x & 31;
+    const int64_t n = (int64_t)blockIdx.x * 32 + nl;
     float acc = 0.f;
-    for (int64_t p = 0; p < P; ++p) acc += part[p * Nn + n];
-    if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(out)[n] = f2bf(acc);
-    else reinterpret_cast<float*>(out)[n] = acc;
+    if (n < Nn) {
+#pragma unroll 4
+        for (int64_t p = q; p < P; p += 8) acc += part[p * Nn + n];
+    }
+    acc8[q][nl] = acc;
+    __syncthreads();
+    if (q == 0 && n < Nn) {
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tot += acc8[j][nl];
+        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(out)[n] = f2bf(tot);
+        else reinterpret_cast<float*>(out)[n] = tot;
+    }
 }
 
 namespace {
@@ -283,8 +338,12 @@ int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int para
 
 size_t rwkv6_ddlerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
     if (T < 0 || B < 1 || C < 8) return 0;
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
-    return (size_t)((nseg > 0 ? nseg : 1) * B * MIX_NE * C) * sizeof(float);
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
+    return (size_t)((ntb > 0 ? ntb : 1) * B * MIX_NE * C) * sizeof(float);
+}
+
+static dim3 bwd_grid(int64_t T, int64_t B, int64_t C) {
+    return dim3((unsigned)((T + MIX_TB - 1) / MIX_TB), (unsigned)((C / 8 + 31) / 32), (unsigned)B);
 }
 
 int rwkv6_ddlerp_bwd(const void* x, const void* d_mixed, int param_dtype, void* d_mexp,
@@ -292,24 +351,25 @@ int rwkv6_ddlerp_bwd(const void* x, const void* d_mixed, int param_dtype, void* 
                      void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
+    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
     if (!d_bias || !workspace || (T > 0 && (!x || !d_mixed || !d_mexp))) return RWKV6_ERR_INVALID_ARG;
     if (!al16(x) || !al16(d_mixed) || !al16(d_mexp) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
     if (T > 0)
-        hipLaunchKernelGGL(rwkv6_ddlerp_bwd_kernel, dim3(nblocks(nseg * B * (C / 8))), dim3(MIX_THR),
-                           0, s, (const uint16_t*)x, (const uint16_t*)d_mixed, (uint16_t*)d_mexp,
-                           part, T, B, C);
-    hipLaunchKernelGGL(rwkv6_col_reduce, dim3(nblocks(MIX_NE * C)), dim3(MIX_THR), 0, s, part,
-                       T > 0 ? nseg * B : (int64_t)0, (int64_t)MIX_NE * C, param_dtype, d_bias);
+        hipLaunchKernelGGL(rwkv6_ddlerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
+                           (const uint16_t*)x, (const uint16_t*)d_mixed, (uint16_t*)d_mexp, part, T,
+                           B, C);
+    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((MIX_NE * C + 31) / 32)), dim3(MIX_THR), 0, s,
+                       part, T > 0 ? ntb * B : (int64_t)0, (int64_t)MIX_NE * C, param_dtype, d_bias);
     return launch_status();
 }
 
 size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
     if (T < 0 || B < 1 || C < 8) return 0;
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
-    return (size_t)((nseg > 0 ? nseg : 1) * B * C) * sizeof(float);
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
+    return (size_t)((ntb > 0 ? ntb : 1) * B * C) * sizeof(float);
 }
 
 int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
@@ -318,21 +378,22 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
                   void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
+    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
     if (!maa || !bias || !d_maa || !workspace || (T > 0 && (!x || !mexp || !d_mixed || !dx)))
         return RWKV6_ERR_INVALID_ARG;
     if (!al16(x) || !al16(maa) || !al16(mexp) || !al16(bias) || !al16(d_mixed) ||
         (d_xxx && !al16(d_xxx)) || !al16(dx) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t nseg = (T + MIX_SEG - 1) / MIX_SEG;
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
     if (T > 0)
-        hipLaunchKernelGGL(rwkv6_mix_bwd_kernel, dim3(nblocks(nseg * B * (C / 8))), dim3(MIX_THR), 0,
-                           s, (const uint16_t*)x, maa, (const uint16_t*)mexp, bias, param_dtype,
+        hipLaunchKernelGGL(rwkv6_mix_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
+                           (const uint16_t*)x, maa, (const uint16_t*)mexp, bias, param_dtype,
                            (const uint16_t*)d_mixed, (const uint16_t*)d_xxx, (uint16_t*)dx, part,
                            T, B, C);
-    hipLaunchKernelGGL(rwkv6_col_reduce, dim3(nblocks(C)), dim3(MIX_THR), 0, s, part,
-                       T > 0 ? nseg * B : (int64_t)0, C, param_dtype, d_maa);
+    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(MIX_THR), 0, s, part,
+                       T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
     return launch_status();
 }
 
