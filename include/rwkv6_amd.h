@@ -78,6 +78,22 @@ int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, co
                   int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
                   void* stream);
 
+/* Sequence-first variant for the time-mix module (the layout of WKV6.forward's inputs
+ * before its rearranges, rwkv6_layer_specs.py:330-336): r, k, v and `decay` are
+ * [T,B,H*K] bf16 straight from the linear layers, the log-decay w = -exp(decay) of :336 is
+ * evaluated inside the kernels, o and dO stay head-first [B,H,T,V] (the layout
+ * rwkv6_gn_gate_* reads with head_first=1).  The backward writes dr, dk, dv and
+ * d_decay = dw * w in [T,B,H*K].  Same `saved` / `workspace` sizes as the head-first calls. */
+int rwkv6_wkv_fwd_seqfirst(const void* r, const void* k, const void* v, const void* decay,
+                           const void* u, int u_dtype, const float* h0, void* o, float* hT,
+                           void* saved, void* workspace, int64_t B, int64_t H, int64_t T,
+                           int64_t K, int64_t V, float scale, void* stream);
+int rwkv6_wkv_bwd_seqfirst(const void* r, const void* k, const void* v, const void* decay,
+                           const void* u, int u_dtype, const void* dO, const float* dhT,
+                           const void* saved, void* dr, void* dk, void* dv, void* d_decay,
+                           void* du, float* dh0, void* workspace, int64_t B, int64_t H,
+                           int64_t T, int64_t K, int64_t V, float scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Token shift and lerps of RWKV6TimeMix.forward, sequence-first [T,B,C] bf16.
  *   shift(x)[t] = x[t-1], shift(x)[0] = 0              (rwkv6_layer_specs.py:294-300)

@@ -9,7 +9,7 @@ Exports
   modules                              RWKV6TimeMix / RWKV6ChannelMix / ... mirrors of
                                        rwkv_megatron/rwkv6_layer_specs.py
 """
-from .wkv import chunk_rwkv6, fused_recurrent_rwkv6  # noqa: F401
+from .wkv import chunk_rwkv6, fused_recurrent_rwkv6, wkv6_seqfirst  # noqa: F401
 from . import _lib, timemix, modules  # noqa: F401
 
-__all__ = ["chunk_rwkv6", "fused_recurrent_rwkv6", "timemix", "modules"]
+__all__ = ["chunk_rwkv6", "fused_recurrent_rwkv6", "wkv6_seqfirst", "timemix", "modules"]

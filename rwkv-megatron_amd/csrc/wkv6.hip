@@ -129,32 +129,62 @@ __device__ __forceinline__ void sstore16(uint16_t (*X)[TS], int row, int c8, uin
     *reinterpret_cast<uint4*>(&X[row][c8]) = v;
 }
 
-// Token-major LDS tile -> global (rows < nvalid), nthr threads.
+// Same with an explicit token (row) stride in elements.
+__device__ __forceinline__ uint4 gload16s(const uint16_t* __restrict__ src, int row, int c8,
+                                          int nvalid, size_t rs) {
+    if (row < nvalid) return *reinterpret_cast<const uint4*>(src + (size_t)row * rs + c8);
+    return make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Token tensors come in two layouts:
+//   head-first  [B,H,T,64]   (fla's contract)                 SEQ = false
+//   seq-first   [T,B,H*64]   (the linear-layer outputs, :454-457) SEQ = true
+// tok_base gives the element offset of (b*H + h, token t0); tok_rs the token stride.
+template <bool SEQ>
+__device__ __forceinline__ size_t tok_base(int bh, int t0, int B, int H, int T) {
+    if (SEQ) {
+        const int b = bh / H, h = bh - b * H;
+        return (((size_t)t0 * B + b) * H + h) * KD;
+    }
+    return ((size_t)bh * T + t0) * KD;
+}
+template <bool SEQ>
+__device__ __forceinline__ size_t tok_rs(int B, int H) {
+    return SEQ ? (size_t)B * H * KD : (size_t)KD;
+}
+
+// Token-major LDS tile -> global (rows < nvalid, token stride rs), NT_ threads.
 template <int NT_>
 __device__ __forceinline__ void store_tile(uint16_t* __restrict__ dst, uint16_t (*tok)[TS],
-                                           int nvalid) {
+                                           int nvalid, size_t rs = KD) {
 #pragma unroll
     for (int p = 0; p < 512 / NT_; ++p) {
         int idx = p * NT_ + threadIdx.x;
         int row = idx >> 3, c8 = (idx & 7) * 8;
         if (row < nvalid)
-            *reinterpret_cast<uint4*>(dst + (size_t)row * KD + c8) =
+            *reinterpret_cast<uint4*>(dst + (size_t)row * rs + c8) =
                 *reinterpret_cast<const uint4*>(&tok[row][c8]);
     }
 }
 
 // Inclusive cumulative log2-decay over the 64 tokens of a chunk (token-major fp32
-// Gm[t][i]) from a token-major bf16 w tile, NT_ threads (NT_/64 token parts).
+// Gm[t][i]) from a token-major bf16 tile, NT_ threads (NT_/64 token parts).  The tile
+// holds the log-decay w, or (DEC) the pre-activation `decay` with w = -exp(decay)
+// (rwkv6_layer_specs.py:336) evaluated here in fp32.  Padding rows must read as w = 0:
+// callers zero-fill them (DEC: the kernel masks rows >= nvalid).
 // `tot` holds NT_ floats.  Ends with a barrier.
-template <int NT_>
-__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], float* tot) {
+template <int NT_, bool DEC = false>
+__device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], float* tot,
+                                        int nvalid = CL) {
     constexpr int NP = NT_ / 64, PL = CL / NP;
     const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
     float loc[PL];
     float run = 0.f;
 #pragma unroll
     for (int s = 0; s < PL; ++s) {
-        run += bf2f(Wm[PL * part + s][i]) * RW_L2E;
+        const float x = bf2f(Wm[PL * part + s][i]);
+        if (DEC) run += (PL * part + s < nvalid) ? -ex2(x * RW_L2E) * RW_L2E : 0.f;
+        else run += x * RW_L2E;
         loc[s] = run;
     }
     tot[part * 64 + i] = run;
@@ -189,28 +219,32 @@ __device__ __forceinline__ float sum8lanes(float v) {
 //   forward : X = k, E = G_63 - G_t,   Y = v      (S_loc)
 //   backward: X = r, E = G_{t-1},      Y = dO     (dS_loc)
 // and, forward only, decay[i] = e^{G_63[i]}.
-template <bool FWD>
+// SEQ: X and w (as pre-activation decay) are sequence-first; Y is v (sequence-first) in
+// the forward and dO (always head-first) in the backward.
+template <bool FWD, bool SEQ>
 __global__ void __launch_bounds__(NTHR)
 wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
                  const uint16_t* __restrict__ w, float* __restrict__ out,
-                 float* __restrict__ decay, float scale, int T, int NT) {
+                 float* __restrict__ decay, float scale, int B, int H, int T, int NT) {
     __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
     __shared__ __attribute__((aligned(16))) float Gstore[CL * GSG];
     __shared__ float tot[NTHR];
     float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(Gstore);
     const int c = blockIdx.x, bh = blockIdx.y;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = ((size_t)bh * T + t0) * KD;
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const size_t ybase = FWD ? base : tok_base<false>(bh, t0, B, H, T);
+    const size_t yrs = FWD ? rs : (size_t)KD;
     uint4 xr[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        xr[p] = gload16(X + base, row, c8, nvalid);
-        sstore16(Ys, row, c8, gload16(Y + base, row, c8, nvalid));
-        sstore16(Wm, row, c8, gload16(w + base, row, c8, nvalid));
+        xr[p] = gload16s(X + base, row, c8, nvalid, rs);
+        sstore16(Ys, row, c8, gload16s(Y + ybase, row, c8, nvalid, yrs));
+        sstore16(Wm, row, c8, gload16s(w + base, row, c8, nvalid, rs));
     }
     __syncthreads();
-    build_G<NTHR>(Wm, Gm, tot);
+    build_G<NTHR, SEQ>(Wm, Gm, tot, nvalid);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
@@ -319,31 +353,36 @@ struct FwdPrefetch {
     uint4 r[2], k[2], v[2], w[2], s[2];
 };
 
+template <bool SEQ>
 __device__ __forceinline__ void fwd_issue(FwdPrefetch& f, const uint16_t* __restrict__ r,
                                           const uint16_t* __restrict__ k,
                                           const uint16_t* __restrict__ v,
                                           const uint16_t* __restrict__ w,
-                                          const uint16_t* __restrict__ Hs, int job, int T, int NT) {
+                                          const uint16_t* __restrict__ Hs, int job, int B, int H,
+                                          int T, int NT) {
     const int bh = job / NT, c = job - bh * NT;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = ((size_t)bh * T + t0) * KD;
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
     const uint16_t* sp = Hs + ((size_t)bh * (NT + 1) + c) * KD * KD;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        f.r[p] = gload16(r + base, row, c8, nvalid);
-        f.k[p] = gload16(k + base, row, c8, nvalid);
-        f.v[p] = gload16(v + base, row, c8, nvalid);
-        f.w[p] = gload16(w + base, row, c8, nvalid);
+        f.r[p] = gload16s(r + base, row, c8, nvalid, rs);
+        f.k[p] = gload16s(k + base, row, c8, nvalid, rs);
+        f.v[p] = gload16s(v + base, row, c8, nvalid, rs);
+        f.w[p] = gload16s(w + base, row, c8, nvalid, rs);
         f.s[p] = gload16(sp, row, c8, KD);
     }
 }
 
+// SEQ: r, k, v and the pre-activation decay are sequence-first; o is always head-first.
+template <bool SEQ>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3, 3)))
 wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                       const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
                       const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ Hs,
-                      uint16_t* __restrict__ o, float scale, int H, int T, int NT, int njobs) {
+                      uint16_t* __restrict__ o, float scale, int B, int H, int T, int NT,
+                      int njobs) {
     __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vm;
     __shared__ __attribute__((aligned(16))) float RegA[CL][GS];   // G, then the S_in tile
     __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD];
@@ -355,11 +394,11 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
     const int t = 16 * W + lr;
 
     FwdPrefetch nx;
-    if ((int)blockIdx.x < njobs) fwd_issue(nx, r, k, v, w, Hs, blockIdx.x, T, NT);
+    if ((int)blockIdx.x < njobs) fwd_issue<SEQ>(nx, r, k, v, w, Hs, blockIdx.x, B, H, T, NT);
     for (int job = blockIdx.x; job < njobs; job += gridDim.x) {
         const int bh = job / NT, c = job - bh * NT, h = bh % H;
         const int t0 = c * CL, nvalid = min(CL, T - t0);
-        const size_t base = ((size_t)bh * T + t0) * KD;
+        const size_t obase = ((size_t)bh * T + t0) * KD;       // o: head-first
         uint4 kc[2], sc[2];                    // k and S_in of this job stay in registers
         __syncthreads();                       // the previous job is done with every tile
 #pragma unroll
@@ -379,9 +418,10 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
             kc[p] = nx.k[p];
             sc[p] = nx.s[p];
         }
-        if (job + (int)gridDim.x < njobs) fwd_issue(nx, r, k, v, w, Hs, job + gridDim.x, T, NT);
+        if (job + (int)gridDim.x < njobs)
+            fwd_issue<SEQ>(nx, r, k, v, w, Hs, job + gridDim.x, B, H, T, NT);
         __syncthreads();
-        build_G<NTHR>(Km, Gm, tot);
+        build_G<NTHR, SEQ>(Km, Gm, tot, nvalid);
         {
             const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
             emu[part][i] = ex2(Gm[16 * part + 7][i]);
@@ -456,7 +496,7 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) Rm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
         __syncthreads();
-        store_tile<NTHR>(o + base, Rm, nvalid);
+        store_tile<NTHR>(o + obase, Rm, nvalid);
     }
 }
 
@@ -481,6 +521,9 @@ struct GradSmem {
     float red[8][KD];               // build_G scratch, du partials, dw block totals
 };
 
+// SEQ: r, k, v, the pre-activation decay and dr, dk, dv, d_decay are sequence-first (dO is
+// head-first); the decay gradient is dw * w with w = -exp(decay).
+template <bool SEQ>
 __global__ void __launch_bounds__(NTHR_G)
 wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                      const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
@@ -488,7 +531,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
                      const uint16_t* __restrict__ Hs, const uint16_t* __restrict__ dHs,
                      uint16_t* __restrict__ dr, uint16_t* __restrict__ dk,
                      uint16_t* __restrict__ dv, uint16_t* __restrict__ dw,
-                     float* __restrict__ du_part, float scale, int H, int T, int NT) {
+                     float* __restrict__ du_part, float scale, int B, int H, int T, int NT) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     GradSmem& sm = *reinterpret_cast<GradSmem*>(smem_raw);
     uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&sm.A[0][0]);
@@ -496,17 +539,18 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     float (*Gv)[GSG] = reinterpret_cast<float (*)[GSG]>(&sm.A[0][0]);   // G view of the same region
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = ((size_t)bh * T + t0) * KD;
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const size_t dbase = ((size_t)bh * T + t0) * KD;           // dO: head-first
     const size_t st_in = ((size_t)bh * (NT + 1) + c) * KD * KD;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
 
     // ---- prologue: one 16-byte piece of every tile per thread ----
-    const uint4 rq = gload16(r + base, row, c8, nvalid), kq = gload16(k + base, row, c8, nvalid);
+    const uint4 rq = gload16s(r + base, row, c8, nvalid, rs), kq = gload16s(k + base, row, c8, nvalid, rs);
     {
-        const uint4 vq = gload16(v + base, row, c8, nvalid), dq = gload16(dO + base, row, c8, nvalid);
+        const uint4 vq = gload16s(v + base, row, c8, nvalid, rs), dq = gload16(dO + dbase, row, c8, nvalid);
         sstore16(sm.Vm, row, c8, vq);
         sstore16(sm.Dm, row, c8, dq);
-        sstore16(sm.RmL, row, c8, gload16(w + base, row, c8, nvalid));     // w scratch
+        sstore16(sm.RmL, row, c8, gload16s(w + base, row, c8, nvalid, rs));     // w scratch
         float rf[8], kf[8], uf[8], vf[8], df[8], b = 0.f, d = 0.f;
         unpack8(rq, rf);
         unpack8(kq, kf);
@@ -540,7 +584,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         if ((threadIdx.x & 7) == 0) sm.Dv[row] = d;
     }
     __syncthreads();
-    build_G<NTHR_G>(sm.RmL, Gv, &sm.red[0][0]);
+    build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int W = wv >> 1, hh = wv & 1;
@@ -777,15 +821,18 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int s = 7; s >= 0; --s) {
             const int tt = 8 * part + s;
-            sm.KmL[tt][i] = f2bf(run + Ys[tt][i]);
+            float g = run + Ys[tt][i];
+            if (SEQ && tt < nvalid)            // d decay = dw * w, w = -exp(decay)
+                g *= -ex2(bf2f(w[base + (size_t)tt * rs + i]) * RW_L2E);
+            sm.KmL[tt][i] = f2bf(g);
             run += Xs[tt][i];
         }
     }
     __syncthreads();
-    store_tile<NTHR_G>(dr + base, sm.RmH, nvalid);
-    store_tile<NTHR_G>(dk + base, sm.RmL, nvalid);
-    store_tile<NTHR_G>(dv + base, sm.KmH, nvalid);
-    store_tile<NTHR_G>(dw + base, sm.KmL, nvalid);
+    store_tile<NTHR_G>(dr + base, sm.RmH, nvalid, rs);
+    store_tile<NTHR_G>(dk + base, sm.RmL, nvalid, rs);
+    store_tile<NTHR_G>(dv + base, sm.KmH, nvalid, rs);
+    store_tile<NTHR_G>(dw + base, sm.KmL, nvalid, rs);
 }
 
 // du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q), q < 16: strided partial sum over
@@ -875,10 +922,15 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
     return sz;
 }
 
-int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
-                     int u_dtype, const float* h0, void* o, float* hT, void* saved,
-                     void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
-                     float scale, void* stream, void* const* phase_events) {
+}  // extern "C"
+
+namespace {
+
+template <bool SEQ>
+int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, const void* u,
+                 int u_dtype, const float* h0, void* o, float* hT, void* saved, void* workspace,
+                 int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                 void* stream, void* const* phase_events) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
@@ -897,9 +949,9 @@ int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL(wkv6_chunk_local<true>, grid, dim3(NTHR), 0, s,
+        hipLaunchKernelGGL((wkv6_chunk_local<true, SEQ>), grid, dim3(NTHR), 0, s,
                            (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, Sloc, decay,
-                           1.0f, (int)T, (int)NT);
+                           1.0f, (int)B, (int)H, (int)T, (int)NT);
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
@@ -908,23 +960,24 @@ int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 3, s);
     mark(phase_events, 4, s);
     if (NT > 0) {
-        dim3 grid((unsigned)NT, (unsigned)BH);
         const int njobs = (int)(NT * BH);
-        const int nwg = std::min(njobs, resident_groups(reinterpret_cast<const void*>(wkv6_fwd_chunk_output),
-                                                        NTHR, 0));
-        hipLaunchKernelGGL(wkv6_fwd_chunk_output, dim3((unsigned)nwg), dim3(NTHR), 0, s, (const uint16_t*)r,
-                           (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, u, u_dtype,
-                           (const uint16_t*)Hs, (uint16_t*)o, scale, (int)H, (int)T, (int)NT, njobs);
+        const int nwg = std::min(
+            njobs, resident_groups(reinterpret_cast<const void*>(wkv6_fwd_chunk_output<SEQ>), NTHR, 0));
+        hipLaunchKernelGGL(wkv6_fwd_chunk_output<SEQ>, dim3((unsigned)nwg), dim3(NTHR), 0, s,
+                           (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
+                           (const uint16_t*)w, u, u_dtype, (const uint16_t*)Hs, (uint16_t*)o, scale,
+                           (int)B, (int)H, (int)T, (int)NT, njobs);
     }
     mark(phase_events, 5, s);
     return launch_status();
 }
 
-int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
-                     int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
-                     void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
-                     int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
-                     void* stream, void* const* phase_events) {
+template <bool SEQ>
+int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, const void* u,
+                 int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                 void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace, int64_t B,
+                 int64_t H, int64_t T, int64_t K, int64_t V, float scale, void* stream,
+                 void* const* phase_events) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
@@ -950,9 +1003,9 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 0, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL(wkv6_chunk_local<false>, grid, dim3(NTHR), 0, s, (const uint16_t*)r,
+        hipLaunchKernelGGL((wkv6_chunk_local<false, SEQ>), grid, dim3(NTHR), 0, s, (const uint16_t*)r,
                            (const uint16_t*)dO, (const uint16_t*)w, dSloc, (float*)nullptr, scale,
-                           (int)T, (int)NT);
+                           (int)B, (int)H, (int)T, (int)NT);
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
@@ -961,16 +1014,16 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
     mark(phase_events, 3, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<SEQ>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)sizeof(GradSmem)) != hipSuccess)
             return RWKV6_ERR_LAUNCH;
         mark(phase_events, 4, s);
-        hipLaunchKernelGGL(wkv6_bwd_chunk_grads, grid, dim3(NTHR_G), sizeof(GradSmem), s,
+        hipLaunchKernelGGL(wkv6_bwd_chunk_grads<SEQ>, grid, dim3(NTHR_G), sizeof(GradSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, Hs,
                            (const uint16_t*)dHs, (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv,
-                           (uint16_t*)dw, du_part, scale, (int)H, (int)T, (int)NT);
+                           (uint16_t*)dw, du_part, scale, (int)B, (int)H, (int)T, (int)NT);
         mark(phase_events, 5, s);
         mark(phase_events, 6, s);
         hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(DU_THR), 0, s, du_part, du, u_dtype,
@@ -983,12 +1036,33 @@ int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w,
     return launch_status();
 }
 
+}  // namespace
+
+extern "C" {
+
+int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const float* h0, void* o, float* hT, void* saved,
+                     void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                     float scale, void* stream, void* const* phase_events) {
+    return wkv_fwd_impl<false>(r, k, v, w, u, u_dtype, h0, o, hT, saved, workspace, B, H, T, K, V,
+                               scale, stream, phase_events);
+}
+
+int rwkv6_wkv_bwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
+                     int u_dtype, const void* dO, const float* dhT, const void* saved, void* dr,
+                     void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
+                     int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
+                     void* stream, void* const* phase_events) {
+    return wkv_bwd_impl<false>(r, k, v, w, u, u_dtype, dO, dhT, saved, dr, dk, dv, dw, du, dh0,
+                               workspace, B, H, T, K, V, scale, stream, phase_events);
+}
+
 int rwkv6_wkv_fwd(const void* r, const void* k, const void* v, const void* w, const void* u,
                   int u_dtype, const float* h0, void* o, float* hT, void* saved,
                   void* workspace, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
                   float scale, void* stream) {
-    return rwkv6_wkv_fwd_ex(r, k, v, w, u, u_dtype, h0, o, hT, saved, workspace, B, H, T, K, V,
-                            scale, stream, nullptr);
+    return wkv_fwd_impl<false>(r, k, v, w, u, u_dtype, h0, o, hT, saved, workspace, B, H, T, K, V,
+                               scale, stream, nullptr);
 }
 
 int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, const void* u,
@@ -996,8 +1070,25 @@ int rwkv6_wkv_bwd(const void* r, const void* k, const void* v, const void* w, co
                   void* dk, void* dv, void* dw, void* du, float* dh0, void* workspace,
                   int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
                   void* stream) {
-    return rwkv6_wkv_bwd_ex(r, k, v, w, u, u_dtype, dO, dhT, saved, dr, dk, dv, dw, du, dh0,
-                            workspace, B, H, T, K, V, scale, stream, nullptr);
+    return wkv_bwd_impl<false>(r, k, v, w, u, u_dtype, dO, dhT, saved, dr, dk, dv, dw, du, dh0,
+                               workspace, B, H, T, K, V, scale, stream, nullptr);
+}
+
+int rwkv6_wkv_fwd_seqfirst(const void* r, const void* k, const void* v, const void* decay,
+                           const void* u, int u_dtype, const float* h0, void* o, float* hT,
+                           void* saved, void* workspace, int64_t B, int64_t H, int64_t T,
+                           int64_t K, int64_t V, float scale, void* stream) {
+    return wkv_fwd_impl<true>(r, k, v, decay, u, u_dtype, h0, o, hT, saved, workspace, B, H, T, K,
+                              V, scale, stream, nullptr);
+}
+
+int rwkv6_wkv_bwd_seqfirst(const void* r, const void* k, const void* v, const void* decay,
+                           const void* u, int u_dtype, const void* dO, const float* dhT,
+                           const void* saved, void* dr, void* dk, void* dv, void* d_decay,
+                           void* du, float* dh0, void* workspace, int64_t B, int64_t H,
+                           int64_t T, int64_t K, int64_t V, float scale, void* stream) {
+    return wkv_bwd_impl<true>(r, k, v, decay, u, u_dtype, dO, dhT, saved, dr, dk, dv, d_decay, du,
+                              dh0, workspace, B, H, T, K, V, scale, stream, nullptr);
 }
 
 }  // extern "C"

@@ -7,7 +7,7 @@ way (Megatron's module prefix aside).  The hot path runs on the HIP kernels:
   RWKV6TimeMix.forward  (:431-468)
     token shift + lerp + LoRA + ddlerp   -> timemix.token_shift_mix   (HIP + hipBLASLt)
     decay LoRA, r/k/v/gate projections   -> torch.matmul (hipBLASLt)
-    WKV6                                 -> wkv.chunk_rwkv6           (HIP)
+    WKV6 (incl. -exp(decay), layout)     -> wkv.wkv6_seqfirst         (HIP, sequence-first entry)
     GroupNorm * silu(gate)               -> timemix.group_norm_gate   (HIP, head-first read)
     output projection                    -> torch.matmul
 
@@ -28,7 +28,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import timemix
-from .wkv import chunk_rwkv6
+from .wkv import chunk_rwkv6, wkv6_seqfirst
 
 
 @dataclass
@@ -180,8 +180,11 @@ class RWKV6TimeMix(nn.Module):
         value = self.linear_value(mixed_value)[0]
         receptance = self.linear_receptance(mixed_receptance)[0]
         gate_pre = self.linear_gate(mixed_gate)[0]
-        r, k, v, w, u = self.core_attention.head_first(receptance, key, value, decay)
-        o, _ = chunk_rwkv6(r, k, v, w, u, scale=1.0)
+        H = self.num_heads_per_partition
+        u = self.core_attention.time_first.view(H, self.head_size)
+        # WKV6 straight on the linear outputs: w = -exp(decay) and the head-first layout of
+        # :333-337 happen inside the kernels; o comes back head-first for GroupNorm*gate.
+        o, _ = wkv6_seqfirst(receptance, key, value, decay.contiguous(), u, H, scale=1.0)
         y = timemix.group_norm_gate(o, gate_pre, self.group_norm.weight, self.group_norm.bias,
                                     self.group_norm.eps, head_first=True)
         output, bias = self.linear_proj(y)

@@ -155,3 +155,74 @@ def fused_recurrent_rwkv6(r, k, v, w, u, scale=-1, initial_state=None, output_fi
     return chunk_rwkv6(r, k, v, w, u, scale=scale, initial_state=initial_state,
                        output_final_state=output_final_state, cu_seqlens=cu_seqlens,
                        head_first=head_first)
+
+
+class _WKV6SeqFirst(torch.autograd.Function):
+    """WKV6 on the time-mix module's own layout: r, k, v, decay [T,B,H*64] bf16 (the linear
+    outputs, rwkv6_layer_specs.py:454-457), w = -exp(decay) (:336) applied in the kernels,
+    output o head-first [B,H,T,64] (what GroupNorm*gate reads)."""
+
+    @staticmethod
+    def forward(ctx, r, k, v, decay, u, scale, H, h0, output_final_state):
+        T, B, C = r.shape
+        K = C // H
+        dev = r.device
+        rb, kb, vb, db = _bf16(r), _bf16(k), _bf16(v), _bf16(decay)
+        ua, u_code = _u_arg(u)
+        h0f = None if h0 is None else _aligned(h0.float())
+        L = _lib.load()
+        saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, K, K), dtype=torch.uint8, device=dev)
+        work = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 0), dtype=torch.uint8, device=dev)
+        o = torch.empty(B, H, T, K, dtype=torch.bfloat16, device=dev)
+        hT = torch.empty(B, H, K, K, dtype=torch.float32, device=dev) if output_final_state else None
+        _lib.check(L.rwkv6_wkv_fwd_seqfirst(_p(rb), _p(kb), _p(vb), _p(db), _p(ua), u_code, _p(h0f), _p(o),
+                                            _p(hT), _p(saved), _p(work), B, H, T, K, K, float(scale),
+                                            _stream_ptr(dev)), "rwkv6_wkv_fwd_seqfirst")
+        ctx.save_for_backward(rb, kb, vb, db, ua, saved)
+        ctx.meta = (scale, u_code, H, h0 is not None, u.dtype, r.dtype, k.dtype, v.dtype, decay.dtype,
+                    None if h0 is None else h0.dtype)
+        return o, hT
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        rb, kb, vb, db, ua, saved = ctx.saved_tensors
+        scale, u_code, H, has_h0, u_dt, r_dt, k_dt, v_dt, d_dt, h0_dt = ctx.meta
+        T, B, C = rb.shape
+        K = C // H
+        dev = rb.device
+        L = _lib.load()
+        dob = _bf16(do) if do is not None else torch.zeros(B, H, T, K, dtype=torch.bfloat16, device=dev)
+        dhtf = None if dht is None else _aligned(dht.float())
+        dr, dk, dv, ddec = (torch.empty_like(rb) for _ in range(4))
+        du = torch.empty(H, K, dtype=ua.dtype, device=dev)
+        need_h0 = has_h0 and ctx.needs_input_grad[7]
+        dh0 = torch.empty(B, H, K, K, dtype=torch.float32, device=dev) if need_h0 else None
+        work = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 1), dtype=torch.uint8, device=dev)
+        _lib.check(L.rwkv6_wkv_bwd_seqfirst(_p(rb), _p(kb), _p(vb), _p(db), _p(ua), u_code, _p(dob),
+                                            _p(dhtf), _p(saved), _p(dr), _p(dk), _p(dv), _p(ddec), _p(du),
+                                            _p(dh0), _p(work), B, H, T, K, K, float(scale),
+                                            _stream_ptr(dev)), "rwkv6_wkv_bwd_seqfirst")
+        cast = lambda t, dt: t if t.dtype == dt else t.to(dt)
+        return (cast(dr, r_dt), cast(dk, k_dt), cast(dv, v_dt), cast(ddec, d_dt), cast(du, u_dt),
+                None, None, None if dh0 is None else cast(dh0, h0_dt), None)
+
+
+def wkv6_seqfirst(r, k, v, decay, u, num_heads, scale=1.0, initial_state=None,
+                  output_final_state=False):
+    """WKV6 for the time-mix module: r, k, v, decay [T,B,H*64] (decay before -exp) ->
+    (o [B,H,T,64] head-first, final_state or None).  Same arithmetic as chunk_rwkv6 with
+    w = -exp(decay)."""
+    for name, t in (("r", r), ("k", k), ("v", v), ("decay", decay)):
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise ValueError(f"{name} must be a CUDA tensor")
+        if t.dim() != 3 or t.shape != r.shape:
+            raise ValueError(f"{name} must be [T,B,C] like r, got {tuple(t.shape)}")
+    T, B, C = r.shape
+    if C % num_heads or C // num_heads != _HEAD:
+        raise NotImplementedError(f"head size must be {_HEAD} (C={C}, heads={num_heads})")
+    if tuple(u.shape) != (num_heads, _HEAD):
+        raise ValueError(f"u must be [H,64], got {tuple(u.shape)}")
+    if initial_state is not None and tuple(initial_state.shape) != (B, num_heads, _HEAD, _HEAD):
+        raise ValueError("initial_state must be [B,H,64,64]")
+    return _WKV6SeqFirst.apply(r, k, v, decay, u, float(scale), int(num_heads), initial_state,
+                               bool(output_final_state))

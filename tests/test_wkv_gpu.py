@@ -153,3 +153,33 @@ def test_wkv_baseline_configs(pkg, cfg):
     ref = run_oracle(x, *args)
     names = ["o", "hT", "dr", "dk", "dv", "dw", "du"] + (["dh0"] if args[1] else [])
     _compare(got, ref, names)
+
+
+@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130)])
+def test_wkv_seqfirst_entry(pkg, shape):
+    """The time-mix module's entry: r, k, v, decay in [T,B,H*64], w = -exp(decay) inside,
+    o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs."""
+    B, H, T = shape
+    K = 64
+    g = torch.Generator().manual_seed(T + B)
+    bf = lambda t: t.to(torch.bfloat16)
+    r, k, v = (bf(torch.randn(T, B, H * K, generator=g)) for _ in range(3))
+    decay = bf(torch.rand(T, B, H * K, generator=g) * 5.5 - 6.0)
+    u = 0.1 * torch.randn(H, K, generator=g)
+    do = bf(torch.randn(B, H, T, K, generator=g))
+    dev = torch.device("cuda:0")
+    leaves = [t.to(dev).requires_grad_(True) for t in (r, k, v, decay, u)]
+    o, _ = pkg.wkv6_seqfirst(*leaves, H, scale=1.0)
+    (o.float() * do.to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    hf = lambda t: t.float().view(T, B, H, K).permute(1, 2, 0, 3).numpy()
+    w_hf = -np.exp(hf(decay).astype(np.float64))
+    a = lambda t: t.detach().float().cpu()
+    o_ref, _ = orc.wkv6_fwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), None, 1.0)
+    gr = orc.wkv6_bwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), _n(do), None, None, 1.0)
+    got = dict(o=_n(o), du=_n(leaves[4].grad))
+    for name, leaf in zip(("dr", "dk", "dv"), leaves[:3]):
+        got[name] = hf(a(leaf.grad))
+    got["dw"] = hf(a(leaves[3].grad))
+    ref = dict(o=o_ref, dr=gr["dr"], dk=gr["dk"], dv=gr["dv"], du=gr["du"], dw=gr["dw"] * w_hf)
+    _compare(got, ref, ["o", "dr", "dk", "dv", "dw", "du"])
