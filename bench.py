@@ -53,6 +53,8 @@ def parse():
                     help="(b,h) sequences in the CPU sample (0 = the whole workload)")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the config-3 training step (RWKV6 1.6B shape) measurement")
+    ap.add_argument("--train-only", action="store_true",
+                    help="run only the config-3 training step (for kernel profiles)")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -169,6 +171,10 @@ def main():
 
     pkg = importlib.import_module("rwkv-megatron_amd")
     L = pkg._lib.load()
+    if args.train_only:
+        print(json.dumps({"train_step": train_step_bench(pkg, args.train_steps, args.train_warmup)}),
+              flush=True)
+        return
     dev = torch.device("cuda:0")
     B, H, T, K = args.B, args.H, args.T, 64
     N_th = B * H * T

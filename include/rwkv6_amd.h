@@ -21,6 +21,8 @@
  *             rwkv6_layer_specs.py:290-300 and :440-452 (bias of :195 folded in)
  *   gn_gate   GroupNorm (rwkv6_layer_specs.py:90-97) applied at :461-465, times
  *             the silu gate of :458, the product formed at :466
+ *   cmix      token shift + static lerp, relu^2 and sigmoid gate of
+ *             RWKV6ChannelMix.forward, rwkv6_layer_specs.py:512-536
  */
 #ifndef RWKV6_AMD_H
 #define RWKV6_AMD_H
@@ -120,6 +122,30 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
                   int param_dtype, const void* d_mixed, const void* d_xxx, void* dx,
                   void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * Channel mix (RWKV6ChannelMix.forward, rwkv6_layer_specs.py:512-536), [T,B,C] bf16.
+ *   mixed[e] = x + (shift(x) - x) * mix[e]    (:513-520), mix = mix_coeffs [2,C] in
+ *              param_dtype, mixed [2,T,B,C]: e = 0 feeds linear_up, e = 1 linear_gate
+ *   h        = relu(up)^2                     (:524), up = linear_up output
+ *   y        = out * sigmoid(gate_pre)        (:533-536), out = linear_down output
+ * The elementwise entries take n = element count (a multiple of 8).
+ * ---------------------------------------------------------------------- */
+int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* mixed, int64_t T,
+                        int64_t B, int64_t C, void* stream);
+/* d_mixed [2,T,B,C] -> dx [T,B,C] and d_mix [2,C] (param_dtype). */
+size_t rwkv6_cmix_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
+int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype, const void* d_mixed,
+                        void* dx, void* d_mix, void* workspace, int64_t T, int64_t B, int64_t C,
+                        void* stream);
+int rwkv6_relu_sq_fwd(const void* up, void* h, int64_t n, void* stream);
+/* d_up = 2 relu(up) dh */
+int rwkv6_relu_sq_bwd(const void* up, const void* dh, void* d_up, int64_t n, void* stream);
+int rwkv6_sigmoid_gate_fwd(const void* out, const void* gate_pre, void* y, int64_t n,
+                           void* stream);
+/* d_out = dy sigmoid(gate_pre); d_gate_pre = dy out sigmoid'(gate_pre) */
+int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy, void* d_out,
+                           void* d_gate_pre, int64_t n, void* stream);
 
 /* ------------------------------------------------------------------------
  * GroupNorm(per head) * silu(gate), fused with the head-first -> sequence-first

@@ -17,6 +17,8 @@ Contents
     - data-dependent lerp    rwkv6_layer_specs.py:447-452 (bias of :195 folded in)
     - GroupNorm * silu gate  rwkv6_layer_specs.py:90-97, :458, :461-466
     - LoRA bottleneck        rwkv6_layer_specs.py:177-195
+  and of ``RWKV6ChannelMix.forward`` (rwkv6_layer_specs.py:512-536): shift + static
+  lerp, relu^2, sigmoid gate, and the whole block with its projections.
 
 Pinning (each checked in tests/test_oracle.py, never by retyping a formula):
 WKV forward against the quadratic (attention-form) closed form, w=0 causal
@@ -24,7 +26,8 @@ linear attention, w->-inf bonus-only output, T=1, segment splitting and
 linearity; WKV backward against torch.autograd of an independent fp64 torch
 formulation; GroupNorm against ``torch.nn.functional.group_norm`` (the
 routine the reference calls); the elementwise backward passes against
-torch.autograd of the reference-shaped torch code.
+torch.autograd of the reference-shaped torch code; the channel-mix lerp against
+its end points (mix = 0 gives x, mix = 1 gives shift(x)).
 """
 from __future__ import annotations
 
@@ -183,6 +186,75 @@ def mix_bwd(x, maa, mexp, bias, d_mixed, d_xxx):
     d_bias = d_mexp.sum(axis=(0, 1))
     d_maa = (dxxx * delta).sum(axis=(0, 1))
     return dx, d_mexp, d_bias, d_maa
+
+
+def cmix_lerp_fwd(x, mix):
+    """Channel-mix inputs (rwkv6_layer_specs.py:512-520): mixed[e] = x + (shift(x) - x) * mix[e],
+    e = 0 (up), 1 (gate).  x: [T,B,C]; mix: [2,C] (mix_coeffs).  Returns [2,T,B,C]."""
+    x = np.asarray(x, np.float64)
+    delta = token_shift(x) - x
+    return x[None] + delta[None] * np.asarray(mix, np.float64)[:, None, None, :]
+
+
+def cmix_lerp_bwd(x, mix, d_mixed):
+    """Adjoint of ``cmix_lerp_fwd``: returns (dx [T,B,C], d_mix [2,C])."""
+    x = np.asarray(x, np.float64)
+    mix = np.asarray(mix, np.float64)
+    g = np.asarray(d_mixed, np.float64)
+    delta = token_shift(x) - x
+    d_delta = (g * mix[:, None, None, :]).sum(axis=0)
+    dx = g.sum(axis=0) - d_delta + token_shift_bwd(d_delta)
+    d_mix = (g * delta[None]).sum(axis=(1, 2))
+    return dx, d_mix
+
+
+def relu_sq_fwd(up):
+    """square(relu(up)) (rwkv6_layer_specs.py:524)."""
+    return np.maximum(np.asarray(up, np.float64), 0.0) ** 2
+
+
+def relu_sq_bwd(up, dh):
+    return 2.0 * np.maximum(np.asarray(up, np.float64), 0.0) * np.asarray(dh, np.float64)
+
+
+def sigmoid_gate_fwd(out, gate_pre):
+    """out * sigmoid(gate_pre) (rwkv6_layer_specs.py:533-536)."""
+    return np.asarray(out, np.float64) * _sigmoid(np.asarray(gate_pre, np.float64))
+
+
+def sigmoid_gate_bwd(out, gate_pre, dy):
+    """Returns (d_out, d_gate_pre)."""
+    sg = _sigmoid(np.asarray(gate_pre, np.float64))
+    dy = np.asarray(dy, np.float64)
+    return dy * sg, dy * np.asarray(out, np.float64) * sg * (1.0 - sg)
+
+
+def channel_mix_fwd(x, mix, w_up, w_gate, w_down):
+    """RWKV6ChannelMix.forward (rwkv6_layer_specs.py:512-536, TP=1, no biases); weights in the
+    Megatron [out, in] layout.  x: [T,B,C] -> [T,B,C]."""
+    mixed = cmix_lerp_fwd(x, mix)
+    h = relu_sq_fwd(mixed[0] @ np.asarray(w_up, np.float64).T)
+    out = h @ np.asarray(w_down, np.float64).T
+    return sigmoid_gate_fwd(out, mixed[1] @ np.asarray(w_gate, np.float64).T)
+
+
+def channel_mix_bwd(x, mix, w_up, w_gate, w_down, dy):
+    """Backward of ``channel_mix_fwd``: returns (dx, d_mix, d_w_up, d_w_gate, d_w_down)."""
+    w_up, w_gate, w_down = (np.asarray(w, np.float64) for w in (w_up, w_gate, w_down))
+    mixed = cmix_lerp_fwd(x, mix)
+    up = mixed[0] @ w_up.T
+    h = relu_sq_fwd(up)
+    out = h @ w_down.T
+    gp = mixed[1] @ w_gate.T
+    d_out, d_gp = sigmoid_gate_bwd(out, gp, dy)
+    C, F = x.shape[-1], w_up.shape[0]
+    d_w_down = d_out.reshape(-1, C).T @ h.reshape(-1, F)
+    d_up = relu_sq_bwd(up, d_out @ w_down)
+    d_w_up = d_up.reshape(-1, F).T @ mixed[0].reshape(-1, C)
+    d_w_gate = d_gp.reshape(-1, C).T @ mixed[1].reshape(-1, C)
+    d_mixed = np.stack([d_up @ w_up, d_gp @ w_gate])
+    dx, d_mix = cmix_lerp_bwd(x, mix, d_mixed)
+    return dx, d_mix, d_w_up, d_w_gate, d_w_down
 
 
 def group_norm_fwd(x, groups, gamma, beta, eps):

@@ -95,7 +95,7 @@ rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
     }
 }
 
-// Backward.  Partial sums of dgamma/dbeta per block: part[((b*nTB + tb)*H + h)][2][64].
+// Backward.  Partial sums of dgamma/dbeta per block: part[b*nTB + tb][which][h][64].
 __global__ void __launch_bounds__(GN_THR)
 rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
                          const uint16_t* __restrict__ g_pre, const void* __restrict__ gamma,
@@ -158,22 +158,33 @@ rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
         float acc = 0.f;
         for (int j = 0; j < 32; ++j) acc += red[which][j][c];
         const int64_t nTB = gridDim.x;
-        part[(((b * nTB + blockIdx.x) * H + h) * 2 + which) * GN_D + c] = acc;
+        part[(((b * nTB + blockIdx.x) * 2 + which) * H + h) * GN_D + c] = acc;
     }
 }
 
-// dgamma[h*64+c] = sum_{b,tb} part[b][tb][h][0][c]; dbeta likewise (fixed order).
-__global__ void rwkv6_gn_param_reduce(const float* __restrict__ part, int64_t B, int64_t nTB,
-                                      int64_t H, int pdt, void* __restrict__ dgamma,
-                                      void* __restrict__ dbeta) {
-    const int64_t h = blockIdx.x;
-    const int which = threadIdx.x / GN_D, c = threadIdx.x % GN_D;
+// Column sums of part[P][2][C] (P = B * nTB rows, C = H * 64): dgamma = column sums of the
+// first C columns, dbeta of the last C.  Thread (q, nl): strided partial over rows p = q mod 8,
+// then a fixed-order combine of the 8 partials (deterministic); 64 columns per block.
+__global__ void __launch_bounds__(GN_THR)
+rwkv6_gn_param_reduce(const float* __restrict__ part, int64_t P, int64_t C, int pdt,
+                      void* __restrict__ dgamma, void* __restrict__ dbeta) {
+    __shared__ float acc4[4][64];
+    const int q = threadIdx.x >> 6, nl = threadIdx.x & 63;
+    const int64_t n = (int64_t)blockIdx.x * 64 + nl;
     float acc = 0.f;
-    for (int64_t b = 0; b < B; ++b)
-        for (int64_t tb = 0; tb < nTB; ++tb) acc += part[(((b * nTB + tb) * H + h) * 2 + which) * GN_D + c];
-    void* dst = which == 0 ? dgamma : dbeta;
-    if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(dst)[h * GN_D + c] = f2bf(acc);
-    else reinterpret_cast<float*>(dst)[h * GN_D + c] = acc;
+    if (n < 2 * C) {
+#pragma unroll 4
+        for (int64_t p = q; p < P; p += 4) acc += part[p * 2 * C + n];
+    }
+    acc4[q][nl] = acc;
+    __syncthreads();
+    if (q == 0 && n < 2 * C) {
+        const float tot = (acc4[0][nl] + acc4[1][nl]) + (acc4[2][nl] + acc4[3][nl]);
+        void* dst = n < C ? dgamma : dbeta;
+        const int64_t i = n < C ? n : n - C;
+        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(dst)[i] = f2bf(tot);
+        else reinterpret_cast<float*>(dst)[i] = tot;
+    }
 }
 
 namespace {
@@ -235,8 +246,9 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
                            (const uint16_t*)dy, (uint16_t*)d_o, (uint16_t*)d_g_pre,
                            (float*)workspace, T, B, H);
     }
-    hipLaunchKernelGGL(rwkv6_gn_param_reduce, dim3((unsigned)H), dim3(2 * GN_D), 0, s,
-                       (const float*)workspace, B, nTB, H, param_dtype, dgamma, dbeta);
+    hipLaunchKernelGGL(rwkv6_gn_param_reduce, dim3((unsigned)((2 * H * GN_D + 63) / 64)),
+                       dim3(GN_THR), 0, s, (const float*)workspace, T > 0 ? B * nTB : (int64_t)0,
+                       H * GN_D, param_dtype, dgamma, dbeta);
     return launch_status();
 }
 

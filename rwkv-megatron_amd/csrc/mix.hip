@@ -8,10 +8,20 @@
 //   mixed_e = x + delta * m_e, e in (w,k,v,r,g)                   :447-452
 // The LoRA output m is laid out e-outer ([5,T,B,C]) so batched GEMMs produce and
 // consume it without copies.
+//
+// Channel mix (RWKV6ChannelMix.forward, :512-536) uses the same shift with static
+// coefficients mix_coeffs [2,C]:
+//   mixed_e = x + delta * mix_coeffs[e], e in (up, gate)          :515-520
+//   h = relu(linear_up(mixed_up))^2                               :522-524
+//   y = linear_down(h) * sigmoid(linear_gate(mixed_gate))         :525-536
+// so it gets a lerp kernel writing [2,T,B,C] (each half a contiguous GEMM operand),
+// its backward, and the relu^2 and sigmoid-gate epilogues with their backwards.
 // The kernels compute in fp32 registers and round once to bf16 on store; each
 // thread owns 8 consecutive channels (one 16-byte vector) so every global
 // access is a coalesced 16-byte load or store.  All parameter-gradient
 // reductions are two-stage with a fixed order (deterministic).
+#include <initializer_list>
+
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
@@ -294,6 +304,239 @@ rwkv6_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Channel mix.
+#define CMIX_NE 2
+
+// mixed[e] = x + (shift(x) - x) * mix[e];  mix [2,C], mixed [2,T,B,C]
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_cmix_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ mix, int pdt,
+                       uint16_t* __restrict__ mixed, int64_t T, int64_t B, int64_t C) {
+    const int64_t C8 = C / 8;
+    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
+    const int64_t N = T * B;
+    if (idx >= N * C8) return;
+    const int64_t cg = idx % C8, tb = idx / C8;
+    const int64_t off = tb * C + 8 * cg;
+    float xv[8], d[8];
+    load8(x + off, xv);
+    if (tb >= B) {
+        load8(x + off - B * C, d);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) d[s] -= xv[s];
+    } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) d[s] = -xv[s];
+    }
+#pragma unroll
+    for (int e = 0; e < CMIX_NE; ++e) {
+        float m[8], out[8];
+        load_param8(mix, pdt, e * C + 8 * cg, m);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) out[s] = xv[s] + d[s] * m[s];
+        store8(mixed + e * N * C + off, out);
+    }
+}
+
+// Backward of the channel-mix lerp (same block shape and hand-off as rwkv6_mix_bwd_kernel):
+//   d_delta[t] = sum_e dmix_e[t] mix_e,  dx[t] = sum_e dmix_e[t] - d_delta[t] + d_delta[t+1],
+//   d_mix_e partial = sum_t dmix_e[t] delta[t]  -> part[(tblk*B + b)][2][C].
+__device__ __forceinline__ void cmix_token(const float* mv, const uint16_t* __restrict__ dmix,
+                                           int64_t off, int64_t NC, float* dd, float* dsum,
+                                           float (*g)[8]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dd[s] = dsum[s] = 0.f;
+#pragma unroll
+    for (int e = 0; e < CMIX_NE; ++e) {
+        load8(dmix + e * NC + off, g[e]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            dd[s] += g[e][s] * mv[e * 8 + s];
+            dsum[s] += g[e][s];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ mix, int pdt,
+                           const uint16_t* __restrict__ dmix, uint16_t* __restrict__ dx,
+                           float* __restrict__ part, int64_t T, int64_t B, int64_t C) {
+    __shared__ float first_dd[MIX_SS][32][8];
+    __shared__ float red[MIX_SS][CMIX_NE][32 * 8 + 4];
+    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
+    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
+    const int64_t b = blockIdx.z, NC = T * B * C;
+    const int64_t t_lo = (int64_t)blockIdx.x * MIX_TB + MIX_SS * ss, t_hi = min(T, t_lo + MIX_SS);
+    const bool active = cg < C8 && t_lo < T;
+    float acc[CMIX_NE][8], pend[8], mv[CMIX_NE * 8];
+#pragma unroll
+    for (int e = 0; e < CMIX_NE; ++e)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc[e][s] = 0.f;
+    if (active) {
+#pragma unroll
+        for (int e = 0; e < CMIX_NE; ++e) load_param8(mix, pdt, e * C + 8 * cg, mv + 8 * e);
+        float xprev[8];
+        if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
+        else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
+        for (int64_t t = t_lo; t < t_hi; ++t) {
+            const int64_t off = (t * B + b) * C + 8 * cg;
+            float xv[8], dd[8], dsum[8], g[CMIX_NE][8], out[8];
+            load8(x + off, xv);
+            cmix_token(mv, dmix, off, NC, dd, dsum, g);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const float delta = xprev[s] - xv[s];
+#pragma unroll
+                for (int e = 0; e < CMIX_NE; ++e) acc[e][s] += g[e][s] * delta;
+                xprev[s] = xv[s];
+            }
+            if (t > t_lo) {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) out[s] = pend[s] + dd[s];
+                store8(dx + off - B * C, out);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) first_dd[ss][cgl][s] = dd[s];
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) pend[s] = dsum[s] - dd[s];
+        }
+    }
+    __syncthreads();
+    if (active) {
+        float nd[8];
+        if (t_hi >= T) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = 0.f;
+        } else if (ss + 1 < MIX_SS) {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = first_dd[ss + 1][cgl][s];
+        } else {
+            float dsum[8], g[CMIX_NE][8];
+            cmix_token(mv, dmix, (t_hi * B + b) * C + 8 * cg, NC, nd, dsum, g);
+        }
+        float out[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) out[s] = pend[s] + nd[s];
+        store8(dx + ((t_hi - 1) * B + b) * C + 8 * cg, out);
+    }
+#pragma unroll
+    for (int e = 0; e < CMIX_NE; ++e)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) red[ss][e][8 * cgl + s] = acc[e][s];
+    __syncthreads();
+    const int64_t P_row = (int64_t)blockIdx.x * B + b;
+    for (int j = threadIdx.x; j < CMIX_NE * 256; j += MIX_THR) {
+        const int e = j >> 8, c = j & 255;
+        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
+        if (ch >= C) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < MIX_SS; ++q) sum += red[q][e][c];
+        part[(P_row * CMIX_NE + e) * C + ch] = sum;
+    }
+}
+
+// Elementwise epilogues over n bf16 elements (n % 8 == 0); each thread owns two 16-byte
+// vectors, both loads issued before any arithmetic.
+#define EW_VEC 2
+__device__ __forceinline__ float sigmoid_(float z) { return 1.f / (1.f + __expf(-z)); }
+
+// h = relu(up)^2
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_relu_sq_kernel(const uint16_t* __restrict__ up, uint16_t* __restrict__ h, int64_t n8) {
+    const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
+    float a[EW_VEC][8];
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v)
+        if (i0 + v < n8) load8(up + 8 * (i0 + v), a[v]);
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v) {
+        if (i0 + v >= n8) break;
+        float o[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float r = fmaxf(a[v][s], 0.f);
+            o[s] = r * r;
+        }
+        store8(h + 8 * (i0 + v), o);
+    }
+}
+
+// d_up = 2 relu(up) dh
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_relu_sq_bwd_kernel(const uint16_t* __restrict__ up, const uint16_t* __restrict__ dh,
+                         uint16_t* __restrict__ dup, int64_t n8) {
+    const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
+    float a[EW_VEC][8], g[EW_VEC][8];
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v)
+        if (i0 + v < n8) {
+            load8(up + 8 * (i0 + v), a[v]);
+            load8(dh + 8 * (i0 + v), g[v]);
+        }
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v) {
+        if (i0 + v >= n8) break;
+        float o[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) o[s] = 2.f * fmaxf(a[v][s], 0.f) * g[v][s];
+        store8(dup + 8 * (i0 + v), o);
+    }
+}
+
+// y = out * sigmoid(gate_pre)
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_sigmoid_gate_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ gp,
+                          uint16_t* __restrict__ y, int64_t n8) {
+    const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
+    float a[EW_VEC][8], z[EW_VEC][8];
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v)
+        if (i0 + v < n8) {
+            load8(out + 8 * (i0 + v), a[v]);
+            load8(gp + 8 * (i0 + v), z[v]);
+        }
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v) {
+        if (i0 + v >= n8) break;
+        float o[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) o[s] = a[v][s] * sigmoid_(z[v][s]);
+        store8(y + 8 * (i0 + v), o);
+    }
+}
+
+// d_out = dy sigmoid(z);  d_gate_pre = dy out sigmoid(z) (1 - sigmoid(z))
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_sigmoid_gate_bwd_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ gp,
+                              const uint16_t* __restrict__ dy, uint16_t* __restrict__ dout,
+                              uint16_t* __restrict__ dgp, int64_t n8) {
+    const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
+    float a[EW_VEC][8], z[EW_VEC][8], g[EW_VEC][8];
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v)
+        if (i0 + v < n8) {
+            load8(out + 8 * (i0 + v), a[v]);
+            load8(gp + 8 * (i0 + v), z[v]);
+            load8(dy + 8 * (i0 + v), g[v]);
+        }
+#pragma unroll
+    for (int v = 0; v < EW_VEC; ++v) {
+        if (i0 + v >= n8) break;
+        float o1[8], o2[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float sg = sigmoid_(z[v][s]);
+            o1[s] = g[v][s] * sg;
+            o2[s] = g[v][s] * a[v][s] * sg * (1.f - sg);
+        }
+        store8(dout + 8 * (i0 + v), o1);
+        store8(dgp + 8 * (i0 + v), o2);
+    }
+}
+
 namespace {
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int mix_check(int64_t T, int64_t B, int64_t C, int pdt) {
@@ -394,6 +637,102 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
                            T, B, C);
     hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(MIX_THR), 0, s, part,
                        T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
+    return launch_status();
+}
+
+int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* mixed, int64_t T,
+                        int64_t B, int64_t C, void* stream) {
+    int st = mix_check(T, B, C, param_dtype);
+    if (st) return st;
+    if (T == 0) return RWKV6_OK;
+    if (!x || !mix || !mixed) return RWKV6_ERR_INVALID_ARG;
+    if (!al16(x) || !al16(mix) || !al16(mixed)) return RWKV6_ERR_ALIGNMENT;
+    const int64_t n = T * B * (C / 8);
+    hipLaunchKernelGGL(rwkv6_cmix_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, mix, param_dtype,
+                       (uint16_t*)mixed, T, B, C);
+    return launch_status();
+}
+
+size_t rwkv6_cmix_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
+    if (T < 0 || B < 1 || C < 8) return 0;
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
+    return (size_t)((ntb > 0 ? ntb : 1) * B * CMIX_NE * C) * sizeof(float);
+}
+
+int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype, const void* d_mixed,
+                        void* dx, void* d_mix, void* workspace, int64_t T, int64_t B, int64_t C,
+                        void* stream) {
+    int st = mix_check(T, B, C, param_dtype);
+    if (st) return st;
+    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
+    if (!mix || !d_mix || !workspace || (T > 0 && (!x || !d_mixed || !dx)))
+        return RWKV6_ERR_INVALID_ARG;
+    if (!al16(x) || !al16(mix) || !al16(d_mixed) || !al16(dx) || !al16(workspace))
+        return RWKV6_ERR_ALIGNMENT;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
+    float* part = reinterpret_cast<float*>(workspace);
+    if (T > 0)
+        hipLaunchKernelGGL(rwkv6_cmix_lerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
+                           (const uint16_t*)x, mix, param_dtype, (const uint16_t*)d_mixed,
+                           (uint16_t*)dx, part, T, B, C);
+    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((CMIX_NE * C + 31) / 32)), dim3(MIX_THR), 0,
+                       s, part, T > 0 ? ntb * B : (int64_t)0, (int64_t)CMIX_NE * C, param_dtype,
+                       d_mix);
+    return launch_status();
+}
+
+static int ew_check(int64_t n, std::initializer_list<const void*> ptrs) {
+    if (n < 0) return RWKV6_ERR_INVALID_ARG;
+    if (n % 8) return RWKV6_ERR_UNSUPPORTED;
+    if (n == 0) return RWKV6_OK;
+    for (const void* p : ptrs) {
+        if (!p) return RWKV6_ERR_INVALID_ARG;
+        if (!al16(p)) return RWKV6_ERR_ALIGNMENT;
+    }
+    return RWKV6_OK;
+}
+static unsigned ew_blocks(int64_t n8) {
+    return (unsigned)((n8 + (int64_t)MIX_THR * EW_VEC - 1) / ((int64_t)MIX_THR * EW_VEC));
+}
+
+int rwkv6_relu_sq_fwd(const void* up, void* h, int64_t n, void* stream) {
+    int st = ew_check(n, {up, h});
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(rwkv6_relu_sq_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)up, (uint16_t*)h,
+                       n / 8);
+    return launch_status();
+}
+
+int rwkv6_relu_sq_bwd(const void* up, const void* dh, void* d_up, int64_t n, void* stream) {
+    int st = ew_check(n, {up, dh, d_up});
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(rwkv6_relu_sq_bwd_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)up,
+                       (const uint16_t*)dh, (uint16_t*)d_up, n / 8);
+    return launch_status();
+}
+
+int rwkv6_sigmoid_gate_fwd(const void* out, const void* gate_pre, void* y, int64_t n,
+                           void* stream) {
+    int st = ew_check(n, {out, gate_pre, y});
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(rwkv6_sigmoid_gate_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)out,
+                       (const uint16_t*)gate_pre, (uint16_t*)y, n / 8);
+    return launch_status();
+}
+
+int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy, void* d_out,
+                           void* d_gate_pre, int64_t n, void* stream) {
+    int st = ew_check(n, {out, gate_pre, dy, d_out, d_gate_pre});
+    if (st || n == 0) return st;
+    hipLaunchKernelGGL(rwkv6_sigmoid_gate_bwd_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)out,
+                       (const uint16_t*)gate_pre, (const uint16_t*)dy, (uint16_t*)d_out,
+                       (uint16_t*)d_gate_pre, n / 8);
     return launch_status();
 }
 

@@ -11,6 +11,11 @@ way (Megatron's module prefix aside).  The hot path runs on the HIP kernels:
     GroupNorm * silu(gate)               -> timemix.group_norm_gate   (HIP, head-first read)
     output projection                    -> torch.matmul
 
+  RWKV6ChannelMix.forward  (:512-536)
+    token shift + 2 static lerps         -> channelmix.cmix_lerp      (HIP)
+    relu^2, sigmoid(gate) * out          -> channelmix.relu_sq / sigmoid_gate (HIP)
+    up / gate / down projections         -> torch.matmul
+
 Deliberate differences, all documented in the reference's own terms:
   * ``mix_coeff_input`` and ``RWKV6ChannelMix.mix_coeffs`` are left uninitialised by
     the reference (torch.empty, :377-385, :475-477); here they get the RWKV-6 ramp
@@ -27,7 +32,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from . import timemix
+from . import channelmix, timemix
 from .wkv import chunk_rwkv6, wkv6_seqfirst
 
 
@@ -209,15 +214,11 @@ class RWKV6ChannelMix(nn.Module):
                 self.mix_coeffs.copy_(torch.stack([ramp, ramp]))
 
     def forward(self, hidden_states):
-        x = hidden_states
-        shifted = torch.cat([torch.zeros_like(x[:1]), x[:-1]], 0)
-        delta = shifted - x
-        mixed = x.unsqueeze(-2) + delta.unsqueeze(-2) * self.mix_coeffs.to(x.dtype)
-        mixed_up, mixed_gate = mixed.unbind(-2)
-        h = torch.square(torch.relu(self.linear_up(mixed_up.contiguous())[0]))
+        """:512-536 with the shift + lerps, relu^2 and sigmoid gate on HIP kernels."""
+        mixed_up, mixed_gate = channelmix.cmix_lerp(hidden_states, self.mix_coeffs)
+        h = channelmix.relu_sq(self.linear_up(mixed_up)[0])
         out = self.linear_down(h)[0]
-        gate = torch.sigmoid(self.linear_gate(mixed_gate.contiguous())[0])
-        return out * gate, None
+        return channelmix.sigmoid_gate(out, self.linear_gate(mixed_gate)[0]), None
 
 
 class RWKV6Layer(nn.Module):

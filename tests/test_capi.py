@@ -70,6 +70,16 @@ def test_validation_rejects_before_launch(pkg):
         pkg._lib.RWKV6_ERR_UNSUPPORTED
     assert L.rwkv6_gn_gate_fwd(None, 1, p, p, p, 0, 1e-5, p, p, p, 4, 2, 2, 64, None) == \
         pkg._lib.RWKV6_ERR_INVALID_ARG
+    E = pkg._lib
+    assert L.rwkv6_cmix_lerp_fwd(p, p, 1, p, 4, 2, 12, None) == E.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_cmix_lerp_fwd(p, None, 1, p, 4, 2, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_cmix_lerp_bwd(p, p, 1, p, p, p, None, 4, 2, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_relu_sq_fwd(p, p, 12, None) == E.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_relu_sq_fwd(p, p, -8, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_relu_sq_bwd(p, None, p, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_sigmoid_gate_fwd(p, _fake(0x100008), p, 16, None) == E.RWKV6_ERR_ALIGNMENT
+    assert L.rwkv6_sigmoid_gate_bwd(p, p, p, p, None, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_relu_sq_fwd(None, None, 0, None) == E.RWKV6_OK       # empty: nothing to do
 
 
 def test_python_checker_maps_codes(pkg):

@@ -268,3 +268,43 @@ def test_bottleneck_backward_matches_autograd():
     dx, dwd, dwu, db = orc.bottleneck_bwd(n(x), n(wd), n(wu), n(dm))
     for got, ref in ((dx, x.grad), (dwd, wd.grad), (dwu, wu.grad), (db, b.grad)):
         assert _rel(got, ref) < 1e-12
+
+
+def _ref_torch_channel_mix(x, mix, w_up, w_gate, w_down):
+    """The reference's RWKV6ChannelMix.forward (rwkv6_layer_specs.py:512-536) in torch, TP=1."""
+    shifted = torch.cat([torch.zeros_like(x[:1]), x[:-1]], 0)
+    delta = shifted - x
+    mixed = x.unsqueeze(-2) + delta.unsqueeze(-2) * mix
+    mixed_up, mixed_gate = mixed.unbind(-2)
+    h = torch.square(torch.relu(mixed_up @ w_up.T))
+    out = h @ w_down.T
+    return out * torch.sigmoid(mixed_gate @ w_gate.T)
+
+
+def test_cmix_lerp_end_points():
+    """mix = 0 passes x through, mix = 1 gives the token-shifted x (a sign or index slip in the
+    delta fails one of the two)."""
+    T, B, C = 5, 2, 8
+    x = np.random.default_rng(0).standard_normal((T, B, C))
+    mixed = orc.cmix_lerp_fwd(x, np.stack([np.zeros(C), np.ones(C)]))
+    assert np.array_equal(mixed[0], x)
+    assert np.allclose(mixed[1][1:], x[:-1]) and np.all(mixed[1][0] == 0)
+
+
+def test_channel_mix_forward_and_backward_match_autograd():
+    T, B, C, F = 6, 2, 16, 24
+    g = torch.Generator().manual_seed(3)
+    d = dict(dtype=torch.float64)
+    x = torch.randn(T, B, C, generator=g, **d, requires_grad=True)
+    mix = torch.rand(2, C, generator=g, **d, requires_grad=True)
+    w_up = (0.3 * torch.randn(F, C, generator=g, **d)).requires_grad_(True)
+    w_gate = (0.3 * torch.randn(C, C, generator=g, **d)).requires_grad_(True)
+    w_down = (0.3 * torch.randn(C, F, generator=g, **d)).requires_grad_(True)
+    y = _ref_torch_channel_mix(x, mix, w_up, w_gate, w_down)
+    dy = torch.randn(y.shape, generator=g, **d)
+    (y * dy).sum().backward()
+    n = lambda t: t.detach().numpy()
+    assert _rel(orc.channel_mix_fwd(n(x), n(mix), n(w_up), n(w_gate), n(w_down)), n(y)) < 1e-12
+    got = orc.channel_mix_bwd(n(x), n(mix), n(w_up), n(w_gate), n(w_down), n(dy))
+    for a, leaf in zip(got, (x, mix, w_up, w_gate, w_down)):
+        assert _rel(a, n(leaf.grad)) < 1e-12
