@@ -102,42 +102,45 @@ int rwkv6_wkv_bwd_seqfirst(const void* r, const void* k, const void* v, const vo
  *   xxx         = x + (shift(x) - x) * maa              (:443-444), maa [C]
  *   mixed[e]    = x + (shift(x) - x) * (mexp[e] + bias[e])   (:446-452)
  *                 mexp [5,T,B,C] is the LoRA up-projection before its bias (:195),
- *                 bias [5,C]; mixed is [5,T,B,C] in the order w,k,v,r,g.
+ *                 bias [5,C]; `mixed` is a host array of 5 device pointers, each a
+ *                 [T,B,C] tensor, in the order w,k,v,r,g (each feeds its own projection).
  * maa and bias are in param_dtype (f32 or bf16).  C must be a multiple of 8.
+ * Gradients w.r.t. the mixes (d_mixed) are passed the same way: 5 device pointers.
  * ---------------------------------------------------------------------- */
 int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* xxx,
                          int64_t T, int64_t B, int64_t C, void* stream);
 int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int param_dtype,
-                     void* mixed, int64_t T, int64_t B, int64_t C, void* stream);
-/* Backward of the data-dependent lerp w.r.t. its LoRA input: d_mixed [5,T,B,C] ->
+                     void* const* mixed, int64_t T, int64_t B, int64_t C, void* stream);
+/* Backward of the data-dependent lerp w.r.t. its LoRA input: d_mixed 5 x [T,B,C] ->
  * d_mexp [5,T,B,C] = d_mixed * (shift(x) - x) and d_bias [5,C] (param_dtype). */
 size_t rwkv6_ddlerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
-int rwkv6_ddlerp_bwd(const void* x, const void* d_mixed, int param_dtype, void* d_mexp,
+int rwkv6_ddlerp_bwd(const void* x, const void* const* d_mixed, int param_dtype, void* d_mexp,
                      void* d_bias, void* workspace, int64_t T, int64_t B, int64_t C,
                      void* stream);
-/* Input gradient of both lerps (they share x): d_mixed [5,T,B,C] and d_xxx [T,B,C]
+/* Input gradient of both lerps (they share x): d_mixed 5 x [T,B,C] and d_xxx [T,B,C]
  * (nullable = 0) -> dx [T,B,C] and d_maa [C] (param_dtype). */
 size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
 int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
-                  int param_dtype, const void* d_mixed, const void* d_xxx, void* dx,
+                  int param_dtype, const void* const* d_mixed, const void* d_xxx, void* dx,
                   void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
                   void* stream);
 
 /* ------------------------------------------------------------------------
  * Channel mix (RWKV6ChannelMix.forward, rwkv6_layer_specs.py:512-536), [T,B,C] bf16.
  *   mixed[e] = x + (shift(x) - x) * mix[e]    (:513-520), mix = mix_coeffs [2,C] in
- *              param_dtype, mixed [2,T,B,C]: e = 0 feeds linear_up, e = 1 linear_gate
+ *              param_dtype; `mixed` is a host array of 2 device pointers, each [T,B,C]:
+ *              e = 0 feeds linear_up, e = 1 linear_gate (d_mixed likewise)
  *   h        = relu(up)^2                     (:524), up = linear_up output
  *   y        = out * sigmoid(gate_pre)        (:533-536), out = linear_down output
  * The elementwise entries take n = element count (a multiple of 8).
  * ---------------------------------------------------------------------- */
-int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* mixed, int64_t T,
-                        int64_t B, int64_t C, void* stream);
-/* d_mixed [2,T,B,C] -> dx [T,B,C] and d_mix [2,C] (param_dtype). */
+int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* const* mixed,
+                        int64_t T, int64_t B, int64_t C, void* stream);
+/* d_mixed 2 x [T,B,C] -> dx [T,B,C] and d_mix [2,C] (param_dtype). */
 size_t rwkv6_cmix_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
-int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype, const void* d_mixed,
-                        void* dx, void* d_mix, void* workspace, int64_t T, int64_t B, int64_t C,
-                        void* stream);
+int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype,
+                        const void* const* d_mixed, void* dx, void* d_mix, void* workspace,
+                        int64_t T, int64_t B, int64_t C, void* stream);
 int rwkv6_relu_sq_fwd(const void* up, void* h, int64_t n, void* stream);
 /* d_up = 2 relu(up) dh */
 int rwkv6_relu_sq_bwd(const void* up, const void* dh, void* d_up, int64_t n, void* stream);

@@ -8,9 +8,10 @@ RWKV6ChannelMix.forward (/root/reference/rwkv_megatron/rwkv6_layer_specs.py:512-
     out = linear_down(h)                                   :525
     y = out * sigmoid(linear_gate(mixed_gate))             :528-536
 
-* ``cmix_lerp``: the shift and both lerps in one pass, written as [2,T,B,C] so each
-  half is a contiguous GEMM operand (the reference's ``unbind`` + ``.contiguous()``
-  copies disappear).  Its backward is one pass producing dx and d mix_coeffs.
+* ``cmix_lerp``: the shift and both lerps in one pass, written as two separate [T,B,C]
+  tensors, each a contiguous GEMM operand (the reference's ``unbind`` + ``.contiguous()``
+  copies, and the stack of their gradients, disappear).  Its backward is one pass
+  producing dx and d mix_coeffs from the two gradients where they lie.
 * ``relu_sq`` and ``sigmoid_gate``: single-pass epilogues with single-pass backwards.
 
 The projections stay on hipBLASLt (torch.nn.functional.linear).  Every function raises
@@ -21,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .timemix import _c, _check_act, _p, _param, _stream
+from .timemix import _c, _check_act, _p, _param, _ptrs, _stream
 
 NE = 2  # (up, gate)
 
@@ -32,31 +33,31 @@ class _CmixLerp(torch.autograd.Function):
         T, B, C = x.shape
         x = _c(x)
         m, pdt = _param(mix)
-        mixed = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
-        _lib.check(_lib.load().rwkv6_cmix_lerp_fwd(_p(x), _p(m), pdt, _p(mixed), T, B, C,
+        mixed = tuple(torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device) for _ in range(NE))
+        _lib.check(_lib.load().rwkv6_cmix_lerp_fwd(_p(x), _p(m), pdt, _ptrs(mixed), T, B, C,
                                                    _stream(x.device)), "rwkv6_cmix_lerp_fwd")
         ctx.save_for_backward(x, m)
         ctx.pdt, ctx.mix_dtype = pdt, mix.dtype
         return mixed
 
     @staticmethod
-    def backward(ctx, d_mixed):
+    def backward(ctx, *d_mixed):
         x, m = ctx.saved_tensors
         T, B, C = x.shape
         L = _lib.load()
-        d_mixed = _c(d_mixed.to(torch.bfloat16))
+        d_mixed = [torch.zeros_like(x) if d is None else _c(d.to(torch.bfloat16)) for d in d_mixed]
         dx = torch.empty_like(x)
         d_mix = torch.empty(NE, C, dtype=m.dtype, device=x.device)
         ws = torch.empty(L.rwkv6_cmix_lerp_bwd_workspace_bytes(T, B, C), dtype=torch.uint8,
                          device=x.device)
-        _lib.check(L.rwkv6_cmix_lerp_bwd(_p(x), _p(m), ctx.pdt, _p(d_mixed), _p(dx), _p(d_mix),
+        _lib.check(L.rwkv6_cmix_lerp_bwd(_p(x), _p(m), ctx.pdt, _ptrs(d_mixed), _p(dx), _p(d_mix),
                                          _p(ws), T, B, C, _stream(x.device)), "rwkv6_cmix_lerp_bwd")
         return dx, d_mix.to(ctx.mix_dtype)
 
 
 def cmix_lerp(x: torch.Tensor, mix: torch.Tensor) -> torch.Tensor:
-    """[T,B,C] bf16, mix_coeffs [2,C] -> mixed [2,T,B,C] (mixed[0] feeds linear_up,
-    mixed[1] linear_gate)."""
+    """[T,B,C] bf16, mix_coeffs [2,C] -> (mixed_up, mixed_gate), each [T,B,C] (the inputs of
+    linear_up and linear_gate)."""
     _check_act("x", x, 3)
     if tuple(mix.shape) != (NE, x.shape[-1]):
         raise ValueError(f"mix must be [2,C] = {(NE, x.shape[-1])}, got {tuple(mix.shape)}")

@@ -28,6 +28,11 @@
 #define MIX_NE 5          // number of data-dependent mixes (w,k,v,r,g)
 #define MIX_THR 256
 
+// The mixes are separate [T,B,C] tensors (each one the input or input-gradient of its own
+// projection); kernels receive their addresses by value.
+template <int N> struct OutPtrs { uint16_t* p[N]; };
+template <int N> struct InPtrs { const uint16_t* p[N]; };
+
 namespace {
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
@@ -73,10 +78,10 @@ rwkv6_shift_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__
     store8(xxx + off, out);
 }
 
-// mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]);  mexp, mixed: [5,T,B,C]
+// mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]);  mexp [5,T,B,C], mixed 5 x [T,B,C]
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_ddlerp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ mexp,
-                    const void* __restrict__ bias, int pdt, uint16_t* __restrict__ mixed,
+                    const void* __restrict__ bias, int pdt, OutPtrs<MIX_NE> mixed,
                     int64_t T, int64_t B, int64_t C) {
     const int64_t C8 = C / 8;
     const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
@@ -101,7 +106,7 @@ rwkv6_ddlerp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
         load_param8(bias, pdt, e * C + 8 * cg, bb);
 #pragma unroll
         for (int s = 0; s < 8; ++s) out[s] = xv[s] + d[s] * (m[s] + bb[s]);
-        store8(mixed + e * N * C + off, out);
+        store8(mixed.p[e] + off, out);
     }
 }
 
@@ -115,7 +120,7 @@ rwkv6_ddlerp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__
 
 // d_mexp[e][t] = d_mixed[e][t] * delta[t];  part rows e = 0..4 (d_bias)
 __global__ void __launch_bounds__(MIX_THR)
-rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dmix,
+rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, InPtrs<MIX_NE> dmix,
                         uint16_t* __restrict__ dmexp, float* __restrict__ part, int64_t T,
                         int64_t B, int64_t C) {
     __shared__ float red[MIX_SS][MIX_NE][32 * 8 + 4];
@@ -145,7 +150,7 @@ rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 #pragma unroll
             for (int e = 0; e < MIX_NE; ++e) {
                 float g[8], out[8];
-                load8(dmix + e * N * C + off, g);
+                load8(dmix.p[e] + off, g);
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
                     out[s] = g[s] * delta[s];
@@ -178,7 +183,7 @@ rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 // Walked forward with dx[t] emitted one token late; d_delta of each sub-segment's first
 // token is handed to the previous sub-segment through LDS.
 __device__ __forceinline__ void mix_token(const uint16_t* __restrict__ mexp, const float* bb,
-                                          const float* mv, const uint16_t* __restrict__ dmix,
+                                          const float* mv, const InPtrs<MIX_NE>& dmix,
                                           const uint16_t* __restrict__ dxxx, int64_t off,
                                           int64_t NC, float* dd, float* dsum, float* dxv) {
     if (dxxx) load8(dxxx + off, dxv);
@@ -192,7 +197,7 @@ __device__ __forceinline__ void mix_token(const uint16_t* __restrict__ mexp, con
     for (int e = 0; e < MIX_NE; ++e) {
         float m[8], g[8];
         load8(mexp + e * NC + off, m);
-        load8(dmix + e * NC + off, g);
+        load8(dmix.p[e] + off, g);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             dd[s] += g[s] * (m[s] + bb[e * 8 + s]);
@@ -204,7 +209,7 @@ __device__ __forceinline__ void mix_token(const uint16_t* __restrict__ mexp, con
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_mix_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa,
                      const uint16_t* __restrict__ mexp, const void* __restrict__ bias, int pdt,
-                     const uint16_t* __restrict__ dmix, const uint16_t* __restrict__ dxxx,
+                     InPtrs<MIX_NE> dmix, const uint16_t* __restrict__ dxxx,
                      uint16_t* __restrict__ dx, float* __restrict__ part, int64_t T, int64_t B,
                      int64_t C) {
     __shared__ float first_dd[MIX_SS][32][8];
@@ -308,10 +313,10 @@ rwkv6_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
 // Channel mix.
 #define CMIX_NE 2
 
-// mixed[e] = x + (shift(x) - x) * mix[e];  mix [2,C], mixed [2,T,B,C]
+// mixed[e] = x + (shift(x) - x) * mix[e];  mix [2,C], mixed 2 x [T,B,C]
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_cmix_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ mix, int pdt,
-                       uint16_t* __restrict__ mixed, int64_t T, int64_t B, int64_t C) {
+                       OutPtrs<CMIX_NE> mixed, int64_t T, int64_t B, int64_t C) {
     const int64_t C8 = C / 8;
     const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
     const int64_t N = T * B;
@@ -334,21 +339,20 @@ rwkv6_cmix_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ 
         load_param8(mix, pdt, e * C + 8 * cg, m);
 #pragma unroll
         for (int s = 0; s < 8; ++s) out[s] = xv[s] + d[s] * m[s];
-        store8(mixed + e * N * C + off, out);
+        store8(mixed.p[e] + off, out);
     }
 }
 
 // Backward of the channel-mix lerp (same block shape and hand-off as rwkv6_mix_bwd_kernel):
 //   d_delta[t] = sum_e dmix_e[t] mix_e,  dx[t] = sum_e dmix_e[t] - d_delta[t] + d_delta[t+1],
 //   d_mix_e partial = sum_t dmix_e[t] delta[t]  -> part[(tblk*B + b)][2][C].
-__device__ __forceinline__ void cmix_token(const float* mv, const uint16_t* __restrict__ dmix,
-                                           int64_t off, int64_t NC, float* dd, float* dsum,
-                                           float (*g)[8]) {
+__device__ __forceinline__ void cmix_token(const float* mv, const InPtrs<CMIX_NE>& dmix,
+                                           int64_t off, float* dd, float* dsum, float (*g)[8]) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) dd[s] = dsum[s] = 0.f;
 #pragma unroll
     for (int e = 0; e < CMIX_NE; ++e) {
-        load8(dmix + e * NC + off, g[e]);
+        load8(dmix.p[e] + off, g[e]);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             dd[s] += g[e][s] * mv[e * 8 + s];
@@ -359,13 +363,13 @@ __device__ __forceinline__ void cmix_token(const float* mv, const uint16_t* __re
 
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ mix, int pdt,
-                           const uint16_t* __restrict__ dmix, uint16_t* __restrict__ dx,
+                           InPtrs<CMIX_NE> dmix, uint16_t* __restrict__ dx,
                            float* __restrict__ part, int64_t T, int64_t B, int64_t C) {
     __shared__ float first_dd[MIX_SS][32][8];
     __shared__ float red[MIX_SS][CMIX_NE][32 * 8 + 4];
     const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
     const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
-    const int64_t b = blockIdx.z, NC = T * B * C;
+    const int64_t b = blockIdx.z;
     const int64_t t_lo = (int64_t)blockIdx.x * MIX_TB + MIX_SS * ss, t_hi = min(T, t_lo + MIX_SS);
     const bool active = cg < C8 && t_lo < T;
     float acc[CMIX_NE][8], pend[8], mv[CMIX_NE * 8];
@@ -383,7 +387,7 @@ rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restric
             const int64_t off = (t * B + b) * C + 8 * cg;
             float xv[8], dd[8], dsum[8], g[CMIX_NE][8], out[8];
             load8(x + off, xv);
-            cmix_token(mv, dmix, off, NC, dd, dsum, g);
+            cmix_token(mv, dmix, off, dd, dsum, g);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const float delta = xprev[s] - xv[s];
@@ -414,7 +418,7 @@ rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restric
             for (int s = 0; s < 8; ++s) nd[s] = first_dd[ss + 1][cgl][s];
         } else {
             float dsum[8], g[CMIX_NE][8];
-            cmix_token(mv, dmix, (t_hi * B + b) * C + 8 * cg, NC, nd, dsum, g);
+            cmix_token(mv, dmix, (t_hi * B + b) * C + 8 * cg, nd, dsum, g);
         }
         float out[8];
 #pragma unroll
@@ -546,6 +550,17 @@ inline int mix_check(int64_t T, int64_t B, int64_t C, int pdt) {
     return RWKV6_OK;
 }
 inline unsigned nblocks(int64_t n) { return (unsigned)((n + MIX_THR - 1) / MIX_THR); }
+// Gathers an array of N device pointers; 0 if one is null, RWKV6_ERR_ALIGNMENT if misaligned.
+template <typename P, int N>
+inline int gather(const void* const* src, P& dst) {
+    if (!src) return RWKV6_ERR_INVALID_ARG;
+    for (int e = 0; e < N; ++e) {
+        if (!src[e]) return RWKV6_ERR_INVALID_ARG;
+        if (!al16(src[e])) return RWKV6_ERR_ALIGNMENT;
+        dst.p[e] = (decltype(dst.p[0]))src[e];
+    }
+    return RWKV6_OK;
+}
 inline int launch_status() { return hipGetLastError() == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH; }
 }  // namespace
 
@@ -566,16 +581,18 @@ int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* 
 }
 
 int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int param_dtype,
-                     void* mixed, int64_t T, int64_t B, int64_t C, void* stream) {
+                     void* const* mixed, int64_t T, int64_t B, int64_t C, void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
     if (T == 0) return RWKV6_OK;
-    if (!x || !mexp || !bias || !mixed) return RWKV6_ERR_INVALID_ARG;
-    if (!al16(x) || !al16(mexp) || !al16(bias) || !al16(mixed)) return RWKV6_ERR_ALIGNMENT;
+    if (!x || !mexp || !bias) return RWKV6_ERR_INVALID_ARG;
+    OutPtrs<MIX_NE> out;
+    if ((st = gather<OutPtrs<MIX_NE>, MIX_NE>((const void* const*)mixed, out))) return st;
+    if (!al16(x) || !al16(mexp) || !al16(bias)) return RWKV6_ERR_ALIGNMENT;
     const int64_t n = T * B * (C / 8);
     hipLaunchKernelGGL(rwkv6_ddlerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x,
-                       (const uint16_t*)mexp, bias, param_dtype, (uint16_t*)mixed, T, B, C);
+                       (const uint16_t*)mexp, bias, param_dtype, out, T, B, C);
     return launch_status();
 }
 
@@ -589,21 +606,22 @@ static dim3 bwd_grid(int64_t T, int64_t B, int64_t C) {
     return dim3((unsigned)((T + MIX_TB - 1) / MIX_TB), (unsigned)((C / 8 + 31) / 32), (unsigned)B);
 }
 
-int rwkv6_ddlerp_bwd(const void* x, const void* d_mixed, int param_dtype, void* d_mexp,
+int rwkv6_ddlerp_bwd(const void* x, const void* const* d_mixed, int param_dtype, void* d_mexp,
                      void* d_bias, void* workspace, int64_t T, int64_t B, int64_t C,
                      void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
     if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
-    if (!d_bias || !workspace || (T > 0 && (!x || !d_mixed || !d_mexp))) return RWKV6_ERR_INVALID_ARG;
-    if (!al16(x) || !al16(d_mixed) || !al16(d_mexp) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
+    if (!d_bias || !workspace || (T > 0 && (!x || !d_mexp))) return RWKV6_ERR_INVALID_ARG;
+    InPtrs<MIX_NE> dm{};
+    if (T > 0 && (st = gather<InPtrs<MIX_NE>, MIX_NE>(d_mixed, dm))) return st;
+    if (!al16(x) || !al16(d_mexp) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
     if (T > 0)
         hipLaunchKernelGGL(rwkv6_ddlerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
-                           (const uint16_t*)x, (const uint16_t*)d_mixed, (uint16_t*)d_mexp, part, T,
-                           B, C);
+                           (const uint16_t*)x, dm, (uint16_t*)d_mexp, part, T, B, C);
     hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((MIX_NE * C + 31) / 32)), dim3(MIX_THR), 0, s,
                        part, T > 0 ? ntb * B : (int64_t)0, (int64_t)MIX_NE * C, param_dtype, d_bias);
     return launch_status();
@@ -616,41 +634,44 @@ size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
 }
 
 int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
-                  int param_dtype, const void* d_mixed, const void* d_xxx, void* dx,
+                  int param_dtype, const void* const* d_mixed, const void* d_xxx, void* dx,
                   void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
                   void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
     if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
-    if (!maa || !bias || !d_maa || !workspace || (T > 0 && (!x || !mexp || !d_mixed || !dx)))
+    if (!maa || !bias || !d_maa || !workspace || (T > 0 && (!x || !mexp || !dx)))
         return RWKV6_ERR_INVALID_ARG;
-    if (!al16(x) || !al16(maa) || !al16(mexp) || !al16(bias) || !al16(d_mixed) ||
-        (d_xxx && !al16(d_xxx)) || !al16(dx) || !al16(workspace))
+    InPtrs<MIX_NE> dm{};
+    if (T > 0 && (st = gather<InPtrs<MIX_NE>, MIX_NE>(d_mixed, dm))) return st;
+    if (!al16(x) || !al16(maa) || !al16(mexp) || !al16(bias) || (d_xxx && !al16(d_xxx)) ||
+        !al16(dx) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
     if (T > 0)
         hipLaunchKernelGGL(rwkv6_mix_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
-                           (const uint16_t*)x, maa, (const uint16_t*)mexp, bias, param_dtype,
-                           (const uint16_t*)d_mixed, (const uint16_t*)d_xxx, (uint16_t*)dx, part,
-                           T, B, C);
+                           (const uint16_t*)x, maa, (const uint16_t*)mexp, bias, param_dtype, dm,
+                           (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
     hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(MIX_THR), 0, s, part,
                        T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
     return launch_status();
 }
 
-int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* mixed, int64_t T,
-                        int64_t B, int64_t C, void* stream) {
+int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* const* mixed,
+                        int64_t T, int64_t B, int64_t C, void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
     if (T == 0) return RWKV6_OK;
-    if (!x || !mix || !mixed) return RWKV6_ERR_INVALID_ARG;
-    if (!al16(x) || !al16(mix) || !al16(mixed)) return RWKV6_ERR_ALIGNMENT;
+    if (!x || !mix) return RWKV6_ERR_INVALID_ARG;
+    OutPtrs<CMIX_NE> out;
+    if ((st = gather<OutPtrs<CMIX_NE>, CMIX_NE>((const void* const*)mixed, out))) return st;
+    if (!al16(x) || !al16(mix)) return RWKV6_ERR_ALIGNMENT;
     const int64_t n = T * B * (C / 8);
     hipLaunchKernelGGL(rwkv6_cmix_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, mix, param_dtype,
-                       (uint16_t*)mixed, T, B, C);
+                       out, T, B, C);
     return launch_status();
 }
 
@@ -660,23 +681,23 @@ size_t rwkv6_cmix_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
     return (size_t)((ntb > 0 ? ntb : 1) * B * CMIX_NE * C) * sizeof(float);
 }
 
-int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype, const void* d_mixed,
-                        void* dx, void* d_mix, void* workspace, int64_t T, int64_t B, int64_t C,
-                        void* stream) {
+int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype,
+                        const void* const* d_mixed, void* dx, void* d_mix, void* workspace,
+                        int64_t T, int64_t B, int64_t C, void* stream) {
     int st = mix_check(T, B, C, param_dtype);
     if (st) return st;
     if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
-    if (!mix || !d_mix || !workspace || (T > 0 && (!x || !d_mixed || !dx)))
-        return RWKV6_ERR_INVALID_ARG;
-    if (!al16(x) || !al16(mix) || !al16(d_mixed) || !al16(dx) || !al16(workspace))
-        return RWKV6_ERR_ALIGNMENT;
+    if (!mix || !d_mix || !workspace || (T > 0 && (!x || !dx))) return RWKV6_ERR_INVALID_ARG;
+    InPtrs<CMIX_NE> dm{};
+    if (T > 0 && (st = gather<InPtrs<CMIX_NE>, CMIX_NE>(d_mixed, dm))) return st;
+    if (!al16(x) || !al16(mix) || !al16(dx) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
     if (T > 0)
         hipLaunchKernelGGL(rwkv6_cmix_lerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
-                           (const uint16_t*)x, mix, param_dtype, (const uint16_t*)d_mixed,
-                           (uint16_t*)dx, part, T, B, C);
+                           (const uint16_t*)x, mix, param_dtype, dm, (uint16_t*)dx, part, T, B,
+                           C);
     hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((CMIX_NE * C + 31) / 32)), dim3(MIX_THR), 0,
                        s, part, T > 0 ? ntb * B : (int64_t)0, (int64_t)CMIX_NE * C, param_dtype,
                        d_mix);

@@ -178,8 +178,8 @@ class RWKV6TimeMix(nn.Module):
         x = hidden_states
         T, B, C = x.shape
         ts = self.bottleneck_token_shift
-        mixed = timemix.token_shift_mix(x, self.mix_coeff_input, ts.weight_down, ts.weight_up, ts.bias)
-        mixed_decay, mixed_key, mixed_value, mixed_receptance, mixed_gate = mixed.unbind(0)
+        mixed_decay, mixed_key, mixed_value, mixed_receptance, mixed_gate = timemix.token_shift_mix(
+            x, self.mix_coeff_input, ts.weight_down, ts.weight_up, ts.bias)
         decay = self.bottleneck_decay(mixed_decay).squeeze(-2)
         key = self.linear_key(mixed_key)[0]
         value = self.linear_value(mixed_value)[0]

@@ -41,6 +41,11 @@ def _param(t: torch.Tensor):
     return _c(t.float()), _lib.RWKV6_F32
 
 
+def _ptrs(ts):
+    """Host array of device pointers (the C ABI's `void* const*` arguments)."""
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
 def _check_act(name, x, ndim):
     if x.device.type != "cuda":
         raise ValueError(f"{name} must live on the GPU")
@@ -66,21 +71,23 @@ def shift_lerp(x: torch.Tensor, maa: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def ddlerp(x: torch.Tensor, mexp: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
-    """mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]); mexp [5,T,B,C] -> [5,T,B,C]."""
+def ddlerp(x: torch.Tensor, mexp: torch.Tensor, bias: torch.Tensor):
+    """mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]); mexp [5,T,B,C] -> tuple of five
+    [T,B,C] tensors (w, k, v, r, g)."""
     _check_act("x", x, 3)
     T, B, C = x.shape
     if tuple(mexp.shape) != (NE, T, B, C):
         raise ValueError(f"mexp must be [5,T,B,C] = {(NE, T, B, C)}, got {tuple(mexp.shape)}")
     x, mexp = _c(x), _c(mexp.to(torch.bfloat16))
     b, pdt = _param(bias)
-    out = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
-    _lib.check(_lib.load().rwkv6_ddlerp_fwd(_p(x), _p(mexp), _p(b), pdt, _p(out), T, B, C,
+    out = tuple(torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device) for _ in range(NE))
+    _lib.check(_lib.load().rwkv6_ddlerp_fwd(_p(x), _p(mexp), _p(b), pdt, _ptrs(out), T, B, C,
                                             _stream(x.device)), "rwkv6_ddlerp_fwd")
     return out
 
 
 def ddlerp_bwd(x, d_mixed, param_dtype):
+    """d_mixed: five [T,B,C] bf16 tensors -> (d_mexp [5,T,B,C], d_bias [5,C])."""
     T, B, C = x.shape
     L = _lib.load()
     d_mexp = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
@@ -88,7 +95,7 @@ def ddlerp_bwd(x, d_mixed, param_dtype):
     d_bias = torch.empty(NE, C, dtype=torch.bfloat16 if pdt == _lib.RWKV6_BF16 else torch.float32,
                          device=x.device)
     ws = torch.empty(L.rwkv6_ddlerp_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
-    _lib.check(L.rwkv6_ddlerp_bwd(_p(x), _p(d_mixed), pdt, _p(d_mexp), _p(d_bias), _p(ws), T, B, C,
+    _lib.check(L.rwkv6_ddlerp_bwd(_p(x), _ptrs(d_mixed), pdt, _p(d_mexp), _p(d_bias), _p(ws), T, B, C,
                                   _stream(x.device)), "rwkv6_ddlerp_bwd")
     return d_mexp, d_bias
 
@@ -103,7 +110,7 @@ def mix_bwd(x, maa, mexp, bias, d_mixed, d_xxx):
     dx = torch.empty_like(x)
     d_maa = torch.empty(C, dtype=m.dtype, device=x.device)
     ws = torch.empty(L.rwkv6_mix_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
-    _lib.check(L.rwkv6_mix_bwd(_p(x), _p(m), _p(mexp), _p(b), pdt, _p(d_mixed), _p(d_xxx), _p(dx),
+    _lib.check(L.rwkv6_mix_bwd(_p(x), _p(m), _p(mexp), _p(b), pdt, _ptrs(d_mixed), _p(d_xxx), _p(dx),
                                _p(d_maa), _p(ws), T, B, C, _stream(x.device)), "rwkv6_mix_bwd")
     return dx, d_maa
 
@@ -134,7 +141,7 @@ def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
 # ---------------------------------------------------------------------------
 
 class _TokenShiftMix(torch.autograd.Function):
-    """x [T,B,C] -> mixed [5,T,B,C] (w,k,v,r,g); params maa [C], w_down [C,5,R],
+    """x [T,B,C] -> five [T,B,C] mixes (w,k,v,r,g); params maa [C], w_down [C,5,R],
     w_up [5,R,C], bias [5,C] with the shapes of rwkv6_layer_specs.py:126-170, :377-385."""
 
     @staticmethod
@@ -154,12 +161,12 @@ class _TokenShiftMix(torch.autograd.Function):
         return mixed
 
     @staticmethod
-    def backward(ctx, d_mixed):
+    def backward(ctx, *d_mixed):
         x, maa, w_down, w_up, bias, xxx, neck_t, mexp = ctx.saved_tensors
         T, B, C = x.shape
         R = w_down.shape[-1]
         N = T * B
-        d_mixed = _c(d_mixed.to(torch.bfloat16))
+        d_mixed = [torch.zeros_like(x) if d is None else _c(d.to(torch.bfloat16)) for d in d_mixed]
         d_mexp, d_bias = ddlerp_bwd(x, d_mixed, bias.dtype)
         d_mexp = d_mexp.view(NE, N, C)
         wu = w_up.to(torch.bfloat16)
@@ -176,7 +183,8 @@ class _TokenShiftMix(torch.autograd.Function):
 
 
 def token_shift_mix(x, maa, w_down, w_up, bias):
-    """Returns mixed [5,T,B,C] = (w, k, v, r, g) inputs of RWKV6TimeMix (:440-452)."""
+    """Returns the five [T,B,C] mixes (w, k, v, r, g), the inputs of RWKV6TimeMix's
+    projections (:440-452)."""
     _check_act("x", x, 3)
     return _TokenShiftMix.apply(x, maa, w_down, w_up, bias)
 

@@ -45,9 +45,10 @@ def test_cmix_lerp_forward_backward(pkg, shape, pdt):
     d_mixed = _bf(torch.randn(2, T, B, C, generator=g))
     xd = x.to(DEV).requires_grad_(True)
     md = mix.to(DEV).requires_grad_(True)
-    mixed = pkg.channelmix.cmix_lerp(xd, md)
-    (mixed.float() * d_mixed.to(DEV).float()).sum().backward()
+    mixes = pkg.channelmix.cmix_lerp(xd, md)
+    sum((m.float() * d.float()).sum() for m, d in zip(mixes, d_mixed.to(DEV))).backward()
     torch.cuda.synchronize()
+    mixed = torch.stack(mixes)
     assert mixed.shape == (2, T, B, C) and md.grad.dtype == pdt
     _check("mixed", _n(mixed), orc.cmix_lerp_fwd(_n(x), _n(mix)))
     dx, d_mix = orc.cmix_lerp_bwd(_n(x), _n(mix), _n(d_mixed))
@@ -86,7 +87,8 @@ def test_cmix_lerp_backward_deterministic(pkg):
     res = []
     for _ in range(2):
         xd, md = x.clone().requires_grad_(True), mix.clone().requires_grad_(True)
-        pkg.channelmix.cmix_lerp(xd, md).backward(dm)
+        up, gate = pkg.channelmix.cmix_lerp(xd, md)
+        torch.autograd.backward([up, gate], [dm[0], dm[1]])
         res.append((xd.grad.clone(), md.grad.clone()))
     assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
 
@@ -117,3 +119,20 @@ def test_channel_mix_module(pkg, T, B, C, F):
            mod.linear_down.weight.grad)
     for name, a, r in zip(("dx", "d_mix", "d_w_up", "d_w_gate", "d_w_down"), got, ref):
         _check(name, _n(a), r, 2e-2)
+
+
+def test_cmix_lerp_one_output_used(pkg):
+    """A loss on mixed_up alone leaves the gate gradient None: it counts as zero."""
+    T, B, C = 40, 2, 64
+    g = torch.Generator().manual_seed(9)
+    x = _bf(torch.randn(T, B, C, generator=g))
+    mix = torch.rand(2, C, generator=g)
+    d_up = _bf(torch.randn(T, B, C, generator=g))
+    xd, md = x.to(DEV).requires_grad_(True), mix.to(DEV).requires_grad_(True)
+    up, _ = pkg.channelmix.cmix_lerp(xd, md)
+    up.backward(d_up.to(DEV))
+    torch.cuda.synchronize()
+    dx, d_mix = orc.cmix_lerp_bwd(_n(x), _n(mix), np.stack([_n(d_up), np.zeros((T, B, C))]))
+    _check("dx", _n(xd.grad), dx)
+    _check("d_mix", _n(md.grad[0]), d_mix[0])
+    assert torch.all(md.grad[1] == 0)

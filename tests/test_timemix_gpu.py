@@ -46,7 +46,7 @@ def test_shift_lerp_and_ddlerp(pkg, shape, pdt):
     mexp = _bf(torch.randn(5, T, B, C, generator=g))
     bias = torch.randn(5, C, generator=g).to(pdt)
     xxx = pkg.timemix.shift_lerp(x.to(DEV), maa.to(DEV))
-    mixed = pkg.timemix.ddlerp(x.to(DEV), mexp.to(DEV), bias.to(DEV))
+    mixed = torch.stack(pkg.timemix.ddlerp(x.to(DEV), mexp.to(DEV), bias.to(DEV)))
     torch.cuda.synchronize()
     _check("xxx", _n(xxx), orc.shift_lerp_fwd(_n(x), _n(maa)))
     _check("mixed", _n(mixed), orc.ddlerp_fwd(_n(x), np.moveaxis(_n(mexp), 0, 2), _n(bias)))
@@ -65,8 +65,10 @@ def test_token_shift_mix_forward_backward(pkg, T, B, C):
     # the GEMMs run in bf16: give the oracle the same bf16-rounded weights
     wd_b, wu_b = _bf(wd), _bf(wu)
     leaves = [t.to(DEV).requires_grad_(True) for t in (x, maa, wd_b, wu_b, bias)]
-    mixed = pkg.timemix.token_shift_mix(*leaves)
-    (mixed.float() * dmix.to(DEV).float()).sum().backward()
+    mixes = pkg.timemix.token_shift_mix(*leaves)
+    assert len(mixes) == 5 and all(t.is_contiguous() for t in mixes)
+    sum((m.float() * d.float()).sum() for m, d in zip(mixes, dmix.to(DEV))).backward()
+    mixed = torch.stack(mixes)
     torch.cuda.synchronize()
     xn, maan, wdn, wun, bn = (_n(t) for t in (x, maa, wd_b, wu_b, bias))
     xxx = orc.shift_lerp_fwd(xn, maan)
@@ -128,7 +130,7 @@ def test_mix_and_gn_deterministic(pkg):
     def run():
         ps = [p.to(DEV).requires_grad_(True) for p in params]
         xi = x.clone().requires_grad_(True)
-        mixed = pkg.timemix.token_shift_mix(xi, *ps)
+        mixed = torch.stack(pkg.timemix.token_shift_mix(xi, *ps))
         gam = torch.ones(C, device=DEV, requires_grad=True)
         bet = torch.zeros(C, device=DEV, requires_grad=True)
         y = pkg.timemix.group_norm_gate(o, gp, gam, bet, 1e-5)
