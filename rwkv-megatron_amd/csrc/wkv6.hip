@@ -5,12 +5,13 @@
 //   o_t = s * r_t^T (S_{t-1} + diag(u) k_t v_t^T),   S_t = diag(exp(w_t)) S_{t-1} + k_t v_t^T.
 //
 // Decomposition (three phases each way, all deterministic):
-//   fwd_chunk_state  per (b,h,chunk): S_loc = sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T  [MFMA]
+//   chunk_local<fwd> per (b,h,chunk): S_loc = sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T  [MFMA]
 //   state_scan_fwd   per (b,h,elem) : S_in(c+1) = e^{G_63(c)} S_in(c) + S_loc(c)  fp32, coalesced
-//   fwd_chunk_output per (b,h,chunk): o = (r e^{G_{t-1}}) S_in + intra-chunk attention   [MFMA]
-//   bwd_chunk_dstate per (b,h,chunk): dS_loc = s * sum_t (r_t e^{G_{t-1}}) dO_t^T        [MFMA]
+//   fwd_chunk_output persistent     : o = (r e^{G_{t-1}}) S_in + intra-chunk attention   [MFMA]
+//   chunk_local<bwd> per (b,h,chunk): dS_loc = s * sum_t (r_t e^{G_{t-1}}) dO_t^T        [MFMA]
 //   state_scan_bwd   per (b,h,elem) : dS_out(c-1) = e^{G_63(c)} dS_out(c) + dS_loc(c)
 //   bwd_chunk_grads  per (b,h,chunk): dr, dk, dv, dw, du-partials                        [MFMA]
+//   du_reduce        per (h, channel): fixed-order sum of the du partials
 //
 // Inside a 64-token chunk G is the inclusive cumulative log-decay (base-2 units, so
 // every exponential is one v_exp_f32) and a chunk is four 16-token sub-blocks with
