@@ -225,7 +225,7 @@ __device__ __forceinline__ float sum8lanes(float v) {
 template <bool FWD, bool SEQ>
 __global__ void __launch_bounds__(NTHR)
 wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
-                 const uint16_t* __restrict__ w, float* __restrict__ out,
+                 const uint16_t* __restrict__ w, void* __restrict__ out,
                  float* __restrict__ decay, float scale, int B, int H, int T, int NT) {
     __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
     __shared__ __attribute__((aligned(16))) float Gstore[CL * GSG];
@@ -269,18 +269,35 @@ wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
 #pragma unroll
         for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Ys[0][0], 32 * ks, 16 * tj), acc[tj]);
     }
-    float* o = out + ((size_t)bh * NT + c) * KD * KD;
+    if (FWD) {
+        // S_loc stays fp32: the dw of the backward takes rowsum(S_out * dS) against terms
+        // that cancel its k v^T part, so S_out carries a single bf16 rounding.
+        float* o = reinterpret_cast<float*>(out) + ((size_t)bh * NT + c) * KD * KD;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
+        for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = scale * acc[tj][rr];
-    if (FWD && threadIdx.x < KD)
-        decay[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
+            for (int rr = 0; rr < 4; ++rr) o[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = scale * acc[tj][rr];
+        if (threadIdx.x < KD)
+            decay[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
+    } else {
+        // dS_loc in bf16, staged through LDS (Wm is free since build_G) for 16-byte stores
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) Wm[16 * wv + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
+        __syncthreads();
+        store_tile<NTHR>(reinterpret_cast<uint16_t*>(out) + ((size_t)bh * NT + c) * KD * KD, Wm, KD);
+    }
 }
 
 // ---------------------------------------------------------------------------
-// phase B: state scans (fp32, one thread per state element, coalesced)
+// phase B: state scans (fp32 carry; fp32 S_loc / bf16 dS_loc in, bf16 states out; one
+// thread per state element, coalesced)
 // ---------------------------------------------------------------------------
+// Each thread issues the loads of SCAN_U chunks before it walks them (the loads do not
+// depend on the carry), so a wave keeps SCAN_U requests in flight.
+#define SCAN_U 32
+
 // Hs[c] = bf16(S_in(c)) for c = 0..NT (Hs[NT] = final state); hT = S_in(NT) fp32.
 __global__ void __launch_bounds__(NTHR)
 wkv6_state_scan_fwd(const float* __restrict__ Sloc, const float* __restrict__ decay,
@@ -294,14 +311,19 @@ wkv6_state_scan_fwd(const float* __restrict__ Sloc, const float* __restrict__ de
     const float* dc = decay + (size_t)bh * NT * KD + i;
     uint16_t* hs = Hs + (size_t)bh * (NT + 1) * KD * KD + e;
     int c = 0;
-    for (; c + 4 <= NT; c += 4) {
-        float l0 = sl[(size_t)(c + 0) * KD * KD], l1 = sl[(size_t)(c + 1) * KD * KD];
-        float l2 = sl[(size_t)(c + 2) * KD * KD], l3 = sl[(size_t)(c + 3) * KD * KD];
-        float d0 = dc[(c + 0) * KD], d1 = dc[(c + 1) * KD], d2 = dc[(c + 2) * KD], d3 = dc[(c + 3) * KD];
-        hs[(size_t)(c + 0) * KD * KD] = f2bf(S); S = d0 * S + l0;
-        hs[(size_t)(c + 1) * KD * KD] = f2bf(S); S = d1 * S + l1;
-        hs[(size_t)(c + 2) * KD * KD] = f2bf(S); S = d2 * S + l2;
-        hs[(size_t)(c + 3) * KD * KD] = f2bf(S); S = d3 * S + l3;
+    for (; c + SCAN_U <= NT; c += SCAN_U) {
+        float l[SCAN_U];
+        float d[SCAN_U];
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            l[q] = sl[(size_t)(c + q) * KD * KD];
+            d[q] = dc[(c + q) * KD];
+        }
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            hs[(size_t)(c + q) * KD * KD] = f2bf(S);
+            S = d[q] * S + l[q];
+        }
     }
     for (; c < NT; ++c) {
         hs[(size_t)c * KD * KD] = f2bf(S);
@@ -313,29 +335,34 @@ wkv6_state_scan_fwd(const float* __restrict__ Sloc, const float* __restrict__ de
 
 // dHs[c] = bf16(dS_out(c)) (gradient w.r.t. the state after chunk c); dh0 = dS_in(0).
 __global__ void __launch_bounds__(NTHR)
-wkv6_state_scan_bwd(const float* __restrict__ dSloc, const float* __restrict__ decay,
+wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict__ decay,
                     const float* __restrict__ dhT, uint16_t* __restrict__ dHs,
                     float* __restrict__ dh0, int NT) {
     const int bh = blockIdx.x >> 4;
     const int e = ((blockIdx.x & 15) << 8) + threadIdx.x;
     const int i = e >> 6;
     float dS = dhT ? dhT[(size_t)bh * KD * KD + e] : 0.f;
-    const float* sl = dSloc + (size_t)bh * NT * KD * KD + e;
+    const uint16_t* sl = dSloc + (size_t)bh * NT * KD * KD + e;
     const float* dc = decay + (size_t)bh * NT * KD + i;
     uint16_t* hs = dHs + (size_t)bh * NT * KD * KD + e;
     int c = NT - 1;
-    for (; c - 3 >= 0; c -= 4) {
-        float l0 = sl[(size_t)(c - 0) * KD * KD], l1 = sl[(size_t)(c - 1) * KD * KD];
-        float l2 = sl[(size_t)(c - 2) * KD * KD], l3 = sl[(size_t)(c - 3) * KD * KD];
-        float d0 = dc[(c - 0) * KD], d1 = dc[(c - 1) * KD], d2 = dc[(c - 2) * KD], d3 = dc[(c - 3) * KD];
-        hs[(size_t)(c - 0) * KD * KD] = f2bf(dS); dS = d0 * dS + l0;
-        hs[(size_t)(c - 1) * KD * KD] = f2bf(dS); dS = d1 * dS + l1;
-        hs[(size_t)(c - 2) * KD * KD] = f2bf(dS); dS = d2 * dS + l2;
-        hs[(size_t)(c - 3) * KD * KD] = f2bf(dS); dS = d3 * dS + l3;
+    for (; c - (SCAN_U - 1) >= 0; c -= SCAN_U) {
+        uint16_t l[SCAN_U];
+        float d[SCAN_U];
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            l[q] = sl[(size_t)(c - q) * KD * KD];
+            d[q] = dc[(c - q) * KD];
+        }
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            hs[(size_t)(c - q) * KD * KD] = f2bf(dS);
+            dS = d[q] * dS + bf2f(l[q]);
+        }
     }
     for (; c >= 0; --c) {
         hs[(size_t)c * KD * KD] = f2bf(dS);
-        dS = dc[c * KD] * dS + sl[(size_t)c * KD * KD];
+        dS = dc[c * KD] * dS + bf2f(sl[(size_t)c * KD * KD]);
     }
     if (dh0) dh0[(size_t)bh * KD * KD + e] = dS;
 }
@@ -918,9 +945,8 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
                                  int for_bwd) {
     if (check_shape(B, H, T, K, V) != RWKV6_OK) return 0;
     const size_t BH = (size_t)(B * H), NT = (size_t)(nchunks(T) > 0 ? nchunks(T) : 1);
-    size_t sz = round_up(BH * NT * KD * KD * 4);                       // S_loc / dS_loc (fp32)
-    if (for_bwd) sz += round_up(BH * NT * KD * KD * 2) + round_up(BH * NT * KD * 4);   // dHs, du_part
-    return sz;
+    if (!for_bwd) return round_up(BH * NT * KD * KD * 4);             // S_loc (fp32)
+    return round_up(BH * NT * KD * KD * 2) * 2 + round_up(BH * NT * KD * 4);   // dS_loc, dHs, du_part
 }
 
 }  // extern "C"
@@ -996,9 +1022,9 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     const float* decay = reinterpret_cast<const float*>(
         reinterpret_cast<const char*>(saved) + round_up((size_t)BH * (NT + 1) * KD * KD * 2));
     const size_t NTa = (size_t)(NT > 0 ? NT : 1);
-    float* dSloc = reinterpret_cast<float*>(workspace);
+    uint16_t* dSloc = reinterpret_cast<uint16_t*>(workspace);
     uint16_t* dHs = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(workspace) +
-                                                round_up((size_t)BH * NTa * KD * KD * 4));
+                                                round_up((size_t)BH * NTa * KD * KD * 2));
     float* du_part = reinterpret_cast<float*>(reinterpret_cast<char*>(dHs) +
                                               round_up((size_t)BH * NTa * KD * KD * 2));
     mark(phase_events, 0, s);
