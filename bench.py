@@ -16,7 +16,9 @@ Also reported:
   * TFLOP/s of the whole op (fwd 32768 + bwd 65536 FLOP per token-head) and the
     fraction of the 2.5 PFLOP/s dense bf16 MFMA peak;
   * cpu_baseline: the CPU oracle (fp64 naive recurrence, C + OpenMP, a port of
-    fla's naive recurrent RWKV-6) timed on this host on the same workload.
+    fla's naive recurrent RWKV-6) timed on this host on the same workload;
+  * config5 (WKV6 long context with carried state), slice_7b (config 4: four 7B-shape
+    layers fwd+bwd) and train_step (config 3: the 1.6B-shape training step).
 """
 from __future__ import annotations
 
@@ -53,6 +55,8 @@ def parse():
                     help="(b,h) sequences in the CPU sample (0 = the whole workload)")
     ap.add_argument("--no-train", action="store_true",
                     help="skip the config-3 training step (RWKV6 1.6B shape) measurement")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the config-5 WKV and config-4 7B-slice measurements")
     ap.add_argument("--train-only", action="store_true",
                     help="run only the config-3 training step (for kernel profiles)")
     ap.add_argument("--train-steps", type=int, default=3)
@@ -63,7 +67,7 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(B, H, T, sample_heads):
+def cpu_baseline(B, H, T, sample_heads, with_state=False):
     """Time the CPU oracle (fwd + bwd) on this host; returns the reported dict."""
     import numpy as np
     from oracle import oracle as orc
@@ -77,19 +81,25 @@ def cpu_baseline(B, H, T, sample_heads):
     r, k, v, dO = f(Bs, Hs, T, K), f(Bs, Hs, T, K), f(Bs, Hs, T, K), f(Bs, Hs, T, K)
     w = -np.exp(rng.uniform(-6, -0.5, (Bs, Hs, T, K))).astype(np.float32)
     u = (0.1 * f(Hs, K)).astype(np.float32)
+    h0 = (0.5 * f(Bs, Hs, K, K)).astype(np.float32) if with_state else None
+    dhT = f(Bs, Hs, K, K) if with_state else None
     threads = orc.max_threads()
-    # warm up on a short prefix, then one timed run
+    # one warm-up on a short prefix, then the median of 3 timed runs
     orc.wkv6_fwd(r[:, :, :64], k[:, :, :64], v[:, :, :64], w[:, :, :64], u)
-    t0 = time.perf_counter()
-    orc.wkv6_fwd(r, k, v, w, u)
-    orc.wkv6_bwd(r, k, v, w, u, dO)
-    dt = time.perf_counter() - t0
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        orc.wkv6_fwd(r, k, v, w, u, h0)
+        orc.wkv6_bwd(r, k, v, w, u, dO, h0, dhT)
+        runs.append(time.perf_counter() - t0)
+    dt = sorted(runs)[1]
     frac = (Bs * Hs) / (B * H)
     tokens_per_s = (B * T) * frac / dt
     return {
         "value": tokens_per_s, "unit": "tokens/s", "cores": threads, "kind": "port",
         "sample": f"oracle fp64 naive recurrence fwd+bwd over {Bs*Hs} of {B*H} (b,h) sequences "
-                  f"at T={T} ({dt:.2f} s), scaled to the whole B={B},H={H} job",
+                  f"at T={T}{' with h0, dhT' if with_state else ''} (median of 3 runs, {dt:.2f} s), "
+                  f"scaled to the whole B={B},H={H} job",
     }
 
 
@@ -107,6 +117,67 @@ def measured_traffic(B, H, T):
     if (d.get("B"), d.get("H"), d.get("T")) != (B, H, T):
         return None
     return d.get("traffic_bytes")
+
+
+def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
+    """WKV6 fwd+bwd through the C ABI (the _ex entries, HIP events around every phase) on
+    synthetic inputs resident in HBM.  with_state: h0 ~ N(0, 0.5^2), dhT ~ N(0,1), dh0 returned
+    (config 5).  Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    K = 64
+    g = torch.Generator().manual_seed(0)
+    bf = lambda t: t.to(torch.bfloat16).to(dev)
+    r, k, v = (bf(torch.randn(B, H, T, K, generator=g)) for _ in range(3))
+    w = bf(-torch.exp(torch.rand(B, H, T, K, generator=g) * 5.5 - 6.0))
+    u = (0.1 * torch.randn(H, K, generator=g)).to(dev)
+    do = bf(torch.randn(B, H, T, K, generator=g))
+    h0 = (0.5 * torch.randn(B, H, K, K, generator=g)).to(dev) if with_state else None
+    dhT = torch.randn(B, H, K, K, generator=g).to(dev) if with_state else None
+    dh0 = torch.empty(B, H, K, K, dtype=torch.float32, device=dev) if with_state else None
+
+    saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, K, K), dtype=torch.uint8, device=dev)
+    ws_f = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 0), dtype=torch.uint8, device=dev)
+    ws_b = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 1), dtype=torch.uint8, device=dev)
+    o = torch.empty_like(v)
+    hT = torch.empty(B, H, K, K, dtype=torch.float32, device=dev)
+    dr, dk, dv, dw = (torch.empty_like(r) for _ in range(4))
+    du = torch.empty(H, K, dtype=torch.float32, device=dev)
+    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def step(fev=None, bev=None):
+        fa = (ctypes.c_void_p * 6)(*[e.cuda_event for e in fev]) if fev else None
+        ba = (ctypes.c_void_p * 8)(*[e.cuda_event for e in bev]) if bev else None
+        pkg._lib.check(L.rwkv6_wkv_fwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, P(h0), P(o),
+                                          P(hT), P(saved), P(ws_f), B, H, T, K, K, 1.0, sp, fa), "fwd")
+        pkg._lib.check(L.rwkv6_wkv_bwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, P(do), P(dhT),
+                                          P(saved), P(dr), P(dk), P(dv), P(dw), P(du), P(dh0), P(ws_b),
+                                          B, H, T, K, K, 1.0, sp, ba), "bwd")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    fevs = [[ev() for _ in range(6)] for _ in range(steps)]
+    bevs = [[ev() for _ in range(8)] for _ in range(steps)]
+    t0 = ev()
+    t1 = ev()
+    for e in [x for evs in fevs + bevs for x in evs]:
+        e.record(stream)               # torch creates the hipEvent_t on first record
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(steps):
+        step(fevs[i], bevs[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    avg = lambda evs, a, b: sum(e[a].elapsed_time(e[b]) for e in evs) / len(evs)
+    fwd_ph = [avg(fevs, 2 * p, 2 * p + 1) for p in range(3)]
+    bwd_ph = [avg(bevs, 2 * p, 2 * p + 1) for p in range(4)]
+    return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph
 
 
 def train_step_bench(pkg, steps, warmup):
@@ -161,6 +232,54 @@ def train_step_bench(pkg, steps, warmup):
     return out
 
 
+def slice_7b_bench(pkg, steps, warmup):
+    """4 RWKV-6 layers of the 7B shape (d_model 4096, 64 heads, ffn 14336),
+    bf16 random-init weights, activations [8192, 2, 4096] ~ N(0,1) (sequence-first, as the
+    reference), fwd + bwd through LN + time mix + channel mix + residual with dY ~ N(0,1)."""
+    import torch
+
+    M = pkg.modules
+    cfg = M.TransformerConfig(hidden_size=4096, num_attention_heads=64, ffn_hidden_size=14336,
+                              num_layers=4, params_dtype=torch.bfloat16)
+    T, B, C = 8192, 2, 4096
+    torch.manual_seed(0)
+    layers = torch.nn.ModuleList(M.RWKV6Layer(cfg, i + 1, device="cuda:0") for i in range(4))
+    g = torch.Generator(device="cuda:0").manual_seed(2)
+    x = torch.randn(T, B, C, device="cuda:0", dtype=torch.bfloat16, generator=g).requires_grad_(True)
+    dy = torch.randn(T, B, C, device="cuda:0", dtype=torch.bfloat16, generator=g)
+
+    def step():
+        y = x
+        for layer in layers:
+            y = layer(y)
+        y.backward(dy)
+        x.grad = None
+        for p in layers.parameters():
+            p.grad = None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # 6 * matmul parameters per token (2-D weights and the LoRA factors) + WKV fwd+bwd per token-head
+    mm = sum(p.numel() for n, p in layers.named_parameters() if p.dim() >= 2)
+    flop = 6 * mm * T * B + 4 * cfg.num_attention_heads * T * B * (FLOP_FWD + FLOP_BWD)
+    out = {"workload": "BASELINE config 4: 4 RWKV-6 layers, d_model 4096, 64 heads, ffn 14336, "
+                       "bf16, activations [8192, 2, 4096], fwd+bwd",
+           "ms_per_step": ms, "tokens_per_s": T * B / (ms * 1e-3), "flop_per_step": flop,
+           "tflops": flop / (ms * 1e-3) / 1e12, "mfu": flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+           "steps": steps, "warmup": warmup}
+    del layers, x, dy
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -179,56 +298,7 @@ def main():
     B, H, T, K = args.B, args.H, args.T, 64
     N_th = B * H * T
 
-    g = torch.Generator().manual_seed(0)
-    bf = lambda t: t.to(torch.bfloat16).to(dev)
-    r, k, v = (bf(torch.randn(B, H, T, K, generator=g)) for _ in range(3))
-    w = bf(-torch.exp(torch.rand(B, H, T, K, generator=g) * 5.5 - 6.0))
-    u = (0.1 * torch.randn(H, K, generator=g)).to(dev)
-    do = bf(torch.randn(B, H, T, K, generator=g))
-
-    NT = (T + 63) // 64
-    saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, K, K), dtype=torch.uint8, device=dev)
-    ws_f = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 0), dtype=torch.uint8, device=dev)
-    ws_b = torch.empty(L.rwkv6_wkv_workspace_bytes(B, H, T, K, K, 1), dtype=torch.uint8, device=dev)
-    o = torch.empty_like(v)
-    hT = torch.empty(B, H, K, K, dtype=torch.float32, device=dev)
-    dr, dk, dv, dw = (torch.empty_like(r) for _ in range(4))
-    du = torch.empty(H, K, dtype=torch.float32, device=dev)
-    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    ev = lambda: torch.cuda.Event(enable_timing=True)
-
-    def step(fev=None, bev=None):
-        fa = (ctypes.c_void_p * 6)(*[e.cuda_event for e in fev]) if fev else None
-        ba = (ctypes.c_void_p * 8)(*[e.cuda_event for e in bev]) if bev else None
-        pkg._lib.check(L.rwkv6_wkv_fwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, None, P(o),
-                                          P(hT), P(saved), P(ws_f), B, H, T, K, K, 1.0, sp, fa), "fwd")
-        pkg._lib.check(L.rwkv6_wkv_bwd_ex(P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, P(do), None,
-                                          P(saved), P(dr), P(dk), P(dv), P(dw), P(du), None, P(ws_b),
-                                          B, H, T, K, K, 1.0, sp, ba), "bwd")
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    fevs = [[ev() for _ in range(6)] for _ in range(args.steps)]
-    bevs = [[ev() for _ in range(8)] for _ in range(args.steps)]
-    t0 = ev()
-    t1 = ev()
-    for e in [x for evs in fevs + bevs for x in evs]:
-        e.record(stream)               # torch creates the hipEvent_t on first record
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for i in range(args.steps):
-        step(fevs[i], bevs[i])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / args.steps
-    avg = lambda evs, a, b: sum(e[a].elapsed_time(e[b]) for e in evs) / len(evs)
-    fwd_ph = [avg(fevs, 2 * p, 2 * p + 1) for p in range(3)]
-    bwd_ph = [avg(bevs, 2 * p, 2 * p + 1) for p in range(4)]
-    fwd_ms = avg(fevs, 0, 5)
-    bwd_ms = avg(bevs, 0, 7)
+    ms_step, fwd_ms, bwd_ms, fwd_ph, bwd_ph = time_wkv(pkg, L, B, H, T, args.steps, args.warmup)
 
     grads_ms = bwd_ph[2]
     achieved = N_th * BYTES_BWD_GRADS / (grads_ms * 1e-3) / 1e9
@@ -264,6 +334,18 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic(B, H, T)},
     }
+    if not args.no_extra_configs:
+        # the long-context one-GPU share with carried state (h0, dhT, dh0)
+        B5, H5, T5 = 1, 32, 32768
+        c5 = time_wkv(pkg, L, B5, H5, T5, max(5, args.steps // 2), args.warmup, with_state=True)
+        out["config5"] = {"workload": "BASELINE config 5: WKV6 B=1, H=32, T=32768, h0 ~ N(0,0.5^2), "
+                                      "dhT ~ N(0,1), final state and dh0 returned",
+                          "ms_per_step": c5[0], "tokens_per_s": B5 * T5 / (c5[0] * 1e-3),
+                          "fwd_ms": c5[1], "bwd_ms": c5[2],
+                          "tflops": B5 * H5 * T5 * (FLOP_FWD + FLOP_BWD) / (c5[0] * 1e-3) / 1e12}
+        if not args.no_cpu_baseline:
+            out["config5"]["cpu_baseline"] = cpu_baseline(B5, H5, T5, 0, with_state=True)
+        out["slice_7b"] = slice_7b_bench(pkg, args.train_steps, args.train_warmup)
     if args.copy_calibration_mb > 0:
         n = args.copy_calibration_mb * (1 << 20) // 2
         src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
