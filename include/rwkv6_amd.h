@@ -21,6 +21,8 @@
  *             rwkv6_layer_specs.py:290-300 and :440-452 (bias of :195 folded in)
  *   gn_gate   GroupNorm (rwkv6_layer_specs.py:90-97) applied at :461-465, times
  *             the silu gate of :458, the product formed at :466
+ *   lora      LoRA up-projections of RWKV6Bottleneck (:177-195) fused with the ddlerp
+ *             of :447-452 or the decay bias of :454
  *   cmix      token shift + static lerp, relu^2 and sigmoid gate of
  *             RWKV6ChannelMix.forward, rwkv6_layer_specs.py:512-536
  */
@@ -124,6 +126,39 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
                   int param_dtype, const void* const* d_mixed, const void* d_xxx, void* dx,
                   void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * LoRA up-projections fused with their consumers (RWKV6Bottleneck.forward,
+ * rwkv6_layer_specs.py:177-195, as used at :446-454).  The caller computes
+ * neck = tanh(input @ W_down) as [N, E*R] bf16 (N = T*B tokens, a hipBLASLt GEMM) and passes
+ * W_up transposed: w_up_t [E, C, R] bf16 (w_up_t[e][c][r] = weight_up[e][r][c]).  R must be a
+ * multiple of 32 (at most 256) and C a multiple of 64.  bias [E, C] in param_dtype.
+ *   ddlerp_lora: E = 5, mixed[e] = x + (shift(x) - x) * (neck_e @ W_up[e] + bias[e]), the five
+ *                mixes written straight to `mixed` (host array of 5 device pointers, [T,B,C])
+ *   lora_bias:   E = 1, out = neck @ W_up[0] + bias[0]  ([N, C]; the decay of :454)
+ * ---------------------------------------------------------------------- */
+int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
+                          int param_dtype, void* const* mixed, int64_t T, int64_t B, int64_t C,
+                          int64_t R, void* stream);
+int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, int param_dtype,
+                        void* out, int64_t N, int64_t C, int64_t R, void* stream);
+/* Backward of rwkv6_ddlerp_lora_fwd for d_mixed (5 device pointers, [T,B,C] bf16):
+ *   d_mexp [5,N,C] bf16 = d_mixed * (shift(x) - x)   (the LoRA up-projection's output gradient)
+ *   d_delta_part [N,C] f32 = sum_e d_mixed_e (m_e + bias_e),   d_sum [N,C] f32 = sum_e d_mixed_e
+ *   d_bias [5,C] (param_dtype).  m is recomputed on MFMA from neck and w_up_t. */
+size_t rwkv6_ddlerp_lora_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
+int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
+                          int param_dtype, const void* const* d_mixed, void* d_mexp,
+                          float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
+                          int64_t T, int64_t B, int64_t C, int64_t R, void* stream);
+/* Input gradient of the time-mix token mixing given d_xxx [T,B,C] bf16 (the gradient of
+ * xxx = x + (shift(x) - x) * maa, :443-444, from the LoRA down-projection) and the two sums of
+ * rwkv6_ddlerp_lora_bwd:  d_delta = d_delta_part + d_xxx * maa,
+ * dx = d_sum + d_xxx - d_delta + shift^T(d_delta) -> dx [T,B,C] bf16, d_maa [C] (param_dtype). */
+size_t rwkv6_shift_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
+int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const float* d_delta_part,
+                         const float* d_sum, const void* d_xxx, void* dx, void* d_maa,
+                         void* workspace, int64_t T, int64_t B, int64_t C, void* stream);
 
 /* ------------------------------------------------------------------------
  * Channel mix (RWKV6ChannelMix.forward, rwkv6_layer_specs.py:512-536), [T,B,C] bf16.

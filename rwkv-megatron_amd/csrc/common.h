@@ -41,6 +41,35 @@ __device__ __forceinline__ void unpack4(uint2 q, float* f) {
     f[2] = __uint_as_float(q.y << 16); f[3] = __uint_as_float(q.y & 0xffff0000u);
 }
 
+// The mixes are separate [T,B,C] tensors (each one the input or input-gradient of its own
+// projection); kernels receive their addresses by value.
+template <int N> struct OutPtrs { uint16_t* p[N]; };
+template <int N> struct InPtrs { const uint16_t* p[N]; };
+
+// 8 consecutive bf16 <-> fp32 through one 16-byte access.
+__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
+    unpack8(*reinterpret_cast<const uint4*>(p), f);
+}
+__device__ __forceinline__ void store8(uint16_t* p, const float* f) {
+    uint4 q;
+    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+    *reinterpret_cast<uint4*>(p) = q;
+}
+// 8 consecutive parameters (RWKV6_BF16 or RWKV6_F32, the codes of rwkv6_amd.h) as fp32.
+__device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {
+    if (dtype == 1) {
+        load8(reinterpret_cast<const uint16_t*>(p) + off, f);
+    } else {
+        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
+        float4 a = q[0], b = q[1];
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    }
+}
+
 // Splits fp32 values into bf16 hi + lo parts (hi + lo carries ~16 mantissa bits):
 // an MFMA against both parts keeps operand rounding out of cancelling sums.
 template <int N>

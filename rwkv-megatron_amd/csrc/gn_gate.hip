@@ -18,27 +18,6 @@
 
 namespace {
 
-__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
-    unpack8(*reinterpret_cast<const uint4*>(p), f);
-}
-__device__ __forceinline__ void store8(uint16_t* p, const float* f) {
-    uint4 q;
-    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
-    *reinterpret_cast<uint4*>(p) = q;
-}
-__device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {
-    if (dtype == RWKV6_BF16) {
-        load8(reinterpret_cast<const uint16_t*>(p) + off, f);
-    } else {
-        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
-        float4 a = q[0], b = q[1];
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    }
-}
 __device__ __forceinline__ float sum8lanes(float v) {
     v += __shfl_xor(v, 1);
     v += __shfl_xor(v, 2);

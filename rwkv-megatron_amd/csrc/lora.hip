@@ -1,0 +1,400 @@
+// The LoRA bottlenecks of RWKV6TimeMix fused with what consumes their output, for MI355X
+// (gfx950).  Sequence-first [T,B,C] bf16, N = T*B tokens.
+//
+// Reference (/root/reference/rwkv_megatron/rwkv6_layer_specs.py):
+//   bottleneck(x) = tanh(x W_down) W_up + bias          :177-195 (W_up [E,R,C], bias [E,C])
+//   token shift:  E = 5, R = 32, m = bottleneck(xxx)     :364-369, :446
+//                 mixed_e = x + (shift(x) - x) * m_e     :447-452
+//   decay:        E = 1, R = 64, decay = bottleneck(mixed_w)  :370-375, :454
+// The down-projection and tanh stay a hipBLASLt GEMM (N x C x E*R, output ~5 MB).  The
+// up-projection is a K = R contraction whose [E,N,C] output is the big tensor, so it is
+// computed here on MFMA and consumed in registers:
+//   rwkv6_ddlerp_lora_fwd  writes the five mixes directly (no m round trip through HBM);
+//   rwkv6_lora_bias_fwd    writes decay = m + bias;
+//   rwkv6_ddlerp_lora_bwd  recomputes m and writes d_mexp = d_mixed * delta (the LoRA GEMMs'
+//                          input), d_delta_part = sum_e d_mixed_e (m_e + bias_e),
+//                          d_sum = sum_e d_mixed_e and d_bias partials;
+//   rwkv6_shift_lerp_bwd   finishes dx and d_maa from those and d_xxx.
+//
+// Up-projection tile: a wave owns 16 tokens x 64 channels.  MFMA 16x16x32 with
+//   A = W_up^T rows (channels, k = rank), B = neck rows (tokens, k = rank),
+// so D[channel][token]; lane (q, L) loads A row L of channel tile tc from channel
+// c0 + 16 (L >> 2) + 4 tc + (L & 3), which leaves lane (q, L) holding channels
+// c0 + 16 q + 0..15 of token L across its four tiles: 32 contiguous bytes per lane, 128 per
+// token row, for every load and store of the epilogue.
+#include "common.h"
+#include "../../include/rwkv6_amd.h"
+
+#define LORA_THR 256      // 4 waves: 64 tokens x 64 channels per block
+#define LORA_NE 5
+
+namespace {
+
+// 16 consecutive bf16 as fp32 (two 16-byte loads); zeros when !valid
+__device__ __forceinline__ void load16(const uint16_t* p, bool valid, float* f) {
+    if (valid) {
+        load8(p, f);
+        load8(p + 8, f + 8);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) f[j] = 0.f;
+    }
+}
+__device__ __forceinline__ void store16(uint16_t* p, const float* f) {
+    store8(p, f);
+    store8(p + 8, f + 8);
+}
+__device__ __forceinline__ void load_param16(const void* p, int pdt, int64_t off, float* f) {
+    load_param8(p, pdt, off, f);
+    load_param8(p, pdt, off + 8, f + 8);
+}
+
+// m[j] = sum_r neck[tok][e*R + r] * W_up[e][r][c0 + 16q + j], j = 0..15 (see the header)
+__device__ __forceinline__ void lora_up(const uint16_t* __restrict__ neck, int64_t ldn,
+                                        const uint16_t* __restrict__ wut, int64_t C, int R, int e,
+                                        int64_t tok, bool tv, int64_t c0, float* m) {
+    const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
+    f32x4 acc[4] = {};
+    for (int ks = 0; ks < R / 32; ++ks) {
+        const int r0 = 32 * ks + 8 * q;
+        const bf16x8 b = tv ? ld_bf16x8(neck + tok * ldn + (int64_t)e * R + r0)
+                            : __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) {
+            const int64_t ch = c0 + 16 * (L >> 2) + 4 * tc + (L & 3);
+            acc[tc] = mfma32(ld_bf16x8(wut + ((int64_t)e * C + ch) * R + r0), b, acc[tc]);
+        }
+    }
+#pragma unroll
+    for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) m[4 * tc + rr] = acc[tc][rr];
+}
+
+}  // namespace
+
+// LERP: out_e = x + (shift(x) - x) * (m_e + bias_e)  (E = 5);  else out_0 = m_0 + bias_0.
+template <int E, bool LERP>
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
+                     const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
+                     OutPtrs<E> out, int64_t N, int64_t B, int64_t C, int R) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
+    const int64_t tok = (int64_t)blockIdx.x * 64 + 16 * wv + L;
+    const int64_t c0 = (int64_t)blockIdx.y * 64, cq = c0 + 16 * q;
+    const bool tv = tok < N;
+    float xv[16], dl[16];
+    if (LERP) {
+        load16(x + tok * C + cq, tv, xv);
+        load16(x + (tok - B) * C + cq, tv && tok >= B, dl);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dl[j] -= xv[j];
+    }
+    for (int e = 0; e < E; ++e) {
+        float m[16], bb[16], o[16];
+        lora_up(neck, (int64_t)E * R, wut, C, R, e, tok, tv, c0, m);
+        load_param16(bias, pdt, (int64_t)e * C + cq, bb);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb[j]) : m[j] + bb[j];
+        if (tv) store16(out.p[e] + tok * C + cq, o);
+    }
+}
+
+// Backward of the token-shift LoRA's up-projection + ddlerp (E = 5), per token:
+//   d_mexp_e = d_mixed_e * delta;  dd = sum_e d_mixed_e (m_e + bias_e);  ds = sum_e d_mixed_e
+// and the d_bias partial of this block's 64 tokens: part[blockIdx.x][e][C].
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
+                             const void* __restrict__ bias, int pdt,
+                             const uint16_t* __restrict__ x, InPtrs<LORA_NE> dmix,
+                             uint16_t* __restrict__ dmexp, float* __restrict__ dd_out,
+                             float* __restrict__ ds_out, float* __restrict__ part, int64_t N,
+                             int64_t B, int64_t C, int R) {
+    __shared__ float red[LORA_NE][4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
+    const int64_t tok = (int64_t)blockIdx.x * 64 + 16 * wv + L;
+    const int64_t c0 = (int64_t)blockIdx.y * 64, cq = c0 + 16 * q;
+    const bool tv = tok < N;
+    float xv[16], dl[16], dd[16], ds[16];
+    load16(x + tok * C + cq, tv, xv);
+    load16(x + (tok - B) * C + cq, tv && tok >= B, dl);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        dl[j] -= xv[j];
+        dd[j] = ds[j] = 0.f;
+    }
+    for (int e = 0; e < LORA_NE; ++e) {
+        float m[16], bb[16], g[16], dm[16];
+        lora_up(neck, (int64_t)LORA_NE * R, wut, C, R, e, tok, tv, c0, m);
+        load_param16(bias, pdt, (int64_t)e * C + cq, bb);
+        load16(dmix.p[e] + tok * C + cq, tv, g);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            dm[j] = g[j] * dl[j];
+            dd[j] += g[j] * (m[j] + bb[j]);
+            ds[j] += g[j];
+        }
+        if (tv) store16(dmexp + ((int64_t)e * N + tok) * C + cq, dm);
+        // d_bias: sum over the wave's 16 tokens (lanes L of one q), fixed butterfly order
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float v = dm[j];
+            v += __shfl_xor(v, 1);
+            v += __shfl_xor(v, 2);
+            v += __shfl_xor(v, 4);
+            v += __shfl_xor(v, 8);
+            dm[j] = v;
+        }
+        if (L == 0) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) red[e][wv][16 * q + j] = dm[j];
+        }
+    }
+    if (tv) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            *reinterpret_cast<float4*>(dd_out + tok * C + cq + 4 * v) =
+                make_float4(dd[4 * v], dd[4 * v + 1], dd[4 * v + 2], dd[4 * v + 3]);
+            *reinterpret_cast<float4*>(ds_out + tok * C + cq + 4 * v) =
+                make_float4(ds[4 * v], ds[4 * v + 1], ds[4 * v + 2], ds[4 * v + 3]);
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < LORA_NE * 64; j += LORA_THR) {
+        const int e = j >> 6, c = j & 63;
+        const float s = (red[e][0][c] + red[e][1][c]) + (red[e][2][c] + red[e][3][c]);
+        part[((int64_t)blockIdx.x * LORA_NE + e) * C + c0 + c] = s;
+    }
+}
+
+// Backward of xxx = x + (shift(x) - x) * maa together with the rest of the input gradient:
+//   d_delta[t] = dd[t] + d_xxx[t] maa,   dx[t] = ds[t] + d_xxx[t] - d_delta[t] + d_delta[t+1]
+//   d_maa partial = sum_t d_xxx[t] (x[t-1] - x[t])  -> part[tblk * B + b][C]
+// Block = 8 token sub-segments x 32 channel groups (8 channels each) over 64 tokens of one
+// batch row; a thread walks its 8 tokens backwards carrying d_delta[t+1].
+#define SLB_TB 64
+#define SLB_SS 8
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa, int pdt,
+                            const float* __restrict__ dd, const float* __restrict__ ds,
+                            const uint16_t* __restrict__ dxxx, uint16_t* __restrict__ dx,
+                            float* __restrict__ part, int64_t T, int64_t B, int64_t C) {
+    __shared__ float red[SLB_SS][32 * 8 + 4];
+    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
+    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
+    const int64_t b = blockIdx.z;
+    const int64_t t_lo = (int64_t)blockIdx.x * SLB_TB + SLB_SS * ss;
+    const int64_t t_hi = t_lo + SLB_SS < T ? t_lo + SLB_SS : T;
+    float acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc[s] = 0.f;
+    if (cg < C8 && t_lo < T) {
+        float mv[8], nd[8], xv[8];
+        load_param8(maa, pdt, 8 * cg, mv);
+        // d_delta of the token after the segment
+        if (t_hi < T) {
+            const int64_t off = (t_hi * B + b) * C + 8 * cg;
+            float g[8], dxx[8];
+            load8(dxxx + off, dxx);
+            const float4 d0 = *reinterpret_cast<const float4*>(dd + off);
+            const float4 d1 = *reinterpret_cast<const float4*>(dd + off + 4);
+            g[0] = d0.x; g[1] = d0.y; g[2] = d0.z; g[3] = d0.w;
+            g[4] = d1.x; g[5] = d1.y; g[6] = d1.z; g[7] = d1.w;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = g[s] + dxx[s] * mv[s];
+        } else {
+#pragma unroll
+            for (int s = 0; s < 8; ++s) nd[s] = 0.f;
+        }
+        load8(x + ((t_hi - 1) * B + b) * C + 8 * cg, xv);
+        for (int64_t t = t_hi - 1; t >= t_lo; --t) {
+            const int64_t off = (t * B + b) * C + 8 * cg;
+            float xp[8], dxx[8], ddv[8], dsv[8], out[8];
+            if (t > 0) load8(x + off - B * C, xp);
+            else for (int s = 0; s < 8; ++s) xp[s] = 0.f;
+            load8(dxxx + off, dxx);
+            {
+                const float4 a0 = *reinterpret_cast<const float4*>(dd + off);
+                const float4 a1 = *reinterpret_cast<const float4*>(dd + off + 4);
+                const float4 b0 = *reinterpret_cast<const float4*>(ds + off);
+                const float4 b1 = *reinterpret_cast<const float4*>(ds + off + 4);
+                ddv[0] = a0.x; ddv[1] = a0.y; ddv[2] = a0.z; ddv[3] = a0.w;
+                ddv[4] = a1.x; ddv[5] = a1.y; ddv[6] = a1.z; ddv[7] = a1.w;
+                dsv[0] = b0.x; dsv[1] = b0.y; dsv[2] = b0.z; dsv[3] = b0.w;
+                dsv[4] = b1.x; dsv[5] = b1.y; dsv[6] = b1.z; dsv[7] = b1.w;
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const float dlt = ddv[s] + dxx[s] * mv[s];
+                out[s] = dsv[s] + dxx[s] - dlt + nd[s];
+                nd[s] = dlt;
+                acc[s] += dxx[s] * (xp[s] - xv[s]);
+                xv[s] = xp[s];
+            }
+            store8(dx + off, out);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) red[ss][8 * cgl + s] = acc[s];
+    __syncthreads();
+    const int64_t P_row = (int64_t)blockIdx.x * B + b;
+    for (int c = threadIdx.x; c < 256; c += LORA_THR) {
+        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
+        if (ch >= C) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < SLB_SS; ++q) sum += red[q][c];
+        part[P_row * C + ch] = sum;
+    }
+}
+
+// out[n] = sum_p part[p][n] (n < Nn) in param dtype: thread (q, n) sums rows p = q mod 8, then
+// a fixed-order combine of the 8 partials (deterministic).
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_lora_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
+                      void* __restrict__ out) {
+    __shared__ float acc8[8][32];
+    const int q = threadIdx.x >> 5, nl = threadIdx.x & 31;
+    const int64_t n = (int64_t)blockIdx.x * 32 + nl;
+    float acc = 0.f;
+    if (n < Nn) {
+#pragma unroll 4
+        for (int64_t p = q; p < P; p += 8) acc += part[p * Nn + n];
+    }
+    acc8[q][nl] = acc;
+    __syncthreads();
+    if (q == 0 && n < Nn) {
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tot += acc8[j][nl];
+        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(out)[n] = f2bf(tot);
+        else reinterpret_cast<float*>(out)[n] = tot;
+    }
+}
+
+namespace {
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int launch_status() { return hipGetLastError() == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH; }
+inline int lora_check(int64_t N, int64_t C, int64_t R, int pdt) {
+    if (N < 0 || C < 1 || R < 1) return RWKV6_ERR_INVALID_ARG;
+    if (C % 64 || R % 32 || R > 256) return RWKV6_ERR_UNSUPPORTED;
+    if (pdt != RWKV6_F32 && pdt != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
+    return RWKV6_OK;
+}
+template <typename P, int NP>
+inline int gather(const void* const* src, P& dst) {
+    if (!src) return RWKV6_ERR_INVALID_ARG;
+    for (int e = 0; e < NP; ++e) {
+        if (!src[e]) return RWKV6_ERR_INVALID_ARG;
+        if (!al16(src[e])) return RWKV6_ERR_ALIGNMENT;
+        dst.p[e] = (decltype(dst.p[0]))src[e];
+    }
+    return RWKV6_OK;
+}
+inline dim3 up_grid(int64_t N, int64_t C) {
+    return dim3((unsigned)((N + 63) / 64), (unsigned)(C / 64));
+}
+}  // namespace
+
+extern "C" {
+
+int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
+                          int param_dtype, void* const* mixed, int64_t T, int64_t B, int64_t C,
+                          int64_t R, void* stream) {
+    if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
+    int st = lora_check(T * B, C, R, param_dtype);
+    if (st) return st;
+    if (T == 0) return RWKV6_OK;
+    if (!x || !neck || !w_up_t || !bias) return RWKV6_ERR_INVALID_ARG;
+    OutPtrs<LORA_NE> out;
+    if ((st = gather<OutPtrs<LORA_NE>, LORA_NE>((const void* const*)mixed, out))) return st;
+    if (!al16(x) || !al16(neck) || !al16(w_up_t) || !al16(bias)) return RWKV6_ERR_ALIGNMENT;
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true>), up_grid(T * B, C), dim3(LORA_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
+                       (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, T * B,
+                       B, C, (int)R);
+    return launch_status();
+}
+
+int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, int param_dtype,
+                        void* out, int64_t N, int64_t C, int64_t R, void* stream) {
+    int st = lora_check(N, C, R, param_dtype);
+    if (st) return st;
+    if (N == 0) return RWKV6_OK;
+    if (!neck || !w_up_t || !bias || !out) return RWKV6_ERR_INVALID_ARG;
+    if (!al16(neck) || !al16(w_up_t) || !al16(bias) || !al16(out)) return RWKV6_ERR_ALIGNMENT;
+    OutPtrs<1> o;
+    o.p[0] = (uint16_t*)out;
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
+                       (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o, N,
+                       (int64_t)1, C, (int)R);
+    return launch_status();
+}
+
+size_t rwkv6_ddlerp_lora_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
+    if (T < 0 || B < 1 || C < 1) return 0;
+    const int64_t nb = (T * B + 63) / 64;
+    return (size_t)((nb > 0 ? nb : 1) * LORA_NE * C) * sizeof(float);
+}
+
+int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
+                          int param_dtype, const void* const* d_mixed, void* d_mexp,
+                          float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
+                          int64_t T, int64_t B, int64_t C, int64_t R, void* stream) {
+    if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
+    int st = lora_check(T * B, C, R, param_dtype);
+    if (st) return st;
+    if (!bias || !d_bias || !workspace ||
+        (T > 0 && (!x || !neck || !w_up_t || !d_mexp || !d_delta_part || !d_sum)))
+        return RWKV6_ERR_INVALID_ARG;
+    InPtrs<LORA_NE> dm{};
+    if (T > 0 && (st = gather<InPtrs<LORA_NE>, LORA_NE>(d_mixed, dm))) return st;
+    if (!al16(x) || !al16(neck) || !al16(w_up_t) || !al16(bias) || !al16(d_mexp) ||
+        !al16(d_delta_part) || !al16(d_sum) || !al16(workspace))
+        return RWKV6_ERR_ALIGNMENT;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t N = T * B, nb = (N + 63) / 64;
+    float* part = reinterpret_cast<float*>(workspace);
+    if (N > 0)
+        hipLaunchKernelGGL(rwkv6_ddlerp_lora_bwd_kernel, up_grid(N, C), dim3(LORA_THR), 0, s,
+                           (const uint16_t*)neck, (const uint16_t*)w_up_t, bias, param_dtype,
+                           (const uint16_t*)x, dm, (uint16_t*)d_mexp, d_delta_part, d_sum, part, N,
+                           B, C, (int)R);
+    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((LORA_NE * C + 31) / 32)),
+                       dim3(LORA_THR), 0, s, part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias);
+    return launch_status();
+}
+
+size_t rwkv6_shift_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
+    if (T < 0 || B < 1 || C < 1) return 0;
+    const int64_t ntb = (T + SLB_TB - 1) / SLB_TB;
+    return (size_t)((ntb > 0 ? ntb : 1) * B * C) * sizeof(float);
+}
+
+int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const float* d_delta_part,
+                         const float* d_sum, const void* d_xxx, void* dx, void* d_maa,
+                         void* workspace, int64_t T, int64_t B, int64_t C, void* stream) {
+    if (T < 0 || B < 1 || C < 8) return RWKV6_ERR_INVALID_ARG;
+    if (C % 8) return RWKV6_ERR_UNSUPPORTED;
+    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
+    if (param_dtype != RWKV6_F32 && param_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
+    if (!maa || !d_maa || !workspace || (T > 0 && (!x || !d_delta_part || !d_sum || !d_xxx || !dx)))
+        return RWKV6_ERR_INVALID_ARG;
+    if (!al16(x) || !al16(maa) || !al16(d_delta_part) || !al16(d_sum) || !al16(d_xxx) ||
+        !al16(dx) || !al16(workspace))
+        return RWKV6_ERR_ALIGNMENT;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t ntb = (T + SLB_TB - 1) / SLB_TB;
+    float* part = reinterpret_cast<float*>(workspace);
+    if (T > 0)
+        hipLaunchKernelGGL(rwkv6_shift_lerp_bwd_kernel,
+                           dim3((unsigned)ntb, (unsigned)((C / 8 + 31) / 32), (unsigned)B),
+                           dim3(LORA_THR), 0, s, (const uint16_t*)x, maa, param_dtype, d_delta_part,
+                           d_sum, (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
+    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(LORA_THR), 0, s,
+                       part, T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
+    return launch_status();
+}
+
+}  // extern "C"

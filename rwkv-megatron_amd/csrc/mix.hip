@@ -28,37 +28,6 @@
 #define MIX_NE 5          // number of data-dependent mixes (w,k,v,r,g)
 #define MIX_THR 256
 
-// The mixes are separate [T,B,C] tensors (each one the input or input-gradient of its own
-// projection); kernels receive their addresses by value.
-template <int N> struct OutPtrs { uint16_t* p[N]; };
-template <int N> struct InPtrs { const uint16_t* p[N]; };
-
-namespace {
-
-__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
-    unpack8(*reinterpret_cast<const uint4*>(p), f);
-}
-__device__ __forceinline__ void store8(uint16_t* p, const float* f) {
-    uint4 q;
-    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
-    *reinterpret_cast<uint4*>(p) = q;
-}
-__device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {
-    if (dtype == RWKV6_BF16) {
-        load8(reinterpret_cast<const uint16_t*>(p) + off, f);
-    } else {
-        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
-        float4 a = q[0], b = q[1];
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    }
-}
-
-}  // namespace
-
 // xxx = x + (shift(x) - x) * maa
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_shift_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa, int pdt,

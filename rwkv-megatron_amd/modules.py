@@ -5,8 +5,9 @@ Same class names, constructor/forward contracts and parameter names/shapes as
 way (Megatron's module prefix aside).  The hot path runs on the HIP kernels:
 
   RWKV6TimeMix.forward  (:431-468)
-    token shift + lerp + LoRA + ddlerp   -> timemix.token_shift_mix   (HIP + hipBLASLt)
-    decay LoRA, r/k/v/gate projections   -> torch.matmul (hipBLASLt)
+    token shift + lerp + LoRA + ddlerp   -> timemix.token_shift_mix   (HIP + HIP MFMA + hipBLASLt)
+    decay LoRA                           -> timemix.decay_lora        (hipBLASLt + HIP MFMA)
+    r/k/v/gate projections               -> torch.matmul (hipBLASLt)
     WKV6 (incl. -exp(decay), layout)     -> wkv.wkv6_seqfirst         (HIP, sequence-first entry)
     GroupNorm * silu(gate)               -> timemix.group_norm_gate   (HIP, head-first read)
     output projection                    -> torch.matmul
@@ -180,7 +181,8 @@ class RWKV6TimeMix(nn.Module):
         ts = self.bottleneck_token_shift
         mixed_decay, mixed_key, mixed_value, mixed_receptance, mixed_gate = timemix.token_shift_mix(
             x, self.mix_coeff_input, ts.weight_down, ts.weight_up, ts.bias)
-        decay = self.bottleneck_decay(mixed_decay).squeeze(-2)
+        bd = self.bottleneck_decay
+        decay = timemix.decay_lora(mixed_decay, bd.weight_down, bd.weight_up, bd.bias)
         key = self.linear_key(mixed_key)[0]
         value = self.linear_value(mixed_value)[0]
         receptance = self.linear_receptance(mixed_receptance)[0]

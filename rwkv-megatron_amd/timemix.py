@@ -2,8 +2,10 @@
 
 * ``token_shift_mix``: token shift + static lerp + LoRA bottleneck + data-dependent
   lerp of RWKV6TimeMix.forward (/root/reference/rwkv_megatron/rwkv6_layer_specs.py
-  :440-452, bottleneck :177-195).  The two elementwise stages are HIP kernels; the
-  LoRA GEMMs run on hipBLASLt through torch.matmul / torch.bmm.
+  :440-452, bottleneck :177-195).  The shift/lerp, the LoRA up-projection fused with
+  the ddlerp (MFMA) and their backwards are HIP kernels; the LoRA down-projection and the
+  weight-gradient GEMMs run on hipBLASLt through torch.matmul / torch.bmm.
+* ``decay_lora``: the decay bottleneck (:454) with its up-projection + bias on MFMA.
 * ``group_norm_gate``: GroupNorm over heads (:90-97, applied at :461-465) times
   silu(gate) (:458, :466), reading the WKV output head-first so the layout copy
   of :341 disappears.
@@ -140,9 +142,25 @@ def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
 # autograd Functions
 # ---------------------------------------------------------------------------
 
+def _wgrad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T @ b for a [N,P], b [N,Q] bf16 with fp32 accumulation, split over N into s batched
+    products (a weight gradient has a small output and a long reduction: one GEMM leaves most
+    CUs idle), the s fp32 partials summed in a fixed order."""
+    N = a.shape[0]
+    s = next(d for d in (8, 4, 2, 1) if N % d == 0)
+    part = torch.bmm(a.reshape(s, N // s, a.shape[1]).transpose(1, 2),
+                     b.reshape(s, N // s, b.shape[1]), out_dtype=torch.float32)
+    return part.sum(0)
+
+
 class _TokenShiftMix(torch.autograd.Function):
     """x [T,B,C] -> five [T,B,C] mixes (w,k,v,r,g); params maa [C], w_down [C,5,R],
-    w_up [5,R,C], bias [5,C] with the shapes of rwkv6_layer_specs.py:126-170, :377-385."""
+    w_up [5,R,C], bias [5,C] with the shapes of rwkv6_layer_specs.py:126-170, :377-385.
+
+    Forward: shift_lerp (HIP) -> neck = tanh(xxx W_down) (hipBLASLt) -> the up-projection,
+    bias and ddlerp in one MFMA kernel writing the five mixes (rwkv6_ddlerp_lora_fwd).
+    Backward: rwkv6_ddlerp_lora_bwd (recomputes the up-projection) -> LoRA GEMMs ->
+    rwkv6_shift_lerp_bwd for dx and d_maa."""
 
     @staticmethod
     def forward(ctx, x, maa, w_down, w_up, bias):
@@ -151,35 +169,100 @@ class _TokenShiftMix(torch.autograd.Function):
         N = T * B
         x = _c(x)
         wd = w_down.to(torch.bfloat16).reshape(C, NE * R)
-        wu = _c(w_up.to(torch.bfloat16))
+        wut = w_up.to(torch.bfloat16).transpose(1, 2).contiguous()             # [5, C, R]
         xxx = shift_lerp(x, maa)
-        neck = torch.tanh(xxx.view(N, C) @ wd)                                  # [N, 5R]
-        neck_t = neck.view(N, NE, R).transpose(0, 1).contiguous()              # [5, N, R]
-        mexp = torch.bmm(neck_t, wu)                                             # [5, N, C]
-        mixed = ddlerp(x, mexp.view(NE, T, B, C), bias)
-        ctx.save_for_backward(x, maa, w_down, w_up, bias, xxx, neck_t, mexp)
+        neck = _c(torch.tanh(xxx.view(N, C) @ wd))                              # [N, 5R]
+        b, pdt = _param(bias)
+        mixed = tuple(torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device) for _ in range(NE))
+        _lib.check(_lib.load().rwkv6_ddlerp_lora_fwd(_p(x), _p(neck), _p(wut), _p(b), pdt, _ptrs(mixed),
+                                                     T, B, C, R, _stream(x.device)),
+                   "rwkv6_ddlerp_lora_fwd")
+        ctx.save_for_backward(x, maa, w_down, w_up, bias, xxx, neck, wut)
         return mixed
 
     @staticmethod
     def backward(ctx, *d_mixed):
-        x, maa, w_down, w_up, bias, xxx, neck_t, mexp = ctx.saved_tensors
+        x, maa, w_down, w_up, bias, xxx, neck, wut = ctx.saved_tensors
         T, B, C = x.shape
         R = w_down.shape[-1]
         N = T * B
+        L = _lib.load()
+        dev = x.device
         d_mixed = [torch.zeros_like(x) if d is None else _c(d.to(torch.bfloat16)) for d in d_mixed]
-        d_mexp, d_bias = ddlerp_bwd(x, d_mixed, bias.dtype)
-        d_mexp = d_mexp.view(NE, N, C)
-        wu = w_up.to(torch.bfloat16)
-        d_w_up = torch.bmm(neck_t.transpose(1, 2).contiguous(), d_mexp)         # [5, R, C]
-        d_neck_t = torch.bmm(d_mexp, wu.transpose(1, 2).contiguous())           # [5, N, R]
+        b, pdt = _param(bias)
+        d_mexp = torch.empty(NE, N, C, dtype=torch.bfloat16, device=dev)
+        dd = torch.empty(N, C, dtype=torch.float32, device=dev)
+        dsum = torch.empty_like(dd)
+        d_bias = torch.empty(NE, C, dtype=b.dtype, device=dev)
+        ws = torch.empty(L.rwkv6_ddlerp_lora_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=dev)
+        _lib.check(L.rwkv6_ddlerp_lora_bwd(_p(x), _p(neck), _p(wut), _p(b), pdt, _ptrs(d_mixed),
+                                           _p(d_mexp), _p(dd), _p(dsum), _p(d_bias), _p(ws), T, B, C,
+                                           R, _stream(dev)), "rwkv6_ddlerp_lora_bwd")
+        neck_t = neck.view(N, NE, R).permute(1, 0, 2).contiguous()              # [5, N, R]
+        s = next(d for d in (8, 4, 2, 1) if N % d == 0)
+        d_w_up = torch.bmm(neck_t.view(NE * s, N // s, R).transpose(1, 2),
+                           d_mexp.view(NE * s, N // s, C),
+                           out_dtype=torch.float32).view(NE, s, R, C).sum(1)    # [5, R, C]
+        d_neck_t = torch.bmm(d_mexp, wut)                                       # [5, N, R]
         d_pre = (d_neck_t.float() * (1.0 - neck_t.float() ** 2)).to(torch.bfloat16)
-        d_pre = d_pre.transpose(0, 1).reshape(N, NE * R)
+        d_pre = d_pre.permute(1, 0, 2).reshape(N, NE * R)
         wd = w_down.to(torch.bfloat16).reshape(C, NE * R)
-        d_w_down = (xxx.view(N, C).t() @ d_pre).view(C, NE, R)
+        d_w_down = _wgrad(xxx.view(N, C), d_pre).view(C, NE, R)
         d_xxx = _c(d_pre @ wd.t())
-        dx, d_maa = mix_bwd(x, maa, mexp.view(NE, T, B, C), bias, d_mixed, d_xxx.view(T, B, C))
+        m, pdt_m = _param(maa)
+        dx = torch.empty_like(x)
+        d_maa = torch.empty(C, dtype=m.dtype, device=dev)
+        ws2 = torch.empty(L.rwkv6_shift_lerp_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=dev)
+        _lib.check(L.rwkv6_shift_lerp_bwd(_p(x), _p(m), pdt_m, _p(dd), _p(dsum), _p(d_xxx), _p(dx),
+                                          _p(d_maa), _p(ws2), T, B, C, _stream(dev)),
+                   "rwkv6_shift_lerp_bwd")
         return (dx, d_maa.to(maa.dtype), d_w_down.to(w_down.dtype), d_w_up.to(w_up.dtype),
                 d_bias.to(bias.dtype))
+
+
+class _DecayLora(torch.autograd.Function):
+    """decay = tanh(x W_down) W_up + bias for the decay bottleneck (E = 1,
+    rwkv6_layer_specs.py:370-375, :454): W_down [C,1,R], W_up [1,R,C], bias [1,C] -> [T,B,C].
+    The up-projection and bias run in one MFMA kernel (rwkv6_lora_bias_fwd)."""
+
+    @staticmethod
+    def forward(ctx, x, w_down, w_up, bias):
+        T, B, C = x.shape
+        R = w_down.shape[-1]
+        N = T * B
+        x = _c(x)
+        wd = w_down.to(torch.bfloat16).reshape(C, R)
+        wut = w_up.to(torch.bfloat16).transpose(1, 2).contiguous()             # [1, C, R]
+        neck = _c(torch.tanh(x.view(N, C) @ wd))                                # [N, R]
+        b, pdt = _param(bias)
+        out = torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device)
+        _lib.check(_lib.load().rwkv6_lora_bias_fwd(_p(neck), _p(wut), _p(b), pdt, _p(out), N, C, R,
+                                                   _stream(x.device)), "rwkv6_lora_bias_fwd")
+        ctx.save_for_backward(x, w_down, w_up, bias, neck, wut)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        x, w_down, w_up, bias, neck, wut = ctx.saved_tensors
+        T, B, C = x.shape
+        R = w_down.shape[-1]
+        N = T * B
+        g = _c(d_out.to(torch.bfloat16)).view(N, C)
+        d_bias = g.float().sum(0, keepdim=True)
+        d_w_up = _wgrad(neck, g).view(1, R, C)
+        d_pre = ((g @ wut[0]).float() * (1.0 - neck.float() ** 2)).to(torch.bfloat16)
+        d_w_down = _wgrad(x.view(N, C), d_pre).view(C, 1, R)
+        wd = w_down.to(torch.bfloat16).reshape(C, R)
+        dx = (d_pre @ wd.t()).view(T, B, C)
+        return dx, d_w_down.to(w_down.dtype), d_w_up.to(w_up.dtype), d_bias.to(bias.dtype)
+
+
+def decay_lora(x, w_down, w_up, bias):
+    """The decay bottleneck of RWKV6TimeMix (:454): tanh(x W_down) W_up + bias, [T,B,C] bf16."""
+    _check_act("x", x, 3)
+    if w_down.dim() != 3 or w_down.shape[1] != 1:
+        raise ValueError("decay_lora expects the E = 1 bottleneck (w_down [C,1,R])")
+    return _DecayLora.apply(x, w_down, w_up, bias)
 
 
 def token_shift_mix(x, maa, w_down, w_up, bias):

@@ -3,7 +3,8 @@ against the numpy oracle on identical bf16 inputs.
 
 Tolerance: max|gpu - oracle| / max|oracle| <= 1e-2 and relative L2 <= 1e-2 for the
 elementwise kernels (their only rounding is the bf16 store); the LoRA weight
-gradients go through bf16 hipBLASLt GEMMs and use 2e-2.
+gradients and the decay bottleneck's input gradient go through bf16 hipBLASLt GEMMs and
+use 2e-2.
 """
 import numpy as np
 import pytest
@@ -52,15 +53,17 @@ def test_shift_lerp_and_ddlerp(pkg, shape, pdt):
     _check("mixed", _n(mixed), orc.ddlerp_fwd(_n(x), np.moveaxis(_n(mexp), 0, 2), _n(bias)))
 
 
-@pytest.mark.parametrize("T,B,C", [(5, 2, 64), (70, 3, 256)])
-def test_token_shift_mix_forward_backward(pkg, T, B, C):
+# N = T*B = 10 (a partial 64-token tile), 210 and 520 (several tiles, C > 64)
+@pytest.mark.parametrize("T,B,C,pdt", [(5, 2, 64, torch.float32), (70, 3, 256, torch.float32),
+                                       (130, 4, 192, torch.bfloat16)])
+def test_token_shift_mix_forward_backward(pkg, T, B, C, pdt):
     R = 32
     g = torch.Generator().manual_seed(C)
     x = _bf(torch.randn(T, B, C, generator=g))
-    maa = torch.rand(C, generator=g)
+    maa = torch.rand(C, generator=g).to(pdt)
     wd = torch.empty(C, 5, R).uniform_(-0.1, 0.1, generator=g)
     wu = torch.empty(5, R, C).uniform_(-0.1, 0.1, generator=g)
-    bias = torch.empty(5, C).uniform_(-1, 1, generator=g)
+    bias = torch.empty(5, C).uniform_(-1, 1, generator=g).to(pdt)
     dmix = _bf(torch.randn(5, T, B, C, generator=g))
     # the GEMMs run in bf16: give the oracle the same bf16-rounded weights
     wd_b, wu_b = _bf(wd), _bf(wu)
@@ -84,6 +87,28 @@ def test_token_shift_mix_forward_backward(pkg, T, B, C):
     _check("d_w_down", _n(leaves[2].grad), d_wd, 2e-2)
     _check("d_w_up", _n(leaves[3].grad), d_wu, 2e-2)
     _check("d_bias", _n(leaves[4].grad), d_bias)
+
+
+@pytest.mark.parametrize("T,B,C,R", [(5, 2, 64, 64), (70, 3, 256, 64), (33, 2, 128, 32)])
+def test_decay_lora_forward_backward(pkg, T, B, C, R):
+    """The decay bottleneck (E = 1): tanh(x W_down) W_up + bias with the fused up-projection."""
+    g = torch.Generator().manual_seed(T + R)
+    x = _bf(torch.randn(T, B, C, generator=g))
+    wd = _bf(torch.empty(C, 1, R).uniform_(-0.1, 0.1, generator=g))
+    wu = _bf(torch.empty(1, R, C).uniform_(-0.3, 0.3, generator=g))
+    bias = torch.empty(1, C).uniform_(-6, -1, generator=g)
+    dy = _bf(torch.randn(T, B, C, generator=g))
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x, wd, wu, bias)]
+    out = pkg.timemix.decay_lora(*leaves)
+    (out.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    xn, wdn, wun, bn = (_n(t) for t in (x, wd, wu, bias))
+    _check("decay", _n(out), orc.bottleneck_fwd(xn, wdn, wun, bn)[:, :, 0])
+    dx, d_wd, d_wu, d_b = orc.bottleneck_bwd(xn, wdn, wun, _n(dy)[:, :, None])
+    _check("dx", _n(leaves[0].grad), dx, 2e-2)
+    _check("d_w_down", _n(leaves[1].grad), d_wd, 2e-2)
+    _check("d_w_up", _n(leaves[2].grad), d_wu, 2e-2)
+    _check("d_bias", _n(leaves[3].grad), d_b)
 
 
 @pytest.mark.parametrize("head_first", [True, False])
