@@ -132,7 +132,8 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
  * rwkv6_layer_specs.py:177-195, as used at :446-454).  The caller computes
  * neck = tanh(input @ W_down) as [N, E*R] bf16 (N = T*B tokens, a hipBLASLt GEMM) and passes
  * W_up transposed: w_up_t [E, C, R] bf16 (w_up_t[e][c][r] = weight_up[e][r][c]).  R must be a
- * multiple of 32 (at most 256) and C a multiple of 64.  bias [E, C] in param_dtype.
+ * multiple of 32 (E = 5: R = 32; E = 1: R <= 128) and C a multiple of 64.  bias [E, C] in
+ * param_dtype.
  *   ddlerp_lora: E = 5, mixed[e] = x + (shift(x) - x) * (neck_e @ W_up[e] + bias[e]), the five
  *                mixes written straight to `mixed` (host array of 5 device pointers, [T,B,C])
  *   lora_bias:   E = 1, out = neck @ W_up[0] + bias[0]  ([N, C]; the decay of :454)

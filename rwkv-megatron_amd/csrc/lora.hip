@@ -18,52 +18,95 @@
 //
 // Up-projection tile: a wave owns 16 tokens x 64 channels.  MFMA 16x16x32 with
 //   A = W_up^T rows (channels, k = rank), B = neck rows (tokens, k = rank),
-// so D[channel][token]; lane (q, L) loads A row L of channel tile tc from channel
-// c0 + 16 (L >> 2) + 4 tc + (L & 3), which leaves lane (q, L) holding channels
-// c0 + 16 q + 0..15 of token L across its four tiles: 32 contiguous bytes per lane, 128 per
-// token row, for every load and store of the epilogue.
+// so D[channel][token]; the A rows are permuted (tile_channel) so that lane (q, L) ends up
+// holding two runs of 8 channels, c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7), of token L:
+// every 16-byte load or store instruction of the epilogue covers 64 contiguous bytes of
+// each of the wave's 16 token rows.  Operands are staged in LDS once per block.
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
-#define LORA_THR 256      // 4 waves: 64 tokens x 64 channels per block
+#define LORA_THR 256      // 4 waves, each 16 tokens x 64 channels at a time
+#define LORA_TT 128       // tokens per block (64-token groups walked in turn)
 #define LORA_NE 5
 
 namespace {
 
-// 16 consecutive bf16 as fp32 (two 16-byte loads); zeros when !valid
-__device__ __forceinline__ void load16(const uint16_t* p, bool valid, float* f) {
+// A lane's 16 values are two runs of 8 channels: c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7),
+// so each 16-byte access instruction of a wave covers 64 contiguous bytes of every token row.
+__device__ __forceinline__ void load16(const uint16_t* row_c0, int q, bool valid, float* f) {
     if (valid) {
-        load8(p, f);
-        load8(p + 8, f + 8);
+        load8(row_c0 + 8 * q, f);
+        load8(row_c0 + 32 + 8 * q, f + 8);
     } else {
 #pragma unroll
         for (int j = 0; j < 16; ++j) f[j] = 0.f;
     }
 }
-__device__ __forceinline__ void store16(uint16_t* p, const float* f) {
-    store8(p, f);
-    store8(p + 8, f + 8);
+__device__ __forceinline__ void store16(uint16_t* row_c0, int q, const float* f) {
+    store8(row_c0 + 8 * q, f);
+    store8(row_c0 + 32 + 8 * q, f + 8);
 }
-__device__ __forceinline__ void load_param16(const void* p, int pdt, int64_t off, float* f) {
-    load_param8(p, pdt, off, f);
-    load_param8(p, pdt, off + 8, f + 8);
+__device__ __forceinline__ void store16f(float* row_c0, int q, const float* f) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+        *reinterpret_cast<float4*>(row_c0 + (v < 2 ? 8 * q + 4 * v : 32 + 8 * q + 4 * (v - 2))) =
+            make_float4(f[4 * v], f[4 * v + 1], f[4 * v + 2], f[4 * v + 3]);
+}
+__device__ __forceinline__ void load_param16(const void* p, int pdt, int64_t off_c0, int q, float* f) {
+    load_param8(p, pdt, off_c0 + 8 * q, f);
+    load_param8(p, pdt, off_c0 + 32 + 8 * q, f + 8);
+}
+// channel (relative to c0) of MFMA tile tc, row 4q' + rr' = L': the run layout above
+__device__ __forceinline__ int tile_channel(int tc, int L) {
+    const int qq = L >> 2, rr = L & 3;
+    return tc < 2 ? 8 * qq + 4 * tc + rr : 32 + 8 * qq + 4 * (tc - 2) + rr;
 }
 
-// m[j] = sum_r neck[tok][e*R + r] * W_up[e][r][c0 + 16q + j], j = 0..15 (see the header)
-__device__ __forceinline__ void lora_up(const uint16_t* __restrict__ neck, int64_t ldn,
-                                        const uint16_t* __restrict__ wut, int64_t C, int R, int e,
-                                        int64_t tok, bool tv, int64_t c0, float* m) {
+// Blocks are dispatched round-robin over the 8 XCDs: XCD x gets the token blocks
+// [x*per, (x+1)*per) (all channel blocks of each, consecutively), so its L2 holds one
+// eighth of neck.  The grid is 8 * per * nCB; blocks past the last token block exit.
+__device__ __forceinline__ bool lora_tile(int64_t nTB, int64_t nCB, int64_t per, int64_t& tb,
+                                          int64_t& cb) {
+    const int64_t id = blockIdx.x, xcd = id & 7, j = id >> 3;
+    tb = xcd * per + j / nCB;
+    cb = j - (j / nCB) * nCB;
+    return tb < nTB;
+}
+
+// Block operand staging: the 64 channel rows of W_up^T (all E mixes), shared by every token
+// of the block, go to LDS once per block, rows padded by 8 elements so the 16 rows a wave
+// reads with 16-byte loads fall on distinct banks.  The neck operand is per token (one lane's
+// own row) and is read straight from global memory.
+__device__ __forceinline__ int lds_rs(int R) { return R + 8; }
+__host__ __device__ __forceinline__ size_t lora_lds_bytes(int E, int R) {
+    return (size_t)E * 64 * (R + 8) * 2;
+}
+
+__device__ __forceinline__ void lora_stage(uint16_t* sw, const uint16_t* __restrict__ wut, int E,
+                                           int64_t C, int R, int64_t c0) {
+    const int rs = lds_rs(R), R8 = R / 8;
+    for (int idx = threadIdx.x; idx < E * 64 * R8; idx += LORA_THR) {
+        const int row = idx / R8, k8 = idx - row * R8;          // row = e*64 + channel
+        const int e = row >> 6, ch = row & 63;
+        *reinterpret_cast<uint4*>(sw + row * rs + 8 * k8) =
+            *reinterpret_cast<const uint4*>(wut + ((int64_t)e * C + c0 + ch) * R + 8 * k8);
+    }
+}
+
+// m[j] = sum_r neck[tok][e*R + r] * W_up[e][r][c], c the lane's j-th channel (run layout).
+__device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __restrict__ neck_row,
+                                        bool tv, int R, int e, float* m) {
     const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
+    const int rs = lds_rs(R);
+    const uint16_t* swe = sw + e * 64 * rs;
     f32x4 acc[4] = {};
     for (int ks = 0; ks < R / 32; ++ks) {
         const int r0 = 32 * ks + 8 * q;
-        const bf16x8 b = tv ? ld_bf16x8(neck + tok * ldn + (int64_t)e * R + r0)
+        const bf16x8 b = tv ? ld_bf16x8(neck_row + e * R + r0)
                             : __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
 #pragma unroll
-        for (int tc = 0; tc < 4; ++tc) {
-            const int64_t ch = c0 + 16 * (L >> 2) + 4 * tc + (L & 3);
-            acc[tc] = mfma32(ld_bf16x8(wut + ((int64_t)e * C + ch) * R + r0), b, acc[tc]);
-        }
+        for (int tc = 0; tc < 4; ++tc)
+            acc[tc] = mfma32(ld_bf16x8(swe + tile_channel(tc, L) * rs + r0), b, acc[tc]);
     }
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc)
@@ -78,25 +121,33 @@ template <int E, bool LERP>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
-                     OutPtrs<E> out, int64_t N, int64_t B, int64_t C, int R) {
+                     OutPtrs<E> out, int64_t N, int64_t B, int64_t C, int R, int64_t per) {
+    int64_t tb, cb;
+    if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
-    const int64_t tok = (int64_t)blockIdx.x * 64 + 16 * wv + L;
-    const int64_t c0 = (int64_t)blockIdx.y * 64, cq = c0 + 16 * q;
-    const bool tv = tok < N;
-    float xv[16], dl[16];
-    if (LERP) {
-        load16(x + tok * C + cq, tv, xv);
-        load16(x + (tok - B) * C + cq, tv && tok >= B, dl);
+    const int64_t c0 = cb * 64;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
+    lora_stage(lora_sm, wut, E, C, R, c0);
+    __syncthreads();
+    for (int g = 0; g < LORA_TT / 64; ++g) {
+        const int64_t tok = tb * LORA_TT + 64 * g + 16 * wv + L;
+        const bool tv = tok < N;
+        float xv[16], dl[16];
+        if (LERP) {
+            load16(x + tok * C + c0, q, tv, xv);
+            load16(x + (tok - B) * C + c0, q, tv && tok >= B, dl);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) dl[j] -= xv[j];
-    }
-    for (int e = 0; e < E; ++e) {
-        float m[16], bb[16], o[16];
-        lora_up(neck, (int64_t)E * R, wut, C, R, e, tok, tv, c0, m);
-        load_param16(bias, pdt, (int64_t)e * C + cq, bb);
+            for (int j = 0; j < 16; ++j) dl[j] -= xv[j];
+        }
+#pragma unroll 1
+        for (int e = 0; e < E; ++e) {
+            float m[16], bb[16], o[16];
+            lora_up(lora_sm, neck + tok * E * R, tv, R, e, m);
+            load_param16(bias, pdt, (int64_t)e * C + c0, q, bb);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb[j]) : m[j] + bb[j];
-        if (tv) store16(out.p[e] + tok * C + cq, o);
+            for (int j = 0; j < 16; ++j) o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb[j]) : m[j] + bb[j];
+            if (tv) store16(out.p[e] + tok * C + c0, q, o);
+        }
     }
 }
 
@@ -109,61 +160,67 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
                              const uint16_t* __restrict__ x, InPtrs<LORA_NE> dmix,
                              uint16_t* __restrict__ dmexp, float* __restrict__ dd_out,
                              float* __restrict__ ds_out, float* __restrict__ part, int64_t N,
-                             int64_t B, int64_t C, int R) {
+                             int64_t B, int64_t C, int R, int64_t per) {
     __shared__ float red[LORA_NE][4][64];
+    int64_t tb, cb;
+    if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
-    const int64_t tok = (int64_t)blockIdx.x * 64 + 16 * wv + L;
-    const int64_t c0 = (int64_t)blockIdx.y * 64, cq = c0 + 16 * q;
-    const bool tv = tok < N;
-    float xv[16], dl[16], dd[16], ds[16];
-    load16(x + tok * C + cq, tv, xv);
-    load16(x + (tok - B) * C + cq, tv && tok >= B, dl);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        dl[j] -= xv[j];
-        dd[j] = ds[j] = 0.f;
-    }
-    for (int e = 0; e < LORA_NE; ++e) {
-        float m[16], bb[16], g[16], dm[16];
-        lora_up(neck, (int64_t)LORA_NE * R, wut, C, R, e, tok, tv, c0, m);
-        load_param16(bias, pdt, (int64_t)e * C + cq, bb);
-        load16(dmix.p[e] + tok * C + cq, tv, g);
+    const int64_t c0 = cb * 64;
+    extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
+    lora_stage(lora_sm, wut, LORA_NE, C, R, c0);
+    __syncthreads();
+    for (int j = threadIdx.x; j < LORA_NE * 4 * 64; j += LORA_THR) (&red[0][0][0])[j] = 0.f;
+    __syncthreads();
+    for (int g = 0; g < LORA_TT / 64; ++g) {
+        const int64_t tok = tb * LORA_TT + 64 * g + 16 * wv + L;
+        const bool tv = tok < N;
+        float xv[16], dl[16], dd[16], ds[16];
+        load16(x + tok * C + c0, q, tv, xv);
+        load16(x + (tok - B) * C + c0, q, tv && tok >= B, dl);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            dm[j] = g[j] * dl[j];
-            dd[j] += g[j] * (m[j] + bb[j]);
-            ds[j] += g[j];
+            dl[j] -= xv[j];
+            dd[j] = ds[j] = 0.f;
         }
-        if (tv) store16(dmexp + ((int64_t)e * N + tok) * C + cq, dm);
-        // d_bias: sum over the wave's 16 tokens (lanes L of one q), fixed butterfly order
+#pragma unroll 1
+        for (int e = 0; e < LORA_NE; ++e) {
+            float m[16], bb[16], gv[16], dm[16];
+            lora_up(lora_sm, neck + tok * LORA_NE * R, tv, R, e, m);
+            load_param16(bias, pdt, (int64_t)e * C + c0, q, bb);
+            load16(dmix.p[e] + tok * C + c0, q, tv, gv);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = dm[j];
-            v += __shfl_xor(v, 1);
-            v += __shfl_xor(v, 2);
-            v += __shfl_xor(v, 4);
-            v += __shfl_xor(v, 8);
-            dm[j] = v;
+            for (int j = 0; j < 16; ++j) {
+                dm[j] = gv[j] * dl[j];
+                dd[j] += gv[j] * (m[j] + bb[j]);
+                ds[j] += gv[j];
+            }
+            if (tv) store16(dmexp + ((int64_t)e * N + tok) * C + c0, q, dm);
+            // d_bias: sum over the wave's 16 tokens (lanes L of one q, fixed butterfly order),
+            // accumulated per (mix, wave, channel) in LDS by a single lane
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                float v = dm[j];
+                v += __shfl_xor(v, 1);
+                v += __shfl_xor(v, 2);
+                v += __shfl_xor(v, 4);
+                v += __shfl_xor(v, 8);
+                dm[j] = v;
+            }
+            if (L == 0) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) red[e][wv][j < 8 ? 8 * q + j : 32 + 8 * q + j - 8] += dm[j];
+            }
         }
-        if (L == 0) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) red[e][wv][16 * q + j] = dm[j];
-        }
-    }
-    if (tv) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            *reinterpret_cast<float4*>(dd_out + tok * C + cq + 4 * v) =
-                make_float4(dd[4 * v], dd[4 * v + 1], dd[4 * v + 2], dd[4 * v + 3]);
-            *reinterpret_cast<float4*>(ds_out + tok * C + cq + 4 * v) =
-                make_float4(ds[4 * v], ds[4 * v + 1], ds[4 * v + 2], ds[4 * v + 3]);
+        if (tv) {
+            store16f(dd_out + tok * C + c0, q, dd);
+            store16f(ds_out + tok * C + c0, q, ds);
         }
     }
     __syncthreads();
     for (int j = threadIdx.x; j < LORA_NE * 64; j += LORA_THR) {
         const int e = j >> 6, c = j & 63;
-        const float s = (red[e][0][c] + red[e][1][c]) + (red[e][2][c] + red[e][3][c]);
-        part[((int64_t)blockIdx.x * LORA_NE + e) * C + c0 + c] = s;
+        const float sum = (red[e][0][c] + red[e][1][c]) + (red[e][2][c] + red[e][3][c]);
+        part[(tb * LORA_NE + e) * C + c0 + c] = sum;
     }
 }
 
@@ -275,9 +332,9 @@ rwkv6_lora_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int
 namespace {
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int launch_status() { return hipGetLastError() == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH; }
-inline int lora_check(int64_t N, int64_t C, int64_t R, int pdt) {
+inline int lora_check(int E, int64_t N, int64_t C, int64_t R, int pdt) {
     if (N < 0 || C < 1 || R < 1) return RWKV6_ERR_INVALID_ARG;
-    if (C % 64 || R % 32 || R > 256) return RWKV6_ERR_UNSUPPORTED;
+    if (C % 64 || R % 32 || R > 256 || lora_lds_bytes(E, (int)R) > 65536) return RWKV6_ERR_UNSUPPORTED;
     if (pdt != RWKV6_F32 && pdt != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
     return RWKV6_OK;
 }
@@ -291,9 +348,9 @@ inline int gather(const void* const* src, P& dst) {
     }
     return RWKV6_OK;
 }
-inline dim3 up_grid(int64_t N, int64_t C) {
-    return dim3((unsigned)((N + 63) / 64), (unsigned)(C / 64));
-}
+// token blocks per XCD and the padded 1-D grid of lora_tile
+inline int64_t up_per(int64_t N) { return ((N + LORA_TT - 1) / LORA_TT + 7) / 8; }
+inline dim3 up_grid(int64_t N, int64_t C) { return dim3((unsigned)(8 * up_per(N) * (C / 64))); }
 }  // namespace
 
 extern "C" {
@@ -302,39 +359,41 @@ int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, c
                           int param_dtype, void* const* mixed, int64_t T, int64_t B, int64_t C,
                           int64_t R, void* stream) {
     if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
-    int st = lora_check(T * B, C, R, param_dtype);
+    int st = lora_check(LORA_NE, T * B, C, R, param_dtype);
     if (st) return st;
     if (T == 0) return RWKV6_OK;
     if (!x || !neck || !w_up_t || !bias) return RWKV6_ERR_INVALID_ARG;
     OutPtrs<LORA_NE> out;
     if ((st = gather<OutPtrs<LORA_NE>, LORA_NE>((const void* const*)mixed, out))) return st;
     if (!al16(x) || !al16(neck) || !al16(w_up_t) || !al16(bias)) return RWKV6_ERR_ALIGNMENT;
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true>), up_grid(T * B, C), dim3(LORA_THR), 0,
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true>), up_grid(T * B, C), dim3(LORA_THR),
+                       lora_lds_bytes(LORA_NE, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
                        (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, T * B,
-                       B, C, (int)R);
+                       B, C, (int)R, up_per(T * B));
     return launch_status();
 }
 
 int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, int param_dtype,
                         void* out, int64_t N, int64_t C, int64_t R, void* stream) {
-    int st = lora_check(N, C, R, param_dtype);
+    int st = lora_check(1, N, C, R, param_dtype);
     if (st) return st;
     if (N == 0) return RWKV6_OK;
     if (!neck || !w_up_t || !bias || !out) return RWKV6_ERR_INVALID_ARG;
     if (!al16(neck) || !al16(w_up_t) || !al16(bias) || !al16(out)) return RWKV6_ERR_ALIGNMENT;
     OutPtrs<1> o;
     o.p[0] = (uint16_t*)out;
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR), 0,
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR),
+                       lora_lds_bytes(1, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
                        (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o, N,
-                       (int64_t)1, C, (int)R);
+                       (int64_t)1, C, (int)R, up_per(N));
     return launch_status();
 }
 
 size_t rwkv6_ddlerp_lora_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
     if (T < 0 || B < 1 || C < 1) return 0;
-    const int64_t nb = (T * B + 63) / 64;
+    const int64_t nb = (T * B + LORA_TT - 1) / LORA_TT;
     return (size_t)((nb > 0 ? nb : 1) * LORA_NE * C) * sizeof(float);
 }
 
@@ -343,7 +402,7 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
                           float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
                           int64_t T, int64_t B, int64_t C, int64_t R, void* stream) {
     if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
-    int st = lora_check(T * B, C, R, param_dtype);
+    int st = lora_check(LORA_NE, T * B, C, R, param_dtype);
     if (st) return st;
     if (!bias || !d_bias || !workspace ||
         (T > 0 && (!x || !neck || !w_up_t || !d_mexp || !d_delta_part || !d_sum)))
@@ -354,13 +413,14 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
         !al16(d_delta_part) || !al16(d_sum) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t N = T * B, nb = (N + 63) / 64;
+    const int64_t N = T * B, nb = (N + LORA_TT - 1) / LORA_TT;
     float* part = reinterpret_cast<float*>(workspace);
     if (N > 0)
-        hipLaunchKernelGGL(rwkv6_ddlerp_lora_bwd_kernel, up_grid(N, C), dim3(LORA_THR), 0, s,
+        hipLaunchKernelGGL(rwkv6_ddlerp_lora_bwd_kernel, up_grid(N, C), dim3(LORA_THR),
+                           lora_lds_bytes(LORA_NE, (int)R), s,
                            (const uint16_t*)neck, (const uint16_t*)w_up_t, bias, param_dtype,
                            (const uint16_t*)x, dm, (uint16_t*)d_mexp, d_delta_part, d_sum, part, N,
-                           B, C, (int)R);
+                           B, C, (int)R, up_per(N));
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((LORA_NE * C + 31) / 32)),
                        dim3(LORA_THR), 0, s, part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias);
     return launch_status();
