@@ -60,6 +60,10 @@ const char* rwkv6_strerror(int code);
  *   h0, hT  : [B,H,K,V] f32, each nullable (initial_state / output_final_state)
  *   scale   : multiplies r (the reference passes 1.0)
  * Only K == V == 64 (RWKV-6 head size) is supported; T >= 0 arbitrary.
+ * Per-token log-decay is floored at -10 (decay factor 4.5e-5; the chunked evaluation
+ * keeps 8-token decay products inside the bf16 exponent range): tokens below the floor
+ * change outputs and states by less than that factor; their dw is the gradient at the
+ * floor (scaled by the same factor) and their d_decay (sequence-first entry) is 0.
  * `saved` (rwkv6_wkv_saved_bytes) receives the per-chunk states and decays that
  * the backward consumes; keep it alive until rwkv6_wkv_bwd.  `workspace`
  * (rwkv6_wkv_workspace_bytes) is scratch for the duration of one call.

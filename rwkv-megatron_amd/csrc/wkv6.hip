@@ -17,11 +17,15 @@
 // every exponential is one v_exp_f32) and a chunk is four 16-token sub-blocks with
 // midpoints mu_I = G[16I+7].  Each chunk kernel first builds, once, the operand tiles
 //   Rm[t] = r_t e^{G_{t-1} - mu_I(t)},      Km[tau] = k_tau e^{mu_J(tau) - G_tau}
-// (bounded by the decay of 8 tokens either way; finite while 8 consecutive log-decays
-// sum to > -88, i.e. |w| < ~11 per token).  The intra-chunk attention is then
-//   A[t][tau] = sum_i Rm[t][i] f_IJ[i] Km[tau][i],   f_IJ = e^{mu_I - mu_J} <= 1 (I > J)
-// on bf16 MFMA; every cross-block factor is a per-channel scalar applied to one
-// operand or to accumulator columns, never a per-element exponential.
+// (bounded by the decay of 8 tokens either way; with w floored at W_MIN the factors stay
+// inside e^{+-80}).  The intra-chunk attention is then, on bf16 MFMA,
+//   I == J:  A[t][tau] = sum_i Rm[t][i] Km[tau][i]
+//   I >  J:  A[t][tau] = sum_i (Rm[t][i] e^{mu_I - b_J}) (Km[tau][i] e^{b_J - mu_J}),
+// b_J = G[16J+15] the end of block J: each factor spans at most 8 tokens next to a block
+// boundary, so neither underflows unless the pair's own decay is already below e^-23
+// (f = e^{mu_I - mu_J} as one factor spans 16+ tokens and would underflow for pairs that
+// still matter).  The cross-block factors are per-channel scalars applied to operands or
+// to accumulator columns, never per-element exponentials.
 //
 // Operands that reduce over tokens are read from the same token-major LDS tile with
 // the gfx950 LDS transpose read (ds_read_b64_tr_b16), so no tile is stored twice.
@@ -41,6 +45,12 @@
                          // the row-wise reads of 8 consecutive rows by 8 lanes each conflict-free
 #define NTHR 256
 #define NTHR_G 512       // threads of the gradient kernel (8 waves)
+// Per-token log-decay floor.  The midpoint-referenced operand tiles scale by the decay of up
+// to 8 tokens either way, which must stay inside the bf16/fp32 exponent range (8 * 10 < 88);
+// a token below the floor keeps a decay factor e^-10 = 4.5e-5 instead of a smaller one
+// (relative change of the state below that); its gradient is the one at the floor, which
+// like the exact one carries that factor (the sequence-first entry returns d decay = 0).
+#define W_MIN (-10.0f)
 
 typedef uint16_t tile_t[CL][TS];
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -171,8 +181,8 @@ __device__ __forceinline__ void store_tile(uint16_t* __restrict__ dst, uint16_t 
 // Inclusive cumulative log2-decay over the 64 tokens of a chunk (token-major fp32
 // Gm[t][i]) from a token-major bf16 tile, NT_ threads (NT_/64 token parts).  The tile
 // holds the log-decay w, or (DEC) the pre-activation `decay` with w = -exp(decay)
-// (rwkv6_layer_specs.py:336) evaluated here in fp32.  Padding rows must read as w = 0:
-// callers zero-fill them (DEC: the kernel masks rows >= nvalid).
+// (rwkv6_layer_specs.py:336) evaluated here in fp32; w is floored at W_MIN.  Padding rows
+// must read as w = 0: callers zero-fill them (DEC: the kernel masks rows >= nvalid).
 // `tot` holds NT_ floats.  Ends with a barrier.
 template <int NT_, bool DEC = false>
 __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], float* tot,
@@ -184,8 +194,8 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], fl
 #pragma unroll
     for (int s = 0; s < PL; ++s) {
         const float x = bf2f(Wm[PL * part + s][i]);
-        if (DEC) run += (PL * part + s < nvalid) ? -ex2(x * RW_L2E) * RW_L2E : 0.f;
-        else run += x * RW_L2E;
+        const float wn = DEC ? ((PL * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+        run += fmaxf(wn, W_MIN) * RW_L2E;
         loc[s] = run;
     }
     tot[part * 64 + i] = run;
@@ -413,7 +423,7 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
                       int njobs) {
     __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vm;
     __shared__ __attribute__((aligned(16))) float RegA[CL][GS];   // G, then the S_in tile
-    __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD];
+    __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD], kb[3][KD];
     __shared__ float tot[NTHR], bonus[CL];
     uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&RegA[0][0]);
     float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(&RegA[0][0]);
@@ -453,9 +463,10 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
         {
             const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
             emu[part][i] = ex2(Gm[16 * part + 7][i]);
+            if (part < 3) kb[part][i] = ex2(Gm[16 * part + 15][i] - Gm[16 * part + 7][i]);
             for (int pi = part; pi < 6; pi += 4) {
                 const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 7][i]);
+                fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 15][i]);
             }
         }
 #pragma unroll
@@ -498,12 +509,15 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 bf16x8 rb = ld_row8(&Rm[0][0], t, 32 * ks);
+                bf16x8 kk = ld_row8(&Km[0][0], 16 * J + lr, 32 * ks);
                 if (!diag) {
                     float f[8];
                     row8_vec(fp[pair_index(W, J)], 32 * ks, f);
                     rb = scale8(rb, f);
+                    row8_vec(kb[J], 32 * ks, f);
+                    kk = scale8(kk, f);
                 }
-                at = mfma32(ld_row8(&Km[0][0], 16 * J + lr, 32 * ks), rb, at);   // A^T[tau][t]
+                at = mfma32(kk, rb, at);                                          // A^T[tau][t]
             }
             bf16x4 aop;
 #pragma unroll
@@ -535,19 +549,23 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
 // dk and dv) and the 32 output columns 32h .. 32h+31.  With dA[t][tau] = dO_t . v_tau,
 // Fm = e^{G_{t-1} - mu}, Fk = e^{mu - G}, s = scale, S_in / S_out the states before /
 // after the chunk and dS the gradient of S_out:
-//   dr = s Fm (e^{mu_W} dO S_in^T + sum_{J<W} f_WJ dA Km + tril(dA) Km)     + s u k dd
-//   dk = Fk (e^{G_63-mu_W} v dS^T + s sum_{I>W} f_IW dA^T Rm + s tril(dA)^T Rm) + s u r dd
+//   dr = s Fm (e^{mu_W} dO S_in^T + sum_{J<W} p_WJ q_J dA Km + tril(dA) Km)        + s u k dd
+//   dk = Fk (e^{G_63-mu_W} v dS^T + s sum_{I>W} q_W p_IW dA^T Rm + s tril(dA)^T Rm) + s u r dd
 //   dv = (Km e^{G_63-mu_W}) dS + s sum_{I>=W} A_IW^T dO
 //   dw[t] = sum_{m>t} (Rm acc_r - Km acc_k)[m] - Km acc_k[t] + D,  D = rowsum(S_out * dS)
-// where acc_r = dr_h / Fm and acc_k = dk_h / Fk are the bracketed accumulators.
+// where acc_r = dr_h / Fm and acc_k = dk_h / Fk are the bracketed accumulators and the
+// cross-block factors are split at the end b_J = G[16J+15] of the source block:
+// p_IJ = e^{mu_I - b_J} (table fp), q_J = e^{b_J - mu_J} (table kb), p_IJ q_J = e^{mu_I - mu_J},
+// applied one after the other to accumulators (dr, dk) or one to each operand (dv).
 struct GradSmem {
     tile_t Vm, Dm;                  // raw v, dO (adjacent: the fp32 y tile in the epilogue)
     tile_t RmH, RmL, KmH, KmL;      // operand tiles (hi/lo); output staging in the epilogue
     float A[CL][GS];                // G -> S_in | dS bf16 tiles -> the fp32 x tile
-    float emu[4][KD], eg[4][KD], fp[6][KD];
+    float emu[4][KD], eg[4][KD], fp[6][KD], kb[3][KD];
     float bonus[CL], dd[CL], Dv[KD];
     float red[8][KD];               // build_G scratch, du partials, dw block totals
 };
+static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit one CU's LDS");
 
 // SEQ: r, k, v, the pre-activation decay and dr, dk, dv, d_decay are sequence-first (dO is
 // head-first); the decay gradient is dw * w with w = -exp(decay).
@@ -641,10 +659,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float m = Gv[16 * part + 7][i];
             sm.emu[part][i] = ex2(m);
             sm.eg[part][i] = ex2(Gv[CL - 1][i] - m);
+            if (part < 3) sm.kb[part][i] = ex2(Gv[16 * part + 15][i] - m);
         } else {
             for (int pi = part - 4; pi < 6; pi += 4) {
                 const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                sm.fp[pi][i] = ex2(Gv[16 * I + 7][i] - Gv[16 * J + 7][i]);
+                sm.fp[pi][i] = ex2(Gv[16 * I + 7][i] - Gv[16 * J + 15][i]);
             }
         }
         // operand tiles Rm, Km (hi/lo); the w scratch in RmL was consumed by build_G
@@ -728,7 +747,9 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             f32x4 tmp = {};
             tmp = mfma16(aop, ld_tr4(KH, 16 * J, cb), tmp);
             tmp = mfma16(aop, ld_tr4(KL, 16 * J, cb), tmp);
-            ar[tp] += diag ? tmp : tmp * sm.fp[pair_index(W, J)][cb + lr];
+            // the two halves of the cross factor one after the other (q_J p_WJ as one
+            // number can underflow where the product with tmp is O(1))
+            ar[tp] += diag ? tmp : (tmp * sm.kb[J][cb + lr]) * sm.fp[pair_index(W, J)][cb + lr];
         }
     }
     // ---------------- dk (source rows in W) ----------------
@@ -758,7 +779,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             f32x4 tmp = {};
             tmp = mfma16(aop, ld_tr4(RH, 16 * I, cb), tmp);
             tmp = mfma16(aop, ld_tr4(RL, 16 * I, cb), tmp);
-            ak[tp] += diag ? tmp : tmp * sm.fp[pair_index(I, W)][cb + lr];
+            ak[tp] += diag ? tmp : (tmp * sm.fp[pair_index(I, W)][cb + lr]) * sm.kb[W][cb + lr];
         }
     }
     // ---------------- dv (source rows in W, value columns 32hh..) ----------------
@@ -776,12 +797,15 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             bf16x8 ra = ld_row8(RH, 16 * I + lr, 32 * ks);
+            bf16x8 kk = ld_row8(KH, rowW, 32 * ks);
             if (!diag) {
                 float f[8];
                 row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
                 ra = scale8(ra, f);
+                row8_vec(sm.kb[W], 32 * ks, f);
+                kk = scale8(kk, f);
             }
-            at = mfma32(ra, ld_row8(KH, rowW, 32 * ks), at);     // A[t = 16I+4lq+rr][tau = 16W+lr]
+            at = mfma32(ra, kk, at);                               // A[t = 16I+4lq+rr][tau = 16W+lr]
         }
         bf16x4 aop;
 #pragma unroll
@@ -850,8 +874,13 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         for (int s = 7; s >= 0; --s) {
             const int tt = 8 * part + s;
             float g = run + Ys[tt][i];
-            if (SEQ && tt < nvalid)            // d decay = dw * w, w = -exp(decay)
-                g *= -ex2(bf2f(w[base + (size_t)tt * rs + i]) * RW_L2E);
+            // d decay = dw * w, w = -exp(decay); a floored token's d decay is 0 (the exact
+            // one carries its decay factor).  The head-first dw of a floored token is the
+            // gradient at the floor, itself scaled by e^W_MIN.
+            if (SEQ && tt < nvalid) {
+                const float wn = -ex2(bf2f(w[base + (size_t)tt * rs + i]) * RW_L2E);
+                g = wn < W_MIN ? 0.f : g * wn;
+            }
             sm.KmL[tt][i] = f2bf(g);
             run += Xs[tt][i];
         }

@@ -273,3 +273,87 @@ class RWKV6Model(nn.Module):
         for layer in self.layers:
             x = layer(x)
         return self.output_layer(self.final_layernorm(x))
+
+    @torch.no_grad()
+    def from_rwkv_lm(self, sd):
+        """Loads RWKV-LM weights into this model (rwkv6_model.py:295-372), cast to the
+        parameters' dtype and device; see rwkv_lm_to_state_dict for the key map."""
+        own = self.state_dict()
+        conv = rwkv_lm_to_state_dict(sd, len(self.layers))
+        missing = sorted(set(own) - set(conv))
+        if missing:
+            raise KeyError(f"no RWKV-LM source for {missing}")
+        for name, t in conv.items():
+            if tuple(t.shape) != tuple(own[name].shape):
+                raise ValueError(f"{name}: checkpoint shape {tuple(t.shape)} != {tuple(own[name].shape)}")
+            own[name].copy_(t.to(own[name].dtype))
+        return self
+
+
+def rwkv_lm_to_state_dict(sd, num_layers, head_size=64):
+    """RWKV-LM (BlinkDL) RWKV-6 checkpoint keys -> this package's RWKV6Model state_dict.
+
+    Mirrors RWKV6Model.from_rwkv_lm (rwkv6_model.py:295-372) at TP = 1 with
+    layernorm_zero_centered_gamma off (norm offset 0):
+      emb.weight -> embedding.weight; blocks.0.ln0 -> pre_norm; ln_out -> final_layernorm;
+      head.weight -> output_layer.weight; per block i:
+      ln1 / ln2 -> input_layernorm / pre_mlp_layernorm;
+      att.time_maa_x -> mix_coeff_input; att.time_maa_w1 [C, 5R] -> bottleneck_token_shift
+      .weight_down [C, 5, R] ("d (e r) -> d e r"); att.time_maa_w2 -> .weight_up;
+      att.time_maa_{w,k,v,r,g} -> .bias[0..4] (order "wkvrg");
+      att.time_decay_w1 [C, R] -> bottleneck_decay.weight_down [C, 1, R];
+      att.time_decay_w2 [R, C] -> .weight_up [1, R, C]; att.time_decay -> .bias [1, C];
+      att.time_faaaa -> core_attention.time_first [C]; att.{receptance,key,value,gate,output}
+      -> linear_{receptance,key,value,gate,proj}; att.ln_x -> group_norm;
+      ffn.time_maa_k / ffn.time_maa_r -> mlp.mix_coeffs[0] / [1];
+      ffn.key / ffn.receptance / ffn.value -> mlp.linear_up / linear_gate / linear_down.
+    Tensors are returned as they come (dtype and device of `sd`); shapes are flattened or
+    split exactly as the reference does."""
+    out = {
+        "embedding.weight": sd["emb.weight"],
+        "pre_norm.weight": sd["blocks.0.ln0.weight"],
+        "pre_norm.bias": sd["blocks.0.ln0.bias"],
+        "final_layernorm.weight": sd["ln_out.weight"],
+        "final_layernorm.bias": sd["ln_out.bias"],
+        "output_layer.weight": sd["head.weight"],
+    }
+    for i in range(num_layers):
+        src = f"blocks.{i}."
+        dst = f"layers.{i}."
+        att = lambda k: sd[src + "att." + k]
+        ffn = lambda k: sd[src + "ffn." + k]
+        C = att("time_maa_x").numel()
+        w1 = att("time_maa_w1")
+        out.update({
+            dst + "input_layernorm.weight": sd[src + "ln1.weight"],
+            dst + "input_layernorm.bias": sd[src + "ln1.bias"],
+            dst + "pre_mlp_layernorm.weight": sd[src + "ln2.weight"],
+            dst + "pre_mlp_layernorm.bias": sd[src + "ln2.bias"],
+            dst + "self_attention.mix_coeff_input": att("time_maa_x").reshape(C),
+            dst + "self_attention.bottleneck_token_shift.weight_down": w1.reshape(C, 5, w1.shape[1] // 5),
+            dst + "self_attention.bottleneck_token_shift.weight_up": att("time_maa_w2"),
+            dst + "self_attention.bottleneck_token_shift.bias": torch.stack(
+                [att("time_maa_" + n).reshape(C) for n in "wkvrg"]),
+            dst + "self_attention.bottleneck_decay.weight_down": att("time_decay_w1").unsqueeze(1),
+            dst + "self_attention.bottleneck_decay.weight_up": att("time_decay_w2").unsqueeze(0),
+            dst + "self_attention.bottleneck_decay.bias": att("time_decay").reshape(1, C),
+            dst + "self_attention.core_attention.time_first": att("time_faaaa").reshape(C),
+            dst + "self_attention.linear_receptance.weight": att("receptance.weight"),
+            dst + "self_attention.linear_key.weight": att("key.weight"),
+            dst + "self_attention.linear_value.weight": att("value.weight"),
+            dst + "self_attention.linear_gate.weight": att("gate.weight"),
+            dst + "self_attention.linear_proj.weight": att("output.weight"),
+            dst + "self_attention.group_norm.weight": att("ln_x.weight"),
+            dst + "self_attention.group_norm.bias": att("ln_x.bias"),
+            dst + "mlp.mix_coeffs": torch.stack([ffn("time_maa_k").reshape(C), ffn("time_maa_r").reshape(C)]),
+            dst + "mlp.linear_up.weight": ffn("key.weight"),
+            dst + "mlp.linear_gate.weight": ffn("receptance.weight"),
+            dst + "mlp.linear_down.weight": ffn("value.weight"),
+        })
+    return out
+
+
+def load_rwkv_lm(path):
+    """Reads an RWKV-LM .pth checkpoint with torch.load(weights_only=True) (tensors only, no
+    code from the file runs); returns the raw state dict for rwkv_lm_to_state_dict."""
+    return torch.load(path, map_location="cpu", weights_only=True)

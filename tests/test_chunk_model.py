@@ -69,3 +69,21 @@ def test_midpoint_form_matches_recurrence(T, strong):
     gm = cm.bwd_mid(r, k, v, w, u, dO, h0, dhT, 0.8)
     for name in ("dr", "dk", "dv", "dw", "du", "dh0"):
         assert _rel(gm[name], g[name]) < 1e-5, name
+
+
+@pytest.mark.parametrize("T", [64, 130])
+def test_midpoint_form_extreme_decay_needs_split_factors(T):
+    """Per-token log-decay down to -exp(5) ~ -148, floored at -10 as the kernels do.  With
+    fp32-range exponentials the midpoint form stays exact only if each cross-block factor
+    e^{mu_I - mu_J} is split at the source block's end (p_IJ q_J): the single factor spans
+    16+ tokens and underflows for pairs that still matter (the control below)."""
+    r, k, v, w, u, h0, dO, dhT = _inputs(1, 2, T, 16, 8, seed=T + 11, w_lo=-3.0, w_hi=5.0)
+    w = np.maximum(w, -10.0).astype(np.float32)
+    o, _ = orc.wkv6_fwd(r, k, v, w, u, h0, 1.0)
+    assert _rel(cm.fwd_mid(r, k, v, w, u, h0, 1.0), o) < 1e-5
+    g = orc.wkv6_bwd(r, k, v, w, u, dO, h0, dhT, 1.0)
+    gm = cm.bwd_mid(r, k, v, w, u, dO, h0, dhT, 1.0)
+    for name in ("dr", "dk", "dv", "dw", "du", "dh0"):
+        assert _rel(gm[name], g[name]) < 1e-5, name
+    # control: the unsplit factor loses those pairs
+    assert _rel(cm.fwd_mid(r, k, v, w, u, h0, 1.0, split=False), o) > 1e-2

@@ -119,6 +119,19 @@ def test_wkv_strong_decay(pkg):
     _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
 
 
+def test_wkv_extreme_decay_is_floored(pkg):
+    """Log-decay down to -exp(5) ~ -148 per token: the kernels floor w at -10 (decay factor
+    4.5e-5; the exact factor is below that, so outputs and states move by less than that
+    relative amount); a floored token's dw is taken at the floor (scaled by the same
+    factor, as the exact one is).  Outputs, states and gradients stay finite and match
+    the exact fp64 oracle."""
+    x = _inputs(1, 2, 130, seed=11, w_lo=-3.0, w_hi=5.0)
+    got = run_gpu(pkg, x, 1.0, True, True)
+    assert all(np.isfinite(v).all() for v in got.values())
+    ref = run_oracle(x, 1.0, True, True)
+    _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
+
+
 def test_wkv_deterministic(pkg):
     x = _inputs(2, 2, 200, seed=3)
     a = run_gpu(pkg, x, 1.0, True, True)

@@ -162,10 +162,25 @@ def bwd(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
 # Midpoint-referenced form (the form of the current kernels).  Per sub-block I,
 # mu_I = G[16I+7]; stored operand tiles
 #   Rm[t] = r_t e^{G_{t-1} - mu_I(t)},   Km[tau] = k_tau e^{mu_J(tau) - G_tau}
-# are bounded by the decay of 8 tokens either way; every cross-block factor is a
-# per-channel scalar f_IJ = e^{mu_I - mu_J} <= 1 (I > J) applied to accumulator
-# columns (dr, dk) or to one operand (A blocks).
+# are bounded by the decay of 8 tokens either way.  A cross-block pair (I > J) uses
+# f_IJ = e^{mu_I - mu_J} split at the end b_J = G[16J+15] of the source block into
+# p_IJ = e^{mu_I - b_J} and q_J = e^{b_J - mu_J}, one on each side of the contraction.
+# Every exponential is evaluated with fp32's range (_ex: underflow below ~e^-103,
+# overflow above e^88.7), as in the kernels, so split=False reproduces the single-factor
+# form that loses pairs whose f underflows while their own decay is still O(1).
 # ---------------------------------------------------------------------------
+
+def _ex(x):
+    with np.errstate(over="ignore", under="ignore"):
+        return np.exp(np.asarray(x, np.float32)).astype(np.float64)
+
+
+def _pq(G, mu, I, J, split):
+    """(operand factor on the target side, factor on the source side) of block pair I > J."""
+    if not split:
+        return _ex(mu[..., I, :] - mu[..., J, :]), np.ones_like(mu[..., J, :])
+    b = G[..., SUB * J + SUB - 1, :]
+    return _ex(mu[..., I, :] - b), _ex(b - mu[..., J, :])
 
 def _mid(G, Gm1):
     NB = L // SUB
@@ -175,7 +190,7 @@ def _mid(G, Gm1):
     return mu, mu_t
 
 
-def fwd_mid(r, k, v, w, u, h0=None, scale=1.0):
+def fwd_mid(r, k, v, w, u, h0=None, scale=1.0, split=True):
     r, k, v, w = (np.asarray(a, np.float64) for a in (r, k, v, w))
     u = np.asarray(u, np.float64)
     B, H, T, K = r.shape
@@ -185,26 +200,29 @@ def fwd_mid(r, k, v, w, u, h0=None, scale=1.0):
     rc, kc, vc, wc = (_chunks(a, T, NT) for a in (r, k, v, w))
     G, Gm1 = _chunk_cumsum(wc)
     mu, mu_t = _mid(G, Gm1)
-    Rm = rc * np.exp(Gm1 - mu_t)
-    Km = kc * np.exp(mu_t - G)
+    Rm = rc * _ex(Gm1 - mu_t)
+    Km = kc * _ex(mu_t - G)
     bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
     O = np.zeros((B, H, NT, L, V))
     tril = np.tril(np.ones((SUB, SUB)), -1)
     for I in range(L // SUB):
         ti = slice(SUB * I, SUB * I + SUB)
-        O[..., ti, :] += np.einsum("bhcti,bhcij->bhctj", Rm[..., ti, :] * np.exp(mu[..., I, None, :]),
+        O[..., ti, :] += np.einsum("bhcti,bhcij->bhctj", Rm[..., ti, :] * _ex(mu[..., I, None, :]),
                                    S_in[:, :, :NT])
         for J in range(I + 1):
             tj = slice(SUB * J, SUB * J + SUB)
-            f = np.exp(mu[..., I, :] - mu[..., J, :])[..., None, :]
-            A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * f, Km[..., tj, :])
             if I == J:
+                A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :], Km[..., tj, :])
                 A = A * tril + np.einsum("bhct,ts->bhcts", bonus[..., ti], np.eye(SUB))
+            else:
+                pf, qf = _pq(G, mu, I, J, split)
+                A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * pf[..., None, :],
+                              Km[..., tj, :] * qf[..., None, :])
             O[..., ti, :] += np.einsum("bhcts,bhcsj->bhctj", A, vc[..., tj, :])
     return scale * O.reshape(B, H, NT * L, V)[:, :, :T]
 
 
-def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
+def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0, split=True):
     r, k, v, w, dO = (np.asarray(a, np.float64) for a in (r, k, v, w, dO))
     u = np.asarray(u, np.float64)
     B, H, T, K = r.shape
@@ -223,10 +241,10 @@ def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
         dS_out[:, :, c] = dS
         dS = np.exp(GL[:, :, c])[..., None] * dS + dSloc[:, :, c]
     dh0 = dS
-    Rm = rc * np.exp(Gm1 - mu_t)
-    Km = kc * np.exp(mu_t - G)
-    Fm = np.exp(Gm1 - mu_t)
-    Fk = np.exp(mu_t - G)
+    Rm = rc * _ex(Gm1 - mu_t)
+    Km = kc * _ex(mu_t - G)
+    Fm = _ex(Gm1 - mu_t)
+    Fk = _ex(mu_t - G)
     dA = np.einsum("bhctj,bhcsj->bhcts", dc, vc)
     dd = np.einsum("bhctt->bhct", dA)
     bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
@@ -238,29 +256,36 @@ def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0):
     NB = L // SUB
     for W in range(NB):
         tw = slice(SUB * W, SUB * W + SUB)
-        f = lambda I, J: np.exp(mu[..., I, :] - mu[..., J, :])
         # dr accumulator (columns i): inter, off-diagonal, diagonal
-        a = np.exp(mu[..., W, :])[..., None, :] * np.einsum("bhctj,bhcij->bhcti", dc[..., tw, :], S_in[:, :, :NT])
+        a = _ex(mu[..., W, :])[..., None, :] * np.einsum("bhctj,bhcij->bhcti", dc[..., tw, :], S_in[:, :, :NT])
         for J in range(W):
             tj = slice(SUB * J, SUB * J + SUB)
-            a += f(W, J)[..., None, :] * np.einsum("bhcts,bhcsi->bhcti", dA[..., tw, tj], Km[..., tj, :])
+            pf, qf = _pq(G, mu, W, J, split)
+            a += pf[..., None, :] * np.einsum("bhcts,bhcsi->bhcti", dA[..., tw, tj],
+                                              Km[..., tj, :] * qf[..., None, :])
         a += np.einsum("bhcts,bhcsi->bhcti", dA[..., tw, tw] * tril, Km[..., tw, :])
         acc_r[..., tw, :] = a
         # dk accumulator
-        a = np.exp(GL - mu[..., W, :])[..., None, :] * np.einsum("bhcsj,bhcij->bhcsi", vc[..., tw, :], dS_out)
+        a = _ex(GL - mu[..., W, :])[..., None, :] * np.einsum("bhcsj,bhcij->bhcsi", vc[..., tw, :], dS_out)
         for I in range(W + 1, NB):
             ti = slice(SUB * I, SUB * I + SUB)
-            a += f(I, W)[..., None, :] * np.einsum("bhcts,bhcti->bhcsi", dA[..., ti, tw], Rm[..., ti, :])
+            pf, qf = _pq(G, mu, I, W, split)
+            a += qf[..., None, :] * np.einsum("bhcts,bhcti->bhcsi", dA[..., ti, tw],
+                                              Rm[..., ti, :] * pf[..., None, :])
         a += np.einsum("bhcts,bhcti->bhcsi", dA[..., tw, tw] * tril, Rm[..., tw, :])
         acc_k[..., tw, :] = a
         # dv
-        dv[..., tw, :] = np.einsum("bhcsi,bhcij->bhcsj", Km[..., tw, :] * np.exp(GL - mu[..., W, :])[..., None, :],
+        dv[..., tw, :] = np.einsum("bhcsi,bhcij->bhcsj", Km[..., tw, :] * _ex(GL - mu[..., W, :])[..., None, :],
                                    dS_out)
         for I in range(W, NB):
             ti = slice(SUB * I, SUB * I + SUB)
-            A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * f(I, W)[..., None, :], Km[..., tw, :])
             if I == W:
+                A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :], Km[..., tw, :])
                 A = A * tril + np.einsum("bhct,ts->bhcts", bonus[..., ti], np.eye(SUB))
+            else:
+                pf, qf = _pq(G, mu, I, W, split)
+                A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :] * pf[..., None, :],
+                              Km[..., tw, :] * qf[..., None, :])
             dv[..., tw, :] += np.einsum("bhcts,bhctj->bhcsj", A, dc[..., ti, :])
     dr = Fm * acc_r + u[None, :, None, None, :] * kc * dd[..., None]
     dk = Fk * acc_k + u[None, :, None, None, :] * rc * dd[..., None]
