@@ -280,8 +280,7 @@ wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
         for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Ys[0][0], 32 * ks, 16 * tj), acc[tj]);
     }
     if (FWD) {
-        // S_loc stays fp32: the dw of the backward takes rowsum(S_out * dS) against terms
-        // that cancel its k v^T part, so S_out carries a single bf16 rounding.
+        // S_loc stays fp32: the state scan adds it into the fp32 carry
         float* o = reinterpret_cast<float*>(out) + ((size_t)bh * NT + c) * KD * KD;
 #pragma unroll
         for (int tj = 0; tj < 4; ++tj)
@@ -553,6 +552,8 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
 //   dk = Fk (e^{G_63-mu_W} v dS^T + s sum_{I>W} q_W p_IW dA^T Rm + s tril(dA)^T Rm) + s u r dd
 //   dv = (Km e^{G_63-mu_W}) dS + s sum_{I>=W} A_IW^T dO
 //   dw[t] = sum_{m>t} (Rm acc_r - Km acc_k)[m] - Km acc_k[t] + D,  D = rowsum(S_out * dS)
+// with D formed as e^{G_63} rowsum(S_in * dS) + sum_t Km (e^{G_63-mu_W} v dS^T)[t], the
+// exact split S_out = e^{G_63} S_in + S_loc written with the dk terms themselves,
 // where acc_r = dr_h / Fm and acc_k = dk_h / Fk are the bracketed accumulators and the
 // cross-block factors are split at the end b_J = G[16J+15] of the source block:
 // p_IJ = e^{mu_I - b_J} (table fp), q_J = e^{b_J - mu_J} (table kb), p_IJ q_J = e^{mu_I - mu_J},
@@ -563,6 +564,7 @@ struct GradSmem {
     float A[CL][GS];                // G -> S_in | dS bf16 tiles -> the fp32 x tile
     float emu[4][KD], eg[4][KD], fp[6][KD], kb[3][KD];
     float bonus[CL], dd[CL], Dv[KD];
+    float Pk[4][KD];                // per-wave sums of Km * (dk from dS), for dw
     float red[8][KD];               // build_G scratch, du partials, dw block totals
 };
 static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit one CU's LDS");
@@ -570,7 +572,7 @@ static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit 
 // SEQ: r, k, v, the pre-activation decay and dr, dk, dv, d_decay are sequence-first (dO is
 // head-first); the decay gradient is dw * w with w = -exp(decay).
 template <bool SEQ>
-__global__ void __launch_bounds__(NTHR_G)
+__global__ void __launch_bounds__(NTHR_G) __attribute__((amdgpu_waves_per_eu(4)))
 wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                      const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
                      const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ dO,
@@ -616,13 +618,12 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         }
     }
     // states: S_in and dS rows (thread row = channel i), kept in registers until G is consumed;
-    // D[i] = sum_j S_out[i][j] dS[i][j]
+    // Dv[i] = sum_j S_in[i][j] dS[i][j] (scaled by e^{G_63} once G is built)
     const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
     const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
     {
-        const uint4 soq = *reinterpret_cast<const uint4*>(Hs + st_in + KD * KD + row * KD + c8);
         float a8[8], b8[8], d = 0.f;
-        unpack8(soq, a8);
+        unpack8(sq, a8);
         unpack8(dsq, b8);
 #pragma unroll
         for (int s = 0; s < 8; ++s) d += a8[s] * b8[s];
@@ -659,6 +660,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float m = Gv[16 * part + 7][i];
             sm.emu[part][i] = ex2(m);
             sm.eg[part][i] = ex2(Gv[CL - 1][i] - m);
+            if (part == 0) sm.Dv[i] *= ex2(Gv[CL - 1][i]);
             if (part < 3) sm.kb[part][i] = ex2(Gv[16 * part + 15][i] - m);
         } else {
             for (int pi = part - 4; pi < 6; pi += 4) {
@@ -763,7 +765,18 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
                 tmp[tp] = mfma32(a, ld_row8(&dSm[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
         }
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) ak[tp] = tmp[tp] * sm.eg[W][16 * (2 * hh + tp) + lr];
+        for (int tp = 0; tp < 2; ++tp) {
+            const int cb = 16 * (2 * hh + tp);
+            ak[tp] = tmp[tp] * sm.eg[W][cb + lr];
+            // this wave's share of sum_t Km[t][i] ak[t][i] = rowsum((S_out - e^{G_63} S_in) dS)
+            const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
+            float p = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) p += ((float)kh[rr] + (float)kl[rr]) * ak[tp][rr];
+            p += __shfl_xor(p, 16);
+            p += __shfl_xor(p, 32);
+            if (lq == 0) sm.Pk[W][cb + lr] = p;
+        }
     }
     for (int I = W; I < 4; ++I) {
         const bool diag = (I == W);
@@ -829,7 +842,6 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         const bf16x4 rh = ld_tr4(RH, 16 * W, cb), rl = ld_tr4(RL, 16 * W, cb);
         const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
         const float ui = scale * load_u(u, u_dtype, h * KD + i);
-        const float Di = sm.Dv[i];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
@@ -840,7 +852,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             drv[tp][rr] = Fm[tp][rr] * accr + udd * (kmv * iFk[tp][rr]);
             dkv[tp][rr] = Fk[tp][rr] * acck + udd * (rmv * iFm[tp][rr]);
             xv[tp][rr] = rmv * accr - kmv * acck;
-            yv[tp][rr] = Di - kmv * acck;
+            yv[tp][rr] = -kmv * acck;
         }
     }
     __syncthreads();                       // all waves are done with the operand tiles
@@ -868,7 +880,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         for (int s = 0; s < 8; ++s) tsum += Xs[8 * part + s][i];
         sm.red[part][i] = tsum;
         __syncthreads();
-        float run = 0.f;                   // sum_{m > t} x[m]
+        // D = rowsum(S_out dS) = e^{G_63} rowsum(S_in dS) + sum_t Km ak(dS part): the second
+        // sum is the one the suffix sums of Km ak take off again, so dw keeps no rounding of a
+        // large D (bf16 S_out) that cancels; what remains scales with e^{G_63}.
+        const float D = sm.Dv[i] + ((sm.Pk[0][i] + sm.Pk[1][i]) + (sm.Pk[2][i] + sm.Pk[3][i]));
+        float run = D;                     // D + sum_{m > t} x[m]
         for (int p = part + 1; p < 8; ++p) run += sm.red[p][i];
 #pragma unroll
         for (int s = 7; s >= 0; --s) {

@@ -248,7 +248,9 @@ def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0, split=True):
     dA = np.einsum("bhctj,bhcsj->bhcts", dc, vc)
     dd = np.einsum("bhctt->bhct", dA)
     bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
-    D = np.einsum("bhcij,bhcij->bhci", S_in[:, :, 1:], dS_out)
+    # D = rowsum(S_out dS) as the kernel forms it: e^{G_63} rowsum(S_in dS) plus the sum of
+    # Km times the dS part of the dk accumulator (S_out = e^{G_63} S_in + S_loc, exactly)
+    D = _ex(GL) * np.einsum("bhcij,bhcij->bhci", S_in[:, :, :NT], dS_out)
     tril = np.tril(np.ones((SUB, SUB)), -1)
     acc_r = np.zeros_like(rc)
     acc_k = np.zeros_like(kc)
@@ -267,6 +269,7 @@ def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0, split=True):
         acc_r[..., tw, :] = a
         # dk accumulator
         a = _ex(GL - mu[..., W, :])[..., None, :] * np.einsum("bhcsj,bhcij->bhcsi", vc[..., tw, :], dS_out)
+        D = D + (Km[..., tw, :] * a).sum(-2)
         for I in range(W + 1, NB):
             ti = slice(SUB * I, SUB * I + SUB)
             pf, qf = _pq(G, mu, I, W, split)
