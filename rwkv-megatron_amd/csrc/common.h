@@ -7,12 +7,26 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // log2(e): decays are kept in base-2 log units so every exponential is one v_exp_f32.
 #define RW_L2E 1.4426950408889634f
 
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// two fp32 -> two bf16 (a in the low half), the same rounding as f2bf, in one
+// v_cvt_pk_bf16_f32 instead of two conversions, a shift and an or
+__device__ __forceinline__ uint32_t pk2(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+    return make_uint4(pk2(f[0], f[1]), pk2(f[2], f[3]), pk2(f[4], f[5]), pk2(f[6], f[7]));
+}
+__device__ __forceinline__ bf16x4 cvt4(float a, float b, float c, float d) {
+    return __builtin_bit_cast(bf16x4, make_uint2(pk2(a, b), pk2(c, d)));
+}
 // 2^x with the hardware base-2 exponential (v_exp_f32).
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -51,12 +65,7 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     unpack8(*reinterpret_cast<const uint4*>(p), f);
 }
 __device__ __forceinline__ void store8(uint16_t* p, const float* f) {
-    uint4 q;
-    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
-    *reinterpret_cast<uint4*>(p) = q;
+    *reinterpret_cast<uint4*>(p) = pack8(f);
 }
 // 8 consecutive parameters (RWKV6_BF16 or RWKV6_F32, the codes of rwkv6_amd.h) as fp32.
 __device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {

@@ -153,7 +153,32 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
 
 // Backward of the token-shift LoRA's up-projection + ddlerp (E = 5), per token:
 //   d_mexp_e = d_mixed_e * delta;  dd = sum_e d_mixed_e (m_e + bias_e);  ds = sum_e d_mixed_e
-// and the d_bias partial of this block's 64 tokens: part[blockIdx.x][e][C].
+// and the d_bias partial of this block's tokens: part[blockIdx.x][e][C].
+// Wave wv takes the channel half h = wv & 1 (32 channels) of the 16 tokens 16 (wv >> 1) + L
+// of each 32-token group; a lane holds the one 16-byte run c0 + 32h + 8q + (0..7), so a load
+// instruction still covers 64 contiguous bytes of 16 token rows, and eight values per lane
+// (instead of sixteen) keep the registers low enough for four waves per SIMD: the kernel
+// is bound by how many loads are in flight.
+__device__ __forceinline__ void lora_up8(const uint16_t* sw, const uint16_t* __restrict__ neck_row,
+                                         bool tv, int R, int e, int h, float* m) {
+    const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
+    const int rs = lds_rs(R);
+    const uint16_t* swe = sw + (e * 64 + 32 * h) * rs;
+    f32x4 acc[2] = {};
+    for (int ks = 0; ks < R / 32; ++ks) {
+        const int r0 = 32 * ks + 8 * q;
+        const bf16x8 b = tv ? ld_bf16x8(neck_row + e * R + r0)
+                            : __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+#pragma unroll
+        for (int tc = 0; tc < 2; ++tc)
+            acc[tc] = mfma32(ld_bf16x8(swe + tile_channel(tc, L) * rs + r0), b, acc[tc]);
+    }
+#pragma unroll
+    for (int tc = 0; tc < 2; ++tc)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) m[4 * tc + rr] = acc[tc][rr];
+}
+
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                              const void* __restrict__ bias, int pdt,
@@ -161,66 +186,75 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
                              uint16_t* __restrict__ dmexp, float* __restrict__ dd_out,
                              float* __restrict__ ds_out, float* __restrict__ part, int64_t N,
                              int64_t B, int64_t C, int R, int64_t per) {
-    __shared__ float red[LORA_NE][4][64];
+    __shared__ float red[LORA_NE][2][64];          // [mix][token half of a group][channel]
     int64_t tb, cb;
     if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
-    const int64_t c0 = cb * 64;
+    const int h = wv & 1, tw = wv >> 1, cw = 32 * h + 8 * q;   // cw: first channel (rel. c0)
+    const int64_t cl = cb * 64 + cw;
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
-    lora_stage(lora_sm, wut, LORA_NE, C, R, c0);
+    lora_stage(lora_sm, wut, LORA_NE, C, R, cb * 64);
+    for (int j = threadIdx.x; j < LORA_NE * 2 * 64; j += LORA_THR) (&red[0][0][0])[j] = 0.f;
     __syncthreads();
-    for (int j = threadIdx.x; j < LORA_NE * 4 * 64; j += LORA_THR) (&red[0][0][0])[j] = 0.f;
-    __syncthreads();
-    for (int g = 0; g < LORA_TT / 64; ++g) {
-        const int64_t tok = tb * LORA_TT + 64 * g + 16 * wv + L;
+    for (int g = 0; g < LORA_TT / 32; ++g) {
+        const int64_t tok = tb * LORA_TT + 32 * g + 16 * tw + L;
         const bool tv = tok < N;
-        float xv[16], dl[16], dd[16], ds[16];
-        load16(x + tok * C + c0, q, tv, xv);
-        load16(x + (tok - B) * C + c0, q, tv && tok >= B, dl);
+        float dl[8], dd[8], ds[8];
+        {
+            float xv[8];
+            if (tv) load8(x + tok * C + cl, xv);
+            else for (int j = 0; j < 8; ++j) xv[j] = 0.f;
+            if (tv && tok >= B) load8(x + (tok - B) * C + cl, dl);
+            else for (int j = 0; j < 8; ++j) dl[j] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            dl[j] -= xv[j];
-            dd[j] = ds[j] = 0.f;
+            for (int j = 0; j < 8; ++j) {
+                dl[j] -= xv[j];
+                dd[j] = ds[j] = 0.f;
+            }
         }
 #pragma unroll 1
         for (int e = 0; e < LORA_NE; ++e) {
-            float m[16], bb[16], gv[16], dm[16];
-            lora_up(lora_sm, neck + tok * LORA_NE * R, tv, R, e, m);
-            load_param16(bias, pdt, (int64_t)e * C + c0, q, bb);
-            load16(dmix.p[e] + tok * C + c0, q, tv, gv);
+            float m[8], bb[8], v[8];
+            lora_up8(lora_sm, neck + tok * LORA_NE * R, tv, R, e, h, m);
+            load_param8(bias, pdt, (int64_t)e * C + cl, bb);
+            if (tv) load8(dmix.p[e] + tok * C + cl, v);
+            else for (int j = 0; j < 8; ++j) v[j] = 0.f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                dm[j] = gv[j] * dl[j];
-                dd[j] += gv[j] * (m[j] + bb[j]);
-                ds[j] += gv[j];
+            for (int j = 0; j < 8; ++j) {
+                dd[j] += v[j] * (m[j] + bb[j]);
+                ds[j] += v[j];
+                v[j] *= dl[j];                                  // d_mexp
             }
-            if (tv) store16(dmexp + ((int64_t)e * N + tok) * C + c0, q, dm);
-            // d_bias: sum over the wave's 16 tokens (lanes L of one q, fixed butterfly order),
-            // accumulated per (mix, wave, channel) in LDS by a single lane
+            if (tv) store8(dmexp + ((int64_t)e * N + tok) * C + cl, v);
+            // d_bias: sum over the wave's 16 tokens (lanes L of one q).  Transposing butterfly:
+            // at each step a lane keeps one half of its values, adds its partner's copy of that
+            // half and hands over the other half; after 4 + 2 + 1 exchanges and a last pairwise
+            // sum, lanes L and L^1 hold the 16-token sum of value j = L >> 1 (fixed order).
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float v = dm[j];
-                v += __shfl_xor(v, 1);
-                v += __shfl_xor(v, 2);
-                v += __shfl_xor(v, 4);
-                v += __shfl_xor(v, 8);
-                dm[j] = v;
-            }
-            if (L == 0) {
+            for (int s = 0; s < 3; ++s) {
+                const int msk = 8 >> s, half = 4 >> s;
+                const bool up = (L & msk) != 0;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) red[e][wv][j < 8 ? 8 * q + j : 32 + 8 * q + j - 8] += dm[j];
+                for (int i = 0; i < half; ++i) {
+                    const float send = up ? v[i] : v[i + half];
+                    const float keep = up ? v[i + half] : v[i];
+                    v[i] = keep + __shfl_xor(send, msk);
+                }
             }
+            v[0] += __shfl_xor(v[0], 1);
+            if ((L & 1) == 0) red[e][tw][cw + (L >> 1)] += v[0];
         }
         if (tv) {
-            store16f(dd_out + tok * C + c0, q, dd);
-            store16f(ds_out + tok * C + c0, q, ds);
+            *reinterpret_cast<float4*>(dd_out + tok * C + cl) = make_float4(dd[0], dd[1], dd[2], dd[3]);
+            *reinterpret_cast<float4*>(dd_out + tok * C + cl + 4) = make_float4(dd[4], dd[5], dd[6], dd[7]);
+            *reinterpret_cast<float4*>(ds_out + tok * C + cl) = make_float4(ds[0], ds[1], ds[2], ds[3]);
+            *reinterpret_cast<float4*>(ds_out + tok * C + cl + 4) = make_float4(ds[4], ds[5], ds[6], ds[7]);
         }
     }
     __syncthreads();
     for (int j = threadIdx.x; j < LORA_NE * 64; j += LORA_THR) {
         const int e = j >> 6, c = j & 63;
-        const float sum = (red[e][0][c] + red[e][1][c]) + (red[e][2][c] + red[e][3][c]);
-        part[(tb * LORA_NE + e) * C + c0 + c] = sum;
+        part[(tb * LORA_NE + e) * C + cb * 64 + c] = red[e][0][c] + red[e][1][c];
     }
 }
 

@@ -101,28 +101,18 @@ __device__ __forceinline__ void row8_vec(const float* v, int c0, float* f) {
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
 }
 __device__ __forceinline__ bf16x8 scale8(bf16x8 x, const float* f) {
-    bf16x8 y;
+    float y[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) y[s] = (__bf16)((float)x[s] * f[s]);
-    return y;
-}
-__device__ __forceinline__ uint4 pack8(const float* f) {
-    uint4 q;
-    q.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-    q.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-    q.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-    q.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
-    return q;
+    for (int s = 0; s < 8; ++s) y[s] = (float)x[s] * f[s];
+    return __builtin_bit_cast(bf16x8, pack8(y));
 }
 // hi / lo split of 8 fp32 values, packed
 __device__ __forceinline__ void pack8_split(const float* f, uint4& hi, uint4& lo) {
     float h[8], l[8];
+    hi = pack8(f);
+    unpack8(hi, h);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        h[s] = bf2f(f2bf(f[s]));
-        l[s] = f[s] - h[s];
-    }
-    hi = pack8(h);
+    for (int s = 0; s < 8; ++s) l[s] = f[s] - h[s];
     lo = pack8(l);
 }
 
@@ -210,11 +200,6 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], fl
 __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
     return u_dtype == RWKV6_BF16 ? bf2f(reinterpret_cast<const uint16_t*>(u)[idx])
                                  : reinterpret_cast<const float*>(u)[idx];
-}
-// 8 consecutive u values as fp32
-__device__ __forceinline__ void load_u8(const void* u, int u_dtype, int idx, float* f) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) f[s] = load_u(u, u_dtype, idx + s);
 }
 __device__ __forceinline__ float sum8lanes(float v) {
     v += __shfl_xor(v, 1);
@@ -447,7 +432,7 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
             float rf[8], kf[8], uf[8], bsum = 0.f;
             unpack8(nx.r[p], rf);
             unpack8(nx.k[p], kf);
-            load_u8(u, u_dtype, h * KD + c8, uf);
+            load_param8(u, u_dtype, h * KD + c8, uf);
 #pragma unroll
             for (int s8 = 0; s8 < 8; ++s8) bsum += rf[s8] * uf[s8] * kf[s8];
             bsum = sum8lanes(bsum);
@@ -518,7 +503,7 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
                 }
                 at = mfma32(kk, rb, at);                                          // A^T[tau][t]
             }
-            bf16x4 aop;
+            float xa[4];
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 float x = at[rr];
@@ -526,8 +511,9 @@ wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict
                     const int tl = 4 * lq + rr;
                     x = tl < lr ? x : (tl == lr ? bonus[t] : 0.f);
                 }
-                aop[rr] = (__bf16)x;
+                xa[rr] = x;
             }
+            const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
             for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma16(aop, ld_tr4(&Vm[0][0], 16 * J, 16 * tj), acc[tj]);
         }
@@ -604,7 +590,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         unpack8(kq, kf);
         unpack8(vq, vf);
         unpack8(dq, df);
-        load_u8(u, u_dtype, h * KD + c8, uf);
+        load_param8(u, u_dtype, h * KD + c8, uf);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             b += rf[s] * uf[s] * kf[s];
@@ -740,9 +726,10 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
-        bf16x4 aop;                                      // dA[t = 16W+lr][tau = 16J+4lq+rr]
+        float xa[4];                                     // dA[t = 16W+lr][tau = 16J+4lq+rr]
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) aop[rr] = (__bf16)((diag && 4 * lq + rr >= lr) ? 0.f : at[rr]);
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = (diag && 4 * lq + rr >= lr) ? 0.f : at[rr];
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
@@ -783,9 +770,10 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
-        bf16x4 aop;                                      // dA[t = 16I+4lq+rr][tau = 16W+lr]
+        float xa[4];                                     // dA[t = 16I+4lq+rr][tau = 16W+lr]
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) aop[rr] = (__bf16)((diag && 4 * lq + rr <= lr) ? 0.f : at[rr] * scale);
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = (diag && 4 * lq + rr <= lr) ? 0.f : at[rr] * scale;
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
@@ -820,7 +808,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             }
             at = mfma32(ra, kk, at);                               // A[t = 16I+4lq+rr][tau = 16W+lr]
         }
-        bf16x4 aop;
+        float xa[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             float x = at[rr];
@@ -828,8 +816,9 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
                 const int tl = 4 * lq + rr;
                 x = tl > lr ? x : (tl == lr ? sm.bonus[rowW] : 0.f);
             }
-            aop[rr] = (__bf16)(x * scale);
+            xa[rr] = x * scale;
         }
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 16 * (2 * hh + tp)), av[tp]);
     }
@@ -1008,7 +997,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
     if (!u || !saved || (T > 0 && (!r || !k || !v || !w || !o || !workspace)))
         return RWKV6_ERR_INVALID_ARG;
-    if (!al16(r) || !al16(k) || !al16(v) || !al16(w) || !al16(o) || !al16(saved) ||
+    if (!al16(r) || !al16(k) || !al16(v) || !al16(w) || !al16(u) || !al16(o) || !al16(saved) ||
         !al16(workspace) || (h0 && !al16(h0)) || (hT && !al16(hT)))
         return RWKV6_ERR_ALIGNMENT;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1056,7 +1045,7 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     if (!u || !du || !saved || !workspace ||
         (T > 0 && (!r || !k || !v || !w || !dO || !dr || !dk || !dv || !dw)))
         return RWKV6_ERR_INVALID_ARG;
-    if (!al16(r) || !al16(k) || !al16(v) || !al16(w) || !al16(dO) || !al16(saved) ||
+    if (!al16(r) || !al16(k) || !al16(v) || !al16(w) || !al16(u) || !al16(dO) || !al16(saved) ||
         !al16(dr) || !al16(dk) || !al16(dv) || !al16(dw) || !al16(workspace) ||
         (dhT && !al16(dhT)) || (dh0 && !al16(dh0)))
         return RWKV6_ERR_ALIGNMENT;
