@@ -92,9 +92,26 @@ __device__ __forceinline__ void split_bf16(const float* f,
     }
 }
 
-__device__ __forceinline__ float warp_sum4(float v) {
-    // sum over groups of 4 consecutive lanes
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
+// Lane exchanges without an address operand: DPP (a modifier of the consuming VALU op)
+// within rows of 16 lanes, ds_swizzle within 32 lanes; only the exchange across the two
+// 32-lane halves goes through ds_bpermute.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_mov<0xB1>(v); }   // quad_perm 1,0,3,2
+__device__ __forceinline__ float lane_xor2(float v) { return dpp_mov<0x4E>(v); }   // quad_perm 2,3,0,1
+__device__ __forceinline__ float lane_xor8(float v) { return dpp_mov<0x128>(v); }  // row_ror:8
+template <int M> __device__ __forceinline__ float lane_xor_swz(float v) {          // M < 32
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v),
+                                                                 0x1F | (M << 10)));
+}
+__device__ __forceinline__ float lane_xor32(float v) { return __shfl_xor(v, 32); }
+// Sum over aligned groups of 8 lanes; all 8 lanes get the same bits.  The last step adds
+// the other quad through row_half_mirror (lane i <-> lane 7 - i of the group).
+__device__ __forceinline__ float sum8lanes(float v) {
+    v += lane_xor1(v);
+    v += lane_xor2(v);
+    v += dpp_mov<0x141>(v);
     return v;
 }

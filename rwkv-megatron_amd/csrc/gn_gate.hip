@@ -18,12 +18,6 @@
 
 namespace {
 
-__device__ __forceinline__ float sum8lanes(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
-}
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.f / (1.f + __expf(-z)); }
 
 // element offset of (t, b, h, channel c0) in o

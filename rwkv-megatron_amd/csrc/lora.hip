@@ -230,18 +230,22 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
             // at each step a lane keeps one half of its values, adds its partner's copy of that
             // half and hands over the other half; after 4 + 2 + 1 exchanges and a last pairwise
             // sum, lanes L and L^1 hold the 16-token sum of value j = L >> 1 (fixed order).
+            {
+                const bool up = L & 8;
 #pragma unroll
-            for (int s = 0; s < 3; ++s) {
-                const int msk = 8 >> s, half = 4 >> s;
-                const bool up = (L & msk) != 0;
-#pragma unroll
-                for (int i = 0; i < half; ++i) {
-                    const float send = up ? v[i] : v[i + half];
-                    const float keep = up ? v[i + half] : v[i];
-                    v[i] = keep + __shfl_xor(send, msk);
-                }
+                for (int i = 0; i < 4; ++i) v[i] = (up ? v[i + 4] : v[i]) + lane_xor8(up ? v[i] : v[i + 4]);
             }
-            v[0] += __shfl_xor(v[0], 1);
+            {
+                const bool up = L & 4;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    v[i] = (up ? v[i + 2] : v[i]) + lane_xor_swz<4>(up ? v[i] : v[i + 2]);
+            }
+            {
+                const bool up = L & 2;
+                v[0] = (up ? v[1] : v[0]) + lane_xor2(up ? v[0] : v[1]);
+            }
+            v[0] += lane_xor1(v[0]);
             if ((L & 1) == 0) red[e][tw][cw + (L >> 1)] += v[0];
         }
         if (tv) {

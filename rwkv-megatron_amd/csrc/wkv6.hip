@@ -201,12 +201,6 @@ __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
     return u_dtype == RWKV6_BF16 ? bf2f(reinterpret_cast<const uint16_t*>(u)[idx])
                                  : reinterpret_cast<const float*>(u)[idx];
 }
-__device__ __forceinline__ float sum8lanes(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    return v;
-}
 
 // ---------------------------------------------------------------------------
 // phase A: chunk-local state (forward) / dstate (backward)
@@ -623,23 +617,33 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
     {
-        // du partial: sum over the wave's 8 rows of r k dd, then over waves in fixed order
-        float rf[8], kf[8], du8[8];
+        // du partial: sum over the wave's 8 rows (lane bits 3..5) of r k dd, then over waves
+        // in fixed order.  Transposing butterfly: at each step a lane keeps one half of its
+        // values, adds its partner's copy of that half and hands over the other half, so
+        // 4 + 2 + 1 exchanges leave lane l with the row sum of its value j(l).
+        float rf[8], kf[8], x[8];
         unpack8(rq, rf);
         unpack8(kq, kf);
         const float ddr = sm.dd[row];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            float x = rf[s] * kf[s] * ddr;
-            x += __shfl_xor(x, 8);
-            x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            du8[s] = x;
-        }
-        if (lane < 8) {
+        for (int s = 0; s < 8; ++s) x[s] = rf[s] * kf[s] * ddr;
+        {
+            const bool up = lane & 8;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) sm.red[wv][8 * lane + s] = du8[s];
+            for (int s = 0; s < 4; ++s) x[s] = (up ? x[s + 4] : x[s]) + lane_xor8(up ? x[s] : x[s + 4]);
         }
+        {
+            const bool up = lane & 16;
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                x[s] = (up ? x[s + 2] : x[s]) + lane_xor_swz<16>(up ? x[s] : x[s + 2]);
+        }
+        {
+            const bool up = lane & 32;
+            x[0] = (up ? x[1] : x[0]) + lane_xor32(up ? x[0] : x[1]);
+        }
+        const int j = ((lane >> 1) & 4) | ((lane >> 3) & 2) | ((lane >> 5) & 1);
+        sm.red[wv][c8 + j] = x[0];
         // tables
         const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
         if (part < 4) {
@@ -751,19 +755,22 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             for (int tp = 0; tp < 2; ++tp)
                 tmp[tp] = mfma32(a, ld_row8(&dSm[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
         }
+        float pk[2];
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
             ak[tp] = tmp[tp] * sm.eg[W][cb + lr];
             // this wave's share of sum_t Km[t][i] ak[t][i] = rowsum((S_out - e^{G_63} S_in) dS)
             const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
-            float p = 0.f;
+            pk[tp] = 0.f;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) p += ((float)kh[rr] + (float)kl[rr]) * ak[tp][rr];
-            p += __shfl_xor(p, 16);
-            p += __shfl_xor(p, 32);
-            if (lq == 0) sm.Pk[W][cb + lr] = p;
+            for (int rr = 0; rr < 4; ++rr) pk[tp] += ((float)kh[rr] + (float)kl[rr]) * ak[tp][rr];
         }
+        // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
+        const bool up = lane & 16;
+        float p = (up ? pk[1] : pk[0]) + lane_xor_swz<16>(up ? pk[0] : pk[1]);
+        p += lane_xor32(p);
+        if (lq < 2) sm.Pk[W][16 * (2 * hh + lq) + lr] = p;
     }
     for (int I = W; I < 4; ++I) {
         const bool diag = (I == W);
