@@ -279,46 +279,53 @@ wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
 }
 
 // ---------------------------------------------------------------------------
-// phase B: state scans (fp32 carry; fp32 S_loc / bf16 dS_loc in, bf16 states out; one
-// thread per state element, coalesced)
+// phase B: state scans (fp32 carry; fp32 S_loc / bf16 dS_loc in, bf16 states out)
 // ---------------------------------------------------------------------------
-// Each thread issues the loads of SCAN_U chunks before it walks them (the loads do not
-// depend on the carry), so a wave keeps SCAN_U requests in flight.
-#define SCAN_U 32
+// A thread carries two adjacent elements of one state row (8-byte fp32 / 4-byte bf16
+// accesses; a wave covers two rows), and issues the loads of SCAN_U chunks before it walks
+// them (the loads do not depend on the carry), so a wave keeps SCAN_U requests in flight.
+#define SCAN_U 32                          // dstate scan: bf16 pairs in flight per thread
+#define SCAN_UF 8                          // state scan: fp32 pairs (8 x 8 B per thread)
+#define SCAN_BLK 8                         // blocks per (b,h): 8 x 256 threads x 2 elements
 
 // Hs[c] = bf16(S_in(c)) for c = 0..NT (Hs[NT] = final state); hT = S_in(NT) fp32.
 __global__ void __launch_bounds__(NTHR)
 wkv6_state_scan_fwd(const float* __restrict__ Sloc, const float* __restrict__ decay,
                     const float* __restrict__ h0, uint16_t* __restrict__ Hs,
                     float* __restrict__ hT, int NT) {
-    const int bh = blockIdx.x >> 4;
-    const int e = ((blockIdx.x & 15) << 8) + threadIdx.x;
+    const int bh = blockIdx.x / SCAN_BLK;
+    const int e = ((blockIdx.x % SCAN_BLK) * NTHR + threadIdx.x) * 2;
     const int i = e >> 6;
-    float S = h0 ? h0[(size_t)bh * KD * KD + e] : 0.f;
+    float2 S = h0 ? *reinterpret_cast<const float2*>(h0 + (size_t)bh * KD * KD + e) : make_float2(0.f, 0.f);
     const float* sl = Sloc + (size_t)bh * NT * KD * KD + e;
     const float* dc = decay + (size_t)bh * NT * KD + i;
-    uint16_t* hs = Hs + (size_t)bh * (NT + 1) * KD * KD + e;
+    uint32_t* hs = reinterpret_cast<uint32_t*>(Hs + (size_t)bh * (NT + 1) * KD * KD + e);
+    constexpr size_t ST = KD * KD / 2;     // state stride in element pairs
     int c = 0;
-    for (; c + SCAN_U <= NT; c += SCAN_U) {
-        float l[SCAN_U];
-        float d[SCAN_U];
+    for (; c + SCAN_UF <= NT; c += SCAN_UF) {
+        float2 l[SCAN_UF];
+        float d[SCAN_UF];
 #pragma unroll
-        for (int q = 0; q < SCAN_U; ++q) {
-            l[q] = sl[(size_t)(c + q) * KD * KD];
+        for (int q = 0; q < SCAN_UF; ++q) {
+            l[q] = *reinterpret_cast<const float2*>(sl + (size_t)(c + q) * KD * KD);
             d[q] = dc[(c + q) * KD];
         }
 #pragma unroll
-        for (int q = 0; q < SCAN_U; ++q) {
-            hs[(size_t)(c + q) * KD * KD] = f2bf(S);
-            S = d[q] * S + l[q];
+        for (int q = 0; q < SCAN_UF; ++q) {
+            hs[(c + q) * ST] = pk2(S.x, S.y);
+            S.x = d[q] * S.x + l[q].x;
+            S.y = d[q] * S.y + l[q].y;
         }
     }
     for (; c < NT; ++c) {
-        hs[(size_t)c * KD * KD] = f2bf(S);
-        S = dc[c * KD] * S + sl[(size_t)c * KD * KD];
+        hs[c * ST] = pk2(S.x, S.y);
+        const float2 l = *reinterpret_cast<const float2*>(sl + (size_t)c * KD * KD);
+        const float d = dc[c * KD];
+        S.x = d * S.x + l.x;
+        S.y = d * S.y + l.y;
     }
-    hs[(size_t)NT * KD * KD] = f2bf(S);
-    if (hT) hT[(size_t)bh * KD * KD + e] = S;
+    hs[NT * ST] = pk2(S.x, S.y);
+    if (hT) *reinterpret_cast<float2*>(hT + (size_t)bh * KD * KD + e) = S;
 }
 
 // dHs[c] = bf16(dS_out(c)) (gradient w.r.t. the state after chunk c); dh0 = dS_in(0).
@@ -326,33 +333,38 @@ __global__ void __launch_bounds__(NTHR)
 wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict__ decay,
                     const float* __restrict__ dhT, uint16_t* __restrict__ dHs,
                     float* __restrict__ dh0, int NT) {
-    const int bh = blockIdx.x >> 4;
-    const int e = ((blockIdx.x & 15) << 8) + threadIdx.x;
+    const int bh = blockIdx.x / SCAN_BLK;
+    const int e = ((blockIdx.x % SCAN_BLK) * NTHR + threadIdx.x) * 2;
     const int i = e >> 6;
-    float dS = dhT ? dhT[(size_t)bh * KD * KD + e] : 0.f;
-    const uint16_t* sl = dSloc + (size_t)bh * NT * KD * KD + e;
+    float2 dS = dhT ? *reinterpret_cast<const float2*>(dhT + (size_t)bh * KD * KD + e) : make_float2(0.f, 0.f);
+    const uint32_t* sl = reinterpret_cast<const uint32_t*>(dSloc + (size_t)bh * NT * KD * KD + e);
     const float* dc = decay + (size_t)bh * NT * KD + i;
-    uint16_t* hs = dHs + (size_t)bh * NT * KD * KD + e;
+    uint32_t* hs = reinterpret_cast<uint32_t*>(dHs + (size_t)bh * NT * KD * KD + e);
+    constexpr size_t ST = KD * KD / 2;
     int c = NT - 1;
     for (; c - (SCAN_U - 1) >= 0; c -= SCAN_U) {
-        uint16_t l[SCAN_U];
+        uint32_t l[SCAN_U];
         float d[SCAN_U];
 #pragma unroll
         for (int q = 0; q < SCAN_U; ++q) {
-            l[q] = sl[(size_t)(c - q) * KD * KD];
+            l[q] = sl[(c - q) * ST];
             d[q] = dc[(c - q) * KD];
         }
 #pragma unroll
         for (int q = 0; q < SCAN_U; ++q) {
-            hs[(size_t)(c - q) * KD * KD] = f2bf(dS);
-            dS = d[q] * dS + bf2f(l[q]);
+            hs[(c - q) * ST] = pk2(dS.x, dS.y);
+            dS.x = d[q] * dS.x + __uint_as_float(l[q] << 16);
+            dS.y = d[q] * dS.y + __uint_as_float(l[q] & 0xffff0000u);
         }
     }
     for (; c >= 0; --c) {
-        hs[(size_t)c * KD * KD] = f2bf(dS);
-        dS = dc[c * KD] * dS + bf2f(sl[(size_t)c * KD * KD]);
+        hs[c * ST] = pk2(dS.x, dS.y);
+        const uint32_t l = sl[c * ST];
+        const float d = dc[c * KD];
+        dS.x = d * dS.x + __uint_as_float(l << 16);
+        dS.y = d * dS.y + __uint_as_float(l & 0xffff0000u);
     }
-    if (dh0) dh0[(size_t)bh * KD * KD + e] = dS;
+    if (dh0) *reinterpret_cast<float2*>(dh0 + (size_t)bh * KD * KD + e) = dS;
 }
 
 // ---------------------------------------------------------------------------
@@ -1023,7 +1035,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
-    hipLaunchKernelGGL(wkv6_state_scan_fwd, dim3((unsigned)BH * 16), dim3(NTHR), 0, s, Sloc, decay,
+    hipLaunchKernelGGL(wkv6_state_scan_fwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, Sloc, decay,
                        h0, Hs, hT, (int)NT);
     mark(phase_events, 3, s);
     mark(phase_events, 4, s);
@@ -1077,7 +1089,7 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
-    hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * 16), dim3(NTHR), 0, s, dSloc,
+    hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
                        decay, dhT, dHs, dh0, (int)NT);
     mark(phase_events, 3, s);
     if (NT > 0) {
