@@ -811,21 +811,28 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) av[tp] = mfma32(a, ld_tr8(&dSm[0][0], 32 * ks, 16 * (2 * hh + tp)), av[tp]);
     }
+    // Km_W q_W, the source operand of every off-diagonal pair (I, W)
+    bf16x8 kqw[2];
+    if (W < 3) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            float f[8];
+            row8_vec(sm.kb[W], 32 * ks, f);
+            kqw[ks] = scale8(ld_row8(KH, rowW, 32 * ks), f);
+        }
+    }
     for (int I = W; I < 4; ++I) {
         const bool diag = (I == W);
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             bf16x8 ra = ld_row8(RH, 16 * I + lr, 32 * ks);
-            bf16x8 kk = ld_row8(KH, rowW, 32 * ks);
             if (!diag) {
                 float f[8];
                 row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
                 ra = scale8(ra, f);
-                row8_vec(sm.kb[W], 32 * ks, f);
-                kk = scale8(kk, f);
             }
-            at = mfma32(ra, kk, at);                               // A[t = 16I+4lq+rr][tau = 16W+lr]
+            at = mfma32(ra, diag ? ld_row8(KH, rowW, 32 * ks) : kqw[ks], at);   // A[16I+4lq+rr][16W+lr]
         }
         float xa[4];
 #pragma unroll
