@@ -41,6 +41,8 @@
 #define CL 64            // chunk length (tokens)
 #define TS 72            // LDS row stride of a bf16 64x64 tile (elements): 144 B rows
 #define GS 72            // LDS row stride of an fp32 64x64 tile (elements)
+#define XS 68            // row stride of the epilogue's fp32 x / y views: rows 4 apart land 16
+                         // banks apart, so the 4 row groups of a wave's column writes do not collide
 #define GSG 69           // row stride of the fp32 cumulative-decay view: 69 = 5 (mod 64) banks keeps
                          // the row-wise reads of 8 consecutive rows by 8 lanes each conflict-free
 #define NTHR 256
@@ -871,8 +873,9 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         }
     }
     __syncthreads();                       // all waves are done with the operand tiles
-    float (*Xs)[GS] = sm.A;
-    float (*Ys)[GS] = reinterpret_cast<float (*)[GS]>(&sm.Vm[0][0]);
+    float (*Xs)[XS] = reinterpret_cast<float (*)[XS]>(&sm.A[0][0]);
+    float (*Ys)[XS] = reinterpret_cast<float (*)[XS]>(&sm.Vm[0][0]);
+    static_assert(CL * XS * 4 <= sizeof(sm.A) && CL * XS * 4 <= 2 * sizeof(tile_t), "x / y views");
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
