@@ -593,6 +593,8 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         sstore16(sm.Vm, row, c8, vq);
         sstore16(sm.Dm, row, c8, dq);
         sstore16(sm.RmL, row, c8, gload16s(w + base, row, c8, nvalid, rs));     // w scratch
+        sstore16(sm.RmH, row, c8, rq);                   // raw r, k: read back below in the
+        sstore16(sm.KmH, row, c8, kq);                   // lane layout of the accumulators
         float rf[8], kf[8], uf[8], vf[8], df[8], b = 0.f, d = 0.f;
         unpack8(rq, rf);
         unpack8(kq, kf);
@@ -624,12 +626,19 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         d = sum8lanes(d);
         if ((threadIdx.x & 7) == 0) sm.Dv[row] = d;
     }
-    __syncthreads();
-    build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
-
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
+    __syncthreads();
+    // raw r, k at this lane's accumulator positions (tokens 16W+4lq+rr, channel 32hh+16tp+lr),
+    // read before build_G's barriers (after them the operand tiles overwrite RmH and KmH)
+    bf16x4 rrw[2], krw[2];
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+        rrw[tp] = ld_tr4(&sm.RmH[0][0], 16 * W, 16 * (2 * hh + tp));
+        krw[tp] = ld_tr4(&sm.KmH[0][0], 16 * W, 16 * (2 * hh + tp));
+    }
+    build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
     {
         // du partial: sum over the wave's 8 rows (lane bits 3..5) of r k dd, then over waves
         // in fixed order.  Transposing butterfly: at each step a lane keeps one half of its
@@ -691,8 +700,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         sstore16(sm.KmL, row, c8, lo);
     }
     // epilogue factors at this lane's accumulator positions (token 16W+4lq+rr, channel cb+lr)
-    // Fm, Fk and the factors r / Rm = 1 / Fm, k / Km = 1 / Fk (as exponentials, not divisions)
-    float Fm[2][4], Fk[2][4], iFm[2][4], iFk[2][4];
+    float Fm[2][4], Fk[2][4];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
@@ -700,11 +708,8 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
-            const float em = (tt > 0 ? Gv[tt - 1][i] : 0.f) - m, ek = m - Gv[tt][i];
-            Fm[tp][rr] = ex2(em);
-            iFm[tp][rr] = ex2(-em);
-            Fk[tp][rr] = ex2(ek);
-            iFk[tp][rr] = ex2(-ek);
+            Fm[tp][rr] = ex2((tt > 0 ? Gv[tt - 1][i] : 0.f) - m);
+            Fk[tp][rr] = ex2(m - Gv[tt][i]);
         }
     }
     __syncthreads();                       // G fully consumed
@@ -774,11 +779,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
             ak[tp] = tmp[tp] * sm.eg[W][cb + lr];
-            // this wave's share of sum_t Km[t][i] ak[t][i] = rowsum((S_out - e^{G_63} S_in) dS)
-            const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
+            // this wave's share of sum_t k Fk ak[t][i] = rowsum((S_out - e^{G_63} S_in) dS),
+            // formed from the same products the epilogue's y terms take off again
             pk[tp] = 0.f;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) pk[tp] += ((float)kh[rr] + (float)kl[rr]) * ak[tp][rr];
+            for (int rr = 0; rr < 4; ++rr) pk[tp] += (float)krw[tp][rr] * (Fk[tp][rr] * ak[tp][rr]);
         }
         // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
         const bool up = lane & 16;
@@ -855,21 +860,19 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     float drv[2][4], dkv[2][4], xv[2][4], yv[2][4];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
-        const int cb = 16 * (2 * hh + tp), i = cb + lr;
-        const bf16x4 rh = ld_tr4(RH, 16 * W, cb), rl = ld_tr4(RL, 16 * W, cb);
-        const bf16x4 kh = ld_tr4(KH, 16 * W, cb), kl = ld_tr4(KL, 16 * W, cb);
+        const int i = 16 * (2 * hh + tp) + lr;
         const float ui = scale * load_u(u, u_dtype, h * KD + i);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
-            const float rmv = (float)rh[rr] + (float)rl[rr];
-            const float kmv = (float)kh[rr] + (float)kl[rr];
-            const float accr = scale * ar[tp][rr], acck = ak[tp][rr];
+            const float rv = (float)rrw[tp][rr], kv = (float)krw[tp][rr];
+            const float drh = Fm[tp][rr] * (scale * ar[tp][rr]);   // r Fm acc_r = Rm acc_r
+            const float dkh = Fk[tp][rr] * ak[tp][rr];             // k Fk acc_k = Km acc_k
             const float udd = ui * sm.dd[tt];
-            drv[tp][rr] = Fm[tp][rr] * accr + udd * (kmv * iFk[tp][rr]);
-            dkv[tp][rr] = Fk[tp][rr] * acck + udd * (rmv * iFm[tp][rr]);
-            xv[tp][rr] = rmv * accr - kmv * acck;
-            yv[tp][rr] = -kmv * acck;
+            drv[tp][rr] = drh + udd * kv;
+            dkv[tp][rr] = dkh + udd * rv;
+            xv[tp][rr] = rv * drh - kv * dkh;
+            yv[tp][rr] = -kv * dkh;
         }
     }
     __syncthreads();                       // all waves are done with the operand tiles
