@@ -4,10 +4,13 @@
 // /root/reference/rwkv_megatron/rwkv6_layer_specs.py:339.  The recurrence is
 //   o_t = s * r_t^T (S_{t-1} + diag(u) k_t v_t^T),   S_t = diag(exp(w_t)) S_{t-1} + k_t v_t^T.
 //
-// Decomposition (three phases each way, all deterministic):
-//   chunk_local<fwd> per (b,h,chunk): S_loc = sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T  [MFMA]
-//   state_scan_fwd   per (b,h,elem) : S_in(c+1) = e^{G_63(c)} S_in(c) + S_loc(c)  fp32, coalesced
-//   fwd_chunk_output persistent     : o = (r e^{G_{t-1}}) S_in + intra-chunk attention   [MFMA]
+// Decomposition (all deterministic):
+//   fwd_walk<pre>    per (b,h,segment), segments 0..P-2 only when B*H is small: the segment's
+//                    local end state and total decay (k, v, w read once)
+//   fwd_walk<out>    per (b,h,segment): walks the chunks in order with the fp32 state in
+//                    registers: o = (r e^{G_{t-1}}) S_in + intra-chunk attention, then
+//                    S_out = e^{G_63} S_in + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T  [MFMA];
+//                    writes o, bf16 S_in per chunk and the chunk decays for the backward
 //   chunk_local<bwd> per (b,h,chunk): dS_loc = s * sum_t (r_t e^{G_{t-1}}) dO_t^T        [MFMA]
 //   state_scan_bwd   per (b,h,elem) : dS_out(c-1) = e^{G_63(c)} dS_out(c) + dS_loc(c)
 //   bwd_chunk_grads  per (b,h,chunk): dr, dk, dv, dw, du-partials                        [MFMA]
@@ -192,8 +195,9 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], fl
     }
     tot[part * 64 + i] = run;
     __syncthreads();
-    float off = 0.f;
-    for (int p = 0; p < part; ++p) off += tot[p * 64 + i];
+    float off = 0.f;                       // same order as a loop over p < part
+#pragma unroll
+    for (int p = 0; p < NP - 1; ++p) off += p < part ? tot[p * 64 + i] : 0.f;
 #pragma unroll
     for (int s = 0; s < PL; ++s) Gm[PL * part + s][i] = loc[s] + off;
     __syncthreads();
@@ -290,46 +294,6 @@ wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
 #define SCAN_UF 8                          // state scan: fp32 pairs (8 x 8 B per thread)
 #define SCAN_BLK 8                         // blocks per (b,h): 8 x 256 threads x 2 elements
 
-// Hs[c] = bf16(S_in(c)) for c = 0..NT (Hs[NT] = final state); hT = S_in(NT) fp32.
-__global__ void __launch_bounds__(NTHR)
-wkv6_state_scan_fwd(const float* __restrict__ Sloc, const float* __restrict__ decay,
-                    const float* __restrict__ h0, uint16_t* __restrict__ Hs,
-                    float* __restrict__ hT, int NT) {
-    const int bh = blockIdx.x / SCAN_BLK;
-    const int e = ((blockIdx.x % SCAN_BLK) * NTHR + threadIdx.x) * 2;
-    const int i = e >> 6;
-    float2 S = h0 ? *reinterpret_cast<const float2*>(h0 + (size_t)bh * KD * KD + e) : make_float2(0.f, 0.f);
-    const float* sl = Sloc + (size_t)bh * NT * KD * KD + e;
-    const float* dc = decay + (size_t)bh * NT * KD + i;
-    uint32_t* hs = reinterpret_cast<uint32_t*>(Hs + (size_t)bh * (NT + 1) * KD * KD + e);
-    constexpr size_t ST = KD * KD / 2;     // state stride in element pairs
-    int c = 0;
-    for (; c + SCAN_UF <= NT; c += SCAN_UF) {
-        float2 l[SCAN_UF];
-        float d[SCAN_UF];
-#pragma unroll
-        for (int q = 0; q < SCAN_UF; ++q) {
-            l[q] = *reinterpret_cast<const float2*>(sl + (size_t)(c + q) * KD * KD);
-            d[q] = dc[(c + q) * KD];
-        }
-#pragma unroll
-        for (int q = 0; q < SCAN_UF; ++q) {
-            hs[(c + q) * ST] = pk2(S.x, S.y);
-            S.x = d[q] * S.x + l[q].x;
-            S.y = d[q] * S.y + l[q].y;
-        }
-    }
-    for (; c < NT; ++c) {
-        hs[c * ST] = pk2(S.x, S.y);
-        const float2 l = *reinterpret_cast<const float2*>(sl + (size_t)c * KD * KD);
-        const float d = dc[c * KD];
-        S.x = d * S.x + l.x;
-        S.y = d * S.y + l.y;
-    }
-    hs[NT * ST] = pk2(S.x, S.y);
-    if (hT) *reinterpret_cast<float2*>(hT + (size_t)bh * KD * KD + e) = S;
-}
-
 // dHs[c] = bf16(dS_out(c)) (gradient w.r.t. the state after chunk c); dh0 = dS_in(0).
 __global__ void __launch_bounds__(NTHR)
 wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict__ decay,
@@ -369,169 +333,307 @@ wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict_
     if (dh0) *reinterpret_cast<float2*>(dh0 + (size_t)bh * KD * KD + e) = dS;
 }
 
-// ---------------------------------------------------------------------------
-// phase C (forward): chunk output
-// ---------------------------------------------------------------------------
-// Wave W owns target tokens [16W, 16W+16) and all 64 value columns:
-//   o_t = s [ (Rm_t e^{mu_W}) S_in + sum_{J<W} A_WJ v_J + A_WW v_W ],
-//   A_WJ[t][tau] = sum_i Rm[t][i] f_WJ[i] Km[tau][i]; A_WW strictly causal + u-bonus diagonal.
-__device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }   // I > J
+// Index of the cross-block pair (I, J), I > J, in the 6-entry tables.
+__device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }
 
-// Persistent: each workgroup walks jobs (b*h, chunk) with a grid stride and prefetches the
-// next job's tiles into registers while it computes the current one.
-struct FwdPrefetch {
-    uint4 r[2], k[2], v[2], w[2], s[2];
+// ---------------------------------------------------------------------------
+// forward as a walk: one workgroup per (b,h, segment) carries the fp32 state in registers
+// ---------------------------------------------------------------------------
+// A segment is a run of consecutive chunks of one sequence.  Per chunk the workgroup reads
+// r, k, v, w once (prefetched into registers one chunk ahead), writes o, the bf16 S_in the
+// backward consumes and the chunk decay, and advances its state
+//   S_out = diag(e^{G_63}) S_in + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T      [MFMA]
+// in the accumulator registers.  When B*H alone gives too few workgroups for the device,
+// each sequence is cut into P segments: wkv6_fwd_walk<.., false> first walks segments
+// 0..P-2 for their local end state and total log-decay only (reading k, v, w), and each
+// output walk starts from
+//   S_start(p) = A(p-1) S_start(p-1) + S_seg(p-1),  S_start(0) = h0.
+// 8 waves: wave (W, hh) owns target tokens [16W, 16W+16) x value columns [32hh, 32hh+32)
+// of o, and state rows [16W, 16W+16) x columns [32hh, 32hh+32): lane (lq, lr) holds
+// S[16W + 4lq + rr][32hh + 16tp + lr] in acc[tp][rr].
+#define NTHR_W 512
+#ifndef WALK_TARGET_ITEMS
+#define WALK_TARGET_ITEMS 256   // workgroups a forward should offer (one per CU of an MI355X)
+#endif
+#define WALK_MIN_CHUNKS 8       // shortest segment worth a pre-pass
+#ifndef WALK_WPE
+#define WALK_WPE 2              // waves per SIMD the walk is compiled for (1 block of 8 waves / CU)
+#endif
+
+struct WalkSmem {
+    tile_t Rm, Km, Kt, Vm, Ot;        // operand tiles, o staging
+    tile_t Sin[2];                    // bf16 S_in of chunk c in Sin[c & 1]
+    float G[CL * GSG];                // cumulative log2-decay
+    float emu[4][KD], fp[6][KD], kb[3][KD];
+    float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
+    float tot[NTHR_W];                // build_G scratch
+    float bonus[CL];
+    float uh[KD];                     // u of this head
 };
+static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
 
-template <bool SEQ>
-__device__ __forceinline__ void fwd_issue(FwdPrefetch& f, const uint16_t* __restrict__ r,
-                                          const uint16_t* __restrict__ k,
-                                          const uint16_t* __restrict__ v,
-                                          const uint16_t* __restrict__ w,
-                                          const uint16_t* __restrict__ Hs, int job, int B, int H,
-                                          int T, int NT) {
-    const int bh = job / NT, c = job - bh * NT;
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
-    const uint16_t* sp = Hs + ((size_t)bh * (NT + 1) + c) * KD * KD;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        f.r[p] = gload16s(r + base, row, c8, nvalid, rs);
-        f.k[p] = gload16s(k + base, row, c8, nvalid, rs);
-        f.v[p] = gload16s(v + base, row, c8, nvalid, rs);
-        f.w[p] = gload16s(w + base, row, c8, nvalid, rs);
-        f.s[p] = gload16(sp, row, c8, KD);
-    }
+// Segments per sequence (shared by the workspace query and the launch).
+inline int walk_segments(int64_t BH, int64_t NT) {
+    if (NT <= 0) return 1;
+    int64_t P = (WALK_TARGET_ITEMS + BH - 1) / BH;
+    P = std::min<int64_t>(P, std::max<int64_t>(1, NT / WALK_MIN_CHUNKS));
+    const int64_t NC = (NT + P - 1) / P;               // chunks per segment
+    return (int)((NT + NC - 1) / NC);                   // no empty segment
 }
 
+struct WalkPrefetch {
+    uint4 r, k, v, w;
+};
+
+// Rows >= nvalid (>= 1) read row nvalid-1 and return zero: no branch around the load.
+__device__ __forceinline__ uint4 gload16c(const uint16_t* __restrict__ src, int row, int c8,
+                                          int nvalid, size_t rs) {
+    const uint4 x = *reinterpret_cast<const uint4*>(src + (size_t)min(row, nvalid - 1) * rs + c8);
+    return row < nvalid ? x : make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <bool SEQ, bool OUT>
+__device__ __forceinline__ void walk_issue(WalkPrefetch& f, const uint16_t* __restrict__ r,
+                                           const uint16_t* __restrict__ k,
+                                           const uint16_t* __restrict__ v,
+                                           const uint16_t* __restrict__ w, int bh, int c, int B,
+                                           int H, int T) {
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    if (OUT) f.r = gload16c(r + base, row, c8, nvalid, rs);
+    f.k = gload16c(k + base, row, c8, nvalid, rs);
+    f.v = gload16c(v + base, row, c8, nvalid, rs);
+    f.w = gload16c(w + base, row, c8, nvalid, rs);
+}
+
+// Global stores of chunk c (o from Ot, S_in from Sin[c & 1], the chunk decay).  Issued one
+// chunk late, before the next prefetch: the wait for a prefetch then never waits on a store.
+__device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restrict__ o,
+                                           uint16_t* __restrict__ Hs, float* __restrict__ decay,
+                                           int bh, int c, int T, int NT) {
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    if (row < nvalid)
+        *reinterpret_cast<uint4*>(o + ((size_t)bh * T + t0 + row) * KD + c8) =
+            *reinterpret_cast<const uint4*>(&sm.Ot[row][c8]);
+    *reinterpret_cast<uint4*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8) =
+        *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8]);
+    if (threadIdx.x < KD) decay[((size_t)bh * NT + c) * KD + threadIdx.x] = sm.dec[c & 1][threadIdx.x];
+}
+
+// OUT = true : output walk over segment blockIdx.x % P of sequence blockIdx.x / P.
+// OUT = false: state pre-pass over segment blockIdx.x % (P-1) (segments 0..P-2): writes
+//              S_seg (fp32 [64][64]) and A_seg (total log2-decay [64]) to Sseg / Aseg.
 // SEQ: r, k, v and the pre-activation decay are sequence-first; o is always head-first.
-template <bool SEQ>
-__global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(3, 3)))
-wkv6_fwd_chunk_output(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
-                      const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
-                      const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ Hs,
-                      uint16_t* __restrict__ o, float scale, int B, int H, int T, int NT,
-                      int njobs) {
-    __shared__ __attribute__((aligned(16))) tile_t Rm, Km, Vm;
-    __shared__ __attribute__((aligned(16))) float RegA[CL][GS];   // G, then the S_in tile
-    __shared__ __attribute__((aligned(16))) float emu[4][KD], fp[6][KD], kb[3][KD];
-    __shared__ float tot[NTHR], bonus[CL];
-    uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&RegA[0][0]);
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(&RegA[0][0]);
-    const int lane = threadIdx.x & 63, W = threadIdx.x >> 6;
+template <bool SEQ, bool OUT>
+__global__ void __launch_bounds__(NTHR_W) __attribute__((amdgpu_waves_per_eu(WALK_WPE)))
+wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+              const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
+              const void* __restrict__ u, int u_dtype, const float* __restrict__ h0,
+              uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float* __restrict__ decay,
+              float* __restrict__ hT, float* __restrict__ Sseg, float* __restrict__ Aseg,
+              float scale, int B, int H, int T, int NT, int P) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    WalkSmem& sm = *reinterpret_cast<WalkSmem*>(smem_raw);
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
+    const int nseg = OUT ? P : P - 1;
+    const int bh = blockIdx.x / nseg, seg = blockIdx.x - bh * nseg, h = bh % H;
+    const int NC = (NT + P - 1) / P;
+    const int c_begin = seg * NC, c_end = min(NT, c_begin + NC);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
-    const int t = 16 * W + lr;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    const size_t sbase = (size_t)bh * KD * KD;
 
-    FwdPrefetch nx;
-    if ((int)blockIdx.x < njobs) fwd_issue<SEQ>(nx, r, k, v, w, Hs, blockIdx.x, B, H, T, NT);
-    for (int job = blockIdx.x; job < njobs; job += gridDim.x) {
-        const int bh = job / NT, c = job - bh * NT, h = bh % H;
-        const int t0 = c * CL, nvalid = min(CL, T - t0);
-        const size_t obase = ((size_t)bh * T + t0) * KD;       // o: head-first
-        uint4 kc[2], sc[2];                    // k and S_in of this job stay in registers
-        __syncthreads();                       // the previous job is done with every tile
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-            sstore16(Vm, row, c8, nx.v[p]);
-            sstore16(Rm, row, c8, nx.r[p]);                  // raw r, scaled in place below
-            sstore16(Km, row, c8, nx.w[p]);                  // w scratch
-            float rf[8], kf[8], uf[8], bsum = 0.f;
-            unpack8(nx.r[p], rf);
-            unpack8(nx.k[p], kf);
-            load_param8(u, u_dtype, h * KD + c8, uf);
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8) bsum += rf[s8] * uf[s8] * kf[s8];
-            bsum = sum8lanes(bsum);
-            if ((threadIdx.x & 7) == 0) bonus[row] = bsum;
-            kc[p] = nx.k[p];
-            sc[p] = nx.s[p];
-        }
-        if (job + (int)gridDim.x < njobs)
-            fwd_issue<SEQ>(nx, r, k, v, w, Hs, job + gridDim.x, B, H, T, NT);
-        __syncthreads();
-        build_G<NTHR, SEQ>(Km, Gm, tot, nvalid);
-        {
-            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-            emu[part][i] = ex2(Gm[16 * part + 7][i]);
-            if (part < 3) kb[part][i] = ex2(Gm[16 * part + 15][i] - Gm[16 * part + 7][i]);
-            for (int pi = part; pi < 6; pi += 4) {
-                const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 15][i]);
-            }
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-            const int mrow = 16 * (row >> 4) + 7;
-            float rf[8], kf[8], a[8], b[8];
-            unpack8(*reinterpret_cast<const uint4*>(&Rm[row][c8]), rf);
-            unpack8(kc[p], kf);
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8) {
-                const float m = Gm[mrow][c8 + s8];
-                const float gm1 = row > 0 ? Gm[row - 1][c8 + s8] : 0.f;
-                a[s8] = rf[s8] * ex2(gm1 - m);
-                b[s8] = kf[s8] * ex2(m - Gm[row][c8 + s8]);
-            }
-            sstore16(Rm, row, c8, pack8(a));
-            sstore16(Km, row, c8, pack8(b));
-        }
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-            sstore16(Sin, row, c8, sc[p]);
-        }
-        __syncthreads();
+    WalkPrefetch nx;
+    if (c_begin < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c_begin, B, H, T);
 
-        f32x4 acc[4] = {};
+    // ---- starting state (a pre-pass segment starts from zero) ----
+    f32x4 acc[2];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            float f[8];
-            dir8_vec(emu[W], 32 * ks, f);
-            const bf16x8 a = scale8(ld_dir8(&Rm[0][0], t, 32 * ks), f);
+    for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Sin[0][0], 32 * ks, 16 * tj), acc[tj]);
-        }
-        for (int J = 0; J <= W; ++J) {
-            const bool diag = (J == W);
-            f32x4 at = {};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                bf16x8 rb = ld_row8(&Rm[0][0], t, 32 * ks);
-                bf16x8 kk = ld_row8(&Km[0][0], 16 * J + lr, 32 * ks);
-                if (!diag) {
-                    float f[8];
-                    row8_vec(fp[pair_index(W, J)], 32 * ks, f);
-                    rb = scale8(rb, f);
-                    row8_vec(kb[J], 32 * ks, f);
-                    kk = scale8(kk, f);
-                }
-                at = mfma32(kk, rb, at);                                          // A^T[tau][t]
-            }
-            float xa[4];
+        for (int rr = 0; rr < 4; ++rr)
+            acc[tp][rr] = (OUT && h0) ? h0[sbase + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr]
+                                      : 0.f;
+    if (OUT) {
+        for (int q = 0; q < seg; ++q) {
+            const size_t sq = (size_t)bh * (P - 1) + q;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-                float x = at[rr];
-                if (diag) {
-                    const int tl = 4 * lq + rr;
-                    x = tl < lr ? x : (tl == lr ? bonus[t] : 0.f);
-                }
-                xa[rr] = x;
-            }
-            const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+                const int i = 16 * W + 4 * lq + rr;
+                const float a = ex2(Aseg[sq * KD + i]);
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma16(aop, ld_tr4(&Vm[0][0], 16 * J, 16 * tj), acc[tj]);
+                for (int tp = 0; tp < 2; ++tp)
+                    acc[tp][rr] = a * acc[tp][rr] + Sseg[sq * KD * KD + i * KD + 32 * hh + 16 * tp + lr];
+            }
+        }
+        if (threadIdx.x < KD) sm.uh[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
+        __syncthreads();
+    }
+    float gsum = 0.f;                      // pre-pass: total log2-decay of channel threadIdx.x
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int nvalid = min(CL, T - c * CL);
+        // Every tile written here was last read before the previous chunk's final barrier
+        // (Sin[c & 1] two chunks ago).  Raw r and k wait in Rm and Km.
+        sstore16(sm.Vm, row, c8, nx.v);
+        sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
+        sstore16(sm.Km, row, c8, nx.k);
+        if (OUT) {
+            sstore16(sm.Rm, row, c8, nx.r);
+            float rf[8], kf[8], bsum = 0.f;
+            unpack8(nx.r, rf);
+            unpack8(nx.k, kf);
+            const float4 ua = *reinterpret_cast<const float4*>(&sm.uh[c8]);
+            const float4 ub = *reinterpret_cast<const float4*>(&sm.uh[c8 + 4]);
+            const float uf[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) bsum += rf[s] * uf[s] * kf[s];
+            bsum = sum8lanes(bsum);
+            if ((threadIdx.x & 7) == 0) sm.bonus[row] = bsum;
+            // S_in of this chunk, bf16, for the inter-chunk product and the backward
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
+            if (c > c_begin) walk_store(sm, o, Hs, decay, bh, c - 1, T, NT);
+        }
+        if (c + 1 < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c + 1, B, H, T);
+        __syncthreads();
+        build_G<NTHR_W, SEQ>(sm.Kt, Gm, sm.tot, nvalid);
+        // tables and operand tiles (the w scratch in Kt was consumed by build_G)
+        {
+            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+            if (OUT) {
+                if (part < 4) {
+                    const float m = Gm[16 * part + 7][i];
+                    sm.emu[part][i] = ex2(m);
+                    if (part < 3) sm.kb[part][i] = ex2(Gm[16 * part + 15][i] - m);
+                } else {
+                    for (int pi = part - 4; pi < 6; pi += 4) {
+                        const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
+                        sm.fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 15][i]);
+                    }
+                }
+            }
+            if (part == 7) {
+                sm.dec[c & 1][i] = ex2(Gm[CL - 1][i]);
+                if (!OUT) gsum += Gm[CL - 1][i];
+            }
+            float kf[8], e[8];
+            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+            if (OUT) {
+                const int mrow = 16 * (row >> 4) + 7;
+                float rf[8], a[8], b[8];
+                unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const float m = Gm[mrow][c8 + s], g = Gm[row][c8 + s];
+                    const float gm1 = row > 0 ? Gm[row - 1][c8 + s] : 0.f;
+                    a[s] = rf[s] * ex2(gm1 - m);
+                    b[s] = kf[s] * ex2(m - g);
+                    e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - g);
+                }
+                sstore16(sm.Rm, row, c8, pack8(a));
+                sstore16(sm.Km, row, c8, pack8(b));
+            } else {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - Gm[row][c8 + s]);
+            }
+            sstore16(sm.Kt, row, c8, pack8(e));
         }
         __syncthreads();
+        if (OUT) {
+            const int t = 16 * W + lr;
+            f32x4 ao[2] = {};
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
+            for (int ks = 0; ks < 2; ++ks) {
+                float f[8];
+                dir8_vec(sm.emu[W], 32 * ks, f);
+                const bf16x8 a = scale8(ld_dir8(&sm.Rm[0][0], t, 32 * ks), f);
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) Rm[16 * W + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
+                for (int tp = 0; tp < 2; ++tp)
+                    ao[tp] = mfma32(a, ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), ao[tp]);
+            }
+            for (int J = 0; J <= W; ++J) {
+                const bool diag = (J == W);
+                f32x4 at = {};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    bf16x8 rb = ld_row8(&sm.Rm[0][0], t, 32 * ks);
+                    bf16x8 kk = ld_row8(&sm.Km[0][0], 16 * J + lr, 32 * ks);
+                    if (!diag) {
+                        float f[8];
+                        row8_vec(sm.fp[pair_index(W, J)], 32 * ks, f);
+                        rb = scale8(rb, f);
+                        row8_vec(sm.kb[J], 32 * ks, f);
+                        kk = scale8(kk, f);
+                    }
+                    at = mfma32(kk, rb, at);                                      // A^T[tau][t]
+                }
+                float xa[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    float x = at[rr];
+                    if (diag) {
+                        const int tl = 4 * lq + rr;
+                        x = tl < lr ? x : (tl == lr ? sm.bonus[t] : 0.f);
+                    }
+                    xa[rr] = x;
+                }
+                const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    ao[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ao[tp]);
+            }
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * ao[tp][rr]);
+        }
+        // state update: S = diag(e^{G_63}) S + Kt^T V
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
+            acc[0][rr] *= d;
+            acc[1][rr] *= d;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+        }
         __syncthreads();
-        store_tile<NTHR>(o + obase, Rm, nvalid);
+    }
+
+    // ---- end of the segment ----
+    if (!OUT) {
+        const size_t sq = (size_t)bh * (P - 1) + seg;
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
+        if (threadIdx.x >= 7 * 64) Aseg[sq * KD + (threadIdx.x & 63)] = gsum;
+    } else {
+        if (c_end > c_begin) walk_store(sm, o, Hs, decay, bh, c_end - 1, T, NT);
+        if (seg == P - 1) {
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const size_t e = (size_t)(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr;
+                    Hs[(size_t)bh * (NT + 1) * KD * KD + (size_t)NT * KD * KD + e] = f2bf(acc[tp][rr]);
+                    if (hT) hT[sbase + e] = acc[tp][rr];
+                }
+        }
     }
 }
 
@@ -978,19 +1080,6 @@ int launch_status() {
     return e == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH;
 }
 
-// Number of workgroups of `kernel` that fit on the current device at once (for persistent
-// grid-stride kernels; correctness does not depend on all of them being resident).
-inline int resident_groups(const void* kernel, int threads, size_t dyn_lds) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, dyn_lds) != hipSuccess ||
-        per_cu <= 0)
-        per_cu = 1;
-    return cus * per_cu;
-}
-
 // Records phase_events[i] (a hipEvent_t) on the stream when the caller asked for timing.
 inline void mark(void* const* ev, int i, hipStream_t s) {
     if (ev && ev[i]) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
@@ -1011,7 +1100,10 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
                                  int for_bwd) {
     if (check_shape(B, H, T, K, V) != RWKV6_OK) return 0;
     const size_t BH = (size_t)(B * H), NT = (size_t)(nchunks(T) > 0 ? nchunks(T) : 1);
-    if (!for_bwd) return round_up(BH * NT * KD * KD * 4);             // S_loc (fp32)
+    if (!for_bwd) {                                                    // S_seg, A_seg (fp32)
+        const size_t P = (size_t)walk_segments((int64_t)BH, nchunks(T));
+        return std::max<size_t>(256, round_up(BH * (P - 1) * KD * KD * 4) + round_up(BH * (P - 1) * KD * 4));
+    }
     return round_up(BH * NT * KD * KD * 2) * 2 + round_up(BH * NT * KD * 4);   // dS_loc, dHs, du_part
 }
 
@@ -1035,32 +1127,32 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);
+    const int P = walk_segments(BH, NT);
     uint16_t* Hs = reinterpret_cast<uint16_t*>(saved);
     float* decay = reinterpret_cast<float*>(reinterpret_cast<char*>(saved) +
                                             round_up((size_t)BH * (NT + 1) * KD * KD * 2));
-    float* Sloc = reinterpret_cast<float*>(workspace);
+    float* Sseg = reinterpret_cast<float*>(workspace);
+    float* Aseg = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                           round_up((size_t)BH * (P - 1) * KD * KD * 4));
+    for (const void* fn : {reinterpret_cast<const void*>(wkv6_fwd_walk<SEQ, false>),
+                           reinterpret_cast<const void*>(wkv6_fwd_walk<SEQ, true>)})
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)sizeof(WalkSmem)) != hipSuccess)
+            return RWKV6_ERR_LAUNCH;
     mark(phase_events, 0, s);
-    if (NT > 0) {
-        dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL((wkv6_chunk_local<true, SEQ>), grid, dim3(NTHR), 0, s,
-                           (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, Sloc, decay,
-                           1.0f, (int)B, (int)H, (int)T, (int)NT);
-    }
+    if (P > 1)
+        hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, false>), dim3((unsigned)(BH * (P - 1))), dim3(NTHR_W),
+                           sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
+                           (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
+                           decay, hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
-    hipLaunchKernelGGL(wkv6_state_scan_fwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, Sloc, decay,
-                       h0, Hs, hT, (int)NT);
     mark(phase_events, 3, s);
     mark(phase_events, 4, s);
-    if (NT > 0) {
-        const int njobs = (int)(NT * BH);
-        const int nwg = std::min(
-            njobs, resident_groups(reinterpret_cast<const void*>(wkv6_fwd_chunk_output<SEQ>), NTHR, 0));
-        hipLaunchKernelGGL(wkv6_fwd_chunk_output<SEQ>, dim3((unsigned)nwg), dim3(NTHR), 0, s,
-                           (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
-                           (const uint16_t*)w, u, u_dtype, (const uint16_t*)Hs, (uint16_t*)o, scale,
-                           (int)B, (int)H, (int)T, (int)NT, njobs);
-    }
+    hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, true>), dim3((unsigned)(BH * P)), dim3(NTHR_W),
+                       sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
+                       (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
+                       decay, hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
     mark(phase_events, 5, s);
     return launch_status();
 }

@@ -152,6 +152,18 @@ def test_wkv_empty_sequence(pkg):
     assert torch.equal(hT, h0)
 
 
+@pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17)])
+def test_wkv_parity_segmented(pkg, shape):
+    """Few sequences of many chunks: the forward cuts each sequence into segments (a state
+    pre-pass per segment, then output walks that start from the combined segment states),
+    here 2 segments of 9 chunks and 5 segments of 9 chunks with a ragged last chunk."""
+    B, H, T = shape
+    x = _inputs(B, H, T, seed=T)
+    got = run_gpu(pkg, x, 0.5, True, True)
+    ref = run_oracle(x, 0.5, True, True)
+    _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
+
+
 @pytest.mark.parametrize("cfg", ["config2", "config5"])
 def test_wkv_baseline_configs(pkg, cfg):
     """BASELINE.json configs 2 and 5 at full size (B=8,H=32,T=4096 / B=1,H=32,T=32768 with
@@ -168,7 +180,7 @@ def test_wkv_baseline_configs(pkg, cfg):
     _compare(got, ref, names)
 
 
-@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64)])
+@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64), (2, 1, 1300)])
 def test_wkv_seqfirst_entry(pkg, shape):
     """The time-mix module's entry: r, k, v, decay in [T,B,H*64], w = -exp(decay) inside,
     o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs."""
