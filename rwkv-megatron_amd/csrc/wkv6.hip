@@ -361,16 +361,69 @@ __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2
 #endif
 
 struct WalkSmem {
-    tile_t Rm, Km, Kt, Vm, Ot;        // operand tiles, o staging
+    tile_t Rm, Km;                    // diagonal-block operands (midpoint-referenced)
+    tile_t Ri, Rp;                    // r e^{G_{t-1}} (inter-chunk), r e^{G_{t-1} - b_{I-1}} (cross)
+    tile_t Kt, Vm, Ot;                // state-update operand k e^{G_63 - G}, v, o staging
     tile_t Sin[2];                    // bf16 S_in of chunk c in Sin[c & 1]
+    uint16_t Kc[6 * 16][TS];          // cross-block sources k e^{b_{I-1} - G}, rows 16 pair(I, J)
     float G[CL * GSG];                // cumulative log2-decay
-    float emu[4][KD], fp[6][KD], kb[3][KD];
+    float emu[4][KD];                 // e^{mu_I}
+    float c1[4][KD];                  // e^{mu_I - b_{I-1}}            (I >= 1)
+    float c3[4][KD];                  // e^{G_63 - mu_J}
+    float c6[6][KD];                  // e^{b_{I-1} - mu_J}, pair (I, J), J < I
     float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
     float tot[NTHR_W];                // build_G scratch
     float bonus[CL];
     float uh[KD];                     // u of this head
 };
 static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
+
+// build_G for the output walk (512 threads, part = 8-token run): also fills the per-channel
+// tables, all from the part-end values ge[p] = G[8p + 7] (mu_I = ge[2I], b_{I-1} =
+// ge[2I - 1], G_63 = ge[7]).  `part` is wave-uniform, so the table branches are scalar.
+template <bool DEC>
+__device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar) {
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
+    const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+    float loc[8];
+    float run = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const float x = bf2f(sm.Kt[8 * part + s][i]);           // w scratch
+        const float wn = DEC ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+        run += fmaxf(wn, W_MIN) * RW_L2E;
+        loc[s] = run;
+    }
+    sm.tot[part * 64 + i] = run;
+    __syncthreads();
+    float ge[8], a = 0.f, off = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        a += sm.tot[p * 64 + i];
+        ge[p] = a;
+        off = p < part ? a : off;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) Gm[8 * part + s][i] = loc[s] + off;
+    if (part < 4) {
+        const float mu = part == 0 ? ge[0] : part == 1 ? ge[2] : part == 2 ? ge[4] : ge[6];
+        sm.emu[part][i] = ex2(mu);
+        sm.c3[part][i] = ex2(ge[7] - mu);
+        // c6 pairs (1,0), (2,0), (2,1), (3,0)
+        const float b = part == 0 ? ge[1] : part == 1 ? ge[3] : part == 2 ? ge[3] : ge[5];
+        const float mj = part == 0 ? ge[0] : part == 1 ? ge[0] : part == 2 ? ge[2] : ge[0];
+        sm.c6[part][i] = ex2(b - mj);
+    } else if (part < 7) {
+        const int I = part - 3;                                  // 1..3
+        const float mu = I == 1 ? ge[2] : I == 2 ? ge[4] : ge[6];
+        const float bp = I == 1 ? ge[1] : I == 2 ? ge[3] : ge[5];
+        sm.c1[I][i] = ex2(mu - bp);
+        if (part < 6) sm.c6[part][i] = ex2(ge[5] - (part == 4 ? ge[2] : ge[4]));   // (3,1), (3,2)
+    } else {
+        sm.dec[cpar][i] = ex2(ge[7]);
+    }
+    __syncthreads();
+}
 
 // Segments per sequence (shared by the workspace query and the launch).
 inline int walk_segments(int64_t BH, int64_t NT) {
@@ -442,7 +495,10 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     const int NC = (NT + P - 1) / P;
     const int c_begin = seg * NC, c_end = min(NT, c_begin + NC);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int W = wv >> 1, hh = wv & 1;
+    // waves 0-3 take token blocks 0,0,1,1 and waves 4-7 blocks 3,3,2,2: with waves dealt
+    // round-robin to the 4 SIMDs, each SIMD gets blocks {0,3} or {1,2}, whose cross-block
+    // work (W products each) sums to the same 3
+    const int W = wv < 4 ? (wv >> 1) : 5 - (wv >> 1), hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
     const size_t sbase = (size_t)bh * KD * KD;
@@ -504,88 +560,102 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         }
         if (c + 1 < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c + 1, B, H, T);
         __syncthreads();
-        build_G<NTHR_W, SEQ>(sm.Kt, Gm, sm.tot, nvalid);
-        // tables and operand tiles (the w scratch in Kt was consumed by build_G)
-        {
-            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-            if (OUT) {
-                if (part < 4) {
-                    const float m = Gm[16 * part + 7][i];
-                    sm.emu[part][i] = ex2(m);
-                    if (part < 3) sm.kb[part][i] = ex2(Gm[16 * part + 15][i] - m);
-                } else {
-                    for (int pi = part - 4; pi < 6; pi += 4) {
-                        const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                        sm.fp[pi][i] = ex2(Gm[16 * I + 7][i] - Gm[16 * J + 15][i]);
-                    }
-                }
+        if (OUT) {
+            walk_build_G<SEQ>(sm, nvalid, c & 1);
+            // Operand tiles of this thread's piece (token t = row in block I; I is
+            // wave-uniform).  Two exponentials per element; every other factor is a
+            // per-(block, channel) table entry <= 1 applied to the fp32 value:
+            //   Rm = r e^{G_{t-1} - mu_I}     Ri = Rm e^{mu_I}          Rp = Rm e^{mu_I - b_{I-1}}
+            //   Km = k e^{mu_I - G_t}         Kt = Km e^{G_63 - mu_I}   Kc(I2) = Km e^{b_{I2-1} - mu_I}
+            const int I = row >> 4;
+            float rf[8], kf[8], rm[8], km[8], y[8], f[8];
+            unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
+            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const float m = Gm[16 * I + 7][c8 + s], g = Gm[row][c8 + s];
+                const float gm1 = row > 0 ? Gm[row - 1][c8 + s] : 0.f;
+                rm[s] = rf[s] * ex2(gm1 - m);
+                km[s] = kf[s] * ex2(m - g);
             }
+            sstore16(sm.Rm, row, c8, pack8(rm));
+            sstore16(sm.Km, row, c8, pack8(km));
+            auto tab8 = [&](const float* tb) {
+                const float4 a = *reinterpret_cast<const float4*>(tb + c8);
+                const float4 b = *reinterpret_cast<const float4*>(tb + c8 + 4);
+                f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+            };
+            tab8(sm.emu[I]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
+            sstore16(sm.Ri, row, c8, pack8(y));
+            if (I > 0) {
+                tab8(sm.c1[I]);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
+                sstore16(sm.Rp, row, c8, pack8(y));
+            }
+            tab8(sm.c3[I]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
+            sstore16(sm.Kt, row, c8, pack8(y));
+            for (int I2 = I + 1; I2 < 4; ++I2) {
+                const int pi = pair_index(I2, I);
+                tab8(sm.c6[pi]);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
+                sstore16(reinterpret_cast<uint16_t (*)[TS]>(sm.Kc[16 * pi]), row & 15, c8, pack8(y));
+            }
+        } else {
+            build_G<NTHR_W, SEQ>(sm.Kt, Gm, sm.tot, nvalid);
+            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
             if (part == 7) {
                 sm.dec[c & 1][i] = ex2(Gm[CL - 1][i]);
-                if (!OUT) gsum += Gm[CL - 1][i];
+                gsum += Gm[CL - 1][i];
             }
             float kf[8], e[8];
             unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
-            if (OUT) {
-                const int mrow = 16 * (row >> 4) + 7;
-                float rf[8], a[8], b[8];
-                unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
 #pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const float m = Gm[mrow][c8 + s], g = Gm[row][c8 + s];
-                    const float gm1 = row > 0 ? Gm[row - 1][c8 + s] : 0.f;
-                    a[s] = rf[s] * ex2(gm1 - m);
-                    b[s] = kf[s] * ex2(m - g);
-                    e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - g);
-                }
-                sstore16(sm.Rm, row, c8, pack8(a));
-                sstore16(sm.Km, row, c8, pack8(b));
-            } else {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - Gm[row][c8 + s]);
-            }
+            for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - Gm[row][c8 + s]);
             sstore16(sm.Kt, row, c8, pack8(e));
         }
         __syncthreads();
         if (OUT) {
             const int t = 16 * W + lr;
             f32x4 ao[2] = {};
+            // inter-chunk: (r e^{G_{t-1}}) S_in
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                float f[8];
-                dir8_vec(sm.emu[W], 32 * ks, f);
-                const bf16x8 a = scale8(ld_dir8(&sm.Rm[0][0], t, 32 * ks), f);
+                const bf16x8 a = ld_dir8(&sm.Ri[0][0], t, 32 * ks);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
                     ao[tp] = mfma32(a, ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), ao[tp]);
             }
-            for (int J = 0; J <= W; ++J) {
-                const bool diag = (J == W);
+            // diagonal block: strictly causal part plus the u-bonus diagonal
+            {
                 f32x4 at = {};
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    bf16x8 rb = ld_row8(&sm.Rm[0][0], t, 32 * ks);
-                    bf16x8 kk = ld_row8(&sm.Km[0][0], 16 * J + lr, 32 * ks);
-                    if (!diag) {
-                        float f[8];
-                        row8_vec(sm.fp[pair_index(W, J)], 32 * ks, f);
-                        rb = scale8(rb, f);
-                        row8_vec(sm.kb[J], 32 * ks, f);
-                        kk = scale8(kk, f);
-                    }
-                    at = mfma32(kk, rb, at);                                      // A^T[tau][t]
-                }
+                for (int ks = 0; ks < 2; ++ks)
+                    at = mfma32(ld_row8(&sm.Km[0][0], 16 * W + lr, 32 * ks), ld_row8(&sm.Rm[0][0], t, 32 * ks), at);
                 float xa[4];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    float x = at[rr];
-                    if (diag) {
-                        const int tl = 4 * lq + rr;
-                        x = tl < lr ? x : (tl == lr ? sm.bonus[t] : 0.f);
-                    }
-                    xa[rr] = x;
+                    const int tl = 4 * lq + rr;
+                    xa[rr] = tl < lr ? at[rr] : (tl == lr ? sm.bonus[t] : 0.f);
                 }
                 const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    ao[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ao[tp]);
+            }
+            // earlier blocks J < W, both operands referenced at b_{W-1}
+            for (int J = 0; J < W; ++J) {
+                f32x4 at = {};
+                const int pr = 16 * pair_index(W, J) + lr;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    at = mfma32(ld_row8(&sm.Kc[0][0], pr, 32 * ks), ld_row8(&sm.Rp[0][0], t, 32 * ks), at);
+                const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
                     ao[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ao[tp]);
