@@ -208,131 +208,6 @@ __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
                                  : reinterpret_cast<const float*>(u)[idx];
 }
 
-// ---------------------------------------------------------------------------
-// phase A: chunk-local state (forward) / dstate (backward)
-// ---------------------------------------------------------------------------
-// out[i][j] = scale * sum_t X[t][i] e^{E[t][i]} Y[t][j] with
-//   forward : X = k, E = G_63 - G_t,   Y = v      (S_loc)
-//   backward: X = r, E = G_{t-1},      Y = dO     (dS_loc)
-// and, forward only, decay[i] = e^{G_63[i]}.
-// SEQ: X and w (as pre-activation decay) are sequence-first; Y is v (sequence-first) in
-// the forward and dO (always head-first) in the backward.
-template <bool FWD, bool SEQ>
-__global__ void __launch_bounds__(NTHR)
-wkv6_chunk_local(const uint16_t* __restrict__ X, const uint16_t* __restrict__ Y,
-                 const uint16_t* __restrict__ w, void* __restrict__ out,
-                 float* __restrict__ decay, float scale, int B, int H, int T, int NT) {
-    __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
-    __shared__ __attribute__((aligned(16))) float Gstore[CL * GSG];
-    __shared__ float tot[NTHR];
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(Gstore);
-    const int c = blockIdx.x, bh = blockIdx.y;
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
-    const size_t ybase = FWD ? base : tok_base<false>(bh, t0, B, H, T);
-    const size_t yrs = FWD ? rs : (size_t)KD;
-    uint4 xr[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        xr[p] = gload16s(X + base, row, c8, nvalid, rs);
-        sstore16(Ys, row, c8, gload16s(Y + ybase, row, c8, nvalid, yrs));
-        sstore16(Wm, row, c8, gload16s(w + base, row, c8, nvalid, rs));
-    }
-    __syncthreads();
-    build_G<NTHR, SEQ>(Wm, Gm, tot, nvalid);
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        float xf[8], e[8];
-        unpack8(xr[p], xf);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float ex = FWD ? Gm[CL - 1][c8 + s] - Gm[row][c8 + s]
-                                 : (row > 0 ? Gm[row - 1][c8 + s] : 0.f);
-            e[s] = xf[s] * ex2(ex);
-        }
-        sstore16(Xs, row, c8, pack8(e));
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int lr = lane & 15, lq = lane >> 4;
-    f32x4 acc[4] = {};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 a = ld_tr8(&Xs[0][0], 32 * ks, 16 * wv);          // row i = 16wv+lr
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Ys[0][0], 32 * ks, 16 * tj), acc[tj]);
-    }
-    if (FWD) {
-        // S_loc stays fp32: the state scan adds it into the fp32 carry
-        float* o = reinterpret_cast<float*>(out) + ((size_t)bh * NT + c) * KD * KD;
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) o[(16 * wv + 4 * lq + rr) * KD + 16 * tj + lr] = scale * acc[tj][rr];
-        if (threadIdx.x < KD)
-            decay[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
-    } else {
-        // dS_loc in bf16, staged through LDS (Wm is free since build_G) for 16-byte stores
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) Wm[16 * wv + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
-        __syncthreads();
-        store_tile<NTHR>(reinterpret_cast<uint16_t*>(out) + ((size_t)bh * NT + c) * KD * KD, Wm, KD);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// phase B: state scans (fp32 carry; fp32 S_loc / bf16 dS_loc in, bf16 states out)
-// ---------------------------------------------------------------------------
-// A thread carries two adjacent elements of one state row (8-byte fp32 / 4-byte bf16
-// accesses; a wave covers two rows), and issues the loads of SCAN_U chunks before it walks
-// them (the loads do not depend on the carry), so a wave keeps SCAN_U requests in flight.
-#define SCAN_U 32                          // dstate scan: bf16 pairs in flight per thread
-#define SCAN_UF 8                          // state scan: fp32 pairs (8 x 8 B per thread)
-#define SCAN_BLK 8                         // blocks per (b,h): 8 x 256 threads x 2 elements
-
-// dHs[c] = bf16(dS_out(c)) (gradient w.r.t. the state after chunk c); dh0 = dS_in(0).
-__global__ void __launch_bounds__(NTHR)
-wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict__ decay,
-                    const float* __restrict__ dhT, uint16_t* __restrict__ dHs,
-                    float* __restrict__ dh0, int NT) {
-    const int bh = blockIdx.x / SCAN_BLK;
-    const int e = ((blockIdx.x % SCAN_BLK) * NTHR + threadIdx.x) * 2;
-    const int i = e >> 6;
-    float2 dS = dhT ? *reinterpret_cast<const float2*>(dhT + (size_t)bh * KD * KD + e) : make_float2(0.f, 0.f);
-    const uint32_t* sl = reinterpret_cast<const uint32_t*>(dSloc + (size_t)bh * NT * KD * KD + e);
-    const float* dc = decay + (size_t)bh * NT * KD + i;
-    uint32_t* hs = reinterpret_cast<uint32_t*>(dHs + (size_t)bh * NT * KD * KD + e);
-    constexpr size_t ST = KD * KD / 2;
-    int c = NT - 1;
-    for (; c - (SCAN_U - 1) >= 0; c -= SCAN_U) {
-        uint32_t l[SCAN_U];
-        float d[SCAN_U];
-#pragma unroll
-        for (int q = 0; q < SCAN_U; ++q) {
-            l[q] = sl[(c - q) * ST];
-            d[q] = dc[(c - q) * KD];
-        }
-#pragma unroll
-        for (int q = 0; q < SCAN_U; ++q) {
-            hs[(c - q) * ST] = pk2(dS.x, dS.y);
-            dS.x = d[q] * dS.x + __uint_as_float(l[q] << 16);
-            dS.y = d[q] * dS.y + __uint_as_float(l[q] & 0xffff0000u);
-        }
-    }
-    for (; c >= 0; --c) {
-        hs[c * ST] = pk2(dS.x, dS.y);
-        const uint32_t l = sl[c * ST];
-        const float d = dc[c * KD];
-        dS.x = d * dS.x + __uint_as_float(l << 16);
-        dS.y = d * dS.y + __uint_as_float(l & 0xffff0000u);
-    }
-    if (dh0) *reinterpret_cast<float2*>(dh0 + (size_t)bh * KD * KD + e) = dS;
-}
-
 // Index of the cross-block pair (I, J), I > J, in the 6-entry tables.
 __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }
 
@@ -356,6 +231,9 @@ __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2
 #define WALK_TARGET_ITEMS 256   // workgroups a forward should offer (one per CU of an MI355X)
 #endif
 #define WALK_MIN_CHUNKS 8       // shortest segment worth a pre-pass
+#ifndef DSTATE_TARGET_ITEMS
+#define DSTATE_TARGET_ITEMS 256 // the same for the backward's reverse walk
+#endif
 #ifndef WALK_WPE
 #define WALK_WPE 2              // waves per SIMD the walk is compiled for (1 block of 8 waves / CU)
 #endif
@@ -425,14 +303,19 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
     __syncthreads();
 }
 
-// Segments per sequence (shared by the workspace query and the launch).
-inline int walk_segments(int64_t BH, int64_t NT) {
+// Segments per sequence (shared by the workspace query and the launch): enough
+// (b,h, segment) workgroups to offer `target`, no segment shorter than WALK_MIN_CHUNKS.
+inline int walk_segments(int64_t BH, int64_t NT, int64_t target = WALK_TARGET_ITEMS) {
     if (NT <= 0) return 1;
-    int64_t P = (WALK_TARGET_ITEMS + BH - 1) / BH;
+    int64_t P = (target + BH - 1) / BH;
     P = std::min<int64_t>(P, std::max<int64_t>(1, NT / WALK_MIN_CHUNKS));
     const int64_t NC = (NT + P - 1) / P;               // chunks per segment
     return (int)((NT + NC - 1) / NC);                   // no empty segment
 }
+
+// The backward's state gradients walk each sequence in one workgroup when that fills the
+// device (a segmented reverse walk reads r, w, dO twice and loses to the chunk-parallel form).
+inline bool dstate_walk(int64_t BH, int64_t NT) { return walk_segments(BH, NT, DSTATE_TARGET_ITEMS) == 1; }
 
 struct WalkPrefetch {
     uint4 r, k, v, w;
@@ -460,11 +343,11 @@ __device__ __forceinline__ void walk_issue(WalkPrefetch& f, const uint16_t* __re
     f.w = gload16c(w + base, row, c8, nvalid, rs);
 }
 
-// Global stores of chunk c (o from Ot, S_in from Sin[c & 1], the chunk decay).  Issued one
+// Global stores of chunk c (o from Ot, S_in from Sin[c & 1]).  Issued one
 // chunk late, before the next prefetch: the wait for a prefetch then never waits on a store.
 __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restrict__ o,
-                                           uint16_t* __restrict__ Hs, float* __restrict__ decay,
-                                           int bh, int c, int T, int NT) {
+                                           uint16_t* __restrict__ Hs, int bh, int c, int T,
+                                           int NT) {
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     if (row < nvalid)
@@ -472,7 +355,6 @@ __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restr
             *reinterpret_cast<const uint4*>(&sm.Ot[row][c8]);
     *reinterpret_cast<uint4*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8) =
         *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8]);
-    if (threadIdx.x < KD) decay[((size_t)bh * NT + c) * KD + threadIdx.x] = sm.dec[c & 1][threadIdx.x];
 }
 
 // OUT = true : output walk over segment blockIdx.x % P of sequence blockIdx.x / P.
@@ -484,8 +366,7 @@ __global__ void __launch_bounds__(NTHR_W) __attribute__((amdgpu_waves_per_eu(WAL
 wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
               const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
               const void* __restrict__ u, int u_dtype, const float* __restrict__ h0,
-              uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float* __restrict__ decay,
-              float* __restrict__ hT, float* __restrict__ Sseg, float* __restrict__ Aseg,
+              uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float* __restrict__ hT, float* __restrict__ Sseg, float* __restrict__ Aseg,
               float scale, int B, int H, int T, int NT, int P) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     WalkSmem& sm = *reinterpret_cast<WalkSmem*>(smem_raw);
@@ -556,7 +437,7 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
-            if (c > c_begin) walk_store(sm, o, Hs, decay, bh, c - 1, T, NT);
+            if (c > c_begin) walk_store(sm, o, Hs, bh, c - 1, T, NT);
         }
         if (c + 1 < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c + 1, B, H, T);
         __syncthreads();
@@ -693,7 +574,7 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
         if (threadIdx.x >= 7 * 64) Aseg[sq * KD + (threadIdx.x & 63)] = gsum;
     } else {
-        if (c_end > c_begin) walk_store(sm, o, Hs, decay, bh, c_end - 1, T, NT);
+        if (c_end > c_begin) walk_store(sm, o, Hs, bh, c_end - 1, T, NT);
         if (seg == P - 1) {
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
@@ -704,6 +585,290 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                     if (hT) hT[sbase + e] = acc[tp][rr];
                 }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward state gradients, chunk-parallel form (used when B*H is too small for one
+// reverse walk per sequence to fill the device)
+// ---------------------------------------------------------------------------
+// Per (b,h, chunk): dS_loc = s sum_t (r_t e^{G_{t-1}}) dO_t^T [MFMA] and dec = e^{G_63}; then
+// one scan thread per pair of state elements: dS_out(c-1) = dec(c) dS_out(c) + dS_loc(c).
+// SEQ: r and w (as pre-activation decay) are sequence-first; dO is head-first.
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR)
+wkv6_bwd_chunk_dstate(const uint16_t* __restrict__ r, const uint16_t* __restrict__ dO,
+                      const uint16_t* __restrict__ w, uint16_t* __restrict__ dSloc,
+                      float* __restrict__ dec, float scale, int B, int H, int T, int NT) {
+    __shared__ __attribute__((aligned(16))) tile_t Xs, Ys, Wm;
+    __shared__ __attribute__((aligned(16))) float Gstore[CL * GSG];
+    __shared__ float tot[NTHR];
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(Gstore);
+    const int c = blockIdx.x, bh = blockIdx.y;
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const size_t dbase = tok_base<false>(bh, t0, B, H, T);
+    uint4 xr[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        xr[p] = gload16s(r + base, row, c8, nvalid, rs);
+        sstore16(Ys, row, c8, gload16(dO + dbase, row, c8, nvalid));
+        sstore16(Wm, row, c8, gload16s(w + base, row, c8, nvalid, rs));
+    }
+    __syncthreads();
+    build_G<NTHR, SEQ>(Wm, Gm, tot, nvalid);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+        float xf[8], e[8];
+        unpack8(xr[p], xf);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) e[s] = xf[s] * ex2(row > 0 ? Gm[row - 1][c8 + s] : 0.f);
+        sstore16(Xs, row, c8, pack8(e));
+    }
+    if (threadIdx.x < KD) dec[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lr = lane & 15, lq = lane >> 4;
+    f32x4 acc[4] = {};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 a = ld_tr8(&Xs[0][0], 32 * ks, 16 * wv);          // row i = 16wv+lr
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) acc[tj] = mfma32(a, ld_tr8(&Ys[0][0], 32 * ks, 16 * tj), acc[tj]);
+    }
+    // bf16, staged through LDS (Wm is free since build_G) for 16-byte stores
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) Wm[16 * wv + 4 * lq + rr][16 * tj + lr] = f2bf(scale * acc[tj][rr]);
+    __syncthreads();
+    store_tile<NTHR>(dSloc + ((size_t)bh * NT + c) * KD * KD, Wm, KD);
+}
+
+// A thread carries two adjacent elements of one state row (4-byte bf16 accesses) and issues
+// the loads of SCAN_U chunks before it walks them (they do not depend on the carry).
+#define SCAN_U 32
+#define SCAN_BLK 8                         // blocks per (b,h): 8 x 256 threads x 2 elements
+
+// dHs[c] = bf16(dS_out(c)) (gradient w.r.t. the state after chunk c); dh0 = dS_out(-1).
+__global__ void __launch_bounds__(NTHR)
+wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict__ decay,
+                    const float* __restrict__ dhT, uint16_t* __restrict__ dHs,
+                    float* __restrict__ dh0, int NT) {
+    const int bh = blockIdx.x / SCAN_BLK;
+    const int e = ((blockIdx.x % SCAN_BLK) * NTHR + threadIdx.x) * 2;
+    const int i = e >> 6;
+    float2 dS = dhT ? *reinterpret_cast<const float2*>(dhT + (size_t)bh * KD * KD + e) : make_float2(0.f, 0.f);
+    const uint32_t* sl = reinterpret_cast<const uint32_t*>(dSloc + (size_t)bh * NT * KD * KD + e);
+    const float* dc = decay + (size_t)bh * NT * KD + i;
+    uint32_t* hs = reinterpret_cast<uint32_t*>(dHs + (size_t)bh * NT * KD * KD + e);
+    constexpr size_t ST = KD * KD / 2;
+    int c = NT - 1;
+    for (; c - (SCAN_U - 1) >= 0; c -= SCAN_U) {
+        uint32_t l[SCAN_U];
+        float d[SCAN_U];
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            l[q] = sl[(c - q) * ST];
+            d[q] = dc[(c - q) * KD];
+        }
+#pragma unroll
+        for (int q = 0; q < SCAN_U; ++q) {
+            hs[(c - q) * ST] = pk2(dS.x, dS.y);
+            dS.x = d[q] * dS.x + __uint_as_float(l[q] << 16);
+            dS.y = d[q] * dS.y + __uint_as_float(l[q] & 0xffff0000u);
+        }
+    }
+    for (; c >= 0; --c) {
+        hs[c * ST] = pk2(dS.x, dS.y);
+        const uint32_t l = sl[c * ST];
+        const float d = dc[c * KD];
+        dS.x = d * dS.x + __uint_as_float(l << 16);
+        dS.y = d * dS.y + __uint_as_float(l & 0xffff0000u);
+    }
+    if (dh0) *reinterpret_cast<float2*>(dh0 + (size_t)bh * KD * KD + e) = dS;
+}
+
+// ---------------------------------------------------------------------------
+// backward: state gradients as a reverse walk (B*H large enough to fill the device)
+// ---------------------------------------------------------------------------
+// dS_out(c) is the gradient w.r.t. the state after chunk c: dS_out(NT-1) = dhT and
+//   dS_out(c-1) = diag(e^{G_63(c)}) dS_out(c) + s sum_{t in c} (r_t e^{G_{t-1}}) dO_t^T,
+// dh0 = dS_out(-1).  One workgroup per (b,h) walks its chunks from the last to the first
+// with dS in the accumulator registers and writes bf16 dS_out(c) per chunk, the gradient
+// kernel's input: r, w, dO are read once and no chunk-local state goes through HBM.
+//
+// Wave (cg, jh) owns state rows [16cg, 16cg+16) x columns [32jh, 32jh+32).  Its MFMA A
+// operand (s r e^{G_{t-1}})^T is built in registers: lane (q, L) holds channel 16cg + L for
+// the tokens 32ks + 8q + s, s = 0..7, ks = 0, 1 -- read from the token-major tiles with the
+// LDS transpose read, scanned along the tokens in registers (the 8-token runs of the four
+// lane rows combined by lane shuffles), exponentiated, and fed to the MFMA as is: no
+// cumulative-decay or operand tile goes through LDS, and one barrier per chunk suffices.
+struct DstateSmem {
+    tile_t Rw[2], Ww[2], Dw[2];       // raw r, w (or pre-activation decay), dO of chunk c in [c & 1]
+    uint16_t Ds[8][16][40];           // per-wave bf16 dS_out staging (16 rows x 32 columns)
+    float g63[8][16];                 // per-wave G_63 of its 16 channels
+};
+static_assert(sizeof(DstateSmem) <= 80 * 1024, "two dstate blocks per CU");
+
+// Lane (q, L) receives X[r0 + 8q + s][c0 + L], s = 0..3: the 16 lanes of row group q read
+// rows r0 + 8q + (0..3) (lanes 4s..4s+3 read row s as 16 consecutive columns).
+__device__ __forceinline__ bf16x4 ld_tr4_g8(const uint16_t* X, int r0, int c0) {
+    const int lane = threadIdx.x & 63;
+    const int L = lane & 15, q = lane >> 4;
+    const uint16_t* p = X + (r0 + 8 * q + (L >> 2)) * TS + c0 + 4 * (L & 3);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
+// 8 consecutive rows r0 + 8q + (0..7) of column c0 + L.
+__device__ __forceinline__ bf16x8 ld_tr8_g8(const uint16_t* X, int r0, int c0) {
+    const bf16x4 a = ld_tr4_g8(X, r0, c0), b = ld_tr4_g8(X, r0 + 4, c0);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+struct DstatePrefetch {
+    uint4 r, w, d;
+};
+
+template <bool SEQ>
+__device__ __forceinline__ void dstate_issue(DstatePrefetch& f, const uint16_t* __restrict__ r,
+                                             const uint16_t* __restrict__ w,
+                                             const uint16_t* __restrict__ dO, int bh, int c,
+                                             int B, int H, int T) {
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    f.r = gload16c(r + base, row, c8, nvalid, rs);
+    f.w = gload16c(w + base, row, c8, nvalid, rs);
+    f.d = gload16c(dO + ((size_t)bh * T + t0) * KD, row, c8, nvalid, KD);
+}
+
+// One chunk of the reverse walk: stores the prefetched tiles, writes dS_out(c) and advances
+// D to dS_out(c - 1).
+template <bool SEQ>
+__device__ __forceinline__ void dstate_chunk(DstateSmem& sm, const DstatePrefetch& f, f32x4 (&D)[2],
+                                             uint16_t* __restrict__ dHs, int bh, int c, int T,
+                                             int NT, float scale) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int cg = wv >> 1, jh = wv & 1;
+    const int L = lane & 15, q = lane >> 4;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    const int nvalid = min(CL, T - c * CL), b = c & 1;
+    sstore16(sm.Rw[b], row, c8, f.r);
+    sstore16(sm.Ww[b], row, c8, f.w);
+    sstore16(sm.Dw[b], row, c8, f.d);
+    __syncthreads();       // chunk c's tiles are in; buffer b ^ 1 was last read before this point
+    // cumulative log2-decay of channel 16cg + L at tokens 32ks + 8q + s (run-local)
+    float g[2][8], run[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 wx = ld_tr8_g8(&sm.Ww[b][0][0], 32 * ks, 16 * cg);
+        float a = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float x = (float)wx[s];
+            const float wn = SEQ ? ((32 * ks + 8 * q + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+            a += fmaxf(wn, W_MIN) * RW_L2E;
+            g[ks][s] = a;
+        }
+        run[ks] = a;
+    }
+    // exclusive prefix of the run totals over the lane rows q (lanes L + 16q); the second
+    // half of the chunk starts after the whole first half
+    float e0, e1;
+    {
+        float x = run[0];
+        float y = __shfl_up(x, 16);
+        x += q >= 1 ? y : 0.f;
+        y = __shfl_up(x, 32);
+        x += q >= 2 ? y : 0.f;                                   // inclusive over q
+        const float tot0 = __shfl(x, 48 + L);
+        e0 = x - run[0];
+        float z = run[1];
+        y = __shfl_up(z, 16);
+        z += q >= 1 ? y : 0.f;
+        y = __shfl_up(z, 32);
+        z += q >= 2 ? y : 0.f;
+        e1 = tot0 + (z - run[1]);
+    }
+    const float g63 = __shfl(e1 + run[1], 48 + L);
+    if (q == 0) sm.g63[wv][L] = g63;
+    // A operand (s r_t e^{G_{t-1}})^T, slot s <-> token 32ks + 8q + s
+    bf16x8 aop[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 rx = ld_tr8_g8(&sm.Rw[b][0][0], 32 * ks, 16 * cg);
+        const float base = ks == 0 ? e0 : e1;
+        float y[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const float gm1 = s == 0 ? base : base + g[ks][s - 1];
+            y[s] = scale * (float)rx[s] * ex2(gm1);
+        }
+        aop[ks] = __builtin_bit_cast(bf16x8, pack8(y));
+    }
+    {
+        // dS_out(c), bf16, staged per wave for 16-byte stores
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) sm.Ds[wv][4 * q + rr][16 * tp + L] = f2bf(D[tp][rr]);
+        const int sr = lane >> 2, sc = (lane & 3) * 8;
+        *reinterpret_cast<uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + (16 * cg + sr) * KD + 32 * jh + sc) =
+            *reinterpret_cast<const uint4*>(&sm.Ds[wv][sr][sc]);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const float d = ex2(sm.g63[wv][4 * q + rr]);
+        D[0][rr] *= d;
+        D[1][rr] *= d;
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+            D[tp] = mfma32(aop[ks], ld_tr8_g8(&sm.Dw[b][0][0], 32 * ks, 32 * jh + 16 * tp), D[tp]);
+}
+
+// One workgroup per (b,h), chunks NT-1 .. 0; writes dHs and dh0.  Loads run two chunks
+// ahead (two register sets, the loop unrolled by two).
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR_W)
+wkv6_bwd_dstate_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
+                     const uint16_t* __restrict__ dO, const float* __restrict__ dhT,
+                     uint16_t* __restrict__ dHs, float* __restrict__ dh0, float scale, int B,
+                     int H, int T, int NT) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    DstateSmem& sm = *reinterpret_cast<DstateSmem*>(smem_raw);
+    const int bh = blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int cg = wv >> 1, jh = wv & 1;
+    const int L = lane & 15, q = lane >> 4;
+    const size_t sbase = (size_t)bh * KD * KD;
+
+    DstatePrefetch fa, fb;
+    if (NT >= 1) dstate_issue<SEQ>(fa, r, w, dO, bh, NT - 1, B, H, T);
+    if (NT >= 2) dstate_issue<SEQ>(fb, r, w, dO, bh, NT - 2, B, H, T);
+    f32x4 D[2];                            // dS_out(NT - 1) = dhT
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            D[tp][rr] = dhT ? dhT[sbase + (16 * cg + 4 * q + rr) * KD + 32 * jh + 16 * tp + L] : 0.f;
+    for (int c = NT - 1; c >= 0; c -= 2) {
+        dstate_chunk<SEQ>(sm, fa, D, dHs, bh, c, T, NT, scale);
+        if (c - 2 >= 0) dstate_issue<SEQ>(fa, r, w, dO, bh, c - 2, B, H, T);
+        if (c - 1 < 0) break;
+        dstate_chunk<SEQ>(sm, fb, D, dHs, bh, c - 1, T, NT, scale);
+        if (c - 3 >= 0) dstate_issue<SEQ>(fb, r, w, dO, bh, c - 3, B, H, T);
+    }
+    if (dh0) {
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                dh0[sbase + (16 * cg + 4 * q + rr) * KD + 32 * jh + 16 * tp + L] = D[tp][rr];
     }
 }
 
@@ -1162,8 +1327,7 @@ extern "C" {
 size_t rwkv6_wkv_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V) {
     if (check_shape(B, H, T, K, V) != RWKV6_OK) return 0;
     const int64_t NT = nchunks(T);
-    return round_up((size_t)(B * H) * (NT + 1) * KD * KD * 2) +
-           round_up((size_t)(B * H) * (NT > 0 ? NT : 1) * KD * 4);
+    return round_up((size_t)(B * H) * (NT + 1) * KD * KD * 2);        // bf16 S_in per chunk + final
 }
 
 size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
@@ -1174,7 +1338,9 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
         const size_t P = (size_t)walk_segments((int64_t)BH, nchunks(T));
         return std::max<size_t>(256, round_up(BH * (P - 1) * KD * KD * 4) + round_up(BH * (P - 1) * KD * 4));
     }
-    return round_up(BH * NT * KD * KD * 2) * 2 + round_up(BH * NT * KD * 4);   // dS_loc, dHs, du_part
+    const size_t base = round_up(BH * NT * KD * KD * 2) + round_up(BH * NT * KD * 4);   // dHs, du_part
+    if (dstate_walk((int64_t)BH, nchunks(T))) return base;
+    return base + round_up(BH * NT * KD * KD * 2) + round_up(BH * NT * KD * 4);         // dS_loc, dec
 }
 
 }  // extern "C"
@@ -1199,8 +1365,6 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     const int BH = (int)(B * H);
     const int P = walk_segments(BH, NT);
     uint16_t* Hs = reinterpret_cast<uint16_t*>(saved);
-    float* decay = reinterpret_cast<float*>(reinterpret_cast<char*>(saved) +
-                                            round_up((size_t)BH * (NT + 1) * KD * KD * 2));
     float* Sseg = reinterpret_cast<float*>(workspace);
     float* Aseg = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                            round_up((size_t)BH * (P - 1) * KD * KD * 4));
@@ -1214,7 +1378,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
         hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, false>), dim3((unsigned)(BH * (P - 1))), dim3(NTHR_W),
                            sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
                            (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
-                           decay, hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
+                           hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
     mark(phase_events, 3, s);
@@ -1222,7 +1386,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, true>), dim3((unsigned)(BH * P)), dim3(NTHR_W),
                        sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
                        (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
-                       decay, hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
+                       hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
     mark(phase_events, 5, s);
     return launch_status();
 }
@@ -1247,25 +1411,35 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);
     const uint16_t* Hs = reinterpret_cast<const uint16_t*>(saved);
-    const float* decay = reinterpret_cast<const float*>(
-        reinterpret_cast<const char*>(saved) + round_up((size_t)BH * (NT + 1) * KD * KD * 2));
     const size_t NTa = (size_t)(NT > 0 ? NT : 1);
-    uint16_t* dSloc = reinterpret_cast<uint16_t*>(workspace);
-    uint16_t* dHs = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(workspace) +
-                                                round_up((size_t)BH * NTa * KD * KD * 2));
-    float* du_part = reinterpret_cast<float*>(reinterpret_cast<char*>(dHs) +
+    uint16_t* dHs = reinterpret_cast<uint16_t*>(workspace);
+    float* du_part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                               round_up((size_t)BH * NTa * KD * KD * 2));
     mark(phase_events, 0, s);
-    if (NT > 0) {
-        dim3 grid((unsigned)NT, (unsigned)BH);
-        hipLaunchKernelGGL((wkv6_chunk_local<false, SEQ>), grid, dim3(NTHR), 0, s, (const uint16_t*)r,
-                           (const uint16_t*)dO, (const uint16_t*)w, dSloc, (float*)nullptr, scale,
-                           (int)B, (int)H, (int)T, (int)NT);
+    if (dstate_walk(BH, NT)) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_dstate_walk<SEQ>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)sizeof(DstateSmem)) != hipSuccess)
+            return RWKV6_ERR_LAUNCH;
+        mark(phase_events, 1, s);
+        mark(phase_events, 2, s);
+        hipLaunchKernelGGL(wkv6_bwd_dstate_walk<SEQ>, dim3((unsigned)BH), dim3(NTHR_W),
+                           sizeof(DstateSmem), s, (const uint16_t*)r, (const uint16_t*)w,
+                           (const uint16_t*)dO, dhT, dHs, dh0, scale, (int)B, (int)H, (int)T,
+                           (int)NT);
+    } else {
+        uint16_t* dSloc = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(du_part) +
+                                                      round_up((size_t)BH * NTa * KD * 4));
+        float* dec = reinterpret_cast<float*>(reinterpret_cast<char*>(dSloc) +
+                                              round_up((size_t)BH * NTa * KD * KD * 2));
+        hipLaunchKernelGGL(wkv6_bwd_chunk_dstate<SEQ>, dim3((unsigned)NT, (unsigned)BH), dim3(NTHR), 0,
+                           s, (const uint16_t*)r, (const uint16_t*)dO, (const uint16_t*)w, dSloc, dec,
+                           scale, (int)B, (int)H, (int)T, (int)NT);
+        mark(phase_events, 1, s);
+        mark(phase_events, 2, s);
+        hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
+                           dec, dhT, dHs, dh0, (int)NT);
     }
-    mark(phase_events, 1, s);
-    mark(phase_events, 2, s);
-    hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
-                       decay, dhT, dHs, dh0, (int)NT);
     mark(phase_events, 3, s);
     if (NT > 0) {
         dim3 grid((unsigned)NT, (unsigned)BH);

@@ -43,12 +43,13 @@ def test_workspace_sizes(pkg):
     B, H, T = 8, 32, 4096
     NT = T // 64
     saved = L.rwkv6_wkv_saved_bytes(B, H, T, 64, 64)
-    assert saved >= B * H * (NT + 1) * 64 * 64 * 2 + B * H * NT * 64 * 4
+    assert saved >= B * H * (NT + 1) * 64 * 64 * 2                  # bf16 state per chunk + final
     # forward: no per-chunk state (the walk carries it); per-segment states only when B*H
     # is far below the device's workgroup count (config 5: 32 sequences of 512 chunks)
     assert 0 < L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 0) < 16 << 20
     assert L.rwkv6_wkv_workspace_bytes(1, 32, 32768, 64, 64, 0) >= 32 * 64 * 64 * 4
-    assert L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 1) > L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 0)
+    # backward: bf16 dS per chunk and fp32 du partials
+    assert L.rwkv6_wkv_workspace_bytes(B, H, T, 64, 64, 1) >= B * H * NT * 64 * (64 * 2 + 4)
     assert L.rwkv6_wkv_saved_bytes(B, H, T, 32, 64) == 0          # unsupported head size
 
 
