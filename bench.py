@@ -326,10 +326,9 @@ def main():
         "wkv6_tflops": tflops,
         "wkv6_pct_bf16_mfma_peak": 100.0 * tflops / BF16_PEAK_TFLOPS,
         "wkv6_alg_hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "phase_ms": {"fwd_chunk_state": fwd_ph[0], "fwd_state_scan": fwd_ph[1],
-                     "fwd_chunk_output": fwd_ph[2], "bwd_chunk_dstate": bwd_ph[0],
-                     "bwd_dstate_scan": bwd_ph[1], "bwd_chunk_grads": bwd_ph[2],
-                     "bwd_du_reduce": bwd_ph[3]},
+        "phase_ms": {"fwd_segment_states": fwd_ph[0], "fwd_walk": fwd_ph[2],
+                     "bwd_chunk_dstate": bwd_ph[0], "bwd_dstate_walk_or_scan": bwd_ph[1],
+                     "bwd_chunk_grads": bwd_ph[2], "bwd_du_reduce": bwd_ph[3]},
         "roofline": {"kernel": "wkv6_bwd_chunk_grads", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic(B, H, T)},

@@ -64,9 +64,10 @@ const char* rwkv6_strerror(int code);
  * keeps 8-token decay products inside the bf16 exponent range): tokens below the floor
  * change outputs and states by less than that factor; their dw is the gradient at the
  * floor (scaled by the same factor) and their d_decay (sequence-first entry) is 0.
- * `saved` (rwkv6_wkv_saved_bytes) receives the per-chunk states and decays that
- * the backward consumes; keep it alive until rwkv6_wkv_bwd.  `workspace`
- * (rwkv6_wkv_workspace_bytes) is scratch for the duration of one call.
+ * `saved` (rwkv6_wkv_saved_bytes) receives the bf16 state entering every chunk
+ * (and the final state), which the backward consumes; keep it alive until
+ * rwkv6_wkv_bwd.  `workspace` (rwkv6_wkv_workspace_bytes) is scratch for the duration
+ * of one call.
  * ---------------------------------------------------------------------- */
 size_t rwkv6_wkv_saved_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V);
 size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
@@ -215,8 +216,10 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
  * rwkv6_wkv_fwd / rwkv6_wkv_bwd, and additionally record caller-created timing
  * hipEvent_t objects around each kernel phase on `stream` (phase_events may be
  * NULL, and so may any entry).  Index pairs (2p, 2p+1) bracket phase p:
- *   fwd: 0 chunk-local states, 1 state scan, 2 chunk outputs
- *   bwd: 0 chunk-local dstates, 1 dstate scan, 2 chunk gradients, 3 du reduction
+ *   fwd: 0 segment-state pre-pass (only when B*H alone cannot fill the device),
+ *        1 unused (empty), 2 the output walk
+ *   bwd: 0 chunk-local dstates (chunk-parallel form only), 1 the reverse dstate walk or
+ *        the dstate scan, 2 chunk gradients, 3 du reduction
  * ---------------------------------------------------------------------- */
 int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
                      int u_dtype, const float* h0, void* o, float* hT, void* saved,

@@ -87,3 +87,17 @@ def test_midpoint_form_extreme_decay_needs_split_factors(T):
         assert _rel(gm[name], g[name]) < 1e-5, name
     # control: the unsplit factor loses those pairs
     assert _rel(cm.fwd_mid(r, k, v, w, u, h0, 1.0, split=False), o) > 1e-2
+
+
+@pytest.mark.parametrize("T", [64, 130])
+@pytest.mark.parametrize("strong", [False, True])
+def test_walk_form_matches_recurrence(T, strong):
+    """The forward walk's form (cross-block operands referenced at the end of the block
+    before the target, built from the midpoint values times fp32-range table factors)
+    equals the recurrence, also with per-token decays down to the -10 floor."""
+    lo, hi = (-3.0, 5.0) if strong else (-6.0, -0.5)
+    r, k, v, w, u, h0, dO, dhT = _inputs(1, 2, T, 16, 8, seed=T + 23, w_lo=lo, w_hi=hi)
+    w = np.maximum(w, -10.0).astype(np.float32)
+    o, hT = orc.wkv6_fwd(r, k, v, w, u, h0, 0.7)
+    o_m, hT_m = cm.fwd_walk(r, k, v, w, u, h0, 0.7)
+    assert _rel(o_m, o) < 1e-5 and _rel(hT_m, hT) < 1e-5

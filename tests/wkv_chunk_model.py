@@ -298,3 +298,46 @@ def bwd_mid(r, k, v, w, u, dO, h0=None, dhT=None, scale=1.0, split=True):
     du = np.einsum("bhcti,bhcti,bhct->hi", rc, kc, dd)
     cut = lambda a: a.reshape(B, H, NT * L, -1)[:, :, :T]
     return dict(dr=cut(dr), dk=cut(dk), dv=cut(dv), dw=cut(dw), du=du, dh0=dh0)
+
+
+# ---------------------------------------------------------------------------
+# Forward walk form (wkv6_fwd_walk).  Diagonal blocks use the midpoint tiles Rm, Km; the
+# inter-chunk term Ri = Rm e^{mu_I} = r e^{G_{t-1}}; cross-block pairs (I > J) reference
+# both operands at b_{I-1} = G[16I-1], the end of the block before the target block:
+#   Rp[t]      = Rm[t] e^{mu_I - b_{I-1}}          = r_t e^{G_{t-1} - b_{I-1}}
+#   Kc_I[tau]  = Km[tau] e^{b_{I-1} - mu_J}        = k_tau e^{b_{I-1} - G_tau}
+# with every table factor evaluated in fp32 range (_ex), as the kernel forms them from the
+# fp32 midpoint-referenced values.
+# ---------------------------------------------------------------------------
+
+def fwd_walk(r, k, v, w, u, h0=None, scale=1.0):
+    r, k, v, w = (np.asarray(a, np.float64) for a in (r, k, v, w))
+    u = np.asarray(u, np.float64)
+    B, H, T, K = r.shape
+    V = v.shape[-1]
+    NT = (T + L - 1) // L
+    _, hT, S_in = fwd(r, k, v, w, u, h0, scale)
+    rc, kc, vc, wc = (_chunks(a, T, NT) for a in (r, k, v, w))
+    G, Gm1 = _chunk_cumsum(wc)
+    mu, mu_t = _mid(G, Gm1)
+    Rm = rc * _ex(Gm1 - mu_t)
+    Km = kc * _ex(mu_t - G)
+    bonus = np.einsum("bhcti,hi,bhcti->bhct", rc, u, kc)
+    O = np.zeros((B, H, NT, L, V))
+    tril = np.tril(np.ones((SUB, SUB)), -1)
+    for I in range(L // SUB):
+        ti = slice(SUB * I, SUB * I + SUB)
+        O[..., ti, :] += np.einsum("bhcti,bhcij->bhctj", Rm[..., ti, :] * _ex(mu[..., I, None, :]),
+                                   S_in[:, :, :NT])
+        A = np.einsum("bhcti,bhcsi->bhcts", Rm[..., ti, :], Km[..., ti, :])
+        A = A * tril + np.einsum("bhct,ts->bhcts", bonus[..., ti], np.eye(SUB))
+        O[..., ti, :] += np.einsum("bhcts,bhcsj->bhctj", A, vc[..., ti, :])
+        if I > 0:
+            bp = G[..., SUB * I - 1, :]
+            Rp = Rm[..., ti, :] * _ex(mu[..., I, :] - bp)[..., None, :]
+            for J in range(I):
+                tj = slice(SUB * J, SUB * J + SUB)
+                Kc = Km[..., tj, :] * _ex(bp - mu[..., J, :])[..., None, :]
+                A = np.einsum("bhcti,bhcsi->bhcts", Rp, Kc)
+                O[..., ti, :] += np.einsum("bhcts,bhcsj->bhctj", A, vc[..., tj, :])
+    return scale * O.reshape(B, H, NT * L, V)[:, :, :T], hT
