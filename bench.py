@@ -62,8 +62,9 @@ def parse():
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
-                    help="after timing, run a plain device copy of this many MiB 3 times (reference "
-                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+                    help="after timing, run an elementwise copy kernel (dst = -src, plain vector loads "
+                         "and stores) over this many MiB 3 times: the reference kernel of known size "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -351,7 +352,7 @@ def main():
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)
         torch.cuda.synchronize()
         out["copy_calibration_bytes"] = 2 * n
     if not args.no_train:
