@@ -58,6 +58,48 @@ def _ramp(C, layer_id, n_layers, device):
     return 1.0 - torch.pow(ddd, ratio)
 
 
+def _splitk_wgrad(dy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """dW = dy^T x for dy [N, O], x [N, I] (N = tokens), fp32-accumulated.
+
+    A projection's weight gradient has a small output (O x I, e.g. 2048 x 2048 = 64 tiles
+    of 256 x 256) and a long reduction (16 K tokens): one GEMM occupies a quarter of the
+    256 CUs.  The tokens are split into s chunks (s doubles while the tile count stays below
+    512), the chunks run as one batched GEMM with fp32 outputs, and the partials are summed
+    in a fixed order."""
+    N, O = dy.shape
+    I = x.shape[1]
+    tiles = -(-O // 256) * -(-I // 256)
+    s = 1
+    while s < 8 and tiles * s < 512 and N % (2 * s) == 0:
+        s *= 2
+    if s == 1:
+        return (dy.t() @ x).to(dtype)
+    part = torch.bmm(dy.view(s, N // s, O).transpose(1, 2), x.view(s, N // s, I),
+                     out_dtype=torch.float32)
+    return part.sum(0).to(dtype)
+
+
+class _LinearFn(torch.autograd.Function):
+    """y = x W^T; backward dx = dy W on hipBLASLt, dW by the split-token GEMM above."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        wc = w.to(x.dtype)
+        ctx.save_for_backward(x, wc)
+        ctx.w_dtype = w.dtype
+        return F.linear(x, wc)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, wc = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1]).contiguous()
+        dx = (dy2 @ wc).view(x.shape) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            dw = _splitk_wgrad(dy2, x.reshape(-1, x.shape[-1]).contiguous(), ctx.w_dtype)
+        return dx, dw
+
+
 class _Linear(nn.Module):
     """Column/RowParallelLinear at TP=1: weight [out, in], y = x @ W^T (no bias)."""
 
@@ -68,7 +110,7 @@ class _Linear(nn.Module):
             nn.init.normal_(self.weight, 0.0, std)
 
     def forward(self, x):
-        return F.linear(x, self.weight.to(x.dtype)), None
+        return _LinearFn.apply(x, self.weight), None
 
 
 class GroupNorm(nn.Module):
