@@ -44,8 +44,6 @@
 #define CL 64            // chunk length (tokens)
 #define TS 72            // LDS row stride of a bf16 64x64 tile (elements): 144 B rows
 #define GS 72            // LDS row stride of an fp32 64x64 tile (elements)
-#define XS 68            // row stride of the epilogue's fp32 x / y views: rows 4 apart land 16
-                         // banks apart, so the 4 row groups of a wave's column writes do not collide
 #define GSG 69           // row stride of the fp32 cumulative-decay view: 69 = 5 (mod 64) banks keeps
                          // the row-wise reads of 8 consecutive rows by 8 lanes each conflict-free
 #define NTHR 256
@@ -1194,11 +1192,16 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     }
 
     // ---------------- epilogue ----------------
-    float drv[2][4], dkv[2][4], xv[2][4], yv[2][4];
+    // dr, dk, dv, dw at this lane's accumulator positions (tokens 16W + 4lq + rr, channel
+    // i = 32hh + 16tp + lr).  dw[t] = D + sum_{m > t} x[m] + y[t] with x = r dr_h - k dk_h,
+    // y = -k dk_h: the suffix sums over the tokens run within the lane (4 tokens), across the
+    // four lane rows (shuffles) and across the token blocks W (per-wave totals in `red`).
+    float drv[2][4], dkv[2][4], dwv[2][4], wtot[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
         const float ui = scale * load_u(u, u_dtype, h * KD + i);
+        float xv[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
@@ -1208,62 +1211,72 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const float udd = ui * sm.dd[tt];
             drv[tp][rr] = drh + udd * kv;
             dkv[tp][rr] = dkh + udd * rv;
-            xv[tp][rr] = rv * drh - kv * dkh;
-            yv[tp][rr] = -kv * dkh;
+            xv[rr] = rv * drh - kv * dkh;
+            dwv[tp][rr] = -kv * dkh;                                // y
         }
+        // within the lane: sum over the later tokens rr' > rr
+        dwv[tp][2] += xv[3];
+        dwv[tp][1] += xv[3] + xv[2];
+        dwv[tp][0] += (xv[3] + xv[2]) + xv[1];
+        const float lt = ((xv[3] + xv[2]) + xv[1]) + xv[0];
+        // across lane rows: sum over lq' > lq (lanes lr + 16 lq').  The shuffles run on all
+        // lanes (a lane outside the exec mask would read as zero).
+        const float d16 = __shfl_down(lt, 16);
+        float v = lt + (lq <= 2 ? d16 : 0.f);
+        const float d32 = __shfl_down(v, 32);
+        v += lq <= 1 ? d32 : 0.f;                                   // sum over lq' >= lq
+        const float later = v - lt;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) dwv[tp][rr] += later;
+        wtot[tp] = v;                                               // the wave's total at lq == 0
     }
-    __syncthreads();                       // all waves are done with the operand tiles
-    float (*Xs)[XS] = reinterpret_cast<float (*)[XS]>(&sm.A[0][0]);
-    float (*Ys)[XS] = reinterpret_cast<float (*)[XS]>(&sm.Vm[0][0]);
-    static_assert(CL * XS * 4 <= sizeof(sm.A) && CL * XS * 4 <= 2 * sizeof(tile_t), "x / y views");
+    // red is free (build_G scratch and du partials were consumed before the products)
+    if (lq == 0) {
+        sm.red[W][32 * hh + lr] = wtot[0];
+        sm.red[W][32 * hh + 16 + lr] = wtot[1];
+    }
+    __syncthreads();                       // all waves are done with the operand tiles; red is in
+    // dr, dk, dv, dw staged channel-major (XT[i][t], 8-byte writes of 4 tokens) in the operand
+    // tiles, read back token-major by transpose reads for 16-byte stores
+    uint16_t (*Ts[4])[TS] = {sm.RmH, sm.RmL, sm.KmH, sm.KmL};
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int tt = 16 * W + 4 * lq + rr;
-            Xs[tt][i] = xv[tp][rr];
-            Ys[tt][i] = yv[tp][rr];
-            sm.RmH[tt][i] = f2bf(drv[tp][rr]);
-            sm.RmL[tt][i] = f2bf(dkv[tp][rr]);
-            sm.KmH[tt][i] = f2bf(av[tp][rr]);
-        }
-    }
-    __syncthreads();
-    {
-        // dw: suffix sums over tokens; thread = (channel i, 8-token part)
-        const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-        float tsum = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) tsum += Xs[8 * part + s][i];
-        sm.red[part][i] = tsum;
-        __syncthreads();
         // D = rowsum(S_out dS) = e^{G_63} rowsum(S_in dS) + sum_t Km ak(dS part): the second
         // sum is the one the suffix sums of Km ak take off again, so dw keeps no rounding of a
         // large D (bf16 S_out) that cancels; what remains scales with e^{G_63}.
-        const float D = sm.Dv[i] + ((sm.Pk[0][i] + sm.Pk[1][i]) + (sm.Pk[2][i] + sm.Pk[3][i]));
-        float run = D;                     // D + sum_{m > t} x[m]
-        for (int p = part + 1; p < 8; ++p) run += sm.red[p][i];
+        float later = sm.Dv[i] + ((sm.Pk[0][i] + sm.Pk[1][i]) + (sm.Pk[2][i] + sm.Pk[3][i]));
+        for (int W2 = W + 1; W2 < 4; ++W2) later += sm.red[W2][i];
+        float g[4];
 #pragma unroll
-        for (int s = 7; s >= 0; --s) {
-            const int tt = 8 * part + s;
-            float g = run + Ys[tt][i];
+        for (int rr = 0; rr < 4; ++rr) {
+            const int tt = 16 * W + 4 * lq + rr;
+            g[rr] = dwv[tp][rr] + later;
             // d decay = dw * w, w = -exp(decay); a floored token's d decay is 0 (the exact
             // one carries its decay factor).  The head-first dw of a floored token is the
             // gradient at the floor, itself scaled by e^W_MIN.
             if (SEQ && tt < nvalid) {
                 const float wn = -ex2(bf2f(w[base + (size_t)tt * rs + i]) * RW_L2E);
-                g = wn < W_MIN ? 0.f : g * wn;
+                g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
             }
-            sm.KmL[tt][i] = f2bf(g);
-            run += Xs[tt][i];
         }
+        const int t4 = 16 * W + 4 * lq;
+        *reinterpret_cast<uint2*>(&Ts[0][i][t4]) = make_uint2(pk2(drv[tp][0], drv[tp][1]), pk2(drv[tp][2], drv[tp][3]));
+        *reinterpret_cast<uint2*>(&Ts[1][i][t4]) = make_uint2(pk2(dkv[tp][0], dkv[tp][1]), pk2(dkv[tp][2], dkv[tp][3]));
+        *reinterpret_cast<uint2*>(&Ts[2][i][t4]) = make_uint2(pk2(av[tp][0], av[tp][1]), pk2(av[tp][2], av[tp][3]));
+        *reinterpret_cast<uint2*>(&Ts[3][i][t4]) = make_uint2(pk2(g[0], g[1]), pk2(g[2], g[3]));
     }
     __syncthreads();
-    store_tile<NTHR_G>(dr + base, sm.RmH, nvalid, rs);
-    store_tile<NTHR_G>(dk + base, sm.RmL, nvalid, rs);
-    store_tile<NTHR_G>(dv + base, sm.KmH, nvalid, rs);
-    store_tile<NTHR_G>(dw + base, sm.KmL, nvalid, rs);
+    {
+        // wave wv stores tokens 16 (wv & 3) + L, channels 32 (wv >> 2) + 8q .. +7 of each tensor
+        const int tk = 16 * (wv & 3) + lr, ch = 32 * (wv >> 2) + 8 * lq;
+        uint16_t* outs[4] = {dr, dk, dv, dw};
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            const uint4 x = __builtin_bit_cast(uint4, ld_tr8_g8(&Ts[n][0][0], 32 * (wv >> 2), 16 * (wv & 3)));
+            if (tk < nvalid) *reinterpret_cast<uint4*>(outs[n] + base + (size_t)tk * rs + ch) = x;
+        }
+    }
 }
 
 // du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q), q < 16: strided partial sum over
