@@ -44,8 +44,10 @@
 #define CL 64            // chunk length (tokens)
 #define TS 72            // LDS row stride of a bf16 64x64 tile (elements): 144 B rows
 #define GS 72            // LDS row stride of an fp32 64x64 tile (elements)
-#define GSG 69           // row stride of the fp32 cumulative-decay view: 69 = 5 (mod 64) banks keeps
-                         // the row-wise reads of 8 consecutive rows by 8 lanes each conflict-free
+#define GSG 68           // row stride of the fp32 cumulative-decay view: 16-byte aligned rows, so a
+                         // thread reads 8 consecutive values with two 16-byte loads (8 rows x 8
+                         // threads of a wave hit distinct banks), and reads of rows 4 apart by 16
+                         // consecutive lanes fall 16 banks apart
 #define NTHR 256
 #define NTHR_G 512       // threads of the gradient kernel (8 waves)
 // Per-token log-decay floor.  The midpoint-referenced operand tiles scale by the decay of up
@@ -199,6 +201,19 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], fl
 #pragma unroll
     for (int s = 0; s < PL; ++s) Gm[PL * part + s][i] = loc[s] + off;
     __syncthreads();
+}
+
+// G[row][c8 .. c8+7] with two 16-byte LDS reads.
+__device__ __forceinline__ void g8(const float (*Gm)[GSG], int row, int c8, float* f) {
+    const float4 a = *reinterpret_cast<const float4*>(&Gm[row][c8]);
+    const float4 b = *reinterpret_cast<const float4*>(&Gm[row][c8 + 4]);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+// G[row - 1][c8 .. c8+7], zero for row 0 (G before the chunk's first token).
+__device__ __forceinline__ void g8m1(const float (*Gm)[GSG], int row, int c8, float* f) {
+    g8(Gm, row > 0 ? row - 1 : 0, c8, f);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) f[s] = row > 0 ? f[s] : 0.f;
 }
 
 __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
@@ -450,12 +465,14 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             float rf[8], kf[8], rm[8], km[8], y[8], f[8];
             unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
             unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+            float gm[8], gg[8], gp[8];
+            g8(Gm, 16 * I + 7, c8, gm);
+            g8(Gm, row, c8, gg);
+            g8m1(Gm, row, c8, gp);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const float m = Gm[16 * I + 7][c8 + s], g = Gm[row][c8 + s];
-                const float gm1 = row > 0 ? Gm[row - 1][c8 + s] : 0.f;
-                rm[s] = rf[s] * ex2(gm1 - m);
-                km[s] = kf[s] * ex2(m - g);
+                rm[s] = rf[s] * ex2(gp[s] - gm[s]);
+                km[s] = kf[s] * ex2(gm[s] - gg[s]);
             }
             sstore16(sm.Rm, row, c8, pack8(rm));
             sstore16(sm.Km, row, c8, pack8(km));
@@ -494,8 +511,13 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             }
             float kf[8], e[8];
             unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+            {
+                float gl[8], gg[8];
+                g8(Gm, CL - 1, c8, gl);
+                g8(Gm, row, c8, gg);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(Gm[CL - 1][c8 + s] - Gm[row][c8 + s]);
+                for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(gl[s] - gg[s]);
+            }
             sstore16(sm.Kt, row, c8, pack8(e));
         }
         __syncthreads();
@@ -622,7 +644,13 @@ wkv6_bwd_chunk_dstate(const uint16_t* __restrict__ r, const uint16_t* __restrict
         float xf[8], e[8];
         unpack8(xr[p], xf);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) e[s] = xf[s] * ex2(row > 0 ? Gm[row - 1][c8 + s] : 0.f);
+        for (int s = 0; s < 8; ++s) e[s] = xf[s];
+        {
+            float gp[8];
+            g8m1(Gm, row, c8, gp);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) e[s] *= ex2(gp[s]);
+        }
         sstore16(Xs, row, c8, pack8(e));
     }
     if (threadIdx.x < KD) dec[((size_t)bh * NT + c) * KD + threadIdx.x] = ex2(Gm[CL - 1][threadIdx.x]);
@@ -1018,13 +1046,14 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         }
         // operand tiles Rm, Km (hi/lo); the w scratch in RmL was consumed by build_G
         const int mrow = 16 * (row >> 4) + 7;
-        float a[8], b[8];
+        float a[8], b[8], gm[8], gg[8], gp[8];
+        g8(Gv, mrow, c8, gm);
+        g8(Gv, row, c8, gg);
+        g8m1(Gv, row, c8, gp);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const float m = Gv[mrow][c8 + s];
-            const float gm1 = row > 0 ? Gv[row - 1][c8 + s] : 0.f;
-            a[s] = rf[s] * ex2(gm1 - m);
-            b[s] = kf[s] * ex2(m - Gv[row][c8 + s]);
+            a[s] = rf[s] * ex2(gp[s] - gm[s]);
+            b[s] = kf[s] * ex2(gm[s] - gg[s]);
         }
         uint4 hi, lo;
         pack8_split(a, hi, lo);
