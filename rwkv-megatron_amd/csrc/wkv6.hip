@@ -80,6 +80,14 @@ __device__ __forceinline__ bf16x8 ld_tr8(const uint16_t* X, int r0, int c0) {
     const bf16x4 a = ld_tr4(X, r0, c0), b = ld_tr4(X, r0 + 16, c0);
     return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
+// Lane l receives X[r0 + s][l], s = 0..3: 16-lane row group q reads columns 16q..16q+15 of
+// rows r0..r0+3 (lanes 4s..4s+3 of the group read row s), so a wave reads 4 rows x 64
+// columns and each lane gets 4 consecutive rows of its own column.
+__device__ __forceinline__ bf16x4 ld_col4(const uint16_t* X, int r0) {
+    const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
+    const uint16_t* p = X + (r0 + (L >> 2)) * TS + 16 * q + 4 * (L & 3);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
 // Direct read of row `row` with the slot order of ld_tr8: columns c0+4q+(0..3), c0+16+4q+(0..3).
 __device__ __forceinline__ bf16x8 ld_dir8(const uint16_t* X, int row, int c0) {
     const int q = (threadIdx.x & 63) >> 4;
@@ -187,11 +195,16 @@ __device__ __forceinline__ void build_G(uint16_t (*Wm)[TS], float (*Gm)[GSG], fl
     float loc[PL];
     float run = 0.f;
 #pragma unroll
-    for (int s = 0; s < PL; ++s) {
-        const float x = bf2f(Wm[PL * part + s][i]);
-        const float wn = DEC ? ((PL * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
-        run += fmaxf(wn, W_MIN) * RW_L2E;
-        loc[s] = run;
+    for (int s4 = 0; s4 < PL; s4 += 4) {
+        const bf16x4 x4 = ld_col4(&Wm[0][0], PL * part + s4);       // column i = lane
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int s = s4 + j;
+            const float x = (float)x4[j];
+            const float wn = DEC ? ((PL * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+            run += fmaxf(wn, W_MIN) * RW_L2E;
+            loc[s] = run;
+        }
     }
     tot[part * 64 + i] = run;
     __syncthreads();
@@ -279,11 +292,16 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
     float loc[8];
     float run = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const float x = bf2f(sm.Kt[8 * part + s][i]);           // w scratch
-        const float wn = DEC ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
-        run += fmaxf(wn, W_MIN) * RW_L2E;
-        loc[s] = run;
+    for (int s4 = 0; s4 < 8; s4 += 4) {
+        const bf16x4 x4 = ld_col4(&sm.Kt[0][0], 8 * part + s4);   // w scratch, column i = lane
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int s = s4 + j;
+            const float x = (float)x4[j];
+            const float wn = DEC ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+            run += fmaxf(wn, W_MIN) * RW_L2E;
+            loc[s] = run;
+        }
     }
     sm.tot[part * 64 + i] = run;
     __syncthreads();
