@@ -969,6 +969,10 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 
     // ---- prologue: one 16-byte piece of every tile per thread ----
     const uint4 rq = gload16s(r + base, row, c8, nvalid, rs), kq = gload16s(k + base, row, c8, nvalid, rs);
+    // states: S_in and dS rows (thread row = channel i), issued with the token tiles so their
+    // latency overlaps; kept in registers until G is consumed
+    const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
+    const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
     {
         const uint4 vq = gload16s(v + base, row, c8, nvalid, rs), dq = gload16(dO + dbase, row, c8, nvalid);
         sstore16(sm.Vm, row, c8, vq);
@@ -994,10 +998,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             sm.dd[row] = d;
         }
     }
-    // states: S_in and dS rows (thread row = channel i), kept in registers until G is consumed;
     // Dv[i] = sum_j S_in[i][j] dS[i][j] (scaled by e^{G_63} once G is built)
-    const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
-    const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
     {
         float a8[8], b8[8], d = 0.f;
         unpack8(sq, a8);
