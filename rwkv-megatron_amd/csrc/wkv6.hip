@@ -1012,13 +1012,17 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
     __syncthreads();
-    // raw r, k at this lane's accumulator positions (tokens 16W+4lq+rr, channel 32hh+16tp+lr),
-    // read before build_G's barriers (after them the operand tiles overwrite RmH and KmH)
-    bf16x4 rrw[2], krw[2];
+    // raw r, k (and for SEQ the pre-activation decay) at this lane's accumulator positions
+    // (tokens 16W+4lq+rr, channel 32hh+16tp+lr), read before build_G's barriers (after them
+    // the operand tiles overwrite RmH, KmH and the w scratch in RmL); u of its two channels
+    bf16x4 rrw[2], krw[2], wrw[2];
+    float ulane[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         rrw[tp] = ld_tr4(&sm.RmH[0][0], 16 * W, 16 * (2 * hh + tp));
         krw[tp] = ld_tr4(&sm.KmH[0][0], 16 * W, 16 * (2 * hh + tp));
+        if (SEQ) wrw[tp] = ld_tr4(&sm.RmL[0][0], 16 * W, 16 * (2 * hh + tp));
+        ulane[tp] = scale * load_u(u, u_dtype, h * KD + 16 * (2 * hh + tp) + lr);
     }
     build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
     {
@@ -1248,7 +1252,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
-        const float ui = scale * load_u(u, u_dtype, h * KD + i);
+        const float ui = ulane[tp];
         float xv[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -1304,7 +1308,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             // one carries its decay factor).  The head-first dw of a floored token is the
             // gradient at the floor, itself scaled by e^W_MIN.
             if (SEQ && tt < nvalid) {
-                const float wn = -ex2(bf2f(w[base + (size_t)tt * rs + i]) * RW_L2E);
+                const float wn = -ex2((float)wrw[tp][rr] * RW_L2E);
                 g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
             }
         }
