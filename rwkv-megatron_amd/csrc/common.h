@@ -68,15 +68,19 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* f) {
     *reinterpret_cast<uint4*>(p) = pack8(f);
 }
 // 8 consecutive parameters (RWKV6_BF16 or RWKV6_F32, the codes of rwkv6_amd.h) as fp32.
+// Branch-free: both forms issue two 16-byte loads from in-bounds addresses (the bf16 form
+// reads its one piece twice) and select the converted values, so the caller's other loads
+// stay in flight (a load under a branch makes the merge wait for every outstanding load).
 __device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t off, float* f) {
-    if (dtype == 1) {
-        load8(reinterpret_cast<const uint16_t*>(p) + off, f);
-    } else {
-        const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
-        float4 a = q[0], b = q[1];
-        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    }
+    const bool h = dtype == 1;
+    const char* b = reinterpret_cast<const char*>(p) + (h ? off * 2 : off * 4);
+    const uint4 x = *reinterpret_cast<const uint4*>(b);
+    const uint4 y = *reinterpret_cast<const uint4*>(b + (h ? 0 : 16));
+    float hf[8];
+    unpack8(x, hf);
+    const unsigned w[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) f[s] = h ? hf[s] : __builtin_bit_cast(float, w[s]);
 }
 
 // Splits fp32 values into bf16 hi + lo parts (hi + lo carries ~16 mantissa bits):

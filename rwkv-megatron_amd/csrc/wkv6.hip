@@ -646,13 +646,32 @@ wkv6_bwd_chunk_dstate(const uint16_t* __restrict__ r, const uint16_t* __restrict
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
     const size_t dbase = tok_base<false>(bh, t0, B, H, T);
-    uint4 xr[2];
+    // all six 16-byte loads in flight before the first LDS store waits on one: the loads are
+    // unconditional (rows past the end read the last token) and a ragged last chunk zeroes
+    // those rows afterwards (a load under a branch makes the merge wait for it)
+    uint4 xr[2], yq[2], wq[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int idx = p * NTHR + threadIdx.x, row = min(idx >> 3, nvalid - 1), c8 = (idx & 7) * 8;
+        xr[p] = *reinterpret_cast<const uint4*>(r + base + (size_t)row * rs + c8);
+        yq[p] = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)row * KD + c8);
+        wq[p] = *reinterpret_cast<const uint4*>(w + base + (size_t)row * rs + c8);
+    }
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
-        xr[p] = gload16s(r + base, row, c8, nvalid, rs);
-        sstore16(Ys, row, c8, gload16(dO + dbase, row, c8, nvalid));
-        sstore16(Wm, row, c8, gload16s(w + base, row, c8, nvalid, rs));
+        sstore16(Ys, row, c8, yq[p]);
+        sstore16(Wm, row, c8, wq[p]);
+    }
+    if (nvalid < CL) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
+            if (row >= nvalid) {
+                sstore16(Ys, row, c8, make_uint4(0u, 0u, 0u, 0u));
+                sstore16(Wm, row, c8, make_uint4(0u, 0u, 0u, 0u));
+            }
+        }
     }
     __syncthreads();
     build_G<NTHR, SEQ>(Wm, Gm, tot, nvalid);
@@ -661,8 +680,9 @@ wkv6_bwd_chunk_dstate(const uint16_t* __restrict__ r, const uint16_t* __restrict
         const int idx = p * NTHR + threadIdx.x, row = idx >> 3, c8 = (idx & 7) * 8;
         float xf[8], e[8];
         unpack8(xr[p], xf);
+        const float keep = row < nvalid ? 1.f : 0.f;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) e[s] = xf[s];
+        for (int s = 0; s < 8; ++s) e[s] = xf[s] * keep;
         {
             float gp[8];
             g8m1(Gm, row, c8, gp);
@@ -967,17 +987,18 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     const size_t st_in = ((size_t)bh * (NT + 1) + c) * KD * KD;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
 
-    // ---- prologue: one 16-byte piece of every tile per thread ----
-    const uint4 rq = gload16s(r + base, row, c8, nvalid, rs), kq = gload16s(k + base, row, c8, nvalid, rs);
-    // states: S_in and dS rows (thread row = channel i), issued with the token tiles so their
-    // latency overlaps; kept in registers until G is consumed
+    // ---- prologue: one 16-byte piece of every tile per thread, all seven loads in flight
+    // together (branch-free loads: a load under a branch makes the merge wait for it) ----
+    const uint4 rq = gload16c(r + base, row, c8, nvalid, rs), kq = gload16c(k + base, row, c8, nvalid, rs);
+    const uint4 vq = gload16c(v + base, row, c8, nvalid, rs), dq = gload16c(dO + dbase, row, c8, nvalid, KD);
+    const uint4 wq = gload16c(w + base, row, c8, nvalid, rs);
+    // states: S_in and dS rows (thread row = channel i), kept in registers until G is consumed
     const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
     const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
     {
-        const uint4 vq = gload16s(v + base, row, c8, nvalid, rs), dq = gload16(dO + dbase, row, c8, nvalid);
         sstore16(sm.Vm, row, c8, vq);
         sstore16(sm.Dm, row, c8, dq);
-        sstore16(sm.RmL, row, c8, gload16s(w + base, row, c8, nvalid, rs));     // w scratch
+        sstore16(sm.RmL, row, c8, wq);                   // w scratch
         sstore16(sm.RmH, row, c8, rq);                   // raw r, k: read back below in the
         sstore16(sm.KmH, row, c8, kq);                   // lane layout of the accumulators
         float rf[8], kf[8], uf[8], vf[8], df[8], b = 0.f, d = 0.f;
