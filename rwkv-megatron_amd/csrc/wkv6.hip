@@ -367,11 +367,14 @@ __device__ __forceinline__ void walk_issue(WalkPrefetch& f, const uint16_t* __re
                                            int H, int T) {
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
-    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
-    if (OUT) f.r = gload16c(r + base, row, c8, nvalid, rs);
-    f.k = gload16c(k + base, row, c8, nvalid, rs);
-    f.v = gload16c(v + base, row, c8, nvalid, rs);
-    f.w = gload16c(w + base, row, c8, nvalid, rs);
+    // unconditional loads (rows past the end read the last token; the walk zeroes those
+    // rows in LDS): a load under a branch makes the next wait a full one
+    const int row = min((int)(threadIdx.x >> 3), nvalid - 1), c8 = (threadIdx.x & 7) * 8;
+    const size_t off = base + (size_t)row * rs + c8;
+    if (OUT) f.r = *reinterpret_cast<const uint4*>(r + off);
+    f.k = *reinterpret_cast<const uint4*>(k + off);
+    f.v = *reinterpret_cast<const uint4*>(v + off);
+    f.w = *reinterpret_cast<const uint4*>(w + off);
 }
 
 // Global stores of chunk c (o from Ot, S_in from Sin[c & 1]).  Issued one
@@ -381,9 +384,11 @@ __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restr
                                            int NT) {
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    if (row < nvalid)
-        *reinterpret_cast<uint4*>(o + ((size_t)bh * T + t0 + row) * KD + c8) =
-            *reinterpret_cast<const uint4*>(&sm.Ot[row][c8]);
+    // unconditional (a store under a branch costs the loop a full wait): rows past the end
+    // store the last token's own values again
+    const int ro = min(row, nvalid - 1);
+    *reinterpret_cast<uint4*>(o + ((size_t)bh * T + t0 + ro) * KD + c8) =
+        *reinterpret_cast<const uint4*>(&sm.Ot[ro][c8]);
     *reinterpret_cast<uint4*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8) =
         *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8]);
 }
@@ -443,10 +448,14 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     }
     float gsum = 0.f;                      // pre-pass: total log2-decay of channel threadIdx.x
 
+    // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
+    // loop's own order (the next chunk's loads, then this chunk's two stores) alone
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(CL, T - c * CL);
         // Every tile written here was last read before the previous chunk's final barrier
         // (Sin[c & 1] two chunks ago).  Raw r and k wait in Rm and Km.
+        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
         sstore16(sm.Vm, row, c8, nx.v);
         sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
         sstore16(sm.Km, row, c8, nx.k);
@@ -468,9 +477,10 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
                     sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
-            if (c > c_begin) walk_store(sm, o, Hs, bh, c - 1, T, NT);
         }
-        if (c + 1 < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c + 1, B, H, T);
+        // unconditional (the last iteration reloads its own chunk): loads under a branch
+        // would cost the loop a full wait
+        walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
         __syncthreads();
         if (OUT) {
             walk_build_G<SEQ>(sm, nvalid, c & 1);
@@ -600,6 +610,10 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
         }
         __syncthreads();
+        // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
+        // for those at the top of the next iteration leaves these stores in flight (vmcnt
+        // counts loads and stores in issue order)
+        if (OUT) walk_store(sm, o, Hs, bh, c, T, NT);
     }
 
     // ---- end of the segment ----
@@ -612,7 +626,6 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
         if (threadIdx.x >= 7 * 64) Aseg[sq * KD + (threadIdx.x & 63)] = gsum;
     } else {
-        if (c_end > c_begin) walk_store(sm, o, Hs, bh, c_end - 1, T, NT);
         if (seg == P - 1) {
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
