@@ -187,6 +187,7 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
                              float* __restrict__ ds_out, float* __restrict__ part, int64_t N,
                              int64_t B, int64_t C, int R, int64_t per) {
     __shared__ float red[LORA_NE][2][64];          // [mix][token half of a group][channel]
+    __shared__ __attribute__((aligned(16))) float bsm[LORA_NE][64];   // bias of the block's channels
     int64_t tb, cb;
     if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
@@ -195,32 +196,68 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
     lora_stage(lora_sm, wut, LORA_NE, C, R, cb * 64);
     for (int j = threadIdx.x; j < LORA_NE * 2 * 64; j += LORA_THR) (&red[0][0][0])[j] = 0.f;
+    if (threadIdx.x < LORA_NE * 8) {
+        const int e = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+        float bb[8];
+        load_param8(bias, pdt, (int64_t)e * C + cb * 64 + c8, bb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bsm[e][c8 + j] = bb[j];
+    }
     __syncthreads();
+    // Loads are unconditional (a token past the end reads the last token; its d_mixed is
+    // multiplied by 0 for the d_bias sums and nothing of it is stored): a load under a branch
+    // makes the merge wait for every outstanding load.
     for (int g = 0; g < LORA_TT / 32; ++g) {
         const int64_t tok = tb * LORA_TT + 32 * g + 16 * tw + L;
         const bool tv = tok < N;
+        const int64_t tc = tv ? tok : N - 1;
+        const float keep = tv ? 1.f : 0.f, keep_p = tc >= B ? 1.f : 0.f;
+        const uint16_t* nrow = neck + tc * LORA_NE * R;
         float dl[8], dd[8], ds[8];
         {
             float xv[8];
-            if (tv) load8(x + tok * C + cl, xv);
-            else for (int j = 0; j < 8; ++j) xv[j] = 0.f;
-            if (tv && tok >= B) load8(x + (tok - B) * C + cl, dl);
-            else for (int j = 0; j < 8; ++j) dl[j] = 0.f;
+            load8(x + tc * C + cl, xv);
+            load8(x + (tc >= B ? tc - B : tc) * C + cl, dl);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                dl[j] -= xv[j];
+                dl[j] = dl[j] * keep_p - xv[j];
                 dd[j] = ds[j] = 0.f;
             }
         }
 #pragma unroll 1
         for (int e = 0; e < LORA_NE; ++e) {
-            float m[8], bb[8], v[8];
-            lora_up8(lora_sm, neck + tok * LORA_NE * R, tv, R, e, h, m);
-            load_param8(bias, pdt, (int64_t)e * C + cl, bb);
-            if (tv) load8(dmix.p[e] + tok * C + cl, v);
-            else for (int j = 0; j < 8; ++j) v[j] = 0.f;
+            // this mix's neck piece and d_mixed, issued together (unconditional loads)
+            const uint4 nk_e = *reinterpret_cast<const uint4*>(nrow + e * R + 8 * q);
+            const uint4 dq_e = *reinterpret_cast<const uint4*>(dmix.p[e] + tc * C + cl);
+            float m[8], v[8];
+            {
+                // m = neck_e W_up_e at the lane's 8 channels (ranks 0..31 from nk_e)
+                const int rs = lds_rs(R);
+                const uint16_t* swe = lora_sm + (e * 64 + 32 * h) * rs;
+                f32x4 acc[2] = {};
+#pragma unroll
+                for (int tcn = 0; tcn < 2; ++tcn)
+                    acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 8 * q),
+                                      __builtin_bit_cast(bf16x8, nk_e), acc[tcn]);
+                for (int ks = 1; ks < R / 32; ++ks) {
+                    const int r0 = 32 * ks + 8 * q;
+                    const bf16x8 bq = ld_bf16x8(nrow + e * R + r0);
+#pragma unroll
+                    for (int tcn = 0; tcn < 2; ++tcn)
+                        acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + r0), bq, acc[tcn]);
+                }
+#pragma unroll
+                for (int tcn = 0; tcn < 2; ++tcn)
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) m[4 * tcn + rr] = acc[tcn][rr];
+            }
+            unpack8(dq_e, v);
+            const float4 b0 = *reinterpret_cast<const float4*>(&bsm[e][cw]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&bsm[e][cw + 4]);
+            const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
+                v[j] *= keep;
                 dd[j] += v[j] * (m[j] + bb[j]);
                 ds[j] += v[j];
                 v[j] *= dl[j];                                  // d_mexp
