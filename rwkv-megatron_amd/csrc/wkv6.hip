@@ -1138,7 +1138,8 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         float acc = 0.f;
 #pragma unroll
         for (int p = 0; p < 8; ++p) acc += sm.red[p][threadIdx.x];
-        du_part[((size_t)bh * NT + c) * KD + threadIdx.x] = scale * acc;
+        // head-major [h][b][c][i]: each head's partials are contiguous for the du reduction
+        du_part[(((size_t)h * B + bh / H) * NT + c) * KD + threadIdx.x] = scale * acc;
     }
     sstore16(Sin, row, c8, sq);
     sstore16(dSm, row, c8, dsq);
@@ -1365,30 +1366,53 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     }
 }
 
-// du[h][i] = sum_b sum_c du_part[b,h,c,i].  Thread (i, q), q < 16: strided partial sum over
-// the B*NT (b, c) pairs with p = q mod 16, then a fixed-order combine (deterministic).
+// du[h][i] = sum_b sum_c du_part[h,b,c,i].  One block per head over its contiguous B*NT*64
+// partials: thread t adds the float4 pieces t, t + 1024, ... (channels 4 (t & 15) .. +3; all
+// its loads in flight together); the four lanes of a wave with the same quad, then the 16
+// waves, are added in a fixed order (deterministic).
 #define DU_THR 1024
 __global__ void __launch_bounds__(DU_THR)
 wkv6_du_reduce(const float* __restrict__ du_part, void* __restrict__ du, int u_dtype, int B,
                int H, int NT) {
-    __shared__ float part[DU_THR / KD][KD];
-    const int h = blockIdx.x, i = threadIdx.x & 63, q = threadIdx.x >> 6;
-    constexpr int NQ = DU_THR / KD;
-    float acc = 0.f;
-    const int P = B * NT;
-#pragma unroll 4
-    for (int p = q; p < P; p += NQ) {
-        const int b = p / NT, c = p - b * NT;
-        acc += du_part[((size_t)(b * H + h) * NT + c) * KD + i];
-    }
-    part[q][i] = acc;
-    __syncthreads();
-    if (q == 0) {
-        float tot = 0.f;
+    __shared__ float4 part[DU_THR / 64][16];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float4* src = reinterpret_cast<const float4*>(du_part + (size_t)h * B * NT * KD);
+    const int n4 = B * NT * (KD / 4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int k = t;
+    for (; k + 7 * DU_THR < n4; k += 8 * DU_THR) {
+        float4 x[8];
 #pragma unroll
-        for (int j = 0; j < NQ; ++j) tot += part[j][i];
-        if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[h * KD + i] = f2bf(tot);
-        else reinterpret_cast<float*>(du)[h * KD + i] = tot;
+        for (int j = 0; j < 8; ++j) x[j] = src[k + j * DU_THR];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc.x += x[j].x; acc.y += x[j].y; acc.z += x[j].z; acc.w += x[j].w;
+        }
+    }
+    for (; k < n4; k += DU_THR) {
+        const float4 x = src[k];
+        acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+    }
+    // within the wave: lanes j, j + 16, j + 32, j + 48 hold quad j (fixed-order exchanges)
+    acc.x += lane_xor_swz<16>(acc.x); acc.y += lane_xor_swz<16>(acc.y);
+    acc.z += lane_xor_swz<16>(acc.z); acc.w += lane_xor_swz<16>(acc.w);
+    acc.x += lane_xor32(acc.x); acc.y += lane_xor32(acc.y);
+    acc.z += lane_xor32(acc.z); acc.w += lane_xor32(acc.w);
+    if ((t & 63) < 16) part[t >> 6][t & 15] = acc;
+    __syncthreads();
+    if (t < 16) {
+        float4 tot = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < DU_THR / 64; ++j) {
+            const float4 x = part[j][t];
+            tot.x += x.x; tot.y += x.y; tot.z += x.z; tot.w += x.w;
+        }
+        const float v[4] = {tot.x, tot.y, tot.z, tot.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[h * KD + 4 * t + e] = f2bf(v[e]);
+            else reinterpret_cast<float*>(du)[h * KD + 4 * t + e] = v[e];
+        }
     }
 }
 
