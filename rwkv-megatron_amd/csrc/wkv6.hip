@@ -815,10 +815,12 @@ __device__ __forceinline__ void dstate_issue(DstatePrefetch& f, const uint16_t* 
                                              int B, int H, int T) {
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
-    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
-    f.r = gload16c(r + base, row, c8, nvalid, rs);
-    f.w = gload16c(w + base, row, c8, nvalid, rs);
-    f.d = gload16c(dO + ((size_t)bh * T + t0) * KD, row, c8, nvalid, KD);
+    // unconditional loads (rows past the end read the last token; dstate_chunk zeroes them):
+    // a load under a branch makes the next wait a full one
+    const int row = min((int)(threadIdx.x >> 3), nvalid - 1), c8 = (threadIdx.x & 7) * 8;
+    f.r = *reinterpret_cast<const uint4*>(r + base + (size_t)row * rs + c8);
+    f.w = *reinterpret_cast<const uint4*>(w + base + (size_t)row * rs + c8);
+    f.d = *reinterpret_cast<const uint4*>(dO + ((size_t)bh * T + t0 + row) * KD + c8);
 }
 
 // One chunk of the reverse walk: stores the prefetched tiles, writes dS_out(c) and advances
@@ -832,9 +834,11 @@ __device__ __forceinline__ void dstate_chunk(DstateSmem& sm, const DstatePrefetc
     const int L = lane & 15, q = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
     const int nvalid = min(CL, T - c * CL), b = c & 1;
-    sstore16(sm.Rw[b], row, c8, f.r);
-    sstore16(sm.Ww[b], row, c8, f.w);
-    sstore16(sm.Dw[b], row, c8, f.d);
+    const bool zero = nvalid < CL && row >= nvalid;
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    sstore16(sm.Rw[b], row, c8, zero ? z : f.r);
+    sstore16(sm.Ww[b], row, c8, zero ? z : f.w);
+    sstore16(sm.Dw[b], row, c8, zero ? z : f.d);
     __syncthreads();       // chunk c's tiles are in; buffer b ^ 1 was last read before this point
     // cumulative log2-decay of channel 16cg + L at tokens 32ks + 8q + s (run-local)
     float g[2][8], run[2];
@@ -933,12 +937,15 @@ wkv6_bwd_dstate_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
             D[tp][rr] = dhT ? dhT[sbase + (16 * cg + 4 * q + rr) * KD + 32 * jh + 16 * tp + L] : 0.f;
+    // the prologue's loads complete here, so the loop's waits follow its own order; the
+    // issues are unconditional (past chunk 0 they reload chunk 0)
+    __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
     for (int c = NT - 1; c >= 0; c -= 2) {
         dstate_chunk<SEQ>(sm, fa, D, dHs, bh, c, T, NT, scale);
-        if (c - 2 >= 0) dstate_issue<SEQ>(fa, r, w, dO, bh, c - 2, B, H, T);
+        dstate_issue<SEQ>(fa, r, w, dO, bh, max(c - 2, 0), B, H, T);
         if (c - 1 < 0) break;
         dstate_chunk<SEQ>(sm, fb, D, dHs, bh, c - 1, T, NT, scale);
-        if (c - 3 >= 0) dstate_issue<SEQ>(fb, r, w, dO, bh, c - 3, B, H, T);
+        dstate_issue<SEQ>(fb, r, w, dO, bh, max(c - 3, 0), B, H, T);
     }
     if (dh0) {
 #pragma unroll
