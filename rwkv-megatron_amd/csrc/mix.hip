@@ -413,7 +413,9 @@ rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restric
 
 // Elementwise epilogues over n bf16 elements (n % 8 == 0); each thread owns two 16-byte
 // vectors, both loads issued before any arithmetic.
-#define EW_VEC 2
+#define EW_VEC 2          // 16-byte pieces per thread.  Loads and stores clamp the index
+                          // (no branch, so all of a thread's loads are in flight together);
+                          // a piece past the end repeats the last one, same value, same place
 __device__ __forceinline__ float sigmoid_(float z) { return 1.f / (1.f + __expf(-z)); }
 
 // h = relu(up)^2
@@ -423,17 +425,17 @@ rwkv6_relu_sq_kernel(const uint16_t* __restrict__ up, uint16_t* __restrict__ h, 
     float a[EW_VEC][8];
 #pragma unroll
     for (int v = 0; v < EW_VEC; ++v)
-        if (i0 + v < n8) load8(up + 8 * (i0 + v), a[v]);
+        load8(up + 8 * min(i0 + v, n8 - 1), a[v]);
 #pragma unroll
     for (int v = 0; v < EW_VEC; ++v) {
-        if (i0 + v >= n8) break;
+        const int64_t jo = min(i0 + v, n8 - 1);         // past the end: last piece again
         float o[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const float r = fmaxf(a[v][s], 0.f);
             o[s] = r * r;
         }
-        store8(h + 8 * (i0 + v), o);
+        store8(h + 8 * jo, o);
     }
 }
 
@@ -444,18 +446,18 @@ rwkv6_relu_sq_bwd_kernel(const uint16_t* __restrict__ up, const uint16_t* __rest
     const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
     float a[EW_VEC][8], g[EW_VEC][8];
 #pragma unroll
-    for (int v = 0; v < EW_VEC; ++v)
-        if (i0 + v < n8) {
-            load8(up + 8 * (i0 + v), a[v]);
-            load8(dh + 8 * (i0 + v), g[v]);
-        }
+    for (int v = 0; v < EW_VEC; ++v) {
+        const int64_t j = min(i0 + v, n8 - 1);
+        load8(up + 8 * j, a[v]);
+        load8(dh + 8 * j, g[v]);
+    }
 #pragma unroll
     for (int v = 0; v < EW_VEC; ++v) {
-        if (i0 + v >= n8) break;
+        const int64_t jo = min(i0 + v, n8 - 1);         // past the end: last piece again
         float o[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) o[s] = 2.f * fmaxf(a[v][s], 0.f) * g[v][s];
-        store8(dup + 8 * (i0 + v), o);
+        store8(dup + 8 * jo, o);
     }
 }
 
@@ -466,18 +468,18 @@ rwkv6_sigmoid_gate_kernel(const uint16_t* __restrict__ out, const uint16_t* __re
     const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
     float a[EW_VEC][8], z[EW_VEC][8];
 #pragma unroll
-    for (int v = 0; v < EW_VEC; ++v)
-        if (i0 + v < n8) {
-            load8(out + 8 * (i0 + v), a[v]);
-            load8(gp + 8 * (i0 + v), z[v]);
-        }
+    for (int v = 0; v < EW_VEC; ++v) {
+        const int64_t j = min(i0 + v, n8 - 1);
+        load8(out + 8 * j, a[v]);
+        load8(gp + 8 * j, z[v]);
+    }
 #pragma unroll
     for (int v = 0; v < EW_VEC; ++v) {
-        if (i0 + v >= n8) break;
+        const int64_t jo = min(i0 + v, n8 - 1);         // past the end: last piece again
         float o[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) o[s] = a[v][s] * sigmoid_(z[v][s]);
-        store8(y + 8 * (i0 + v), o);
+        store8(y + 8 * jo, o);
     }
 }
 
@@ -489,15 +491,15 @@ rwkv6_sigmoid_gate_bwd_kernel(const uint16_t* __restrict__ out, const uint16_t* 
     const int64_t i0 = ((int64_t)blockIdx.x * MIX_THR + threadIdx.x) * EW_VEC;
     float a[EW_VEC][8], z[EW_VEC][8], g[EW_VEC][8];
 #pragma unroll
-    for (int v = 0; v < EW_VEC; ++v)
-        if (i0 + v < n8) {
-            load8(out + 8 * (i0 + v), a[v]);
-            load8(gp + 8 * (i0 + v), z[v]);
-            load8(dy + 8 * (i0 + v), g[v]);
-        }
+    for (int v = 0; v < EW_VEC; ++v) {
+        const int64_t j = min(i0 + v, n8 - 1);
+        load8(out + 8 * j, a[v]);
+        load8(gp + 8 * j, z[v]);
+        load8(dy + 8 * j, g[v]);
+    }
 #pragma unroll
     for (int v = 0; v < EW_VEC; ++v) {
-        if (i0 + v >= n8) break;
+        const int64_t jo = min(i0 + v, n8 - 1);         // past the end: last piece again
         float o1[8], o2[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -505,8 +507,8 @@ rwkv6_sigmoid_gate_bwd_kernel(const uint16_t* __restrict__ out, const uint16_t* 
             o1[s] = g[v][s] * sg;
             o2[s] = g[v][s] * a[v][s] * sg * (1.f - sg);
         }
-        store8(dout + 8 * (i0 + v), o1);
-        store8(dgp + 8 * (i0 + v), o2);
+        store8(dout + 8 * jo, o1);
+        store8(dgp + 8 * jo, o2);
     }
 }
 
