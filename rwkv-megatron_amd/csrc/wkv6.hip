@@ -978,9 +978,9 @@ struct GradSmem {
     tile_t RmH, RmL, KmH, KmL;      // operand tiles (hi/lo); output staging in the epilogue
     float A[CL][GS];                // G -> S_in | dS bf16 tiles -> the fp32 x tile
     float emu[4][KD], eg[4][KD], fp[6][KD], kb[3][KD];
-    float bonus[CL], dd[CL], Dv[KD];
+    float bonus[CL], Dv[KD];
     float Pk[4][KD];                // per-wave sums of Km * (dk from dS), for dw
-    float red[8][KD];               // build_G scratch, du partials, dw block totals
+    float red[8][KD];               // build_G scratch; dw block totals [0..3], du partials [4..7]
 };
 static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit one CU's LDS");
 
@@ -1021,23 +1021,14 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         sstore16(sm.RmL, row, c8, wq);                   // w scratch
         sstore16(sm.RmH, row, c8, rq);                   // raw r, k: read back below in the
         sstore16(sm.KmH, row, c8, kq);                   // lane layout of the accumulators
-        float rf[8], kf[8], uf[8], vf[8], df[8], b = 0.f, d = 0.f;
+        float rf[8], kf[8], uf[8], b = 0.f;
         unpack8(rq, rf);
         unpack8(kq, kf);
-        unpack8(vq, vf);
-        unpack8(dq, df);
         load_param8(u, u_dtype, h * KD + c8, uf);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            b += rf[s] * uf[s] * kf[s];
-            d += df[s] * vf[s];
-        }
+        for (int s = 0; s < 8; ++s) b += rf[s] * uf[s] * kf[s];
         b = sum8lanes(b);
-        d = sum8lanes(d);
-        if ((threadIdx.x & 7) == 0) {
-            sm.bonus[row] = b;
-            sm.dd[row] = d;
-        }
+        if ((threadIdx.x & 7) == 0) sm.bonus[row] = b;
     }
     // Dv[i] = sum_j S_in[i][j] dS[i][j] (scaled by e^{G_63} once G is built)
     {
@@ -1067,33 +1058,9 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     }
     build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
     {
-        // du partial: sum over the wave's 8 rows (lane bits 3..5) of r k dd, then over waves
-        // in fixed order.  Transposing butterfly: at each step a lane keeps one half of its
-        // values, adds its partner's copy of that half and hands over the other half, so
-        // 4 + 2 + 1 exchanges leave lane l with the row sum of its value j(l).
-        float rf[8], kf[8], x[8];
+        float rf[8], kf[8];
         unpack8(rq, rf);
         unpack8(kq, kf);
-        const float ddr = sm.dd[row];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) x[s] = rf[s] * kf[s] * ddr;
-        {
-            const bool up = lane & 8;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) x[s] = (up ? x[s + 4] : x[s]) + lane_xor8(up ? x[s] : x[s + 4]);
-        }
-        {
-            const bool up = lane & 16;
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-                x[s] = (up ? x[s + 2] : x[s]) + lane_xor_swz<16>(up ? x[s] : x[s + 2]);
-        }
-        {
-            const bool up = lane & 32;
-            x[0] = (up ? x[1] : x[0]) + lane_xor32(up ? x[0] : x[1]);
-        }
-        const int j = ((lane >> 1) & 4) | ((lane >> 3) & 2) | ((lane >> 5) & 1);
-        sm.red[wv][c8 + j] = x[0];
         // tables
         const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
         if (part < 4) {
@@ -1141,13 +1108,6 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         }
     }
     __syncthreads();                       // G fully consumed
-    if (threadIdx.x < KD) {
-        float acc = 0.f;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) acc += sm.red[p][threadIdx.x];
-        // head-major [h][b][c][i]: each head's partials are contiguous for the du reduction
-        du_part[(((size_t)h * B + bh / H) * NT + c) * KD + threadIdx.x] = scale * acc;
-    }
     sstore16(Sin, row, c8, sq);
     sstore16(dSm, row, c8, dsq);
     __syncthreads();
@@ -1173,15 +1133,11 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) ar[tp] = tmp[tp] * sm.emu[W][16 * (2 * hh + tp) + lr];
     }
-    for (int J = 0; J <= W; ++J) {
-        const bool diag = (J == W);
+    for (int J = 0; J < W; ++J) {
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
-        float xa[4];                                     // dA[t = 16W+lr][tau = 16J+4lq+rr]
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) xa[rr] = (diag && 4 * lq + rr >= lr) ? 0.f : at[rr];
-        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+        const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);   // dA[t = 16W+lr][tau = 16J+4lq+rr]
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
@@ -1190,7 +1146,29 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             tmp = mfma16(aop, ld_tr4(KL, 16 * J, cb), tmp);
             // the two halves of the cross factor one after the other (q_J p_WJ as one
             // number can underflow where the product with tmp is O(1))
-            ar[tp] += diag ? tmp : (tmp * sm.kb[J][cb + lr]) * sm.fp[pair_index(W, J)][cb + lr];
+            ar[tp] += (tmp * sm.kb[J][cb + lr]) * sm.fp[pair_index(W, J)][cb + lr];
+        }
+    }
+    // diagonal block J = W; its diagonal dA[t][t] = dO_t . v_t = dd[t].  Lane (lq, lr) takes
+    // dd of its epilogue tokens 16W + 4lq + rr from lane (lq, 4lq + rr), element rr.
+    float ddv[4];
+    {
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * W + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) ddv[rr] = __shfl(at[rr], 20 * lq + rr);
+        float xa[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr >= lr ? 0.f : at[rr];
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) {
+            const int cb = 16 * (2 * hh + tp);
+            f32x4 tmp = {};
+            tmp = mfma16(aop, ld_tr4(KH, 16 * W, cb), tmp);
+            tmp = mfma16(aop, ld_tr4(KL, 16 * W, cb), tmp);
+            ar[tp] += tmp;
         }
     }
     // ---------------- dk (source rows in W) ----------------
@@ -1290,19 +1268,20 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     // i = 32hh + 16tp + lr).  dw[t] = D + sum_{m > t} x[m] + y[t] with x = r dr_h - k dk_h,
     // y = -k dk_h: the suffix sums over the tokens run within the lane (4 tokens), across the
     // four lane rows (shuffles) and across the token blocks W (per-wave totals in `red`).
-    float drv[2][4], dkv[2][4], dwv[2][4], wtot[2];
+    float drv[2][4], dkv[2][4], dwv[2][4], wtot[2], dup[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         const int i = 16 * (2 * hh + tp) + lr;
         const float ui = ulane[tp];
         float xv[4];
+        dup[tp] = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const int tt = 16 * W + 4 * lq + rr;
             const float rv = (float)rrw[tp][rr], kv = (float)krw[tp][rr];
             const float drh = Fm[tp][rr] * (scale * ar[tp][rr]);   // r Fm acc_r = Rm acc_r
             const float dkh = Fk[tp][rr] * ak[tp][rr];             // k Fk acc_k = Km acc_k
-            const float udd = ui * sm.dd[tt];
+            const float udd = ui * ddv[rr];
+            dup[tp] += (rv * kv) * ddv[rr];                         // du partial: r k dd
             drv[tp][rr] = drh + udd * kv;
             dkv[tp][rr] = dkh + udd * rv;
             xv[rr] = rv * drh - kv * dkh;
@@ -1324,12 +1303,26 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         for (int rr = 0; rr < 4; ++rr) dwv[tp][rr] += later;
         wtot[tp] = v;                                               // the wave's total at lq == 0
     }
-    // red is free (build_G scratch and du partials were consumed before the products)
+    // du partial over the wave's 16 tokens: sum over lq (lanes of odd lq keep tp = 1, even
+    // lq tp = 0, as for Pk), then over the four token blocks in fixed order below
+    {
+        const bool up = lane & 16;
+        float p = (up ? dup[1] : dup[0]) + lane_xor_swz<16>(up ? dup[0] : dup[1]);
+        p += lane_xor32(p);
+        if (lq < 2) sm.red[4 + W][16 * (2 * hh + lq) + lr] = p;
+    }
+    // red[0..3] (the build_G scratch before the products) takes the dw block totals
     if (lq == 0) {
         sm.red[W][32 * hh + lr] = wtot[0];
         sm.red[W][32 * hh + 16 + lr] = wtot[1];
     }
     __syncthreads();                       // all waves are done with the operand tiles; red is in
+    if (threadIdx.x < KD) {
+        const float acc = (sm.red[4][threadIdx.x] + sm.red[5][threadIdx.x]) +
+                          (sm.red[6][threadIdx.x] + sm.red[7][threadIdx.x]);
+        // head-major [h][b][c][i]: each head's partials are contiguous for the du reduction
+        du_part[(((size_t)h * B + bh / H) * NT + c) * KD + threadIdx.x] = scale * acc;
+    }
     // dr, dk, dv, dw staged channel-major (XT[i][t], 8-byte writes of 4 tokens) in the operand
     // tiles, read back token-major by transpose reads for 16-byte stores
     uint16_t (*Ts[4])[TS] = {sm.RmH, sm.RmL, sm.KmH, sm.KmL};
