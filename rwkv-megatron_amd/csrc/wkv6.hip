@@ -1198,22 +1198,36 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         p += lane_xor32(p);
         if (lq < 2) sm.Pk[W][16 * (2 * hh + lq) + lr] = p;
     }
-    for (int I = W; I < 4; ++I) {
-        const bool diag = (I == W);
+    // diagonal block I = W first, then the target blocks I > W
+    {
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * W + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+        float xa[4];                                     // dA[t = 16W+4lq+rr][tau = 16W+lr]
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr <= lr ? 0.f : at[rr] * scale;
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) {
+            const int cb = 16 * (2 * hh + tp);
+            f32x4 tmp = {};
+            tmp = mfma16(aop, ld_tr4(RH, 16 * W, cb), tmp);
+            tmp = mfma16(aop, ld_tr4(RL, 16 * W, cb), tmp);
+            ak[tp] += tmp;
+        }
+    }
+    for (int I = W + 1; I < 4; ++I) {
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
-        float xa[4];                                     // dA[t = 16I+4lq+rr][tau = 16W+lr]
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) xa[rr] = (diag && 4 * lq + rr <= lr) ? 0.f : at[rr] * scale;
-        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+        const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) {
             const int cb = 16 * (2 * hh + tp);
             f32x4 tmp = {};
             tmp = mfma16(aop, ld_tr4(RH, 16 * I, cb), tmp);
             tmp = mfma16(aop, ld_tr4(RL, 16 * I, cb), tmp);
-            ak[tp] += diag ? tmp : (tmp * sm.fp[pair_index(I, W)][cb + lr]) * sm.kb[W][cb + lr];
+            ak[tp] += (tmp * sm.fp[pair_index(I, W)][cb + lr]) * sm.kb[W][cb + lr];
         }
     }
     // ---------------- dv (source rows in W, value columns 32hh..) ----------------
@@ -1235,30 +1249,32 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             kqw[ks] = scale8(ld_row8(KH, rowW, 32 * ks), f);
         }
     }
-    for (int I = W; I < 4; ++I) {
-        const bool diag = (I == W);
+    // diagonal block I = W (the bonus on the diagonal), then the target blocks I > W
+    {
         f32x4 at = {};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 ra = ld_row8(RH, 16 * I + lr, 32 * ks);
-            if (!diag) {
-                float f[8];
-                row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
-                ra = scale8(ra, f);
-            }
-            at = mfma32(ra, diag ? ld_row8(KH, rowW, 32 * ks) : kqw[ks], at);   // A[16I+4lq+rr][16W+lr]
-        }
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_row8(RH, 16 * W + lr, 32 * ks), ld_row8(KH, rowW, 32 * ks), at);   // A[16W+4lq+rr][16W+lr]
+        const float bon = sm.bonus[rowW];
         float xa[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            float x = at[rr];
-            if (diag) {
-                const int tl = 4 * lq + rr;
-                x = tl > lr ? x : (tl == lr ? sm.bonus[rowW] : 0.f);
-            }
-            xa[rr] = x * scale;
+            const int tl = 4 * lq + rr;
+            xa[rr] = (tl > lr ? at[rr] : (tl == lr ? bon : 0.f)) * scale;
         }
         const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * W, 16 * (2 * hh + tp)), av[tp]);
+    }
+    for (int I = W + 1; I < 4; ++I) {
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            float f[8];
+            row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
+            at = mfma32(scale8(ld_row8(RH, 16 * I + lr, 32 * ks), f), kqw[ks], at);   // A[16I+4lq+rr][16W+lr]
+        }
+        const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 16 * (2 * hh + tp)), av[tp]);
     }
