@@ -127,26 +127,41 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
     const int64_t c0 = cb * 64;
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
+    __shared__ __attribute__((aligned(16))) float bsm[E][64];          // bias of the block's channels
     lora_stage(lora_sm, wut, E, C, R, c0);
+    if (threadIdx.x < E * 8) {
+        const int e = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+        float bb[8];
+        load_param8(bias, pdt, (int64_t)e * C + c0 + c8, bb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bsm[e][c8 + j] = bb[j];
+    }
     __syncthreads();
+    // Loads and stores are unconditional: a token past the end works on the last token and
+    // stores its values again (same value, same place); a load under a branch makes the
+    // merge wait for every outstanding load.
     for (int g = 0; g < LORA_TT / 64; ++g) {
         const int64_t tok = tb * LORA_TT + 64 * g + 16 * wv + L;
-        const bool tv = tok < N;
+        const int64_t tc = tok < N ? tok : N - 1;
         float xv[16], dl[16];
         if (LERP) {
-            load16(x + tok * C + c0, q, tv, xv);
-            load16(x + (tok - B) * C + c0, q, tv && tok >= B, dl);
+            const float keep_p = tc >= B ? 1.f : 0.f;
+            load16(x + tc * C + c0, q, true, xv);
+            load16(x + (tc >= B ? tc - B : tc) * C + c0, q, true, dl);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) dl[j] -= xv[j];
+            for (int j = 0; j < 16; ++j) dl[j] = dl[j] * keep_p - xv[j];
         }
 #pragma unroll 1
         for (int e = 0; e < E; ++e) {
-            float m[16], bb[16], o[16];
-            lora_up(lora_sm, neck + tok * E * R, tv, R, e, m);
-            load_param16(bias, pdt, (int64_t)e * C + c0, q, bb);
+            float m[16], o[16];
+            lora_up(lora_sm, neck + tc * E * R, true, R, e, m);
+            const float* bq = &bsm[e][0];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb[j]) : m[j] + bb[j];
-            if (tv) store16(out.p[e] + tok * C + c0, q, o);
+            for (int j = 0; j < 16; ++j) {
+                const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
+                o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb) : m[j] + bb;
+            }
+            store16(out.p[e] + tc * C + c0, q, o);
         }
     }
 }
