@@ -222,90 +222,110 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
     // Loads are unconditional (a token past the end reads the last token; its d_mixed is
     // multiplied by 0 for the d_bias sums and nothing of it is stored): a load under a branch
     // makes the merge wait for every outstanding load.
-    for (int g = 0; g < LORA_TT / 32; ++g) {
-        const int64_t tok = tb * LORA_TT + 32 * g + 16 * tw + L;
-        const bool tv = tok < N;
-        const int64_t tc = tv ? tok : N - 1;
-        const float keep = tv ? 1.f : 0.f, keep_p = tc >= B ? 1.f : 0.f;
-        const uint16_t* nrow = neck + tc * LORA_NE * R;
-        float dl[8], dd[8], ds[8];
-        {
+    // two 32-token groups at a time (tokens g and g + 32 of this lane): four 16-byte loads
+    // in flight per mix, and one d_bias butterfly over their sum
+    for (int g = 0; g < LORA_TT / 32; g += 2) {
+        int64_t tok[2], tc[2];
+        bool tv[2];
+        float keep[2], dl[2][8], dd[2][8], ds[2][8];
+        const uint16_t* nrow[2];
+#pragma unroll
+        for (int P = 0; P < 2; ++P) {
+            tok[P] = tb * LORA_TT + 32 * (g + P) + 16 * tw + L;
+            tv[P] = tok[P] < N;
+            tc[P] = tv[P] ? tok[P] : N - 1;
+            keep[P] = tv[P] ? 1.f : 0.f;
+            nrow[P] = neck + tc[P] * LORA_NE * R;
+            const float keep_p = tc[P] >= B ? 1.f : 0.f;
             float xv[8];
-            load8(x + tc * C + cl, xv);
-            load8(x + (tc >= B ? tc - B : tc) * C + cl, dl);
+            load8(x + tc[P] * C + cl, xv);
+            load8(x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + cl, dl[P]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                dl[j] = dl[j] * keep_p - xv[j];
-                dd[j] = ds[j] = 0.f;
+                dl[P][j] = dl[P][j] * keep_p - xv[j];
+                dd[P][j] = ds[P][j] = 0.f;
             }
         }
 #pragma unroll 1
         for (int e = 0; e < LORA_NE; ++e) {
-            // this mix's neck piece and d_mixed, issued together (unconditional loads)
-            const uint4 nk_e = *reinterpret_cast<const uint4*>(nrow + e * R + 8 * q);
-            const uint4 dq_e = *reinterpret_cast<const uint4*>(dmix.p[e] + tc * C + cl);
-            float m[8], v[8];
-            {
-                // m = neck_e W_up_e at the lane's 8 channels (ranks 0..31 from nk_e)
-                const int rs = lds_rs(R);
-                const uint16_t* swe = lora_sm + (e * 64 + 32 * h) * rs;
-                f32x4 acc[2] = {};
+            // this mix's neck pieces and d_mixed of both tokens, issued together
+            uint4 nk_e[2], dq_e[2];
 #pragma unroll
-                for (int tcn = 0; tcn < 2; ++tcn)
-                    acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 8 * q),
-                                      __builtin_bit_cast(bf16x8, nk_e), acc[tcn]);
-                for (int ks = 1; ks < R / 32; ++ks) {
-                    const int r0 = 32 * ks + 8 * q;
-                    const bf16x8 bq = ld_bf16x8(nrow + e * R + r0);
-#pragma unroll
-                    for (int tcn = 0; tcn < 2; ++tcn)
-                        acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + r0), bq, acc[tcn]);
-                }
-#pragma unroll
-                for (int tcn = 0; tcn < 2; ++tcn)
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) m[4 * tcn + rr] = acc[tcn][rr];
+            for (int P = 0; P < 2; ++P) {
+                nk_e[P] = *reinterpret_cast<const uint4*>(nrow[P] + e * R + 8 * q);
+                dq_e[P] = *reinterpret_cast<const uint4*>(dmix.p[e] + tc[P] * C + cl);
             }
-            unpack8(dq_e, v);
+            const int rs = lds_rs(R);
+            const uint16_t* swe = lora_sm + (e * 64 + 32 * h) * rs;
             const float4 b0 = *reinterpret_cast<const float4*>(&bsm[e][cw]);
             const float4 b1 = *reinterpret_cast<const float4*>(&bsm[e][cw + 4]);
             const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+            float vs[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                v[j] *= keep;
-                dd[j] += v[j] * (m[j] + bb[j]);
-                ds[j] += v[j];
-                v[j] *= dl[j];                                  // d_mexp
+            for (int P = 0; P < 2; ++P) {
+                float m[8], v[8];
+                {
+                    // m = neck_e W_up_e at the lane's 8 channels (ranks 0..31 from nk_e)
+                    f32x4 acc[2] = {};
+#pragma unroll
+                    for (int tcn = 0; tcn < 2; ++tcn)
+                        acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 8 * q),
+                                          __builtin_bit_cast(bf16x8, nk_e[P]), acc[tcn]);
+                    for (int ks = 1; ks < R / 32; ++ks) {
+                        const int r0 = 32 * ks + 8 * q;
+                        const bf16x8 bq = ld_bf16x8(nrow[P] + e * R + r0);
+#pragma unroll
+                        for (int tcn = 0; tcn < 2; ++tcn)
+                            acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + r0), bq, acc[tcn]);
+                    }
+#pragma unroll
+                    for (int tcn = 0; tcn < 2; ++tcn)
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr) m[4 * tcn + rr] = acc[tcn][rr];
+                }
+                unpack8(dq_e[P], v);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    v[j] *= keep[P];
+                    dd[P][j] += v[j] * (m[j] + bb[j]);
+                    ds[P][j] += v[j];
+                    v[j] *= dl[P][j];                               // d_mexp
+                    vs[j] = P == 0 ? v[j] : vs[j] + v[j];
+                }
+                if (tv[P]) store8(dmexp + ((int64_t)e * N + tok[P]) * C + cl, v);
             }
-            if (tv) store8(dmexp + ((int64_t)e * N + tok) * C + cl, v);
-            // d_bias: sum over the wave's 16 tokens (lanes L of one q).  Transposing butterfly:
-            // at each step a lane keeps one half of its values, adds its partner's copy of that
-            // half and hands over the other half; after 4 + 2 + 1 exchanges and a last pairwise
-            // sum, lanes L and L^1 hold the 16-token sum of value j = L >> 1 (fixed order).
+            // d_bias: sum over the wave's 2 x 16 tokens (lanes L of one q).  Transposing
+            // butterfly: at each step a lane keeps one half of its values, adds its partner's
+            // copy of that half and hands over the other half; after 4 + 2 + 1 exchanges and a
+            // last pairwise sum, lanes L and L^1 hold the sum of value j = L >> 1 (fixed order).
             {
                 const bool up = L & 8;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = (up ? v[i + 4] : v[i]) + lane_xor8(up ? v[i] : v[i + 4]);
+                for (int i = 0; i < 4; ++i) vs[i] = (up ? vs[i + 4] : vs[i]) + lane_xor8(up ? vs[i] : vs[i + 4]);
             }
             {
                 const bool up = L & 4;
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
-                    v[i] = (up ? v[i + 2] : v[i]) + lane_xor_swz<4>(up ? v[i] : v[i + 2]);
+                    vs[i] = (up ? vs[i + 2] : vs[i]) + lane_xor_swz<4>(up ? vs[i] : vs[i + 2]);
             }
             {
                 const bool up = L & 2;
-                v[0] = (up ? v[1] : v[0]) + lane_xor2(up ? v[0] : v[1]);
+                vs[0] = (up ? vs[1] : vs[0]) + lane_xor2(up ? vs[0] : vs[1]);
             }
-            v[0] += lane_xor1(v[0]);
-            if ((L & 1) == 0) red[e][tw][cw + (L >> 1)] += v[0];
+            vs[0] += lane_xor1(vs[0]);
+            if ((L & 1) == 0) red[e][tw][cw + (L >> 1)] += vs[0];
         }
-        if (tv) {
-            *reinterpret_cast<float4*>(dd_out + tok * C + cl) = make_float4(dd[0], dd[1], dd[2], dd[3]);
-            *reinterpret_cast<float4*>(dd_out + tok * C + cl + 4) = make_float4(dd[4], dd[5], dd[6], dd[7]);
-            *reinterpret_cast<float4*>(ds_out + tok * C + cl) = make_float4(ds[0], ds[1], ds[2], ds[3]);
-            *reinterpret_cast<float4*>(ds_out + tok * C + cl + 4) = make_float4(ds[4], ds[5], ds[6], ds[7]);
-        }
+#pragma unroll
+        for (int P = 0; P < 2; ++P)
+            if (tv[P]) {
+                float* o1 = dd_out + tok[P] * C + cl;
+                float* o2 = ds_out + tok[P] * C + cl;
+                *reinterpret_cast<float4*>(o1) = make_float4(dd[P][0], dd[P][1], dd[P][2], dd[P][3]);
+                *reinterpret_cast<float4*>(o1 + 4) = make_float4(dd[P][4], dd[P][5], dd[P][6], dd[P][7]);
+                *reinterpret_cast<float4*>(o2) = make_float4(ds[P][0], ds[P][1], ds[P][2], ds[P][3]);
+                *reinterpret_cast<float4*>(o2 + 4) = make_float4(ds[P][4], ds[P][5], ds[P][6], ds[P][7]);
+            }
     }
     __syncthreads();
     for (int j = threadIdx.x; j < LORA_NE * 64; j += LORA_THR) {
