@@ -140,28 +140,40 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
     // Loads and stores are unconditional: a token past the end works on the last token and
     // stores its values again (same value, same place); a load under a branch makes the
     // merge wait for every outstanding load.
-    for (int g = 0; g < LORA_TT / 64; ++g) {
-        const int64_t tok = tb * LORA_TT + 64 * g + 16 * wv + L;
-        const int64_t tc = tok < N ? tok : N - 1;
-        float xv[16], dl[16];
-        if (LERP) {
-            const float keep_p = tc >= B ? 1.f : 0.f;
-            load16(x + tc * C + c0, q, true, xv);
-            load16(x + (tc >= B ? tc - B : tc) * C + c0, q, true, dl);
+    static_assert(LORA_TT == 128, "two 64-token groups per block");
+    // both 64-token groups at a time (tokens g = 0, 1 of this lane): their neck loads of a
+    // mix are in flight together
+    {
+        int64_t tc[2];
+        float xv[2][16], dl[2][16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) dl[j] = dl[j] * keep_p - xv[j];
+        for (int P = 0; P < 2; ++P) {
+            const int64_t tok = tb * LORA_TT + 64 * P + 16 * wv + L;
+            tc[P] = tok < N ? tok : N - 1;
+            if (LERP) {
+                const float keep_p = tc[P] >= B ? 1.f : 0.f;
+                load16(x + tc[P] * C + c0, q, true, xv[P]);
+                load16(x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + c0, q, true, dl[P]);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) dl[P][j] = dl[P][j] * keep_p - xv[P][j];
+            }
         }
 #pragma unroll 1
         for (int e = 0; e < E; ++e) {
-            float m[16], o[16];
-            lora_up(lora_sm, neck + tc * E * R, true, R, e, m);
+            float m[2][16];
+#pragma unroll
+            for (int P = 0; P < 2; ++P) lora_up(lora_sm, neck + tc[P] * E * R, true, R, e, m[P]);
             const float* bq = &bsm[e][0];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
-                o[j] = LERP ? xv[j] + dl[j] * (m[j] + bb) : m[j] + bb;
+            for (int P = 0; P < 2; ++P) {
+                float o[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
+                    o[j] = LERP ? xv[P][j] + dl[P][j] * (m[P][j] + bb) : m[P][j] + bb;
+                }
+                store16(out.p[e] + tc[P] * C + c0, q, o);
             }
-            store16(out.p[e] + tc * C + c0, q, o);
         }
     }
 }
