@@ -133,22 +133,11 @@ __device__ __forceinline__ void pack8_split(const float* f, uint4& hi, uint4& lo
 // tile movement and the chunk cumulative decay
 // ---------------------------------------------------------------------------
 
-// One 16-byte piece per thread per pass: row = idx >> 3, columns 8*(idx & 7) .. +7.
-__device__ __forceinline__ uint4 gload16(const uint16_t* __restrict__ src, int row, int c8,
-                                         int nvalid) {
-    if (row < nvalid) return *reinterpret_cast<const uint4*>(src + (size_t)row * KD + c8);
-    return make_uint4(0u, 0u, 0u, 0u);
-}
+// One 16-byte piece of a token-major tile: row, columns c8 .. c8 + 7.
 __device__ __forceinline__ void sstore16(uint16_t (*X)[TS], int row, int c8, uint4 v) {
     *reinterpret_cast<uint4*>(&X[row][c8]) = v;
 }
 
-// Same with an explicit token (row) stride in elements.
-__device__ __forceinline__ uint4 gload16s(const uint16_t* __restrict__ src, int row, int c8,
-                                          int nvalid, size_t rs) {
-    if (row < nvalid) return *reinterpret_cast<const uint4*>(src + (size_t)row * rs + c8);
-    return make_uint4(0u, 0u, 0u, 0u);
-}
 
 // Token tensors come in two layouts:
 //   head-first  [B,H,T,64]   (fla's contract)                 SEQ = false
