@@ -9,6 +9,8 @@
  *     allocates, frees or synchronises the host).  Work is enqueued on `stream`
  *     (a hipStream_t; NULL = the default stream).
  *   - Tensors are dense, row-major, and 16-byte aligned.
+ *   - Outputs (workspace included) must not overlap inputs or each other; an entry point
+ *     that finds an overlap returns RWKV6_ERR_INVALID_ARG without launching.
  *   - Return value: RWKV6_OK or an rwkv6_status code; rwkv6_strerror() maps it
  *     to text.  Validation failures never launch anything.
  *   - Calls are re-entrant: no mutable global state; the same inputs give
@@ -36,7 +38,7 @@
 extern "C" {
 #endif
 
-#define RWKV6_ABI_VERSION 1
+#define RWKV6_ABI_VERSION 2
 
 enum rwkv6_status {
     RWKV6_OK = 0,
@@ -62,8 +64,8 @@ const char* rwkv6_strerror(int code);
  * Only K == V == 64 (RWKV-6 head size) is supported; T >= 0 arbitrary.
  * Per-token log-decay is floored at -10 (decay factor 4.5e-5; the chunked evaluation
  * keeps 8-token decay products inside the bf16 exponent range): tokens below the floor
- * change outputs and states by less than that factor; their dw is the gradient at the
- * floor (scaled by the same factor) and their d_decay (sequence-first entry) is 0.
+ * change outputs and states by less than that factor; their dw (d_decay in the
+ * sequence-first entry) is 0, the derivative of the floored forward.
  * `saved` (rwkv6_wkv_saved_bytes) receives the bf16 state entering every chunk
  * (and the final state), which the backward consumes; keep it alive until
  * rwkv6_wkv_bwd.  `workspace` (rwkv6_wkv_workspace_bytes) is scratch for the duration
@@ -104,33 +106,14 @@ int rwkv6_wkv_bwd_seqfirst(const void* r, const void* k, const void* v, const vo
                            int64_t T, int64_t K, int64_t V, float scale, void* stream);
 
 /* ------------------------------------------------------------------------
- * Token shift and lerps of RWKV6TimeMix.forward, sequence-first [T,B,C] bf16.
+ * Token shift and static lerp of RWKV6TimeMix.forward, sequence-first [T,B,C] bf16.
  *   shift(x)[t] = x[t-1], shift(x)[0] = 0              (rwkv6_layer_specs.py:294-300)
- *   xxx         = x + (shift(x) - x) * maa              (:443-444), maa [C]
- *   mixed[e]    = x + (shift(x) - x) * (mexp[e] + bias[e])   (:446-452)
- *                 mexp [5,T,B,C] is the LoRA up-projection before its bias (:195),
- *                 bias [5,C]; `mixed` is a host array of 5 device pointers, each a
- *                 [T,B,C] tensor, in the order w,k,v,r,g (each feeds its own projection).
- * maa and bias are in param_dtype (f32 or bf16).  C must be a multiple of 8.
- * Gradients w.r.t. the mixes (d_mixed) are passed the same way: 5 device pointers.
+ *   xxx         = x + (shift(x) - x) * maa              (:443-444), maa [C] in param_dtype
+ * C must be a multiple of 8.  The data-dependent lerp of :446-452 is written by
+ * rwkv6_ddlerp_lora_fwd below, whose backward (with rwkv6_shift_lerp_bwd) covers both lerps.
  * ---------------------------------------------------------------------- */
 int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* xxx,
                          int64_t T, int64_t B, int64_t C, void* stream);
-int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int param_dtype,
-                     void* const* mixed, int64_t T, int64_t B, int64_t C, void* stream);
-/* Backward of the data-dependent lerp w.r.t. its LoRA input: d_mixed 5 x [T,B,C] ->
- * d_mexp [5,T,B,C] = d_mixed * (shift(x) - x) and d_bias [5,C] (param_dtype). */
-size_t rwkv6_ddlerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
-int rwkv6_ddlerp_bwd(const void* x, const void* const* d_mixed, int param_dtype, void* d_mexp,
-                     void* d_bias, void* workspace, int64_t T, int64_t B, int64_t C,
-                     void* stream);
-/* Input gradient of both lerps (they share x): d_mixed 5 x [T,B,C] and d_xxx [T,B,C]
- * (nullable = 0) -> dx [T,B,C] and d_maa [C] (param_dtype). */
-size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
-int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
-                  int param_dtype, const void* const* d_mixed, const void* d_xxx, void* dx,
-                  void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
-                  void* stream);
 
 /* ------------------------------------------------------------------------
  * LoRA up-projections fused with their consumers (RWKV6Bottleneck.forward,
@@ -141,13 +124,14 @@ int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* 
  * param_dtype.
  *   ddlerp_lora: E = 5, mixed[e] = x + (shift(x) - x) * (neck_e @ W_up[e] + bias[e]), the five
  *                mixes written straight to `mixed` (host array of 5 device pointers, [T,B,C])
- *   lora_bias:   E = 1, out = neck @ W_up[0] + bias[0]  ([N, C]; the decay of :454)
+ *   lora_bias:   E = 1 or 5, out[n][e] = neck_e[n] @ W_up[e] + bias[e]: the bottleneck's own
+ *                output [N, E, C] (:195); for E = 1 the decay of :454 ([N, C])
  * ---------------------------------------------------------------------- */
 int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
                           int param_dtype, void* const* mixed, int64_t T, int64_t B, int64_t C,
                           int64_t R, void* stream);
 int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, int param_dtype,
-                        void* out, int64_t N, int64_t C, int64_t R, void* stream);
+                        void* out, int64_t N, int64_t E, int64_t C, int64_t R, void* stream);
 /* Backward of rwkv6_ddlerp_lora_fwd for d_mixed (5 device pointers, [T,B,C] bf16):
  *   d_mexp [5,N,C] bf16 = d_mixed * (shift(x) - x)   (the LoRA up-projection's output gradient)
  *   d_delta_part [N,C] f32 = sum_e d_mixed_e (m_e + bias_e),   d_sum [N,C] f32 = sum_e d_mixed_e
@@ -195,7 +179,9 @@ int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy
  * GroupNorm(per head) * silu(gate), fused with the head-first -> sequence-first
  * layout change of rwkv6_layer_specs.py:341 and :461-465.
  *   o      : WKV output, [B,H,T,K] bf16 (head_first=1) or [T,B,H*K] (head_first=0)
- *   g_pre  : [T,B,H*K] bf16, linear_gate output before silu (:458)
+ *   g_pre  : [T,B,H*K] bf16, linear_gate output before silu (:458); nullable: without a
+ *            gate, y = GN(o) is the reference's GroupNorm.forward over [N, C] (:90-97),
+ *            called with head_first = 0, T = N, B = 1 (group size 64 only)
  *   gamma, beta : [H*K] in param_dtype; eps = config.layernorm_epsilon (:68)
  *   y      : [T,B,H*K] bf16 = GN(o) * silu(g_pre)
  *   mean, rstd : [T*B*H] f32 statistics saved for the backward
@@ -204,7 +190,8 @@ int rwkv6_gn_gate_fwd(const void* o, int head_first, const void* g_pre, const vo
                       const void* beta, int param_dtype, float eps, void* y, float* mean,
                       float* rstd, int64_t T, int64_t B, int64_t H, int64_t K, void* stream);
 size_t rwkv6_gn_gate_bwd_workspace_bytes(int64_t T, int64_t B, int64_t H, int64_t K);
-/* dy [T,B,H*K] -> d_o (layout of o), d_g_pre [T,B,H*K], dgamma, dbeta [H*K] (param_dtype). */
+/* dy [T,B,H*K] -> d_o (layout of o), d_g_pre [T,B,H*K] (NULL exactly when g_pre is NULL),
+ * dgamma, dbeta [H*K] (param_dtype). */
 int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const void* gamma,
                       const void* beta, int param_dtype, const float* mean, const float* rstd,
                       const void* dy, void* d_o, void* d_g_pre, void* dgamma, void* dbeta,

@@ -43,13 +43,8 @@ SIGNATURES = {
     "rwkv6_wkv_bwd_seqfirst": (_int, [_vp] * 5 + [_int] + [_vp, _fp, _vp] + [_vp] * 5 + [_fp, _vp]
                                + [_i64] * 5 + [_f32, _vp]),
     "rwkv6_shift_lerp_fwd": (_int, [_vp, _vp, _int, _vp] + [_i64] * 3 + [_vp]),
-    "rwkv6_ddlerp_fwd": (_int, [_vp, _vp, _vp, _int, _vp] + [_i64] * 3 + [_vp]),
-    "rwkv6_ddlerp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
-    "rwkv6_ddlerp_bwd": (_int, [_vp, _vp, _int, _vp, _vp, _vp] + [_i64] * 3 + [_vp]),
-    "rwkv6_mix_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
-    "rwkv6_mix_bwd": (_int, [_vp] * 4 + [_int] + [_vp] * 5 + [_i64] * 3 + [_vp]),
     "rwkv6_ddlerp_lora_fwd": (_int, [_vp] * 4 + [_int, _vp] + [_i64] * 4 + [_vp]),
-    "rwkv6_lora_bias_fwd": (_int, [_vp] * 3 + [_int, _vp] + [_i64] * 3 + [_vp]),
+    "rwkv6_lora_bias_fwd": (_int, [_vp] * 3 + [_int, _vp] + [_i64] * 4 + [_vp]),
     "rwkv6_ddlerp_lora_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
     "rwkv6_ddlerp_lora_bwd": (_int, [_vp] * 4 + [_int] + [_vp] * 6 + [_i64] * 4 + [_vp]),
     "rwkv6_shift_lerp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),

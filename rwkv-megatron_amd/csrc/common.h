@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -118,4 +120,31 @@ __device__ __forceinline__ float sum8lanes(float v) {
     v += lane_xor2(v);
     v += dpp_mov<0x141>(v);
     return v;
+}
+
+// Host side: a device buffer as (address, bytes).  Entry points reject calls where an output
+// overlaps an input or another output: several kernels re-load a clamped last piece after
+// other threads have stored theirs, and the walks read chunk c + 1 before storing chunk c, so
+// an aliased output would be read back as an input.  Null pointers and empty spans never
+// overlap.
+struct Span {
+    const void* p;
+    size_t n;
+};
+inline bool spans_overlap(const Span& a, const Span& b) {
+    if (!a.p || !b.p || !a.n || !b.n) return false;
+    const char* x = static_cast<const char*>(a.p);
+    const char* y = static_cast<const char*>(b.p);
+    return x < y + b.n && y < x + a.n;
+}
+// bytes of one parameter element (RWKV6_BF16 = 1 -> 2, RWKV6_F32 = 0 -> 4)
+inline size_t param_bytes(int dtype) { return dtype == 1 ? 2 : 4; }
+inline bool any_alias(std::initializer_list<Span> outs, std::initializer_list<Span> ins) {
+    for (const Span* o = outs.begin(); o != outs.end(); ++o) {
+        for (const Span& i : ins)
+            if (spans_overlap(*o, i)) return true;
+        for (const Span* o2 = o + 1; o2 != outs.end(); ++o2)
+            if (spans_overlap(*o, *o2)) return true;
+    }
+    return false;
 }

@@ -4,11 +4,12 @@
 //   o = rearrange(wkv_out, "b h t n -> t b (h n)")                     :341
 //   y = group_norm(o as [(t b), c], groups = heads, weight, bias, eps)  :90-97, :461-465
 //   y = y * silu(linear_gate(mixed_gate))                               :458, :466
-// eps is config.layernorm_epsilon (:68).  One group is the 64 channels of one
-// (token, batch, head); 8 lanes own a group, 8 channels (16 bytes) each, and
-// reduce with cross-lane shuffles.  The WKV output may be read head-first, which
-// fuses away the layout copy of :341.  Parameter-gradient sums are two-stage
-// with a fixed order (deterministic).
+// eps is config.layernorm_epsilon (:68).  Without a gate (g_pre = NULL) the kernels are the
+// plain GroupNorm of the reference's GroupNorm.forward over [N, C] (:90-97).  One group is
+// the 64 channels of one (token, batch, head); 8 lanes own a group, 8 channels (16 bytes)
+// each, and reduce with cross-lane shuffles.  The WKV output may be read head-first, which
+// fuses away the layout copy of :341.  Parameter-gradient sums are two-stage with a fixed
+// order (deterministic).
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
@@ -29,6 +30,7 @@ __device__ __forceinline__ int64_t o_off(int head_first, int64_t t, int64_t b, i
 }  // namespace
 
 // grid: (ceil(T / GN_TT), B*H); thread = (group slot gs = tid/8, lane8 = tid%8)
+template <bool GATE>
 __global__ void __launch_bounds__(GN_THR)
 rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
                          const uint16_t* __restrict__ g_pre, const void* __restrict__ gamma,
@@ -48,7 +50,7 @@ rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
         float x[8], z[8], out[8];
         load8(o + o_off(head_first, t, b, h, c0, T, B, H), x);
         const int64_t yo = (t * B + b) * C + h * GN_D + c0;
-        load8(g_pre + yo, z);
+        if (GATE) load8(g_pre + yo, z);
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) s += x[i];
@@ -59,7 +61,7 @@ rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
         const float rstd = rsqrtf(sum8lanes(v) * (1.f / GN_D) + eps);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            out[i] = ((x[i] - mean) * rstd * ga[i] + be[i]) * (z[i] * sigmoidf_(z[i]));
+            out[i] = ((x[i] - mean) * rstd * ga[i] + be[i]) * (GATE ? z[i] * sigmoidf_(z[i]) : 1.f);
         store8(y + yo, out);
         if (l8 == 0) {
             mean_out[(t * B + b) * H + h] = mean;
@@ -69,6 +71,7 @@ rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
 }
 
 // Backward.  Partial sums of dgamma/dbeta per block: part[b*nTB + tb][which][h][64].
+template <bool GATE>
 __global__ void __launch_bounds__(GN_THR)
 rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
                          const uint16_t* __restrict__ g_pre, const void* __restrict__ gamma,
@@ -94,18 +97,20 @@ rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
         const int64_t oo = o_off(head_first, t, b, h, c0, T, B, H);
         const int64_t yo = (t * B + b) * C + h * GN_D + c0;
         load8(o + oo, x);
-        load8(g_pre + yo, z);
+        if (GATE) load8(g_pre + yo, z);
         load8(dy + yo, g);
         const float mean = mean_in[(t * B + b) * H + h], rstd = rstd_in[(t * B + b) * H + h];
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             xh[i] = (x[i] - mean) * rstd;
-            const float sg = sigmoidf_(z[i]);
-            const float gate = z[i] * sg;
-            const float n = xh[i] * ga[i] + be[i];
-            outg[i] = g[i] * n * sg * (1.f + z[i] * (1.f - sg));
-            const float dn = g[i] * gate;
+            float dn = g[i];
+            if (GATE) {
+                const float sg = sigmoidf_(z[i]);
+                const float n = xh[i] * ga[i] + be[i];
+                outg[i] = g[i] * n * sg * (1.f + z[i] * (1.f - sg));
+                dn = g[i] * (z[i] * sg);
+            }
             accg[i] += dn * xh[i];
             accb[i] += dn;
             dxh[i] = dn * ga[i];
@@ -117,7 +122,7 @@ rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
 #pragma unroll
         for (int i = 0; i < 8; ++i) outo[i] = rstd * (dxh[i] - s1 - xh[i] * s2);
         store8(d_o + oo, outo);
-        store8(d_g + yo, outg);
+        if (GATE) store8(d_g + yo, outg);
     }
     // reduce the 32 group slots of this block (fixed order)
 #pragma unroll
@@ -180,14 +185,19 @@ int rwkv6_gn_gate_fwd(const void* o, int head_first, const void* g_pre, const vo
     int st = gn_check(T, B, H, K, param_dtype);
     if (st) return st;
     if (T == 0) return RWKV6_OK;
-    if (!o || !g_pre || !gamma || !beta || !y || !mean || !rstd) return RWKV6_ERR_INVALID_ARG;
+    if (!o || !gamma || !beta || !y || !mean || !rstd) return RWKV6_ERR_INVALID_ARG;
     if (!al16(o) || !al16(g_pre) || !al16(gamma) || !al16(beta) || !al16(y))
         return RWKV6_ERR_ALIGNMENT;
+    const size_t act = (size_t)(T * B * H * GN_D) * 2, st4 = (size_t)(T * B * H) * 4,
+                 par = (size_t)(H * GN_D) * param_bytes(param_dtype);
+    if (any_alias({{y, act}, {mean, st4}, {rstd, st4}},
+                  {{o, act}, {g_pre, act}, {gamma, par}, {beta, par}}))
+        return RWKV6_ERR_INVALID_ARG;
     dim3 grid((unsigned)((T + GN_TT - 1) / GN_TT), (unsigned)(B * H));
-    hipLaunchKernelGGL(rwkv6_gn_gate_fwd_kernel, grid, dim3(GN_THR), 0,
-                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)o, head_first,
-                       (const uint16_t*)g_pre, gamma, beta, param_dtype, eps, (uint16_t*)y, mean,
-                       rstd, T, B, H);
+    hipLaunchKernelGGL(g_pre ? rwkv6_gn_gate_fwd_kernel<true> : rwkv6_gn_gate_fwd_kernel<false>,
+                       grid, dim3(GN_THR), 0, reinterpret_cast<hipStream_t>(stream),
+                       (const uint16_t*)o, head_first, (const uint16_t*)g_pre, gamma, beta,
+                       param_dtype, eps, (uint16_t*)y, mean, rstd, T, B, H);
     return launch_status();
 }
 
@@ -204,18 +214,28 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
                       void* stream) {
     int st = gn_check(T, B, H, K, param_dtype);
     if (st) return st;
-    if (!gamma || !beta || !dgamma || !dbeta || !workspace ||
-        (T > 0 && (!o || !g_pre || !mean || !rstd || !dy || !d_o || !d_g_pre)))
+    if (!gamma || !beta || !dgamma || !dbeta || !workspace || (!g_pre != !d_g_pre) ||
+        (T > 0 && (!o || !mean || !rstd || !dy || !d_o)))
         return RWKV6_ERR_INVALID_ARG;
     if (!al16(o) || !al16(g_pre) || !al16(gamma) || !al16(beta) || !al16(dy) || !al16(d_o) ||
         !al16(d_g_pre) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(T * B * H * GN_D) * 2, st4 = (size_t)(T * B * H) * 4,
+                     par = (size_t)(H * GN_D) * param_bytes(param_dtype);
+        if (any_alias({{d_o, act}, {d_g_pre, act}, {dgamma, par}, {dbeta, par},
+                       {workspace, rwkv6_gn_gate_bwd_workspace_bytes(T, B, H, K)}},
+                      {{o, act}, {g_pre, act}, {gamma, par}, {beta, par}, {mean, st4}, {rstd, st4},
+                       {dy, act}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t nTB = (T + GN_TT - 1) / GN_TT;
     if (T > 0) {
         dim3 grid((unsigned)nTB, (unsigned)(B * H));
-        hipLaunchKernelGGL(rwkv6_gn_gate_bwd_kernel, grid, dim3(GN_THR), 0, s, (const uint16_t*)o,
-                           head_first, (const uint16_t*)g_pre, gamma, beta, param_dtype, mean, rstd,
+        hipLaunchKernelGGL(g_pre ? rwkv6_gn_gate_bwd_kernel<true> : rwkv6_gn_gate_bwd_kernel<false>,
+                           grid, dim3(GN_THR), 0, s, (const uint16_t*)o, head_first,
+                           (const uint16_t*)g_pre, gamma, beta, param_dtype, mean, rstd,
                            (const uint16_t*)dy, (uint16_t*)d_o, (uint16_t*)d_g_pre,
                            (float*)workspace, T, B, H);
     }

@@ -10,7 +10,8 @@
 // up-projection is a K = R contraction whose [E,N,C] output is the big tensor, so it is
 // computed here on MFMA and consumed in registers:
 //   rwkv6_ddlerp_lora_fwd  writes the five mixes directly (no m round trip through HBM);
-//   rwkv6_lora_bias_fwd    writes decay = m + bias;
+//   rwkv6_lora_bias_fwd    writes m + bias, the bottleneck's own output [N,E,C] (for E = 1
+//                          the decay of :454);
 //   rwkv6_ddlerp_lora_bwd  recomputes m and writes d_mexp = d_mixed * delta (the LoRA GEMMs'
 //                          input), d_delta_part = sum_e d_mixed_e (m_e + bias_e),
 //                          d_sum = sum_e d_mixed_e and d_bias partials;
@@ -45,16 +46,6 @@ __device__ __forceinline__ void load16(const uint16_t* row_c0, int q, bool valid
 __device__ __forceinline__ void store16(uint16_t* row_c0, int q, const float* f) {
     store8(row_c0 + 8 * q, f);
     store8(row_c0 + 32 + 8 * q, f + 8);
-}
-__device__ __forceinline__ void store16f(float* row_c0, int q, const float* f) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-        *reinterpret_cast<float4*>(row_c0 + (v < 2 ? 8 * q + 4 * v : 32 + 8 * q + 4 * (v - 2))) =
-            make_float4(f[4 * v], f[4 * v + 1], f[4 * v + 2], f[4 * v + 3]);
-}
-__device__ __forceinline__ void load_param16(const void* p, int pdt, int64_t off_c0, int q, float* f) {
-    load_param8(p, pdt, off_c0 + 8 * q, f);
-    load_param8(p, pdt, off_c0 + 32 + 8 * q, f + 8);
 }
 // channel (relative to c0) of MFMA tile tc, row 4q' + rr' = L': the run layout above
 __device__ __forceinline__ int tile_channel(int tc, int L) {
@@ -116,12 +107,15 @@ __device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __re
 
 }  // namespace
 
-// LERP: out_e = x + (shift(x) - x) * (m_e + bias_e)  (E = 5);  else out_0 = m_0 + bias_0.
+// LERP: out_e = x + (shift(x) - x) * (m_e + bias_e)  (E = 5);  else out_e = m_e + bias_e.
+// Token n of output e starts at out.p[e] + n * ors (ors = C for separate [N,C] tensors, E * C
+// for one [N,E,C] tensor).
 template <int E, bool LERP>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
-                     OutPtrs<E> out, int64_t N, int64_t B, int64_t C, int R, int64_t per) {
+                     OutPtrs<E> out, int64_t ors, int64_t N, int64_t B, int64_t C, int R,
+                     int64_t per) {
     int64_t tb, cb;
     if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
@@ -172,7 +166,7 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
                     const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
                     o[j] = LERP ? xv[P][j] + dl[P][j] * (m[P][j] + bb) : m[P][j] + bb;
                 }
-                store16(out.p[e] + tc[P] * C + c0, q, o);
+                store16(out.p[e] + tc[P] * ors + c0, q, o);
             }
         }
     }
@@ -488,28 +482,50 @@ int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, c
     OutPtrs<LORA_NE> out;
     if ((st = gather<OutPtrs<LORA_NE>, LORA_NE>((const void* const*)mixed, out))) return st;
     if (!al16(x) || !al16(neck) || !al16(w_up_t) || !al16(bias)) return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(T * B * C) * 2;
+        if (any_alias({{out.p[0], act}, {out.p[1], act}, {out.p[2], act}, {out.p[3], act}, {out.p[4], act}},
+                      {{x, act}, {neck, (size_t)(T * B * LORA_NE * R) * 2},
+                       {w_up_t, (size_t)(LORA_NE * C * R) * 2},
+                       {bias, (size_t)(LORA_NE * C) * param_bytes(param_dtype)}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true>), up_grid(T * B, C), dim3(LORA_THR),
                        lora_lds_bytes(LORA_NE, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
-                       (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, T * B,
-                       B, C, (int)R, up_per(T * B));
+                       (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, C,
+                       T * B, B, C, (int)R, up_per(T * B));
     return launch_status();
 }
 
 int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, int param_dtype,
-                        void* out, int64_t N, int64_t C, int64_t R, void* stream) {
-    int st = lora_check(1, N, C, R, param_dtype);
+                        void* out, int64_t N, int64_t E, int64_t C, int64_t R, void* stream) {
+    if (E != 1 && E != LORA_NE) return E < 1 ? RWKV6_ERR_INVALID_ARG : RWKV6_ERR_UNSUPPORTED;
+    int st = lora_check((int)E, N, C, R, param_dtype);
     if (st) return st;
     if (N == 0) return RWKV6_OK;
     if (!neck || !w_up_t || !bias || !out) return RWKV6_ERR_INVALID_ARG;
     if (!al16(neck) || !al16(w_up_t) || !al16(bias) || !al16(out)) return RWKV6_ERR_ALIGNMENT;
-    OutPtrs<1> o;
-    o.p[0] = (uint16_t*)out;
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR),
-                       lora_lds_bytes(1, (int)R),
-                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
-                       (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o, N,
-                       (int64_t)1, C, (int)R, up_per(N));
+    if (any_alias({{out, (size_t)(N * E * C) * 2}},
+                  {{neck, (size_t)(N * E * R) * 2}, {w_up_t, (size_t)(E * C * R) * 2},
+                   {bias, (size_t)(E * C) * param_bytes(param_dtype)}}))
+        return RWKV6_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (E == 1) {
+        OutPtrs<1> o;
+        o.p[0] = (uint16_t*)out;
+        hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR),
+                           lora_lds_bytes(1, (int)R), s, (const uint16_t*)neck,
+                           (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
+                           C, N, (int64_t)1, C, (int)R, up_per(N));
+    } else {
+        OutPtrs<LORA_NE> o;
+        for (int e = 0; e < LORA_NE; ++e) o.p[e] = (uint16_t*)out + (int64_t)e * C;
+        hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, false>), up_grid(N, C), dim3(LORA_THR),
+                           lora_lds_bytes(LORA_NE, (int)R), s, (const uint16_t*)neck,
+                           (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
+                           (int64_t)LORA_NE * C, N, (int64_t)1, C, (int)R, up_per(N));
+    }
     return launch_status();
 }
 
@@ -534,6 +550,15 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
     if (!al16(x) || !al16(neck) || !al16(w_up_t) || !al16(bias) || !al16(d_mexp) ||
         !al16(d_delta_part) || !al16(d_sum) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
+    if (T > 0) {
+        const size_t act = (size_t)(T * B * C) * 2, par = (size_t)(LORA_NE * C) * param_bytes(param_dtype);
+        if (any_alias({{d_mexp, LORA_NE * act}, {d_delta_part, 2 * act}, {d_sum, 2 * act}, {d_bias, par},
+                       {workspace, rwkv6_ddlerp_lora_bwd_workspace_bytes(T, B, C)}},
+                      {{x, act}, {neck, (size_t)(T * B * LORA_NE * R) * 2},
+                       {w_up_t, (size_t)(LORA_NE * C * R) * 2}, {bias, par}, {dm.p[0], act},
+                       {dm.p[1], act}, {dm.p[2], act}, {dm.p[3], act}, {dm.p[4], act}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t N = T * B, nb = (N + LORA_TT - 1) / LORA_TT;
     float* part = reinterpret_cast<float*>(workspace);
@@ -566,6 +591,12 @@ int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const 
     if (!al16(x) || !al16(maa) || !al16(d_delta_part) || !al16(d_sum) || !al16(d_xxx) ||
         !al16(dx) || !al16(workspace))
         return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(T * B * C) * 2, par = (size_t)C * param_bytes(param_dtype);
+        if (any_alias({{dx, act}, {d_maa, par}, {workspace, rwkv6_shift_lerp_bwd_workspace_bytes(T, B, C)}},
+                      {{x, act}, {maa, par}, {d_delta_part, 2 * act}, {d_sum, 2 * act}, {d_xxx, act}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t ntb = (T + SLB_TB - 1) / SLB_TB;
     float* part = reinterpret_cast<float*>(workspace);

@@ -1,13 +1,11 @@
-// Fused token shift + lerp + data-dependent lerp of RWKV6TimeMix.forward, and
-// the fused backward of both, for MI355X (gfx950).  Sequence-first [T,B,C] bf16.
+// Token shift + static lerp of RWKV6TimeMix.forward (the input of its token-shift LoRA)
+// and the channel-mix kernels, for MI355X (gfx950).  Sequence-first [T,B,C] bf16.
 //
 // Reference (/root/reference/rwkv_megatron/rwkv6_layer_specs.py):
 //   shift(x)[t] = x[t-1], shift(x)[0] = 0                        :290-300
 //   delta = shift(x) - x ; xxx = x + delta * maa_x                :443-444
-//   m = bottleneck_token_shift(xxx) (LoRA; its bias is :195)      :446
-//   mixed_e = x + delta * m_e, e in (w,k,v,r,g)                   :447-452
-// The LoRA output m is laid out e-outer ([5,T,B,C]) so batched GEMMs produce and
-// consume it without copies.
+// The data-dependent lerp of :447-452 is written by the LoRA up-projection kernel
+// (lora.hip), which also holds the backward of both lerps.
 //
 // Channel mix (RWKV6ChannelMix.forward, :512-536) uses the same shift with static
 // coefficients mix_coeffs [2,C]:
@@ -25,7 +23,6 @@
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
-#define MIX_NE 5          // number of data-dependent mixes (w,k,v,r,g)
 #define MIX_THR 256
 
 // xxx = x + (shift(x) - x) * maa
@@ -47,212 +44,13 @@ rwkv6_shift_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__
     store8(xxx + off, out);
 }
 
-// mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]);  mexp [5,T,B,C], mixed 5 x [T,B,C]
-__global__ void __launch_bounds__(MIX_THR)
-rwkv6_ddlerp_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ mexp,
-                    const void* __restrict__ bias, int pdt, OutPtrs<MIX_NE> mixed,
-                    int64_t T, int64_t B, int64_t C) {
-    const int64_t C8 = C / 8;
-    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    const int64_t N = T * B;
-    if (idx >= N * C8) return;
-    const int64_t cg = idx % C8, tb = idx / C8;
-    const int64_t off = tb * C + 8 * cg;
-    float xv[8], d[8];
-    load8(x + off, xv);
-    if (tb >= B) {
-        load8(x + off - B * C, d);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) d[s] -= xv[s];
-    } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) d[s] = -xv[s];
-    }
-#pragma unroll
-    for (int e = 0; e < MIX_NE; ++e) {
-        float m[8], bb[8], out[8];
-        load8(mexp + e * N * C + off, m);
-        load_param8(bias, pdt, e * C + 8 * cg, bb);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = xv[s] + d[s] * (m[s] + bb[s]);
-        store8(mixed.p[e] + off, out);
-    }
-}
-
-// Backward kernels: block = 8 token sub-segments x 32 channel groups (256 threads); the
+// Backward kernel: block = 8 token sub-segments x 32 channel groups (256 threads); the
 // block covers tokens [64*blockIdx.x, +64) of batch blockIdx.z and channels
 // [256*blockIdx.y, +256).  Thread (ss, cgl) walks 8 tokens of 8 channels.  Parameter
 // partial sums are reduced over the 8 sub-segments in LDS (fixed order) and written
 // per (token block, batch): part[(tblk*B + b)][rows][C].
 #define MIX_TB 64          // tokens per block
 #define MIX_SS 8           // tokens per thread
-
-// d_mexp[e][t] = d_mixed[e][t] * delta[t];  part rows e = 0..4 (d_bias)
-__global__ void __launch_bounds__(MIX_THR)
-rwkv6_ddlerp_bwd_kernel(const uint16_t* __restrict__ x, InPtrs<MIX_NE> dmix,
-                        uint16_t* __restrict__ dmexp, float* __restrict__ part, int64_t T,
-                        int64_t B, int64_t C) {
-    __shared__ float red[MIX_SS][MIX_NE][32 * 8 + 4];
-    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
-    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
-    const int64_t b = blockIdx.z, N = T * B;
-    const int64_t t_lo = (int64_t)blockIdx.x * MIX_TB + MIX_SS * ss;
-    const int64_t t_hi = min(T, t_lo + MIX_SS);
-    float acc[MIX_NE][8];
-#pragma unroll
-    for (int e = 0; e < MIX_NE; ++e)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) acc[e][s] = 0.f;
-    if (cg < C8 && t_lo < T) {
-        float xprev[8];
-        if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
-        else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
-        for (int64_t t = t_lo; t < t_hi; ++t) {
-            const int64_t off = (t * B + b) * C + 8 * cg;
-            float xv[8], delta[8];
-            load8(x + off, xv);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                delta[s] = xprev[s] - xv[s];
-                xprev[s] = xv[s];
-            }
-#pragma unroll
-            for (int e = 0; e < MIX_NE; ++e) {
-                float g[8], out[8];
-                load8(dmix.p[e] + off, g);
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    out[s] = g[s] * delta[s];
-                    acc[e][s] += out[s];
-                }
-                store8(dmexp + e * N * C + off, out);
-            }
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < MIX_NE; ++e)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) red[ss][e][8 * cgl + s] = acc[e][s];
-    __syncthreads();
-    const int64_t P_row = (int64_t)blockIdx.x * B + b;
-    for (int j = threadIdx.x; j < MIX_NE * 256; j += MIX_THR) {
-        const int e = j >> 8, c = j & 255;
-        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
-        if (ch >= C) continue;
-        float sum = 0.f;
-#pragma unroll
-        for (int q = 0; q < MIX_SS; ++q) sum += red[q][e][c];
-        part[(P_row * MIX_NE + e) * C + ch] = sum;
-    }
-}
-
-// Input gradient of both lerps, d_maa partial (part row 0):
-//   d_delta[t] = sum_e dmix_e[t] m_e[t] + dxxx[t] maa,   m_e = mexp_e + bias_e
-//   dx[t]      = sum_e dmix_e[t] + dxxx[t] - d_delta[t] + d_delta[t+1]
-// Walked forward with dx[t] emitted one token late; d_delta of each sub-segment's first
-// token is handed to the previous sub-segment through LDS.
-__device__ __forceinline__ void mix_token(const uint16_t* __restrict__ mexp, const float* bb,
-                                          const float* mv, const InPtrs<MIX_NE>& dmix,
-                                          const uint16_t* __restrict__ dxxx, int64_t off,
-                                          int64_t NC, float* dd, float* dsum, float* dxv) {
-    if (dxxx) load8(dxxx + off, dxv);
-    else for (int s = 0; s < 8; ++s) dxv[s] = 0.f;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        dd[s] = dxv[s] * mv[s];
-        dsum[s] = dxv[s];
-    }
-#pragma unroll
-    for (int e = 0; e < MIX_NE; ++e) {
-        float m[8], g[8];
-        load8(mexp + e * NC + off, m);
-        load8(dmix.p[e] + off, g);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            dd[s] += g[s] * (m[s] + bb[e * 8 + s]);
-            dsum[s] += g[s];
-        }
-    }
-}
-
-__global__ void __launch_bounds__(MIX_THR)
-rwkv6_mix_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa,
-                     const uint16_t* __restrict__ mexp, const void* __restrict__ bias, int pdt,
-                     InPtrs<MIX_NE> dmix, const uint16_t* __restrict__ dxxx,
-                     uint16_t* __restrict__ dx, float* __restrict__ part, int64_t T, int64_t B,
-                     int64_t C) {
-    __shared__ float first_dd[MIX_SS][32][8];
-    __shared__ float red[MIX_SS][32 * 8 + 4];
-    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
-    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
-    const int64_t b = blockIdx.z, NC = T * B * C;
-    const int64_t tb0 = (int64_t)blockIdx.x * MIX_TB;
-    const int64_t t_lo = tb0 + MIX_SS * ss, t_hi = min(T, t_lo + MIX_SS);
-    const bool active = cg < C8 && t_lo < T;
-    float acc[8], pend[8], mv[8], bb[MIX_NE * 8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) acc[s] = 0.f;
-    if (active) {
-        load_param8(maa, pdt, 8 * cg, mv);
-#pragma unroll
-        for (int e = 0; e < MIX_NE; ++e) load_param8(bias, pdt, e * C + 8 * cg, bb + 8 * e);
-        float xprev[8];
-        if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
-        else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
-        for (int64_t t = t_lo; t < t_hi; ++t) {
-            const int64_t off = (t * B + b) * C + 8 * cg;
-            float xv[8], dd[8], dsum[8], dxv[8], out[8];
-            load8(x + off, xv);
-            mix_token(mexp, bb, mv, dmix, dxxx, off, NC, dd, dsum, dxv);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                acc[s] += dxv[s] * (xprev[s] - xv[s]);
-                xprev[s] = xv[s];
-            }
-            if (t > t_lo) {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) out[s] = pend[s] + dd[s];
-                store8(dx + off - B * C, out);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) first_dd[ss][cgl][s] = dd[s];
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) pend[s] = dsum[s] - dd[s];
-        }
-    }
-    __syncthreads();
-    if (active) {
-        // d_delta of the token after this sub-segment
-        float nd[8];
-        if (t_hi >= T) {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) nd[s] = 0.f;
-        } else if (ss + 1 < MIX_SS) {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) nd[s] = first_dd[ss + 1][cgl][s];
-        } else {
-            float dsum[8], dxv[8];
-            mix_token(mexp, bb, mv, dmix, dxxx, (t_hi * B + b) * C + 8 * cg, NC, nd, dsum, dxv);
-        }
-        float out[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = pend[s] + nd[s];
-        store8(dx + ((t_hi - 1) * B + b) * C + 8 * cg, out);
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) red[ss][8 * cgl + s] = acc[s];
-    __syncthreads();
-    const int64_t P_row = (int64_t)blockIdx.x * B + b;
-    for (int c = threadIdx.x; c < 256; c += MIX_THR) {
-        const int64_t ch = (int64_t)blockIdx.y * 256 + c;
-        if (ch >= C) continue;
-        float sum = 0.f;
-#pragma unroll
-        for (int q = 0; q < MIX_SS; ++q) sum += red[q][c];
-        part[P_row * C + ch] = sum;
-    }
-}
 
 // out[n] = sum_p part[p][n] for n < Nn, in param dtype; thread (n, q): strided partial over
 // p = q mod 8, then a fixed-order combine (deterministic).
@@ -312,7 +110,8 @@ rwkv6_cmix_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ 
     }
 }
 
-// Backward of the channel-mix lerp (same block shape and hand-off as rwkv6_mix_bwd_kernel):
+// Backward of the channel-mix lerp (walked forward with dx[t] emitted one token late; d_delta
+// of each sub-segment's first token is handed to the previous sub-segment through LDS):
 //   d_delta[t] = sum_e dmix_e[t] mix_e,  dx[t] = sum_e dmix_e[t] - d_delta[t] + d_delta[t+1],
 //   d_mix_e partial = sum_t dmix_e[t] delta[t]  -> part[(tblk*B + b)][2][C].
 __device__ __forceinline__ void cmix_token(const float* mv, const InPtrs<CMIX_NE>& dmix,
@@ -544,6 +343,9 @@ int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* 
     if (T == 0) return RWKV6_OK;
     if (!x || !maa || !xxx) return RWKV6_ERR_INVALID_ARG;
     if (!al16(x) || !al16(maa) || !al16(xxx)) return RWKV6_ERR_ALIGNMENT;
+    const size_t act = (size_t)(T * B * C) * 2;
+    if (any_alias({{xxx, act}}, {{x, act}, {maa, (size_t)C * param_bytes(param_dtype)}}))
+        return RWKV6_ERR_INVALID_ARG;
     const int64_t n = T * B * (C / 8);
     hipLaunchKernelGGL(rwkv6_shift_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, maa, param_dtype,
@@ -551,85 +353,9 @@ int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* 
     return launch_status();
 }
 
-int rwkv6_ddlerp_fwd(const void* x, const void* mexp, const void* bias, int param_dtype,
-                     void* const* mixed, int64_t T, int64_t B, int64_t C, void* stream) {
-    int st = mix_check(T, B, C, param_dtype);
-    if (st) return st;
-    if (T == 0) return RWKV6_OK;
-    if (!x || !mexp || !bias) return RWKV6_ERR_INVALID_ARG;
-    OutPtrs<MIX_NE> out;
-    if ((st = gather<OutPtrs<MIX_NE>, MIX_NE>((const void* const*)mixed, out))) return st;
-    if (!al16(x) || !al16(mexp) || !al16(bias)) return RWKV6_ERR_ALIGNMENT;
-    const int64_t n = T * B * (C / 8);
-    hipLaunchKernelGGL(rwkv6_ddlerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
-                       reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x,
-                       (const uint16_t*)mexp, bias, param_dtype, out, T, B, C);
-    return launch_status();
-}
-
-size_t rwkv6_ddlerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
-    if (T < 0 || B < 1 || C < 8) return 0;
-    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
-    return (size_t)((ntb > 0 ? ntb : 1) * B * MIX_NE * C) * sizeof(float);
-}
-
 static dim3 bwd_grid(int64_t T, int64_t B, int64_t C) {
     return dim3((unsigned)((T + MIX_TB - 1) / MIX_TB), (unsigned)((C / 8 + 31) / 32), (unsigned)B);
 }
-
-int rwkv6_ddlerp_bwd(const void* x, const void* const* d_mixed, int param_dtype, void* d_mexp,
-                     void* d_bias, void* workspace, int64_t T, int64_t B, int64_t C,
-                     void* stream) {
-    int st = mix_check(T, B, C, param_dtype);
-    if (st) return st;
-    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
-    if (!d_bias || !workspace || (T > 0 && (!x || !d_mexp))) return RWKV6_ERR_INVALID_ARG;
-    InPtrs<MIX_NE> dm{};
-    if (T > 0 && (st = gather<InPtrs<MIX_NE>, MIX_NE>(d_mixed, dm))) return st;
-    if (!al16(x) || !al16(d_mexp) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
-    float* part = reinterpret_cast<float*>(workspace);
-    if (T > 0)
-        hipLaunchKernelGGL(rwkv6_ddlerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
-                           (const uint16_t*)x, dm, (uint16_t*)d_mexp, part, T, B, C);
-    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((MIX_NE * C + 31) / 32)), dim3(MIX_THR), 0, s,
-                       part, T > 0 ? ntb * B : (int64_t)0, (int64_t)MIX_NE * C, param_dtype, d_bias);
-    return launch_status();
-}
-
-size_t rwkv6_mix_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
-    if (T < 0 || B < 1 || C < 8) return 0;
-    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
-    return (size_t)((ntb > 0 ? ntb : 1) * B * C) * sizeof(float);
-}
-
-int rwkv6_mix_bwd(const void* x, const void* maa, const void* mexp, const void* bias,
-                  int param_dtype, const void* const* d_mixed, const void* d_xxx, void* dx,
-                  void* d_maa, void* workspace, int64_t T, int64_t B, int64_t C,
-                  void* stream) {
-    int st = mix_check(T, B, C, param_dtype);
-    if (st) return st;
-    if (B > 65535) return RWKV6_ERR_UNSUPPORTED;
-    if (!maa || !bias || !d_maa || !workspace || (T > 0 && (!x || !mexp || !dx)))
-        return RWKV6_ERR_INVALID_ARG;
-    InPtrs<MIX_NE> dm{};
-    if (T > 0 && (st = gather<InPtrs<MIX_NE>, MIX_NE>(d_mixed, dm))) return st;
-    if (!al16(x) || !al16(maa) || !al16(mexp) || !al16(bias) || (d_xxx && !al16(d_xxx)) ||
-        !al16(dx) || !al16(workspace))
-        return RWKV6_ERR_ALIGNMENT;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
-    float* part = reinterpret_cast<float*>(workspace);
-    if (T > 0)
-        hipLaunchKernelGGL(rwkv6_mix_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
-                           (const uint16_t*)x, maa, (const uint16_t*)mexp, bias, param_dtype, dm,
-                           (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
-    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(MIX_THR), 0, s, part,
-                       T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
-    return launch_status();
-}
-
 int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* const* mixed,
                         int64_t T, int64_t B, int64_t C, void* stream) {
     int st = mix_check(T, B, C, param_dtype);
@@ -639,6 +365,10 @@ int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* c
     OutPtrs<CMIX_NE> out;
     if ((st = gather<OutPtrs<CMIX_NE>, CMIX_NE>((const void* const*)mixed, out))) return st;
     if (!al16(x) || !al16(mix)) return RWKV6_ERR_ALIGNMENT;
+    const size_t act = (size_t)(T * B * C) * 2;
+    if (any_alias({{out.p[0], act}, {out.p[1], act}},
+                  {{x, act}, {mix, (size_t)CMIX_NE * C * param_bytes(param_dtype)}}))
+        return RWKV6_ERR_INVALID_ARG;
     const int64_t n = T * B * (C / 8);
     hipLaunchKernelGGL(rwkv6_cmix_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, mix, param_dtype,
@@ -662,6 +392,12 @@ int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype,
     InPtrs<CMIX_NE> dm{};
     if (T > 0 && (st = gather<InPtrs<CMIX_NE>, CMIX_NE>(d_mixed, dm))) return st;
     if (!al16(x) || !al16(mix) || !al16(dx) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(T * B * C) * 2, par = (size_t)CMIX_NE * C * param_bytes(param_dtype);
+        if (any_alias({{dx, act}, {d_mix, par}, {workspace, rwkv6_cmix_lerp_bwd_workspace_bytes(T, B, C)}},
+                      {{x, act}, {mix, par}, {dm.p[0], act}, {dm.p[1], act}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t ntb = (T + MIX_TB - 1) / MIX_TB;
     float* part = reinterpret_cast<float*>(workspace);
@@ -692,6 +428,7 @@ static unsigned ew_blocks(int64_t n8) {
 int rwkv6_relu_sq_fwd(const void* up, void* h, int64_t n, void* stream) {
     int st = ew_check(n, {up, h});
     if (st || n == 0) return st;
+    if (any_alias({{h, (size_t)n * 2}}, {{up, (size_t)n * 2}})) return RWKV6_ERR_INVALID_ARG;
     hipLaunchKernelGGL(rwkv6_relu_sq_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)up, (uint16_t*)h,
                        n / 8);
@@ -701,6 +438,8 @@ int rwkv6_relu_sq_fwd(const void* up, void* h, int64_t n, void* stream) {
 int rwkv6_relu_sq_bwd(const void* up, const void* dh, void* d_up, int64_t n, void* stream) {
     int st = ew_check(n, {up, dh, d_up});
     if (st || n == 0) return st;
+    const size_t nb = (size_t)n * 2;
+    if (any_alias({{d_up, nb}}, {{up, nb}, {dh, nb}})) return RWKV6_ERR_INVALID_ARG;
     hipLaunchKernelGGL(rwkv6_relu_sq_bwd_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)up,
                        (const uint16_t*)dh, (uint16_t*)d_up, n / 8);
@@ -711,6 +450,8 @@ int rwkv6_sigmoid_gate_fwd(const void* out, const void* gate_pre, void* y, int64
                            void* stream) {
     int st = ew_check(n, {out, gate_pre, y});
     if (st || n == 0) return st;
+    const size_t nb = (size_t)n * 2;
+    if (any_alias({{y, nb}}, {{out, nb}, {gate_pre, nb}})) return RWKV6_ERR_INVALID_ARG;
     hipLaunchKernelGGL(rwkv6_sigmoid_gate_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)out,
                        (const uint16_t*)gate_pre, (uint16_t*)y, n / 8);
@@ -721,6 +462,9 @@ int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy
                            void* d_gate_pre, int64_t n, void* stream) {
     int st = ew_check(n, {out, gate_pre, dy, d_out, d_gate_pre});
     if (st || n == 0) return st;
+    const size_t nb = (size_t)n * 2;
+    if (any_alias({{d_out, nb}, {d_gate_pre, nb}}, {{out, nb}, {gate_pre, nb}, {dy, nb}}))
+        return RWKV6_ERR_INVALID_ARG;
     hipLaunchKernelGGL(rwkv6_sigmoid_gate_bwd_kernel, dim3(ew_blocks(n / 8)), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)out,
                        (const uint16_t*)gate_pre, (const uint16_t*)dy, (uint16_t*)d_out,

@@ -53,8 +53,8 @@
 // Per-token log-decay floor.  The midpoint-referenced operand tiles scale by the decay of up
 // to 8 tokens either way, which must stay inside the bf16/fp32 exponent range (8 * 10 < 88);
 // a token below the floor keeps a decay factor e^-10 = 4.5e-5 instead of a smaller one
-// (relative change of the state below that); its gradient is the one at the floor, which
-// like the exact one carries that factor (the sequence-first entry returns d decay = 0).
+// (relative change of the state below that); its dw (d decay in the sequence-first entry) is
+// 0, the derivative of the floored forward, within e^-10 of the exact one.
 #define W_MIN (-10.0f)
 
 typedef uint16_t tile_t[CL][TS];
@@ -1038,11 +1038,17 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     // the operand tiles overwrite RmH, KmH and the w scratch in RmL); u of its two channels
     bf16x4 rrw[2], krw[2], wrw[2];
     float ulane[2];
+    unsigned floored = 0;                  // head-first: bit 4tp + rr set if w < W_MIN there
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
         rrw[tp] = ld_tr4(&sm.RmH[0][0], 16 * W, 16 * (2 * hh + tp));
         krw[tp] = ld_tr4(&sm.KmH[0][0], 16 * W, 16 * (2 * hh + tp));
-        if (SEQ) wrw[tp] = ld_tr4(&sm.RmL[0][0], 16 * W, 16 * (2 * hh + tp));
+        wrw[tp] = ld_tr4(&sm.RmL[0][0], 16 * W, 16 * (2 * hh + tp));
+        if (!SEQ) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+                floored |= (float)wrw[tp][rr] < W_MIN ? 1u << (4 * tp + rr) : 0u;
+        }
         ulane[tp] = scale * load_u(u, u_dtype, h * KD + 16 * (2 * hh + tp) + lr);
     }
     build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
@@ -1276,7 +1282,6 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
     float drv[2][4], dkv[2][4], dwv[2][4], wtot[2], dup[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
-        const int i = 16 * (2 * hh + tp) + lr;
         const float ui = ulane[tp];
         float xv[4];
         dup[tp] = 0.f;
@@ -1344,13 +1349,14 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
         for (int rr = 0; rr < 4; ++rr) {
             const int tt = 16 * W + 4 * lq + rr;
             g[rr] = dwv[tp][rr] + later;
-            // d decay = dw * w, w = -exp(decay); a floored token's d decay is 0 (the exact
-            // one carries its decay factor).  The head-first dw of a floored token is the
-            // gradient at the floor, itself scaled by e^W_MIN.
+            // A floored token's gradient is 0: the derivative of the floored forward, within
+            // e^W_MIN of the exact one (which carries the token's own decay factor).  The
+            // sequence-first entry returns d decay = dw * w, w = -exp(decay).
             if (SEQ && tt < nvalid) {
                 const float wn = -ex2((float)wrw[tp][rr] * RW_L2E);
                 g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
             }
+            if (!SEQ && ((floored >> (4 * tp + rr)) & 1u)) g[rr] = 0.f;
         }
         const int t4 = 16 * W + 4 * lq;
         *reinterpret_cast<uint2*>(&Ts[0][i][t4]) = make_uint2(pk2(drv[tp][0], drv[tp][1]), pk2(drv[tp][2], drv[tp][3]));
@@ -1488,6 +1494,14 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     if (!al16(r) || !al16(k) || !al16(v) || !al16(w) || !al16(u) || !al16(o) || !al16(saved) ||
         !al16(workspace) || (h0 && !al16(h0)) || (hT && !al16(hT)))
         return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(B * H * T) * KD * 2, st = (size_t)(B * H) * KD * KD * 4;
+        const size_t ub = (size_t)H * KD * (u_dtype == RWKV6_BF16 ? 2 : 4);
+        if (any_alias({{o, act}, {hT, st}, {saved, rwkv6_wkv_saved_bytes(B, H, T, K, V)},
+                       {workspace, rwkv6_wkv_workspace_bytes(B, H, T, K, V, 0)}},
+                      {{r, act}, {k, act}, {v, act}, {w, act}, {u, ub}, {h0, st}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);
@@ -1535,6 +1549,15 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
         !al16(dr) || !al16(dk) || !al16(dv) || !al16(dw) || !al16(workspace) ||
         (dhT && !al16(dhT)) || (dh0 && !al16(dh0)))
         return RWKV6_ERR_ALIGNMENT;
+    {
+        const size_t act = (size_t)(B * H * T) * KD * 2, st = (size_t)(B * H) * KD * KD * 4;
+        const size_t ub = (size_t)H * KD * (u_dtype == RWKV6_BF16 ? 2 : 4);
+        if (any_alias({{dr, act}, {dk, act}, {dv, act}, {dw, act}, {du, ub}, {dh0, st},
+                       {workspace, rwkv6_wkv_workspace_bytes(B, H, T, K, V, 1)}},
+                      {{r, act}, {k, act}, {v, act}, {w, act}, {u, ub}, {dO, act}, {dhT, st},
+                       {saved, rwkv6_wkv_saved_bytes(B, H, T, K, V)}}))
+            return RWKV6_ERR_INVALID_ARG;
+    }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);

@@ -21,8 +21,12 @@ Deliberate differences, all documented in the reference's own terms:
   * ``mix_coeff_input`` and ``RWKV6ChannelMix.mix_coeffs`` are left uninitialised by
     the reference (torch.empty, :377-385, :475-477); here they get the RWKV-6 ramp
     ``1 - (c / C) ** (1 - l / L)`` so a freshly built model is finite.
+  * The decay bias keeps the reference's uniform(-1, 1) (:173-175) unless
+    ``TransformerConfig.rwkv_lm_decay_init`` asks for RWKV-LM's ramp.
   * Biases on the linear layers are absent (config ``add_bias_linear = False``,
     the reference's example config), matching ``bias=...add_bias_linear`` (:393, :416).
+  * LayerNorms and the output head cast their parameters to the activations' dtype, so fp32
+    parameters train with bf16 activations (the HIP kernels take bf16 activations).
 """
 from __future__ import annotations
 
@@ -50,6 +54,10 @@ class TransformerConfig:
     init_method_std: float = 0.02                # example_config.yaml:31
     params_dtype: torch.dtype = torch.bfloat16
     perform_initialization: bool = True
+    # The reference initialises the decay bottleneck's bias uniform(-1, 1) (:173-175).  True
+    # selects RWKV-LM's per-channel ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1)) instead (the
+    # tiny-LM benchmark configuration asks for it).
+    rwkv_lm_decay_init: bool = False
 
 
 def _ramp(C, layer_id, n_layers, device):
@@ -113,6 +121,24 @@ class _Linear(nn.Module):
         return _LinearFn.apply(x, self.weight), None
 
 
+class LayerNorm(nn.LayerNorm):
+    """Megatron's LayerNorm at TP = 1 (the layer spec's input_layernorm / pre_mlp_layernorm,
+    :543, :546, and the model's pre_norm / final_layernorm); the parameters are cast to the
+    activations' dtype, so fp32 parameters run with bf16 activations."""
+
+    def forward(self, x):
+        return F.layer_norm(x, self.normalized_shape, self.weight.to(x.dtype), self.bias.to(x.dtype),
+                            self.eps)
+
+
+class OutputLayer(nn.Linear):
+    """The untied output head (rwkv6_model.py, output_layer) as y = x W^T with the parameter cast
+    to the activations' dtype; the weight gradient by the split-token GEMM of _LinearFn."""
+
+    def forward(self, x):
+        return _LinearFn.apply(x, self.weight)
+
+
 class GroupNorm(nn.Module):
     """rwkv6_layer_specs.py:50-109 (eps taken from config.layernorm_epsilon, :68)."""
 
@@ -125,9 +151,9 @@ class GroupNorm(nn.Module):
         self.bias = nn.Parameter(torch.zeros(num_channels, device=device, dtype=config.params_dtype))
 
     def forward(self, hidden_states):
-        """Plain GroupNorm over [N, C] (the reference's forward)."""
-        return F.group_norm(hidden_states, self.num_groups, self.weight.to(hidden_states.dtype),
-                            self.bias.to(hidden_states.dtype), eps=self.eps)
+        """GroupNorm over [N, C] (the reference's forward), on the HIP GroupNorm kernel
+        (groups of 64 channels, bf16 activations)."""
+        return timemix.group_norm(hidden_states, self.num_groups, self.weight, self.bias, self.eps)
 
 
 class RWKV6Bottleneck(nn.Module):
@@ -149,12 +175,10 @@ class RWKV6Bottleneck(nn.Module):
             nn.init.uniform_(self.bias, -1, 1)
 
     def forward(self, x):
-        """[T,B,C] -> [T,B,E,C] (reference layout, :177-195)."""
-        T, B, C = x.shape
-        neck = torch.tanh(x.reshape(T * B, C) @ self.weight_down.to(x.dtype).reshape(C, -1))
-        neck = neck.view(T * B, self.expansion, self.bottleneck_size).transpose(0, 1).contiguous()
-        up = torch.bmm(neck, self.weight_up.to(x.dtype).contiguous())          # [E, N, C]
-        return up.transpose(0, 1).reshape(T, B, self.expansion, C) + self.bias.to(x.dtype)
+        """[T,B,C] -> [T,B,E,C] (reference layout, :177-195), the up-projection and bias on the
+        HIP MFMA kernel.  RWKV6TimeMix does not call this: it runs each bottleneck fused with
+        its consumer (timemix.token_shift_mix, timemix.decay_lora)."""
+        return timemix.lora(x, self.weight_down, self.weight_up, self.bias)
 
 
 class WKV6(nn.Module):
@@ -211,10 +235,12 @@ class RWKV6TimeMix(nn.Module):
         if config.perform_initialization:
             with torch.no_grad():
                 self.mix_coeff_input.copy_(_ramp(C, layer_number - 1, config.num_layers, device))
-                # decay bias: RWKV-6 ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1))
-                L = max(config.num_layers - 1, 1)
-                c = torch.arange(C, dtype=torch.float32, device=device) / max(C - 1, 1)
-                self.bottleneck_decay.bias.copy_((-6 + 5 * c ** (0.7 + 1.3 * (layer_number - 1) / L))[None])
+                if config.rwkv_lm_decay_init:
+                    # RWKV-LM's decay ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1))
+                    L = max(config.num_layers - 1, 1)
+                    c = torch.arange(C, dtype=torch.float32, device=device) / max(C - 1, 1)
+                    self.bottleneck_decay.bias.copy_(
+                        (-6 + 5 * c ** (0.7 + 1.3 * (layer_number - 1) / L))[None])
 
     def forward(self, hidden_states, attention_mask=None, key_value_states=None,
                 inference_params=None, rotary_pos_emb=None, packed_seq_params=None):
@@ -272,11 +298,11 @@ class RWKV6Layer(nn.Module):
     def __init__(self, config, layer_number=1, device=None):
         super().__init__()
         C = config.hidden_size
-        self.input_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device,
-                                            dtype=config.params_dtype)
+        self.input_layernorm = LayerNorm(C, eps=config.layernorm_epsilon, device=device,
+                                         dtype=config.params_dtype)
         self.self_attention = RWKV6TimeMix(config, layer_number, device)
-        self.pre_mlp_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device,
-                                              dtype=config.params_dtype)
+        self.pre_mlp_layernorm = LayerNorm(C, eps=config.layernorm_epsilon, device=device,
+                                           dtype=config.params_dtype)
         self.mlp = RWKV6ChannelMix(config, layer_number, device)
 
     def forward(self, x):
@@ -289,13 +315,14 @@ class RWKV6Layer(nn.Module):
 def get_rwkv6_layer_spec():
     """Mirror of rwkv6_layer_specs.py:539-550 as a plain description (no Megatron here)."""
     return dict(module=RWKV6Layer,
-                submodules=dict(input_layernorm=nn.LayerNorm, self_attention=RWKV6TimeMix,
-                                pre_mlp_layernorm=nn.LayerNorm, mlp=RWKV6ChannelMix))
+                submodules=dict(input_layernorm=LayerNorm, self_attention=RWKV6TimeMix,
+                                pre_mlp_layernorm=LayerNorm, mlp=RWKV6ChannelMix))
 
 
 class RWKV6Model(nn.Module):
     """One-GPU RWKV-6 LM mirroring RWKV6Model (rwkv6_model.py:28-184): embedding ->
-    pre_norm (ln0, :34-37, :108-112) -> layers -> final LayerNorm -> untied output head."""
+    pre_norm (ln0, :34-37, :108-112) -> layers -> final LayerNorm -> untied output head.
+    Activations are bf16 (the HIP kernels' dtype) whatever the parameters' dtype."""
 
     def __init__(self, config, vocab_size, device=None):
         super().__init__()
@@ -303,15 +330,15 @@ class RWKV6Model(nn.Module):
         dt = config.params_dtype
         self.embedding = nn.Embedding(vocab_size, C, device=device, dtype=dt)
         nn.init.normal_(self.embedding.weight, 0.0, config.init_method_std)
-        self.pre_norm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
+        self.pre_norm = LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
         self.layers = nn.ModuleList(RWKV6Layer(config, i + 1, device) for i in range(config.num_layers))
-        self.final_layernorm = nn.LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
-        self.output_layer = nn.Linear(C, vocab_size, bias=False, device=device, dtype=dt)
+        self.final_layernorm = LayerNorm(C, eps=config.layernorm_epsilon, device=device, dtype=dt)
+        self.output_layer = OutputLayer(C, vocab_size, bias=False, device=device, dtype=dt)
         nn.init.normal_(self.output_layer.weight, 0.0, config.init_method_std)
 
     def forward(self, tokens):
         """tokens [B,T] -> logits [T,B,V] (sequence-first inside, as Megatron)."""
-        x = self.pre_norm(self.embedding(tokens.t()))
+        x = self.pre_norm(self.embedding(tokens.t()).to(torch.bfloat16))
         for layer in self.layers:
             x = layer(x)
         return self.output_layer(self.final_layernorm(x))

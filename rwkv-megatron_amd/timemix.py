@@ -5,10 +5,12 @@
   :440-452, bottleneck :177-195).  The shift/lerp, the LoRA up-projection fused with
   the ddlerp (MFMA) and their backwards are HIP kernels; the LoRA down-projection and the
   weight-gradient GEMMs run on hipBLASLt through torch.matmul / torch.bmm.
-* ``decay_lora``: the decay bottleneck (:454) with its up-projection + bias on MFMA.
+* ``decay_lora``: the decay bottleneck (:454) with its up-projection + bias on MFMA;
+  ``lora``: the same for either bottleneck as RWKV6Bottleneck.forward returns it (:177-195).
 * ``group_norm_gate``: GroupNorm over heads (:90-97, applied at :461-465) times
   silu(gate) (:458, :466), reading the WKV output head-first so the layout copy
-  of :341 disappears.
+  of :341 disappears; ``group_norm``: the same kernels without the gate (GroupNorm.forward,
+  :90-97).
 
 Every function raises if the HIP library is missing; there is no fallback.
 """
@@ -73,58 +75,16 @@ def shift_lerp(x: torch.Tensor, maa: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def ddlerp(x: torch.Tensor, mexp: torch.Tensor, bias: torch.Tensor):
-    """mixed[e] = x + (shift(x) - x) * (mexp[e] + bias[e]); mexp [5,T,B,C] -> tuple of five
-    [T,B,C] tensors (w, k, v, r, g)."""
-    _check_act("x", x, 3)
-    T, B, C = x.shape
-    if tuple(mexp.shape) != (NE, T, B, C):
-        raise ValueError(f"mexp must be [5,T,B,C] = {(NE, T, B, C)}, got {tuple(mexp.shape)}")
-    x, mexp = _c(x), _c(mexp.to(torch.bfloat16))
-    b, pdt = _param(bias)
-    out = tuple(torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device) for _ in range(NE))
-    _lib.check(_lib.load().rwkv6_ddlerp_fwd(_p(x), _p(mexp), _p(b), pdt, _ptrs(out), T, B, C,
-                                            _stream(x.device)), "rwkv6_ddlerp_fwd")
-    return out
-
-
-def ddlerp_bwd(x, d_mixed, param_dtype):
-    """d_mixed: five [T,B,C] bf16 tensors -> (d_mexp [5,T,B,C], d_bias [5,C])."""
-    T, B, C = x.shape
-    L = _lib.load()
-    d_mexp = torch.empty(NE, T, B, C, dtype=torch.bfloat16, device=x.device)
-    pdt = _lib.RWKV6_BF16 if param_dtype == torch.bfloat16 else _lib.RWKV6_F32
-    d_bias = torch.empty(NE, C, dtype=torch.bfloat16 if pdt == _lib.RWKV6_BF16 else torch.float32,
-                         device=x.device)
-    ws = torch.empty(L.rwkv6_ddlerp_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
-    _lib.check(L.rwkv6_ddlerp_bwd(_p(x), _ptrs(d_mixed), pdt, _p(d_mexp), _p(d_bias), _p(ws), T, B, C,
-                                  _stream(x.device)), "rwkv6_ddlerp_bwd")
-    return d_mexp, d_bias
-
-
-def mix_bwd(x, maa, mexp, bias, d_mixed, d_xxx):
-    T, B, C = x.shape
-    L = _lib.load()
-    m, pdt = _param(maa)
-    b, pdt_b = _param(bias)
-    if pdt_b != pdt:
-        b = _c(b.to(m.dtype))
-    dx = torch.empty_like(x)
-    d_maa = torch.empty(C, dtype=m.dtype, device=x.device)
-    ws = torch.empty(L.rwkv6_mix_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=x.device)
-    _lib.check(L.rwkv6_mix_bwd(_p(x), _p(m), _p(mexp), _p(b), pdt, _ptrs(d_mixed), _p(d_xxx), _p(dx),
-                               _p(d_maa), _p(ws), T, B, C, _stream(x.device)), "rwkv6_mix_bwd")
-    return dx, d_maa
-
-
 def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
+    """GroupNorm over heads of 64 channels times silu(g_pre); g_pre None: GroupNorm alone."""
     if head_first:
         B, H, T, K = o.shape
     else:
         T, B, C = o.shape
         K = 64
         H = C // K
-    o, g_pre = _c(o), _c(g_pre)
+    o = _c(o)
+    g_pre = None if g_pre is None else _c(g_pre)
     ga, pdt = _param(gamma)
     be, pdt_b = _param(beta)
     if pdt_b != pdt:
@@ -220,23 +180,24 @@ class _TokenShiftMix(torch.autograd.Function):
                 d_bias.to(bias.dtype))
 
 
-class _DecayLora(torch.autograd.Function):
-    """decay = tanh(x W_down) W_up + bias for the decay bottleneck (E = 1,
-    rwkv6_layer_specs.py:370-375, :454): W_down [C,1,R], W_up [1,R,C], bias [1,C] -> [T,B,C].
-    The up-projection and bias run in one MFMA kernel (rwkv6_lora_bias_fwd)."""
+class _Lora(torch.autograd.Function):
+    """out = tanh(x W_down) W_up + bias, RWKV6Bottleneck.forward (rwkv6_layer_specs.py:177-195):
+    x [T,B,C], W_down [C,E,R], W_up [E,R,C], bias [E,C] -> [T,B,E,C], E = 1 (decay, :370-375)
+    or 5 (token shift, :364-369).  The up-projection and bias run in one MFMA kernel
+    (rwkv6_lora_bias_fwd); the down-projection and the weight-gradient GEMMs on hipBLASLt."""
 
     @staticmethod
     def forward(ctx, x, w_down, w_up, bias):
         T, B, C = x.shape
-        R = w_down.shape[-1]
+        E, R = w_down.shape[1], w_down.shape[2]
         N = T * B
         x = _c(x)
-        wd = w_down.to(torch.bfloat16).reshape(C, R)
-        wut = w_up.to(torch.bfloat16).transpose(1, 2).contiguous()             # [1, C, R]
-        neck = _c(torch.tanh(x.view(N, C) @ wd))                                # [N, R]
+        wd = w_down.to(torch.bfloat16).reshape(C, E * R)
+        wut = w_up.to(torch.bfloat16).transpose(1, 2).contiguous()             # [E, C, R]
+        neck = _c(torch.tanh(x.view(N, C) @ wd))                                # [N, E*R]
         b, pdt = _param(bias)
-        out = torch.empty(T, B, C, dtype=torch.bfloat16, device=x.device)
-        _lib.check(_lib.load().rwkv6_lora_bias_fwd(_p(neck), _p(wut), _p(b), pdt, _p(out), N, C, R,
+        out = torch.empty(T, B, E, C, dtype=torch.bfloat16, device=x.device)
+        _lib.check(_lib.load().rwkv6_lora_bias_fwd(_p(neck), _p(wut), _p(b), pdt, _p(out), N, E, C, R,
                                                    _stream(x.device)), "rwkv6_lora_bias_fwd")
         ctx.save_for_backward(x, w_down, w_up, bias, neck, wut)
         return out
@@ -245,16 +206,27 @@ class _DecayLora(torch.autograd.Function):
     def backward(ctx, d_out):
         x, w_down, w_up, bias, neck, wut = ctx.saved_tensors
         T, B, C = x.shape
-        R = w_down.shape[-1]
+        E, R = w_down.shape[1], w_down.shape[2]
         N = T * B
-        g = _c(d_out.to(torch.bfloat16)).view(N, C)
-        d_bias = g.float().sum(0, keepdim=True)
-        d_w_up = _wgrad(neck, g).view(1, R, C)
-        d_pre = ((g @ wut[0]).float() * (1.0 - neck.float() ** 2)).to(torch.bfloat16)
-        d_w_down = _wgrad(x.view(N, C), d_pre).view(C, 1, R)
-        wd = w_down.to(torch.bfloat16).reshape(C, R)
+        g = _c(d_out.to(torch.bfloat16)).view(N, E, C)
+        d_bias = g.float().sum(0)                                               # [E, C]
+        neck3 = neck.view(N, E, R)
+        d_w_up = torch.stack([_wgrad(_c(neck3[:, e]), _c(g[:, e])) for e in range(E)])   # [E, R, C]
+        d_neck = torch.stack([_c(g[:, e]) @ wut[e] for e in range(E)], 1)       # [N, E, R]
+        d_pre = (d_neck.float() * (1.0 - neck3.float() ** 2)).to(torch.bfloat16).view(N, E * R)
+        d_w_down = _wgrad(x.view(N, C), d_pre).view(C, E, R)
+        wd = w_down.to(torch.bfloat16).reshape(C, E * R)
         dx = (d_pre @ wd.t()).view(T, B, C)
         return dx, d_w_down.to(w_down.dtype), d_w_up.to(w_up.dtype), d_bias.to(bias.dtype)
+
+
+def lora(x, w_down, w_up, bias):
+    """RWKV6Bottleneck.forward (:177-195): tanh(x W_down) W_up + bias, x [T,B,C] bf16 ->
+    [T,B,E,C] bf16 (E = 1 or 5)."""
+    _check_act("x", x, 3)
+    if w_down.dim() != 3 or w_up.dim() != 3 or w_down.shape[1] != w_up.shape[0]:
+        raise ValueError("expected w_down [C,E,R], w_up [E,R,C]")
+    return _Lora.apply(x, w_down, w_up, bias)
 
 
 def decay_lora(x, w_down, w_up, bias):
@@ -262,7 +234,7 @@ def decay_lora(x, w_down, w_up, bias):
     _check_act("x", x, 3)
     if w_down.dim() != 3 or w_down.shape[1] != 1:
         raise ValueError("decay_lora expects the E = 1 bottleneck (w_down [C,1,R])")
-    return _DecayLora.apply(x, w_down, w_up, bias)
+    return _Lora.apply(x, w_down, w_up, bias).view(x.shape)
 
 
 def token_shift_mix(x, maa, w_down, w_up, bias):
@@ -273,6 +245,8 @@ def token_shift_mix(x, maa, w_down, w_up, bias):
 
 
 class _GroupNormGate(torch.autograd.Function):
+    """y = GroupNorm_heads(o) * silu(g_pre), or GroupNorm alone when g_pre is None."""
+
     @staticmethod
     def forward(ctx, o, head_first, g_pre, gamma, beta, eps):
         y, mean, rstd = gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps)
@@ -291,13 +265,14 @@ class _GroupNormGate(torch.autograd.Function):
             K = 64
             H = C // K
         L = _lib.load()
-        o, g_pre, dy = _c(o), _c(g_pre), _c(dy.to(torch.bfloat16))
+        o, dy = _c(o), _c(dy.to(torch.bfloat16))
+        g_pre = None if g_pre is None else _c(g_pre)
         ga, pdt = _param(gamma)
         be, pdt_b = _param(beta)
         if pdt_b != pdt:
             be = _c(be.to(ga.dtype))
         d_o = torch.empty_like(o)
-        d_g = torch.empty_like(g_pre)
+        d_g = None if g_pre is None else torch.empty_like(g_pre)
         dgamma = torch.empty(H * K, dtype=ga.dtype, device=o.device)
         dbeta = torch.empty_like(dgamma)
         ws = torch.empty(L.rwkv6_gn_gate_bwd_workspace_bytes(T, B, H, K), dtype=torch.uint8,
@@ -313,6 +288,21 @@ def group_norm_gate(o, g_pre, gamma, beta, eps, head_first=True):
     """y [T,B,C] = GroupNorm_heads(o) * silu(g_pre); o is [B,H,T,64] (head_first) or [T,B,C]."""
     _check_act("o", o, 4 if head_first else 3)
     _check_act("g_pre", g_pre, 3)
+    return _group_norm(o, g_pre, gamma, beta, eps, head_first)
+
+
+def group_norm(x, num_groups, gamma, beta, eps):
+    """The reference's GroupNorm.forward (rwkv6_layer_specs.py:90-97) over x [N, C] bf16 with
+    groups of 64 channels (the RWKV-6 head size; other group sizes raise)."""
+    _check_act("x", x, 2)
+    N, C = x.shape
+    if C % num_groups or C // num_groups != 64:
+        raise NotImplementedError(f"GroupNorm kernels support groups of 64 channels (C={C}, "
+                                  f"groups={num_groups})")
+    return _group_norm(x.view(N, 1, C), None, gamma, beta, eps, False).view(N, C)
+
+
+def _group_norm(o, g_pre, gamma, beta, eps, head_first):
     if head_first:
         B, H, T, K = o.shape
     else:
@@ -320,6 +310,6 @@ def group_norm_gate(o, g_pre, gamma, beta, eps, head_first=True):
         K, H = 64, o.shape[-1] // 64
     if K != 64 or (not head_first and o.shape[-1] % 64):
         raise NotImplementedError("GroupNorm gate supports head size 64 only")
-    if tuple(g_pre.shape) != (T, B, H * K):
+    if g_pre is not None and tuple(g_pre.shape) != (T, B, H * K):
         raise ValueError(f"g_pre must be [T,B,C] = {(T, B, H * K)}, got {tuple(g_pre.shape)}")
     return _GroupNormGate.apply(o, bool(head_first), g_pre, gamma, beta, float(eps))

@@ -1,0 +1,72 @@
+"""Error metrics that every GPU parity test computes and prints for each tensor.
+
+* ``max_rel`` = max|got - ref| / max|ref| and ``l2_rel`` = ||got - ref||_2 / ||ref||_2: the
+  bars the tests assert (bf16 I/O with fp32 accumulation against an fp64 oracle on the same
+  bf16-rounded inputs);
+* the reference's own comparison, ``diff = |got - ref| / (|ref| + 1e-4)`` reduced to its max
+  and mean (/root/reference/rwkv_megatron/rwkv6_model.py:161-163, where RWKV-Megatron
+  compares its hidden states with the HF model's).  Its max is dominated by entries whose
+  reference value is near zero (a bf16 output rounds to 2^-9 of its own magnitude, and an
+  entry of 1e-3 next to entries of 1 gets an absolute error of ~1e-3 from the accumulation),
+  so the tests bound its mean (budgets below, per kind of tensor) and print the max.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+TOL_MAX = 1e-2
+TOL_L2 = 1e-2
+# Budgets for the mean of the reference's elementwise metric, per kind of tensor (about twice
+# the largest value measured on MI355X across the GPU tests).  The mean is not asserted for
+# tensors of fewer than MIN_ELEMS entries, where one near-zero reference entry decides it.
+ELEM_MEAN = 5e-3         # elementwise kernels: one bf16 rounding of an fp32 result (<= 2.1e-3)
+ELEM_MEAN_LORA = 8e-2    # kernels around bf16 hipBLASLt GEMMs (LoRA, channel-mix block; <= 3.8e-2)
+ELEM_MEAN_WKV = 6e-2     # WKV o, final state and gradients other than dw (<= 3.3e-2)
+ELEM_MEAN_WKV_DW = 2e-1  # WKV dw / d decay: a cancelling suffix sum, many near-zero entries (<= 8.7e-2)
+ELEM_MEAN_BLOCK = 3e-1   # whole blocks / layers / models, bf16 activations (<= 1.6e-1)
+MIN_ELEMS = 4096
+
+
+def metrics(got, ref) -> dict:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if ref.size == 0:
+        return dict(max_rel=0.0, l2_rel=0.0, elem_max=0.0, elem_mean=0.0)
+    d = np.abs(got - ref)
+    diff = d / (np.abs(ref) + 1e-4)
+    return dict(max_rel=float(d.max() / max(np.abs(ref).max(), 1e-30)),
+                l2_rel=float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)),
+                elem_max=float(diff.max()), elem_mean=float(diff.mean()))
+
+
+def fmt(name: str, m: dict) -> str:
+    return (f"{name}: max_rel {m['max_rel']:.1e} l2_rel {m['l2_rel']:.1e} | "
+            f"ref-diff max {m['elem_max']:.1e} mean {m['elem_mean']:.1e}")
+
+
+def check(name, got, ref, tol_max=TOL_MAX, tol_l2=TOL_L2, elem_mean=ELEM_MEAN) -> dict:
+    """Prints all four metrics of one tensor and asserts the bars (elem_mean None: printed only)."""
+    m = metrics(got, ref)
+    print(fmt(name, m), flush=True)
+    ok = m["max_rel"] <= tol_max and m["l2_rel"] <= tol_l2
+    if elem_mean is not None and np.size(ref) >= MIN_ELEMS:
+        ok = ok and m["elem_mean"] <= elem_mean
+    assert ok, f"{name}: parity failed {m} (bars max_rel {tol_max}, l2_rel {tol_l2}, " \
+               f"ref-diff mean {elem_mean})"
+    return m
+
+
+def check_all(got: dict, ref: dict, names, elem_mean_of=None, **bars) -> dict:
+    """check() over several tensors; reports every one before failing.  elem_mean_of(name), if
+    given, picks the reference-metric budget per tensor."""
+    out, bad = {}, []
+    for n in names:
+        b = dict(bars)
+        if elem_mean_of is not None:
+            b["elem_mean"] = elem_mean_of(n)
+        try:
+            out[n] = check(n, got[n], ref[n], **b)
+        except AssertionError as e:
+            bad.append(str(e))
+    assert not bad, "\n".join(bad)
+    return out

@@ -17,8 +17,9 @@ def _declared():
 
 def test_header_declares_entry_points():
     names = _declared()
-    for must in ("rwkv6_wkv_fwd", "rwkv6_wkv_bwd", "rwkv6_shift_lerp_fwd", "rwkv6_ddlerp_fwd",
-                 "rwkv6_mix_bwd", "rwkv6_gn_gate_fwd", "rwkv6_gn_gate_bwd", "rwkv6_strerror"):
+    for must in ("rwkv6_wkv_fwd", "rwkv6_wkv_bwd", "rwkv6_shift_lerp_fwd", "rwkv6_ddlerp_lora_fwd",
+                 "rwkv6_ddlerp_lora_bwd", "rwkv6_lora_bias_fwd", "rwkv6_gn_gate_fwd",
+                 "rwkv6_gn_gate_bwd", "rwkv6_strerror"):
         assert must in names
 
 
@@ -32,7 +33,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_version_and_strerror(pkg):
     L = pkg._lib.load()
-    assert L.rwkv6_abi_version() == 1
+    assert L.rwkv6_abi_version() == 2
     assert L.rwkv6_strerror(0) == b"ok"
     assert b"64" in L.rwkv6_strerror(2)
     assert L.rwkv6_strerror(12345) == b"unknown rwkv6 status code"
@@ -69,7 +70,9 @@ def test_validation_rejects_before_launch(pkg):
     assert L.rwkv6_wkv_fwd(*args(saved=None)) == pkg._lib.RWKV6_ERR_INVALID_ARG
     assert L.rwkv6_wkv_fwd(*args(r=_fake(0x100002))) == pkg._lib.RWKV6_ERR_ALIGNMENT
     assert L.rwkv6_shift_lerp_fwd(p, p, 1, p, 4, 2, 12, None) == pkg._lib.RWKV6_ERR_UNSUPPORTED
-    assert L.rwkv6_ddlerp_fwd(p, p, p, 3, p, 4, 2, 16, None) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_lora_bias_fwd(p, p, p, 3, p, 4, 1, 64, 32, None) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_lora_bias_fwd(p, p, p, 1, p, 4, 3, 64, 32, None) == pkg._lib.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_lora_bias_fwd(p, p, p, 1, p, 4, 0, 64, 32, None) == pkg._lib.RWKV6_ERR_INVALID_ARG
     assert L.rwkv6_gn_gate_fwd(p, 1, p, p, p, 0, 1e-5, p, p, p, 4, 2, 2, 32, None) == \
         pkg._lib.RWKV6_ERR_UNSUPPORTED
     assert L.rwkv6_gn_gate_fwd(None, 1, p, p, p, 0, 1e-5, p, p, p, 4, 2, 2, 64, None) == \
@@ -84,6 +87,28 @@ def test_validation_rejects_before_launch(pkg):
     assert L.rwkv6_sigmoid_gate_fwd(p, _fake(0x100008), p, 16, None) == E.RWKV6_ERR_ALIGNMENT
     assert L.rwkv6_sigmoid_gate_bwd(p, p, p, p, None, 16, None) == E.RWKV6_ERR_INVALID_ARG
     assert L.rwkv6_relu_sq_fwd(None, None, 0, None) == E.RWKV6_OK       # empty: nothing to do
+
+
+def test_overlapping_outputs_are_rejected(pkg):
+    """An output that overlaps an input (or another output) is refused before any launch:
+    several kernels re-load a clamped last piece after other threads stored theirs, and the
+    walks read chunk c + 1 before storing chunk c (the pointers are fake; nothing is read)."""
+    L = pkg._lib.load()
+    E = pkg._lib
+    a, b, c, d = (_fake(0x100000 * i) for i in (1, 2, 3, 4))
+    inside = _fake(0x100000 + 16)                                   # 16 bytes into a
+    assert L.rwkv6_relu_sq_fwd(a, a, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_relu_sq_fwd(a, inside, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_sigmoid_gate_bwd(a, b, c, d, d, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_sigmoid_gate_fwd(a, b, inside, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_shift_lerp_fwd(a, b, 1, a, 4, 2, 16, None) == E.RWKV6_ERR_INVALID_ARG
+    # WKV forward: o on top of v
+    assert L.rwkv6_wkv_fwd(a, b, c, d, _fake(0x500000), 1, None, c, None, _fake(0x600000),
+                           _fake(0x700000), 1, 1, 64, 64, 64, 1.0, None) == E.RWKV6_ERR_INVALID_ARG
+    # GroupNorm backward: a gate gradient without a gate input
+    assert L.rwkv6_gn_gate_bwd(a, 1, None, b, b, 0, p_ := _fake(0x500000), p_, c, d, _fake(0x600000),
+                               _fake(0x700000), _fake(0x800000), _fake(0x900000), 4, 2, 2, 64,
+                               None) == E.RWKV6_ERR_INVALID_ARG
 
 
 def test_python_checker_maps_codes(pkg):

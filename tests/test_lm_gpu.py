@@ -1,0 +1,63 @@
+"""BASELINE config 1 on the GPU: the tiny RWKV-6 language model (2 layers, d_model 512,
+8 heads of 64, ffn 1792, vocab 65536, fp32 weights with normal(0, 0.02) init and RWKV-LM's
+decay ramp), batch 2 x 512 uniform random token ids, one forward + backward with cross
+entropy on next-token targets (the last position masked; pretrain_rwkv6.py:144-160).
+
+The package runs it with fp32 parameters and bf16 activations (the kernels' dtype); the
+checker is oracle/lm.py in fp64 on the same fp32 weights (rwkv6_model.py:28-37, :108-112;
+rwkv6_layer_specs.py:431-550) with the C oracle's WKV.  Bars: the loss to 1e-3 relative;
+logits and every parameter gradient max_rel 5e-2, l2_rel 3e-2, reference-metric mean
+parity.ELEM_MEAN_BLOCK (bf16 activations through two layers).
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import parity
+from oracle import lm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+BARS = dict(tol_max=5e-2, tol_l2=3e-2, elem_mean=parity.ELEM_MEAN_BLOCK)
+
+
+def config1_batch(V=65536, B=2, T=512, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    tokens = torch.randint(0, V, (B, T), generator=g)
+    targets = torch.cat([tokens[:, 1:], torch.zeros(B, 1, dtype=tokens.dtype)], 1)
+    mask = torch.ones(B, T)
+    mask[:, -1] = 0
+    return tokens, targets, mask
+
+
+def test_config1_tiny_lm_forward_backward(pkg):
+    M = pkg.modules
+    cfg = M.TransformerConfig(hidden_size=512, num_attention_heads=8, ffn_hidden_size=1792,
+                              num_layers=2, params_dtype=torch.float32, rwkv_lm_decay_init=True)
+    V = 65536
+    torch.manual_seed(0)
+    model = M.RWKV6Model(cfg, V, device=DEV)
+    tokens, targets, mask = config1_batch(V)
+
+    logits = model(tokens.to(DEV))
+    assert logits.shape == (512, 2, V) and logits.dtype == torch.bfloat16
+    flat = logits.float().transpose(0, 1).reshape(-1, V)
+    losses = F.cross_entropy(flat, targets.to(DEV).reshape(-1), reduction="none")
+    m = mask.to(DEV).reshape(-1)
+    loss = (losses * m).sum() / m.sum()
+    loss.backward()
+    torch.cuda.synchronize()
+
+    p = lm.params_from_state_dict(model.state_dict())
+    ref_logits = lm.model_forward(p, tokens, cfg.num_layers, cfg.num_attention_heads,
+                                  cfg.layernorm_epsilon)
+    ref_loss = lm.lm_loss(ref_logits, targets, mask)
+    ref_loss.backward()
+
+    print(f"loss gpu {loss.item():.6f} ref {ref_loss.item():.6f}", flush=True)
+    assert abs(loss.item() - ref_loss.item()) <= 1e-3 * abs(ref_loss.item())
+    n = lambda t: t.detach().double().cpu().numpy()
+    parity.check("logits", n(logits), n(ref_logits), **BARS)
+    got = {name: n(prm.grad) for name, prm in model.named_parameters()}
+    want = {name: n(p[name].grad) for name in got}
+    parity.check_all(got, want, sorted(got), **BARS)

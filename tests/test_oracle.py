@@ -308,3 +308,54 @@ def test_channel_mix_forward_and_backward_match_autograd():
     got = orc.channel_mix_bwd(n(x), n(mix), n(w_up), n(w_gate), n(w_down), n(dy))
     for a, leaf in zip(got, (x, mix, w_up, w_gate, w_down)):
         assert _rel(a, n(leaf.grad)) < 1e-12
+
+
+# ---------------------------------------------------------------------------------------
+# oracle/lm.py: the whole-model restatement (checker for the layer / LM tests, config-1
+# CPU baseline)
+# ---------------------------------------------------------------------------------------
+
+def test_lm_forward_matches_rwkv_lm_forward(pkg):
+    """oracle.lm.model_forward (torch, the reference's module names and tensor shapes) equals
+    the fp64 numpy forward written against RWKV-LM's own names (tests/rwkv_lm_reference.py,
+    built from the numpy oracle pieces) on the same weights mapped by the checkpoint key map."""
+    import rwkv_lm_reference as ref
+    from oracle import lm
+
+    C, H, F_, L, V = 128, 2, 448, 2, 200
+    sd = ref.make_state_dict(C, H, F_, L, V, seed=5)
+    p = lm.params_from_state_dict(pkg.modules.rwkv_lm_to_state_dict(sd, L), requires_grad=False)
+    tokens = torch.randint(0, V, (2, 40), generator=torch.Generator().manual_seed(2))
+    got = lm.model_forward(p, tokens, L, H).numpy()
+    want = ref.forward(sd, tokens.numpy(), L, H)
+    assert _rel(got, want) < 1e-6
+
+
+def test_lm_wkv_wrapper_gradcheck():
+    """The autograd wrapper around the C oracle against finite differences (the oracle's
+    I/O is fp32, so the step is 1e-3 and the bars are loose; a dropped or swapped gradient
+    fails by O(1))."""
+    from oracle import lm
+
+    g = torch.Generator().manual_seed(0)
+    B, H, T, K = 1, 1, 5, 64
+    r, k, v = (torch.randn(B, H, T, K, generator=g, dtype=torch.float64) for _ in range(3))
+    w = -torch.exp(torch.rand(B, H, T, K, generator=g, dtype=torch.float64) * 3 - 3)
+    u = 0.3 * torch.randn(H, K, generator=g, dtype=torch.float64)
+    leaves = [t.requires_grad_(True) for t in (r, k, v, w, u)]
+    assert torch.autograd.gradcheck(lm.OracleWKV.apply, leaves, eps=1e-3, atol=2e-3, rtol=2e-2)
+
+
+def test_lm_loss_is_masked_mean_cross_entropy():
+    from oracle import lm
+
+    g = torch.Generator().manual_seed(1)
+    T, B, V = 9, 3, 17
+    logits = torch.randn(T, B, V, generator=g, dtype=torch.float64)
+    tgt = torch.randint(0, V, (B, T), generator=g)
+    mask = torch.ones(B, T)
+    mask[:, -1] = 0
+    got = lm.lm_loss(logits, tgt, mask)
+    want = torch.nn.functional.cross_entropy(logits[:-1].transpose(0, 1).reshape(-1, V),
+                                             tgt[:, :-1].reshape(-1))
+    assert abs(float(got) - float(want)) < 1e-12

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+import parity
 import rwkv_lm_reference as ref
 
 C, H, F, L, V = 128, 2, 448, 2, 256
@@ -78,9 +79,7 @@ def test_converted_model_logits_match_rwkv_lm_forward(pkg):
     want = ref.forward(sd_bf, tokens.numpy(), L, H)
     err = lambda a: (np.abs(a - want).max() / np.abs(want).max(),
                      np.linalg.norm(a - want) / np.linalg.norm(want))
-    e_max, e_l2 = err(logits)
-    print(f"logits: {e_max:.1e}/{e_l2:.1e}")
-    assert e_max <= TOL and e_l2 <= TOL
+    parity.check("logits", logits, want, tol_max=TOL, tol_l2=TOL, elem_mean=parity.ELEM_MEAN_BLOCK)
     # control: a converter that swapped two of the five token-shift mixes (k <-> v) is caught
     bad = dict(sd)
     for i in range(L):

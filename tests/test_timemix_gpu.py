@@ -1,15 +1,16 @@
-"""GPU parity of the fused time-mix kernels (token shift / lerp / ddlerp, GroupNorm*gate)
-against the numpy oracle on identical bf16 inputs.
+"""GPU parity of the fused time-mix kernels (token shift / lerp, the LoRA bottlenecks fused
+with the ddlerp or bias, GroupNorm*gate) against the numpy oracle on identical bf16 inputs.
 
 Tolerance: max|gpu - oracle| / max|oracle| <= 1e-2 and relative L2 <= 1e-2 for the
 elementwise kernels (their only rounding is the bf16 store); the LoRA weight
 gradients and the decay bottleneck's input gradient go through bf16 hipBLASLt GEMMs and
-use 2e-2.
+use 2e-2.  The reference's elementwise metric is reported for every tensor (tests/parity.py).
 """
 import numpy as np
 import pytest
 import torch
 
+import parity
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -20,17 +21,13 @@ def _n(t):
     return t.detach().float().cpu().numpy()
 
 
-def _err(got, ref):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    return (np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30),
-            np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+def _check(name, got, ref, tol=1e-2, elem_mean=parity.ELEM_MEAN):
+    parity.check(name, got, ref, tol_max=tol, tol_l2=tol, elem_mean=elem_mean)
 
 
-def _check(name, got, ref, tol=1e-2):
-    e = _err(got, ref)
-    print(f"{name}: {e[0]:.1e}/{e[1]:.1e}")
-    assert e[0] <= tol and e[1] <= tol, (name, e)
+def _check_lora(name, got, ref, tol=1e-2):
+    """Tensors of the LoRA paths: an hipBLASLt GEMM with bf16 operands sits on the way."""
+    parity.check(name, got, ref, tol_max=tol, tol_l2=tol, elem_mean=parity.ELEM_MEAN_LORA)
 
 
 def _bf(t):
@@ -39,18 +36,76 @@ def _bf(t):
 
 @pytest.mark.parametrize("shape", [(1, 1, 8), (7, 3, 64), (130, 2, 512)])
 @pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
-def test_shift_lerp_and_ddlerp(pkg, shape, pdt):
+def test_shift_lerp(pkg, shape, pdt):
     T, B, C = shape
     g = torch.Generator().manual_seed(T + C)
     x = _bf(torch.randn(T, B, C, generator=g))
     maa = torch.rand(C, generator=g).to(pdt)
-    mexp = _bf(torch.randn(5, T, B, C, generator=g))
-    bias = torch.randn(5, C, generator=g).to(pdt)
     xxx = pkg.timemix.shift_lerp(x.to(DEV), maa.to(DEV))
-    mixed = torch.stack(pkg.timemix.ddlerp(x.to(DEV), mexp.to(DEV), bias.to(DEV)))
     torch.cuda.synchronize()
     _check("xxx", _n(xxx), orc.shift_lerp_fwd(_n(x), _n(maa)))
-    _check("mixed", _n(mixed), orc.ddlerp_fwd(_n(x), np.moveaxis(_n(mexp), 0, 2), _n(bias)))
+
+
+@pytest.mark.parametrize("E,R", [(5, 32), (1, 64)])
+def test_bottleneck_module(pkg, E, R):
+    """RWKV6Bottleneck.forward (:177-195) on its own, both expansions: [T,B,C] -> [T,B,E,C]
+    through the HIP up-projection + bias, forward and every gradient, against the oracle."""
+    M = pkg.modules
+    T, B, C = 67, 2, 192
+    cfg = M.TransformerConfig(hidden_size=C, num_attention_heads=3, params_dtype=torch.float32)
+    bn = M.RWKV6Bottleneck(cfg, R, E, E == 1, device=DEV)
+    g = torch.Generator().manual_seed(E * 100 + R)
+    with torch.no_grad():      # GEMM operands are bf16: keep the weights bf16-representable
+        bn.weight_down.copy_(_bf(torch.empty(C, E, R).uniform_(-0.1, 0.1, generator=g)).float())
+        bn.weight_up.copy_(_bf(torch.empty(E, R, C).uniform_(-0.3, 0.3, generator=g)).float())
+        bn.bias.uniform_(-1, 1)
+    x = _bf(torch.randn(T, B, C, generator=g))
+    dy = _bf(torch.randn(T, B, E, C, generator=g))
+    xg = x.to(DEV).requires_grad_(True)
+    out = bn(xg)
+    assert out.shape == (T, B, E, C)
+    (out.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    xn, wdn, wun, bnn = (_n(t) for t in (x, bn.weight_down, bn.weight_up, bn.bias))
+    _check_lora("out", _n(out), orc.bottleneck_fwd(xn, wdn, wun, bnn))
+    dx, d_wd, d_wu, d_b = orc.bottleneck_bwd(xn, wdn, wun, _n(dy))
+    _check_lora("dx", _n(xg.grad), dx, 2e-2)
+    _check_lora("d_w_down", _n(bn.weight_down.grad), d_wd, 2e-2)
+    _check_lora("d_w_up", _n(bn.weight_up.grad), d_wu, 2e-2)
+    _check_lora("d_bias", _n(bn.bias.grad), d_b)
+
+
+@pytest.mark.parametrize("pdt", [torch.float32, torch.bfloat16])
+def test_group_norm_module(pkg, pdt):
+    """GroupNorm.forward (:90-97) on its own over [N, C] (groups of 64), on the HIP kernel
+    without the gate: forward and gradients against torch.nn.functional.group_norm in fp64,
+    the routine the reference calls."""
+    M = pkg.modules
+    N, H = 300, 4
+    C = 64 * H
+    cfg = M.TransformerConfig(hidden_size=C, num_attention_heads=H, params_dtype=pdt)
+    gn = M.GroupNorm(cfg, H, C, device=DEV)
+    g = torch.Generator().manual_seed(7)
+    with torch.no_grad():
+        gn.weight.copy_((1 + 0.3 * torch.randn(C, generator=g)).to(pdt))
+        gn.bias.copy_((0.2 * torch.randn(C, generator=g)).to(pdt))
+    x = _bf(torch.randn(N, C, generator=g) * 2 + 0.5)
+    dy = _bf(torch.randn(N, C, generator=g))
+    xg = x.to(DEV).requires_grad_(True)
+    y = gn(xg)
+    (y.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    xr = x.double().requires_grad_(True)
+    wr = gn.weight.detach().double().cpu().requires_grad_(True)
+    br = gn.bias.detach().double().cpu().requires_grad_(True)
+    yr = torch.nn.functional.group_norm(xr, H, wr, br, eps=cfg.layernorm_epsilon)
+    (yr * dy.double()).sum().backward()
+    _check("y", _n(y), yr.detach().numpy())
+    _check("dx", _n(xg.grad), xr.grad.numpy())
+    _check("dgamma", _n(gn.weight.grad), wr.grad.numpy())
+    _check("dbeta", _n(gn.bias.grad), br.grad.numpy())
+    with pytest.raises(NotImplementedError):
+        M.GroupNorm(cfg, 2 * H, C, device=DEV)(xg)          # 32-channel groups: no kernel
 
 
 # N = T*B = 10 (a partial 64-token tile), 210 and 520 (several tiles, C > 64)
@@ -77,16 +132,16 @@ def test_token_shift_mix_forward_backward(pkg, T, B, C, pdt):
     xxx = orc.shift_lerp_fwd(xn, maan)
     m = orc.bottleneck_fwd(xxx, wdn, wun, np.zeros_like(bn))           # [T,B,5,C] without bias
     ref_mixed = orc.ddlerp_fwd(xn, m, bn)
-    _check("mixed", _n(mixed), ref_mixed)
+    _check_lora("mixed", _n(mixed), ref_mixed)
     dmn = _n(dmix)
     _, d_m, _, _ = orc.mix_bwd(xn, maan, m, bn, dmn, np.zeros_like(xn))
     d_xxx, d_wd, d_wu, _ = orc.bottleneck_bwd(xxx, wdn, wun, d_m)
     dx, _, d_bias, d_maa = orc.mix_bwd(xn, maan, m, bn, dmn, d_xxx)
-    _check("dx", _n(leaves[0].grad), dx)
-    _check("d_maa", _n(leaves[1].grad), d_maa)
-    _check("d_w_down", _n(leaves[2].grad), d_wd, 2e-2)
-    _check("d_w_up", _n(leaves[3].grad), d_wu, 2e-2)
-    _check("d_bias", _n(leaves[4].grad), d_bias)
+    _check_lora("dx", _n(leaves[0].grad), dx)
+    _check_lora("d_maa", _n(leaves[1].grad), d_maa)
+    _check_lora("d_w_down", _n(leaves[2].grad), d_wd, 2e-2)
+    _check_lora("d_w_up", _n(leaves[3].grad), d_wu, 2e-2)
+    _check_lora("d_bias", _n(leaves[4].grad), d_bias)
 
 
 @pytest.mark.parametrize("T,B,C,R", [(5, 2, 64, 64), (70, 3, 256, 64), (33, 2, 128, 32)])
@@ -103,12 +158,12 @@ def test_decay_lora_forward_backward(pkg, T, B, C, R):
     (out.float() * dy.to(DEV).float()).sum().backward()
     torch.cuda.synchronize()
     xn, wdn, wun, bn = (_n(t) for t in (x, wd, wu, bias))
-    _check("decay", _n(out), orc.bottleneck_fwd(xn, wdn, wun, bn)[:, :, 0])
+    _check_lora("decay", _n(out), orc.bottleneck_fwd(xn, wdn, wun, bn)[:, :, 0])
     dx, d_wd, d_wu, d_b = orc.bottleneck_bwd(xn, wdn, wun, _n(dy)[:, :, None])
-    _check("dx", _n(leaves[0].grad), dx, 2e-2)
-    _check("d_w_down", _n(leaves[1].grad), d_wd, 2e-2)
-    _check("d_w_up", _n(leaves[2].grad), d_wu, 2e-2)
-    _check("d_bias", _n(leaves[3].grad), d_b)
+    _check_lora("dx", _n(leaves[0].grad), dx, 2e-2)
+    _check_lora("d_w_down", _n(leaves[1].grad), d_wd, 2e-2)
+    _check_lora("d_w_up", _n(leaves[2].grad), d_wu, 2e-2)
+    _check_lora("d_bias", _n(leaves[3].grad), d_b)
 
 
 @pytest.mark.parametrize("head_first", [True, False])
