@@ -25,6 +25,14 @@ ELEM_MEAN_WKV = 6e-2     # WKV o, final state and gradients other than dw (<= 3.
 ELEM_MEAN_WKV_DW = 2e-1  # WKV dw / d decay: a cancelling suffix sum, many near-zero entries (<= 8.7e-2)
 ELEM_MEAN_BLOCK = 3e-1   # whole blocks / layers / models, bf16 activations (<= 1.6e-1)
 MIN_ELEMS = 4096
+# Whole blocks / layers / models keep bf16 activations between the bf16 hipBLASLt GEMMs (as
+# bf16 training does); each kernel on the way is pinned on its own at 1e-2.  The relative L2
+# error is the bar that matters there; the max-normalised error of a tensor of millions of
+# entries sits in the tail of the bf16 storage errors (up to 5.6e-2 measured on the 16.8 M
+# entries of a 4096 x 4096 weight gradient whose l2_rel is 1.8e-2).
+BLOCK_TOL_MAX = 1e-1
+BLOCK_TOL_L2 = 3e-2
+BLOCK_BARS = dict(tol_max=BLOCK_TOL_MAX, tol_l2=BLOCK_TOL_L2, elem_mean=ELEM_MEAN_BLOCK)
 
 
 def metrics(got, ref) -> dict:

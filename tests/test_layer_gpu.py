@@ -8,8 +8,8 @@ B=2 x T=8192).
   (bf16) weights.  The residual carries x through unchanged, so the block's own output
   y - x and the input gradient's non-identity part dx - dy are compared.  Bars for a block
   that keeps bf16 activations between hipBLASLt GEMMs (as bf16 training does; every kernel
-  on it is pinned separately at 1e-2): max_rel 5e-2, l2_rel 3e-2, reference-metric mean
-  parity.ELEM_MEAN_BLOCK.
+  on it is pinned separately at 1e-2): parity.BLOCK_BARS (max_rel 1e-1, l2_rel 3e-2,
+  reference-metric mean 3e-1).
 * Full shape: the same layer over the config's whole T x B: finite, bit-identical on a
   second run, and a gradient for every parameter.
 """
@@ -24,7 +24,7 @@ DEV = "cuda:0"
 
 # name: (C, H, F, B, T)
 WIDTHS = {"config3": (2048, 32, 7168, 4, 4096), "config4": (4096, 64, 14336, 2, 8192)}
-BARS = dict(tol_max=5e-2, tol_l2=3e-2, elem_mean=parity.ELEM_MEAN_BLOCK)
+BARS = parity.BLOCK_BARS
 
 
 def _layer(pkg, C, H, F):
@@ -67,6 +67,9 @@ def test_full_width_layer_parity(pkg, cfg_name):
     ref.backward(dy.double())
 
     n = lambda t: t.detach().double().cpu().numpy()
+    # out and dx are stored in bf16, rounded at the scale of x and dy (2^-9 of it), while the
+    # block's own parts y - x and dx - dy are several times smaller: their errors carry that
+    # storage rounding on top of the block's own
     parity.check("y - x", n(out) - n(x), n(ref) - n(x), **BARS)
     parity.check("dx - dy", n(xg.grad) - n(dy), n(xr.grad) - n(dy), **BARS)
     got = {name: n(prm.grad) for name, prm in layer.named_parameters()}

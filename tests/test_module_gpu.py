@@ -2,8 +2,8 @@
 the reference's forward (rwkv6_layer_specs.py:431-468, oracle/lm.py) in torch fp32, with
 the WKV of :339 provided by the CPU oracle through its autograd wrapper.
 
-Block-level tolerance: relative L2 <= 3e-2 and max|err|/max|ref| <= 5e-2 — the GPU
-path keeps activations in bf16 between the GEMMs (as bf16 training does); every
+Block-level tolerance (parity.BLOCK_BARS): relative L2 <= 3e-2 and max|err|/max|ref| <= 1e-1
+— the GPU path keeps activations in bf16 between the GEMMs (as bf16 training does); every
 kernel on it is pinned separately at 1e-2.  The reference's elementwise metric is printed
 (tests/parity.py).
 """
@@ -45,7 +45,7 @@ def test_timemix_module_matches_reference_forward(pkg, params_dtype):
     (ref * dy.float()).sum().backward()
 
     n = lambda t: t.detach().double().cpu().numpy()
-    bars = dict(tol_max=5e-2, tol_l2=3e-2, elem_mean=parity.ELEM_MEAN_BLOCK)
+    bars = parity.BLOCK_BARS
     parity.check("out", n(out), n(ref), **bars)
     parity.check("dx", n(xg.grad), n(xc.grad), **bars)
     got = {name: n(prm.grad) for name, prm in mod.named_parameters()}
