@@ -38,6 +38,8 @@ SIGNATURES = {
                          + [_f32, _vp, _vp]),
     "rwkv6_wkv_bwd_ex": (_int, [_vp] * 5 + [_int] + [_vp, _fp, _vp] + [_vp] * 5 + [_fp, _vp]
                          + [_i64] * 5 + [_f32, _vp, _vp]),
+    "rwkv6_wkv_fwd_noalloc": (_int, [_vp] * 5 + [_int] + [_fp, _vp, _fp, _vp] + [_i64] * 5
+                              + [_f32, _vp]),
     "rwkv6_wkv_fwd_seqfirst": (_int, [_vp] * 5 + [_int] + [_fp, _vp, _fp, _vp, _vp] + [_i64] * 5
                                + [_f32, _vp]),
     "rwkv6_wkv_bwd_seqfirst": (_int, [_vp] * 5 + [_int] + [_vp, _fp, _vp] + [_vp] * 5 + [_fp, _vp]

@@ -36,6 +36,7 @@
 // contractions Rm / Km are bf16 hi + lo pairs: dw is a cancelling suffix sum of
 // r*dr - k*dk, and single-bf16 operands there would dominate its error.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
@@ -1618,7 +1619,71 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// forward without a workspace argument
+// ---------------------------------------------------------------------------
+// For callers that cannot allocate (code under HIP graph capture, tight serving loops): the
+// forward's only scratch, the segment states of its pre-pass (S_seg fp32 [64][64] and A_seg
+// fp32 [64] per segment), lives in this file-scope device array instead of the caller's
+// workspace.  walk_segments() gives P <= ceil(256 / (B*H)) segments per sequence, so a forward
+// never needs more than B*H*(P-1) < 256 segment states: WKV_SCRATCH_BYTES covers every shape.
+// Each GPU holds its own copy for the life of the process; calls on one GPU share it (the
+// last call's contents stay), so such calls must not overlap in time on one GPU.  Nothing in
+// it has to start at zero: the pre-pass writes every segment state the output walk reads.
+#define WKV_SCRATCH_SEGS 256
+#define WKV_SCRATCH_BYTES ((size_t)WKV_SCRATCH_SEGS * (KD * KD * 4 + KD * 4))
+static __device__ __align__(256) unsigned char scratch[WKV_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    int status = RWKV6_ERR_LAUNCH;
+    void* ptr = nullptr;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the GPU that runs `stream` (the current device for the
+// NULL stream).  Looked up once per device, with that device current; in host code the
+// array's name is only a stand-in, never a device address.
+int scratch_address(hipStream_t stream, void** out) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return RWKV6_ERR_LAUNCH;
+    int dev = cur;
+    if (stream) {
+        hipDevice_t d = 0;
+        if (hipStreamGetDevice(stream, &d) != hipSuccess) return RWKV6_ERR_INVALID_ARG;
+        dev = d;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return RWKV6_ERR_UNSUPPORTED;
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&slot, dev, cur] {
+        hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+        if (e == hipSuccess) e = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        slot.status = (e == hipSuccess && slot.ptr) ? RWKV6_OK : RWKV6_ERR_LAUNCH;
+    });
+    *out = slot.ptr;
+    return slot.status;
+}
+
+}  // namespace
+
 extern "C" {
+
+int rwkv6_wkv_fwd_noalloc(const void* r, const void* k, const void* v, const void* w,
+                          const void* u, int u_dtype, const float* h0, void* o, float* hT,
+                          void* saved, int64_t B, int64_t H, int64_t T, int64_t K, int64_t V,
+                          float scale, void* stream) {
+    int st = check_shape(B, H, T, K, V);
+    if (st != RWKV6_OK) return st;
+    if (rwkv6_wkv_workspace_bytes(B, H, T, K, V, 0) > WKV_SCRATCH_BYTES) return RWKV6_ERR_UNSUPPORTED;
+    void* ws = nullptr;
+    if ((st = scratch_address(reinterpret_cast<hipStream_t>(stream), &ws)) != RWKV6_OK) return st;
+    return wkv_fwd_impl<false>(r, k, v, w, u, u_dtype, h0, o, hT, saved, ws, B, H, T, K, V, scale,
+                               stream, nullptr);
+}
 
 int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
                      int u_dtype, const float* h0, void* o, float* hT, void* saved,
