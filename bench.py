@@ -18,7 +18,10 @@ Also reported:
   * cpu_baseline: the CPU oracle (fp64 naive recurrence, C + OpenMP, a port of
     fla's naive recurrent RWKV-6) timed on this host on the same workload;
   * config5 (WKV6 long context with carried state), slice_7b (config 4: four 7B-shape
-    layers fwd+bwd) and train_step (config 3: the 1.6B-shape training step).
+    layers fwd+bwd), train_step (config 3: the 1.6B-shape training step) and config1 (the
+    tiny LM's fwd+bwd step on the GPU and, as its CPU baseline, the reference model restated
+    in torch fp32 on this host); the CPU baselines also give forward-only times, and
+    cpu_host names the CPU model and thread counts.
 """
 from __future__ import annotations
 
@@ -68,8 +71,27 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_info():
+    """The host the CPU baselines ran on: CPU model, logical CPUs, and the threads used."""
+    import torch
+    from oracle import oracle as orc
+
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads(), "oracle_omp_threads": orc.max_threads()}
+
+
 def cpu_baseline(B, H, T, sample_heads, with_state=False):
-    """Time the CPU oracle (fwd + bwd) on this host; returns the reported dict."""
+    """Time the CPU oracle on this host: forward + backward (the reported value) and forward
+    alone; returns the reported dict."""
     import numpy as np
     from oracle import oracle as orc
 
@@ -87,13 +109,16 @@ def cpu_baseline(B, H, T, sample_heads, with_state=False):
     threads = orc.max_threads()
     # one warm-up on a short prefix, then the median of 3 timed runs
     orc.wkv6_fwd(r[:, :, :64], k[:, :, :64], v[:, :, :64], w[:, :, :64], u)
-    runs = []
+    runs, fwd_runs = [], []
     for _ in range(3):
         t0 = time.perf_counter()
         orc.wkv6_fwd(r, k, v, w, u, h0)
+        t1 = time.perf_counter()
         orc.wkv6_bwd(r, k, v, w, u, dO, h0, dhT)
         runs.append(time.perf_counter() - t0)
+        fwd_runs.append(t1 - t0)
     dt = sorted(runs)[1]
+    dt_f = sorted(fwd_runs)[1]
     frac = (Bs * Hs) / (B * H)
     tokens_per_s = (B * T) * frac / dt
     return {
@@ -101,7 +126,82 @@ def cpu_baseline(B, H, T, sample_heads, with_state=False):
         "sample": f"oracle fp64 naive recurrence fwd+bwd over {Bs*Hs} of {B*H} (b,h) sequences "
                   f"at T={T}{' with h0, dhT' if with_state else ''} (median of 3 runs, {dt:.2f} s), "
                   f"scaled to the whole B={B},H={H} job",
+        "fwd_bwd_ms": dt / frac * 1e3, "fwd_ms": dt_f / frac * 1e3,
+        "fwd_tokens_per_s": (B * T) * frac / dt_f,
     }
+
+
+def config1_bench(pkg, gpu_steps, with_cpu):
+    """the tiny RWKV-6 LM (2 layers, d_model 512, 8 heads, ffn 1792, vocab
+    65536, fp32 weights with RWKV-LM's decay ramp), batch 2 x 512 random token ids, one
+    forward + backward with next-token cross entropy (the last position masked).  GPU: the
+    package's model (fp32 parameters, bf16 activations).  CPU: the reference's forward restated
+    in torch fp32 with the C oracle's WKV (oracle/lm.py), 1 warm-up and the median of 3."""
+    import torch
+    import torch.nn.functional as F
+
+    M = pkg.modules
+    cfg = M.TransformerConfig(hidden_size=512, num_attention_heads=8, ffn_hidden_size=1792,
+                              num_layers=2, params_dtype=torch.float32, rwkv_lm_decay_init=True)
+    V, B, T = 65536, 2, 512
+    torch.manual_seed(0)
+    model = M.RWKV6Model(cfg, V, device="cuda:0")
+    g = torch.Generator().manual_seed(0)
+    tokens = torch.randint(0, V, (B, T), generator=g)
+    targets = torch.cat([tokens[:, 1:], torch.zeros(B, 1, dtype=tokens.dtype)], 1)
+    mask = torch.ones(B, T)
+    mask[:, -1] = 0
+    tok_d, tgt_d, mask_d = tokens.cuda(), targets.cuda().reshape(-1), mask.cuda().reshape(-1)
+
+    def gpu_step():
+        logits = model(tok_d)
+        losses = F.cross_entropy(logits.float().transpose(0, 1).reshape(-1, V), tgt_d, reduction="none")
+        loss = (losses * mask_d).sum() / mask_d.sum()
+        loss.backward()
+        model.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(3):
+        gpu_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(gpu_steps):
+        gpu_step()
+    e1.record()
+    torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1) / gpu_steps
+    out = {"workload": "BASELINE config 1: tiny RWKV-6 LM (2 layers, d_model 512, 8 heads, ffn 1792, "
+                       "vocab 65536, fp32 weights), batch 2 x 512, fwd+bwd with next-token CE",
+           "gpu_ms_per_step": gpu_ms, "gpu_tokens_per_s": B * T / (gpu_ms * 1e-3),
+           "gpu_steps": gpu_steps}
+    if with_cpu:
+        from oracle import lm
+
+        p = lm.params_from_state_dict(model.state_dict(), dtype=torch.float32)
+
+        def cpu_step():
+            loss = lm.lm_loss(lm.model_forward(p, tokens, cfg.num_layers, cfg.num_attention_heads,
+                                               cfg.layernorm_epsilon), targets, mask)
+            loss.backward()
+            for t in p.values():
+                t.grad = None
+
+        cpu_step()
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cpu_step()
+            runs.append(time.perf_counter() - t0)
+        dt = sorted(runs)[1]
+        out["cpu_baseline"] = {"value": B * T / dt, "unit": "tokens/s", "ms_per_step": dt * 1e3,
+                               "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": "the whole config-1 step (torch fp32 restatement of the "
+                                         "reference model, oracle/lm.py, with the C oracle's WKV), "
+                                         "median of 3 runs after 1 warm-up"}
+    del model
+    torch.cuda.empty_cache()
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "wkv6_bwd_chunk_grads_traffic.json")
@@ -366,8 +466,11 @@ def main():
         out["copy_calibration_bytes"] = 2 * n
     if not args.no_train:
         out["train_step"] = train_step_bench(pkg, args.train_steps, args.train_warmup)
+    if not args.no_extra_configs:
+        out["config1"] = config1_bench(pkg, max(5, args.steps // 2), not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, H, T, args.cpu_sample_heads)
+        out["cpu_host"] = cpu_info()
     print(json.dumps(out), flush=True)
 
 

@@ -57,6 +57,7 @@
 // (relative change of the state below that); its dw (d decay in the sequence-first entry) is
 // 0, the derivative of the floored forward, within e^-10 of the exact one.
 #define W_MIN (-10.0f)
+#define FLOOR_FF 21807.29f    // e^{-W_MIN - 0.01}: Fm Fk above it marks a floored token
 
 typedef uint16_t tile_t[CL][TS];
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -947,32 +948,257 @@ wkv6_bwd_dstate_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// phase C (backward): gradients of one chunk
+// backward: gradients of one chunk
 // ---------------------------------------------------------------------------
-// 8 waves: wave (W, h) owns tokens [16W, 16W+16) (as target for dr, as source for
-// dk and dv) and the 32 output columns 32h .. 32h+31.  With dA[t][tau] = dO_t . v_tau,
-// Fm = e^{G_{t-1} - mu}, Fk = e^{mu - G}, s = scale, S_in / S_out the states before /
-// after the chunk and dS the gradient of S_out:
+// 8 waves: wave (W, hh) owns tokens [16W, 16W+16) (the targets of dr, the sources of dk and
+// dv) and channels 32hh .. 32hh+31.  Lane (lq, lr) holds, for tp = 0, 1 and rr = 0..3, the
+// positions t = 16W + 4lq + rr, i = 32hh + 16tp + lr: the layout of an MFMA accumulator, so the
+// lane that builds an operand element is the lane that finishes that element's gradients.
+// G is the cumulative log2-decay, mu_W = G[16W+7], b_W = G[16W+15], Fm = e^{G_{t-1} - mu_W},
+// Fk = e^{mu_W - G_t}, s = scale, S_in / S_out the states before / after the chunk, dS the
+// gradient of S_out, dA[t][tau] = dO_t . v_tau, and Rm = r Fm, Km = k Fk the bf16 operands:
 //   dr = s Fm (e^{mu_W} dO S_in^T + sum_{J<W} p_WJ q_J dA Km + tril(dA) Km)        + s u k dd
 //   dk = Fk (e^{G_63-mu_W} v dS^T + s sum_{I>W} q_W p_IW dA^T Rm + s tril(dA)^T Rm) + s u r dd
-//   dv = (Km e^{G_63-mu_W}) dS + s sum_{I>=W} A_IW^T dO
-//   dw[t] = sum_{m>t} (Rm acc_r - Km acc_k)[m] - Km acc_k[t] + D,  D = rowsum(S_out * dS)
-// with D formed as e^{G_63} rowsum(S_in * dS) + sum_t Km (e^{G_63-mu_W} v dS^T)[t], the
-// exact split S_out = e^{G_63} S_in + S_loc written with the dk terms themselves,
-// where acc_r = dr_h / Fm and acc_k = dk_h / Fk are the bracketed accumulators and the
-// cross-block factors are split at the end b_J = G[16J+15] of the source block:
-// p_IJ = e^{mu_I - b_J} (table fp), q_J = e^{b_J - mu_J} (table kb), p_IJ q_J = e^{mu_I - mu_J},
-// applied one after the other to accumulators (dr, dk) or one to each operand (dv).
+//   dv = Kt dS + s sum_{I>=W} A_IW^T dO,   Kt = Km e^{G_63-mu_W}
+//   dw[t] = D + sum_{m>t} (Rm s acc_r - Km acc_k)[m] - (Km acc_k)[t]
+// with acc_r = dr_h / (s Fm), acc_k = dk_h / Fk the bracketed accumulators, cross-block factors
+// split at the end of the source block, p_IJ = e^{mu_I - b_J} (table fp), q_J = e^{b_J - mu_J}
+// (table kb), applied one after the other to the accumulators (dr, dk) or one to each operand
+// (dv), and D = rowsum(S_out * dS) = e^{G_63} rowsum(S_in * dS) + sum_t (Km acc_k^{inter})[t],
+// the exact split S_out = e^{G_63} S_in + S_loc written with the dk terms themselves.
+// dw is a suffix sum whose terms for pairs (m, tau) both after t cancel; they cancel exactly
+// because the epilogue multiplies the accumulators by the very bf16 Rm, Km the products used
+// (a rounding the epilogue did not see would survive in dw at the size of the cancelling terms).
+// Operand tiles Rm, Km, Kt and Kq = Km q_W are stored channel-major (X^T[i][t]): a lane writes
+// its 4 tokens of a channel with one 8-byte store and reads them back the same way.
 struct GradSmem {
-    tile_t Vm, Dm;                  // raw v, dO (adjacent: the fp32 y tile in the epilogue)
-    tile_t RmH, RmL, KmH, KmL;      // operand tiles (hi/lo); output staging in the epilogue
-    float A[CL][GS];                // G -> S_in | dS bf16 tiles -> the fp32 x tile
-    float emu[4][KD], eg[4][KD], fp[6][KD], kb[3][KD];
+    tile_t Vt, Dt;                  // raw v, dO (token-major); output staging at the end
+    tile_t RT, KT;                  // raw r, k (token-major), then Rm^T, Km^T (channel-major)
+    tile_t KtT, KqT;                // Kt^T, Kq^T (channel-major)
+    tile_t Sin, dS;                 // raw w in Sin first, then S_in, dS (bf16 [i][j])
+    float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD];
     float bonus[CL], Dv[KD];
-    float Pk[4][KD];                // per-wave sums of Km * (dk from dS), for dw
-    float red[8][KD];               // build_G scratch; dw block totals [0..3], du partials [4..7]
+    float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
+    float red[8][KD];               // block totals and mu of the decay scan, then dw block totals
+                                    // [0..3] and du partials [4..7]
 };
 static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit one CU's LDS");
+
+// Channel-major tile X^T (row = channel, stride TS): tokens t0 .. t0 + 3 of channel i in one
+// 8-byte access (t0 a multiple of 4).
+__device__ __forceinline__ bf16x4 ld_ch4(const uint16_t* XT, int i, int t0) {
+    return __builtin_bit_cast(bf16x4, *reinterpret_cast<const uint2*>(XT + i * TS + t0));
+}
+__device__ __forceinline__ void st_ch4(uint16_t* XT, int i, int t0, const float* f) {
+    *reinterpret_cast<uint2*>(XT + i * TS + t0) = make_uint2(pk2(f[0], f[1]), pk2(f[2], f[3]));
+}
+
+// What a lane carries from the operand build into the products, and what it hands on to the
+// cross-lane and cross-wave part of the epilogue.
+struct GradLane {
+    bf16x4 rrw[2], krw[2], rmb[2], kmb[2];   // raw r, k and the bf16 operands Rm, Km at its positions
+    float Fm[2][4], Fk[2][4], ulane[2];      // epilogue factors; s u of its two channels
+};
+struct GradOut {
+    bf16x4 drb[2], dkb[2];                   // dr, dk (bf16) at the lane's positions
+    float dwv[2][4];                         // dw less D and the later lanes / blocks
+    float lt[2];                             // the lane's sum of x = Rm s acc_r - Km acc_k
+    float dup[2];                            // du partial: sum over the lane's tokens of r k dd
+    unsigned floored;                        // head-first: bit 4tp + rr for a floored token
+    f32x4 av[2];                             // dv
+};
+
+// The products of token block W (wave-uniform, in a scalar register) for the two 16-channel
+// columns cb = 32hh + 16tp of the wave, with dr and dk finished as soon as their accumulators
+// are complete (their factors, raw r, k and dd are then dead while dv is formed).
+template <bool SEQ>
+__device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, float scale,
+                                               const GradLane& g, GradOut& out) {
+    const int TW = 16 * W;
+    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    const int rowW = TW + lr;
+    const uint16_t* Vp = &sm.Vt[0][0];
+    const uint16_t* Dp = &sm.Dt[0][0];
+    const uint16_t* RTp = &sm.RT[0][0];
+    const uint16_t* KTp = &sm.KT[0][0];
+    const int cbl[2] = {32 * hh + lr, 32 * hh + 16 + lr};      // the lane's channel of each tp
+    f32x4 ar[2], ak[2];
+    float ddv[4], xr[2][4];
+    // ---------------- dr (targets t in W) ----------------
+    {
+        f32x4 tmp[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_row8(Dp, rowW, 32 * ks);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&sm.Sin[0][0], cbl[tp], 32 * ks), tmp[tp]);
+        }
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) ar[tp] = tmp[tp] * sm.emu[W][cbl[tp]];
+    }
+    for (int J = 0; J < W; ++J) {          // dA[t = 16W+lr][tau = 16J+4lq+rr], then x Km_J
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+        const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) {
+            const f32x4 t2 = mfma16(aop, ld_ch4(KTp, cbl[tp], 16 * J + 4 * lq), f32x4{});
+            // the two halves of the cross factor one after the other (q_J p_WJ as one number can
+            // underflow where the product with t2 is O(1))
+            ar[tp] += (t2 * sm.kb[J][cbl[tp]]) * sm.fp[(W * (W - 1)) / 2 + J][cbl[tp]];
+        }
+    }
+    {   // diagonal block: strictly causal part; its diagonal dA[t][t] = dd[t]
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_row8(Vp, rowW, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+        // the lane's tokens 16W + 4lq + rr take dd from lane (lq, 4lq + rr), element rr
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) ddv[rr] = __shfl(at[rr], 20 * lq + rr);
+        float xa[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr < lr ? at[rr] : 0.f;
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) ar[tp] = mfma16(aop, ld_ch4(KTp, cbl[tp], TW + 4 * lq), ar[tp]);
+    }
+    // dr = s Fm acc_r + s u k dd;  Rm s acc_r, the first half of x
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+        float d[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float sar = scale * ar[tp][rr];
+            d[rr] = g.Fm[tp][rr] * sar + (g.ulane[tp] * ddv[rr]) * (float)g.krw[tp][rr];
+            xr[tp][rr] = (float)g.rmb[tp][rr] * sar;
+        }
+        out.drb[tp] = cvt4(d[0], d[1], d[2], d[3]);
+    }
+    // ---------------- dk (sources tau in W) ----------------
+    {
+        f32x4 tmp[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_row8(Vp, rowW, 32 * ks);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&sm.dS[0][0], cbl[tp], 32 * ks), tmp[tp]);
+        }
+        float pk[2];
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) {
+            ak[tp] = tmp[tp] * sm.eg[W][cbl[tp]];
+            // this wave's share of sum_tau Km acc_k^{inter}[tau] (the dk terms of D)
+            pk[tp] = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) pk[tp] += (float)g.kmb[tp][rr] * ak[tp][rr];
+        }
+        // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
+        const bool up = lane & 16;
+        float p = (up ? pk[1] : pk[0]) + lane_xor_swz<16>(up ? pk[0] : pk[1]);
+        p += lane_xor32(p);
+        if (lq < 2) sm.Pk[W][32 * hh + 16 * lq + lr] = p;
+    }
+    {   // diagonal block: dA[t = 16W+4lq+rr][tau = 16W+lr], t > tau
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_row8(Dp, rowW, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+        float xa[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr > lr ? at[rr] * scale : 0.f;
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) ak[tp] = mfma16(aop, ld_ch4(RTp, cbl[tp], TW + 4 * lq), ak[tp]);
+    }
+    {
+        for (int I = W + 1; I < 4; ++I) {  // dA[t = 16I+4lq+rr][tau = 16W+lr], then x Rm_I
+            f32x4 at = {};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+            const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp) {
+                const f32x4 t2 = mfma16(aop, ld_ch4(RTp, cbl[tp], 16 * I + 4 * lq), f32x4{});
+                ak[tp] += (t2 * sm.fp[(I * (I - 1)) / 2 + W][cbl[tp]]) * sm.kb[W][cbl[tp]];
+            }
+        }
+    }
+    // dk = Fk acc_k + s u r dd;  x = Rm s acc_r - Km acc_k, y = -Km acc_k, summed within the
+    // lane over the later tokens; du partial r k dd
+    out.floored = 0u;
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+        float d[4], xv[4];
+        out.dup[tp] = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float rv = (float)g.rrw[tp][rr], kv = (float)g.krw[tp][rr];
+            d[rr] = g.Fk[tp][rr] * ak[tp][rr] + (g.ulane[tp] * ddv[rr]) * rv;
+            out.dup[tp] += (rv * kv) * ddv[rr];
+            const float y = -(float)g.kmb[tp][rr] * ak[tp][rr];
+            xv[rr] = xr[tp][rr] + y;
+            out.dwv[tp][rr] = y;
+            // head-first: Fm Fk = e^{G_{t-1} - G_t} = e^{-max(w_t, W_MIN)} is e^{-W_MIN} exactly
+            // at the floor; the test also takes tokens within 1 % of the floor's decay factor
+            // (w in [W_MIN, W_MIN + 0.01)), whose exact dw carries a factor below 4.6e-5 too
+            if (!SEQ && g.Fm[tp][rr] * g.Fk[tp][rr] > FLOOR_FF) out.floored |= 1u << (4 * tp + rr);
+        }
+        out.dkb[tp] = cvt4(d[0], d[1], d[2], d[3]);
+        out.dwv[tp][2] += xv[3];
+        out.dwv[tp][1] += xv[3] + xv[2];
+        out.dwv[tp][0] += (xv[3] + xv[2]) + xv[1];
+        out.lt[tp] = ((xv[3] + xv[2]) + xv[1]) + xv[0];
+    }
+    // ---------------- dv (sources tau in W, value columns 32hh..) ----------------
+    f32x4 av[2] = {};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const bf16x8 a = ld_tr8(&sm.KtT[0][0], 32 * ks, TW);           // Kt[tau = 16W+lr][i]
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+            av[tp] = mfma32(a, ld_tr8(&sm.dS[0][0], 32 * ks, 32 * hh + 16 * tp), av[tp]);
+    }
+    {   // diagonal block: A[t = 16W+4lq+rr][tau = 16W+lr], t > tau, the u-bonus at t == tau
+        f32x4 at = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_tr8_g8(RTp, 32 * ks, TW), ld_tr8_g8(KTp, 32 * ks, TW), at);
+        const float bon = sm.bonus[rowW];
+        float xa[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int tl = 4 * lq + rr;
+            xa[rr] = (tl > lr ? at[rr] : (tl == lr ? bon : 0.f)) * scale;
+        }
+        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, TW, 32 * hh + 16 * tp), av[tp]);
+    }
+    {
+        for (int I = W + 1; I < 4; ++I) {  // A[t = 16I+4lq+rr][tau = 16W+lr] = (Rm_I p_IW) Kq_W
+            f32x4 at = {};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                float f[8];
+                row8_vec(sm.fp[(I * (I - 1)) / 2 + W], 32 * ks, f);
+                at = mfma32(scale8(ld_tr8_g8(RTp, 32 * ks, 16 * I), f),
+                            ld_tr8_g8(&sm.KqT[0][0], 32 * ks, TW), at);    // Kq[tau = 16W+lr][i]
+            }
+            const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 32 * hh + 16 * tp), av[tp]);
+        }
+    }
+    out.av[0] = av[0];
+    out.av[1] = av[1];
+}
 
 // SEQ: r, k, v, the pre-activation decay and dr, dk, dv, d_decay are sequence-first (dO is
 // head-first); the decay gradient is dw * w with w = -exp(decay).
@@ -987,383 +1213,223 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
                      float* __restrict__ du_part, float scale, int B, int H, int T, int NT) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     GradSmem& sm = *reinterpret_cast<GradSmem*>(smem_raw);
-    uint16_t (*Sin)[TS] = reinterpret_cast<uint16_t (*)[TS]>(&sm.A[0][0]);
-    uint16_t (*dSm)[TS] = Sin + CL;
-    float (*Gv)[GSG] = reinterpret_cast<float (*)[GSG]>(&sm.A[0][0]);   // G view of the same region
     const int c = blockIdx.x, bh = blockIdx.y, h = bh % H;
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
     const size_t dbase = ((size_t)bh * T + t0) * KD;           // dO: head-first
-    const size_t st_in = ((size_t)bh * (NT + 1) + c) * KD * KD;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
 
-    // ---- prologue: one 16-byte piece of every tile per thread, all seven loads in flight
-    // together (branch-free loads: a load under a branch makes the merge wait for it) ----
-    const uint4 rq = gload16c(r + base, row, c8, nvalid, rs), kq = gload16c(k + base, row, c8, nvalid, rs);
-    const uint4 vq = gload16c(v + base, row, c8, nvalid, rs), dq = gload16c(dO + dbase, row, c8, nvalid, KD);
-    const uint4 wq = gload16c(w + base, row, c8, nvalid, rs);
-    // states: S_in and dS rows (thread row = channel i), kept in registers until G is consumed
-    const uint4 sq = *reinterpret_cast<const uint4*>(Hs + st_in + row * KD + c8);
+    // ---- P0: one 16-byte piece of every tile per thread, all loads in flight together (rows
+    // past a ragged end read the last token and are zeroed below) ----
+    const int lrow = min(row, nvalid - 1);
+    uint4 rq = *reinterpret_cast<const uint4*>(r + base + (size_t)lrow * rs + c8);
+    uint4 kq = *reinterpret_cast<const uint4*>(k + base + (size_t)lrow * rs + c8);
+    uint4 vq = *reinterpret_cast<const uint4*>(v + base + (size_t)lrow * rs + c8);
+    uint4 wq = *reinterpret_cast<const uint4*>(w + base + (size_t)lrow * rs + c8);
+    uint4 dq = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)lrow * KD + c8);
+    // states: S_in and dS rows (thread row = channel i), into LDS once the w scratch is consumed
+    const uint4 sq = *reinterpret_cast<const uint4*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8);
     const uint4 dsq = *reinterpret_cast<const uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + row * KD + c8);
+    float uf[8];
+    load_param8(u, u_dtype, h * KD + c8, uf);
+    if (nvalid < CL) {
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        if (row >= nvalid) rq = kq = vq = wq = dq = z;
+    }
+    sstore16(sm.Vt, row, c8, vq);
+    sstore16(sm.Dt, row, c8, dq);
+    sstore16(sm.RT, row, c8, rq);
+    sstore16(sm.KT, row, c8, kq);
+    sstore16(sm.Sin, row, c8, wq);                       // w scratch until the scan has read it
     {
-        sstore16(sm.Vm, row, c8, vq);
-        sstore16(sm.Dm, row, c8, dq);
-        sstore16(sm.RmL, row, c8, wq);                   // w scratch
-        sstore16(sm.RmH, row, c8, rq);                   // raw r, k: read back below in the
-        sstore16(sm.KmH, row, c8, kq);                   // lane layout of the accumulators
-        float rf[8], kf[8], uf[8], b = 0.f;
+        // bonus[t] = sum_i r u k (token t = row);  Dv[i] = sum_j S_in dS (channel i = row)
+        float rf[8], kf[8], a8[8], b8[8], b = 0.f, d = 0.f;
         unpack8(rq, rf);
         unpack8(kq, kf);
-        load_param8(u, u_dtype, h * KD + c8, uf);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) b += rf[s] * uf[s] * kf[s];
-        b = sum8lanes(b);
-        if ((threadIdx.x & 7) == 0) sm.bonus[row] = b;
-    }
-    // Dv[i] = sum_j S_in[i][j] dS[i][j] (scaled by e^{G_63} once G is built)
-    {
-        float a8[8], b8[8], d = 0.f;
         unpack8(sq, a8);
         unpack8(dsq, b8);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) d += a8[s] * b8[s];
+        for (int s = 0; s < 8; ++s) {
+            b += (rf[s] * uf[s]) * kf[s];
+            d += a8[s] * b8[s];
+        }
+        b = sum8lanes(b);
         d = sum8lanes(d);
-        if ((threadIdx.x & 7) == 0) sm.Dv[row] = d;
+        if ((threadIdx.x & 7) == 0) {
+            sm.bonus[row] = b;
+            sm.Dv[row] = d;
+        }
     }
+    __syncthreads();
+
+    // ---- P1: raw r, k, w at the lane's positions; the decay scan in registers; Fm, Fk; Rm, Km ----
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
-    __syncthreads();
-    // raw r, k (and for SEQ the pre-activation decay) at this lane's accumulator positions
-    // (tokens 16W+4lq+rr, channel 32hh+16tp+lr), read before build_G's barriers (after them
-    // the operand tiles overwrite RmH, KmH and the w scratch in RmL); u of its two channels
-    bf16x4 rrw[2], krw[2], wrw[2];
-    float ulane[2];
-    unsigned floored = 0;                  // head-first: bit 4tp + rr set if w < W_MIN there
+    const int t4 = 16 * W + 4 * lq;                       // the lane's first token
+    GradLane gl;
+    bf16x4 wrw[2];
+    float kmf[2][4], qloc[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
-        rrw[tp] = ld_tr4(&sm.RmH[0][0], 16 * W, 16 * (2 * hh + tp));
-        krw[tp] = ld_tr4(&sm.KmH[0][0], 16 * W, 16 * (2 * hh + tp));
-        wrw[tp] = ld_tr4(&sm.RmL[0][0], 16 * W, 16 * (2 * hh + tp));
-        if (!SEQ) {
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                floored |= (float)wrw[tp][rr] < W_MIN ? 1u << (4 * tp + rr) : 0u;
-        }
-        ulane[tp] = scale * load_u(u, u_dtype, h * KD + 16 * (2 * hh + tp) + lr);
-    }
-    build_G<NTHR_G, SEQ>(sm.RmL, Gv, &sm.red[0][0], nvalid);
-    {
-        float rf[8], kf[8];
-        unpack8(rq, rf);
-        unpack8(kq, kf);
-        // tables
-        const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-        if (part < 4) {
-            const float m = Gv[16 * part + 7][i];
-            sm.emu[part][i] = ex2(m);
-            sm.eg[part][i] = ex2(Gv[CL - 1][i] - m);
-            if (part == 0) sm.Dv[i] *= ex2(Gv[CL - 1][i]);
-            if (part < 3) sm.kb[part][i] = ex2(Gv[16 * part + 15][i] - m);
-        } else {
-            for (int pi = part - 4; pi < 6; pi += 4) {
-                const int I = pi < 1 ? 1 : (pi < 3 ? 2 : 3), J = pi - pair_index(I, 0);
-                sm.fp[pi][i] = ex2(Gv[16 * I + 7][i] - Gv[16 * J + 15][i]);
-            }
-        }
-        // operand tiles Rm, Km (hi/lo); the w scratch in RmL was consumed by build_G
-        const int mrow = 16 * (row >> 4) + 7;
-        float a[8], b[8], gm[8], gg[8], gp[8];
-        g8(Gv, mrow, c8, gm);
-        g8(Gv, row, c8, gg);
-        g8m1(Gv, row, c8, gp);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            a[s] = rf[s] * ex2(gp[s] - gm[s]);
-            b[s] = kf[s] * ex2(gm[s] - gg[s]);
-        }
-        uint4 hi, lo;
-        pack8_split(a, hi, lo);
-        sstore16(sm.RmH, row, c8, hi);
-        sstore16(sm.RmL, row, c8, lo);
-        pack8_split(b, hi, lo);
-        sstore16(sm.KmH, row, c8, hi);
-        sstore16(sm.KmL, row, c8, lo);
-    }
-    // epilogue factors at this lane's accumulator positions (token 16W+4lq+rr, channel cb+lr)
-    float Fm[2][4], Fk[2][4];
-#pragma unroll
-    for (int tp = 0; tp < 2; ++tp) {
-        const int i = 16 * (2 * hh + tp) + lr;
-        const float m = Gv[16 * W + 7][i];
+        const int cb = 32 * hh + 16 * tp;
+        gl.rrw[tp] = ld_tr4(&sm.RT[0][0], 16 * W, cb);      // x[16W + 4lq + s][cb + lr]
+        gl.krw[tp] = ld_tr4(&sm.KT[0][0], 16 * W, cb);
+        wrw[tp] = ld_tr4(&sm.Sin[0][0], 16 * W, cb);
+        gl.ulane[tp] = scale * load_u(u, u_dtype, h * KD + cb + lr);
+        // cumulative log2-decay within the block: the lane's 4 tokens, then the lanes before
+        // it in the block (lanes lr + 16 lq' of the same wave)
+        float cs[4], run = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const int tt = 16 * W + 4 * lq + rr;
-            Fm[tp][rr] = ex2((tt > 0 ? Gv[tt - 1][i] : 0.f) - m);
-            Fk[tp][rr] = ex2(m - Gv[tt][i]);
+            float x = (float)wrw[tp][rr];
+            if (SEQ) x = t4 + rr < nvalid ? -ex2(x * RW_L2E) : 0.f;   // w = -exp(decay), :336
+            run += fmaxf(x, W_MIN) * RW_L2E;
+            cs[rr] = run;
+        }
+        float xi = run, y = __shfl_up(xi, 16);
+        xi += lq >= 1 ? y : 0.f;
+        y = __shfl_up(xi, 32);
+        xi += lq >= 2 ? y : 0.f;                            // inclusive over lq
+        const float excl = xi - run;
+        const float tot = __shfl(xi, 48 + lr);              // the block's total
+        const float m7 = __shfl(excl + cs[3], 16 + lr);     // G at token 16W+7 (lane lq = 1, rr = 3)
+        qloc[tp] = tot - m7;                                // b_W - mu_W
+        if (lq == 0) {
+            sm.red[W][cb + lr] = tot;
+            sm.red[4 + W][cb + lr] = m7;
+        }
+        float rm[4], km[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            gl.Fm[tp][rr] = ex2(excl + (rr ? cs[rr - 1] : 0.f) - m7);
+            gl.Fk[tp][rr] = ex2(m7 - (excl + cs[rr]));
+            rm[rr] = (float)gl.rrw[tp][rr] * gl.Fm[tp][rr];
+            km[rr] = (float)gl.krw[tp][rr] * gl.Fk[tp][rr];
+            kmf[tp][rr] = km[rr];
+        }
+        gl.rmb[tp] = cvt4(rm[0], rm[1], rm[2], rm[3]);
+        gl.kmb[tp] = cvt4(km[0], km[1], km[2], km[3]);
+    }
+    __syncthreads();                       // raw r, k, w read; block totals and mu in `red`
+
+    // ---- P2: operand tiles (channel-major), S_in / dS, the per-block factor tables ----
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {
+        const int i = 32 * hh + 16 * tp + lr;
+        *reinterpret_cast<bf16x4*>(&sm.RT[i][t4]) = gl.rmb[tp];
+        *reinterpret_cast<bf16x4*>(&sm.KT[i][t4]) = gl.kmb[tp];
+        float after = 0.f;                                  // G_63 - b_W
+        for (int J = W + 1; J < 4; ++J) after += sm.red[J][i];
+        const float eg = ex2(after + qloc[tp]), kq = ex2(qloc[tp]);
+        float x[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[tp][rr] * eg;
+        st_ch4(&sm.KtT[0][0], i, t4, x);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[tp][rr] * kq;
+        st_ch4(&sm.KqT[0][0], i, t4, x);
+    }
+    sstore16(sm.Sin, row, c8, sq);
+    sstore16(sm.dS, row, c8, dsq);
+    {
+        // tables per channel i = lane from the block totals and mu: b_J = G[16J+15],
+        // mu_J = b_{J-1} + m7_J; wave wv fills its share (the branches are wave-uniform)
+        const int i = lane;
+        float bnd[4], mu[4], a = 0.f;
+#pragma unroll
+        for (int J = 0; J < 4; ++J) {
+            mu[J] = a + sm.red[4 + J][i];
+            a += sm.red[J][i];
+            bnd[J] = a;
+        }
+        if (wv < 4) {
+            const float m = wv == 0 ? mu[0] : wv == 1 ? mu[1] : wv == 2 ? mu[2] : mu[3];
+            sm.emu[wv][i] = ex2(m);
+            sm.eg[wv][i] = ex2(bnd[3] - m);
+            if (wv < 3) sm.kb[wv][i] = ex2((wv == 0 ? bnd[0] : wv == 1 ? bnd[1] : bnd[2]) - m);
+            else sm.Dv[i] *= ex2(bnd[3]);
+        } else if (wv == 4) {
+            sm.fp[0][i] = ex2(mu[1] - bnd[0]);              // (1, 0)
+            sm.fp[1][i] = ex2(mu[2] - bnd[0]);              // (2, 0)
+        } else if (wv == 5) {
+            sm.fp[2][i] = ex2(mu[2] - bnd[1]);              // (2, 1)
+            sm.fp[3][i] = ex2(mu[3] - bnd[0]);              // (3, 0)
+        } else if (wv == 6) {
+            sm.fp[4][i] = ex2(mu[3] - bnd[1]);              // (3, 1)
+            sm.fp[5][i] = ex2(mu[3] - bnd[2]);              // (3, 2)
         }
     }
-    __syncthreads();                       // G fully consumed
-    sstore16(Sin, row, c8, sq);
-    sstore16(dSm, row, c8, dsq);
     __syncthreads();
 
-    const uint16_t* Vp = &sm.Vm[0][0];
-    const uint16_t* Dp = &sm.Dm[0][0];
-    const uint16_t* RH = &sm.RmH[0][0];
-    const uint16_t* RL = &sm.RmL[0][0];
-    const uint16_t* KH = &sm.KmH[0][0];
-    const uint16_t* KL = &sm.KmL[0][0];
-    const int rowW = 16 * W + lr;
-    f32x4 ar[2], ak[2], av[2] = {};
-    // ---------------- dr (target rows in W, channels 32hh..) ----------------
-    {
-        f32x4 tmp[2] = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_row8(Dp, rowW, 32 * ks);
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                tmp[tp] = mfma32(a, ld_row8(&Sin[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
-        }
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) ar[tp] = tmp[tp] * sm.emu[W][16 * (2 * hh + tp) + lr];
-    }
-    for (int J = 0; J < W; ++J) {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
-        const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);   // dA[t = 16W+lr][tau = 16J+4lq+rr]
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-            const int cb = 16 * (2 * hh + tp);
-            f32x4 tmp = {};
-            tmp = mfma16(aop, ld_tr4(KH, 16 * J, cb), tmp);
-            tmp = mfma16(aop, ld_tr4(KL, 16 * J, cb), tmp);
-            // the two halves of the cross factor one after the other (q_J p_WJ as one
-            // number can underflow where the product with tmp is O(1))
-            ar[tp] += (tmp * sm.kb[J][cb + lr]) * sm.fp[pair_index(W, J)][cb + lr];
-        }
-    }
-    // diagonal block J = W; its diagonal dA[t][t] = dO_t . v_t = dd[t].  Lane (lq, lr) takes
-    // dd of its epilogue tokens 16W + 4lq + rr from lane (lq, 4lq + rr), element rr.
-    float ddv[4];
-    {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Vp, 16 * W + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) ddv[rr] = __shfl(at[rr], 20 * lq + rr);
-        float xa[4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr >= lr ? 0.f : at[rr];
-        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-            const int cb = 16 * (2 * hh + tp);
-            f32x4 tmp = {};
-            tmp = mfma16(aop, ld_tr4(KH, 16 * W, cb), tmp);
-            tmp = mfma16(aop, ld_tr4(KL, 16 * W, cb), tmp);
-            ar[tp] += tmp;
-        }
-    }
-    // ---------------- dk (source rows in W) ----------------
-    {
-        f32x4 tmp[2] = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_row8(Vp, rowW, 32 * ks);
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                tmp[tp] = mfma32(a, ld_row8(&dSm[0][0], 16 * (2 * hh + tp) + lr, 32 * ks), tmp[tp]);
-        }
-        float pk[2];
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-            const int cb = 16 * (2 * hh + tp);
-            ak[tp] = tmp[tp] * sm.eg[W][cb + lr];
-            // this wave's share of sum_t k Fk ak[t][i] = rowsum((S_out - e^{G_63} S_in) dS),
-            // formed from the same products the epilogue's y terms take off again
-            pk[tp] = 0.f;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) pk[tp] += (float)krw[tp][rr] * (Fk[tp][rr] * ak[tp][rr]);
-        }
-        // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
-        const bool up = lane & 16;
-        float p = (up ? pk[1] : pk[0]) + lane_xor_swz<16>(up ? pk[0] : pk[1]);
-        p += lane_xor32(p);
-        if (lq < 2) sm.Pk[W][16 * (2 * hh + lq) + lr] = p;
-    }
-    // diagonal block I = W first, then the target blocks I > W
-    {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * W + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
-        float xa[4];                                     // dA[t = 16W+4lq+rr][tau = 16W+lr]
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr <= lr ? 0.f : at[rr] * scale;
-        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-            const int cb = 16 * (2 * hh + tp);
-            f32x4 tmp = {};
-            tmp = mfma16(aop, ld_tr4(RH, 16 * W, cb), tmp);
-            tmp = mfma16(aop, ld_tr4(RL, 16 * W, cb), tmp);
-            ak[tp] += tmp;
-        }
-    }
-    for (int I = W + 1; I < 4; ++I) {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
-        const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
-            const int cb = 16 * (2 * hh + tp);
-            f32x4 tmp = {};
-            tmp = mfma16(aop, ld_tr4(RH, 16 * I, cb), tmp);
-            tmp = mfma16(aop, ld_tr4(RL, 16 * I, cb), tmp);
-            ak[tp] += (tmp * sm.fp[pair_index(I, W)][cb + lr]) * sm.kb[W][cb + lr];
-        }
-    }
-    // ---------------- dv (source rows in W, value columns 32hh..) ----------------
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        float f[8];
-        dir8_vec(sm.eg[W], 32 * ks, f);
-        const bf16x8 a = scale8(ld_dir8(KH, rowW, 32 * ks), f);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma32(a, ld_tr8(&dSm[0][0], 32 * ks, 16 * (2 * hh + tp)), av[tp]);
-    }
-    // Km_W q_W, the source operand of every off-diagonal pair (I, W)
-    bf16x8 kqw[2];
-    if (W < 3) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            float f[8];
-            row8_vec(sm.kb[W], 32 * ks, f);
-            kqw[ks] = scale8(ld_row8(KH, rowW, 32 * ks), f);
-        }
-    }
-    // diagonal block I = W (the bonus on the diagonal), then the target blocks I > W
-    {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_row8(RH, 16 * W + lr, 32 * ks), ld_row8(KH, rowW, 32 * ks), at);   // A[16W+4lq+rr][16W+lr]
-        const float bon = sm.bonus[rowW];
-        float xa[4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int tl = 4 * lq + rr;
-            xa[rr] = (tl > lr ? at[rr] : (tl == lr ? bon : 0.f)) * scale;
-        }
-        const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * W, 16 * (2 * hh + tp)), av[tp]);
-    }
-    for (int I = W + 1; I < 4; ++I) {
-        f32x4 at = {};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            float f[8];
-            row8_vec(sm.fp[pair_index(I, W)], 32 * ks, f);
-            at = mfma32(scale8(ld_row8(RH, 16 * I + lr, 32 * ks), f), kqw[ks], at);   // A[16I+4lq+rr][16W+lr]
-        }
-        const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 16 * (2 * hh + tp)), av[tp]);
-    }
+    // ---- P3: the products, dr and dk finished on the way ----
+    GradOut go;
+    grads_products<SEQ>(sm, __builtin_amdgcn_readfirstlane(W), hh, scale, gl, go);
 
     // ---------------- epilogue ----------------
-    // dr, dk, dv, dw at this lane's accumulator positions (tokens 16W + 4lq + rr, channel
-    // i = 32hh + 16tp + lr).  dw[t] = D + sum_{m > t} x[m] + y[t] with x = r dr_h - k dk_h,
-    // y = -k dk_h: the suffix sums over the tokens run within the lane (4 tokens), across the
-    // four lane rows (shuffles) and across the token blocks W (per-wave totals in `red`).
-    float drv[2][4], dkv[2][4], dwv[2][4], wtot[2], dup[2];
+    // dw[t] = D + sum_{m > t} x[m] + y[t]: the suffix sums within the lane are in go.dwv; here
+    // across the four lane rows (shuffles) and across the token blocks W (per-wave totals in
+    // `red`).
+    float wtot[2];
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
-        const float ui = ulane[tp];
-        float xv[4];
-        dup[tp] = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const float rv = (float)rrw[tp][rr], kv = (float)krw[tp][rr];
-            const float drh = Fm[tp][rr] * (scale * ar[tp][rr]);   // r Fm acc_r = Rm acc_r
-            const float dkh = Fk[tp][rr] * ak[tp][rr];             // k Fk acc_k = Km acc_k
-            const float udd = ui * ddv[rr];
-            dup[tp] += (rv * kv) * ddv[rr];                         // du partial: r k dd
-            drv[tp][rr] = drh + udd * kv;
-            dkv[tp][rr] = dkh + udd * rv;
-            xv[rr] = rv * drh - kv * dkh;
-            dwv[tp][rr] = -kv * dkh;                                // y
-        }
-        // within the lane: sum over the later tokens rr' > rr
-        dwv[tp][2] += xv[3];
-        dwv[tp][1] += xv[3] + xv[2];
-        dwv[tp][0] += (xv[3] + xv[2]) + xv[1];
-        const float lt = ((xv[3] + xv[2]) + xv[1]) + xv[0];
-        // across lane rows: sum over lq' > lq (lanes lr + 16 lq').  The shuffles run on all
-        // lanes (a lane outside the exec mask would read as zero).
+        // sum over lq' > lq (lanes lr + 16 lq').  The shuffles run on all lanes (a lane outside
+        // the exec mask would read as zero).
+        const float lt = go.lt[tp];
         const float d16 = __shfl_down(lt, 16);
-        float v = lt + (lq <= 2 ? d16 : 0.f);
-        const float d32 = __shfl_down(v, 32);
-        v += lq <= 1 ? d32 : 0.f;                                   // sum over lq' >= lq
-        const float later = v - lt;
+        float vsum = lt + (lq <= 2 ? d16 : 0.f);
+        const float d32 = __shfl_down(vsum, 32);
+        vsum += lq <= 1 ? d32 : 0.f;                                // sum over lq' >= lq
+        const float later = vsum - lt;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) dwv[tp][rr] += later;
-        wtot[tp] = v;                                               // the wave's total at lq == 0
+        for (int rr = 0; rr < 4; ++rr) go.dwv[tp][rr] += later;
+        wtot[tp] = vsum;                                            // the wave's total at lq == 0
     }
     // du partial over the wave's 16 tokens: sum over lq (lanes of odd lq keep tp = 1, even
     // lq tp = 0, as for Pk), then over the four token blocks in fixed order below
     {
         const bool up = lane & 16;
-        float p = (up ? dup[1] : dup[0]) + lane_xor_swz<16>(up ? dup[0] : dup[1]);
+        float p = (up ? go.dup[1] : go.dup[0]) + lane_xor_swz<16>(up ? go.dup[0] : go.dup[1]);
         p += lane_xor32(p);
-        if (lq < 2) sm.red[4 + W][16 * (2 * hh + lq) + lr] = p;
+        if (lq < 2) sm.red[4 + W][32 * hh + 16 * lq + lr] = p;
     }
-    // red[0..3] (the build_G scratch before the products) takes the dw block totals
     if (lq == 0) {
         sm.red[W][32 * hh + lr] = wtot[0];
         sm.red[W][32 * hh + 16 + lr] = wtot[1];
     }
-    __syncthreads();                       // all waves are done with the operand tiles; red is in
+    __syncthreads();                       // all products done; red, Pk in
     if (threadIdx.x < KD) {
         const float acc = (sm.red[4][threadIdx.x] + sm.red[5][threadIdx.x]) +
                           (sm.red[6][threadIdx.x] + sm.red[7][threadIdx.x]);
         // head-major [h][b][c][i]: each head's partials are contiguous for the du reduction
         du_part[(((size_t)h * B + bh / H) * NT + c) * KD + threadIdx.x] = scale * acc;
     }
-    // dr, dk, dv, dw staged channel-major (XT[i][t], 8-byte writes of 4 tokens) in the operand
-    // tiles, read back token-major by transpose reads for 16-byte stores
-    uint16_t (*Ts[4])[TS] = {sm.RmH, sm.RmL, sm.KmH, sm.KmL};
+    // dr, dk, dv, dw staged channel-major (X^T[i][t], 8-byte writes of 4 tokens) in tiles the
+    // products no longer read, read back token-major by transpose reads for 16-byte stores
+    uint16_t (*Ts[4])[TS] = {sm.Vt, sm.Dt, sm.RT, sm.KT};
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp) {
-        const int i = 16 * (2 * hh + tp) + lr;
-        // D = rowsum(S_out dS) = e^{G_63} rowsum(S_in dS) + sum_t Km ak(dS part): the second
-        // sum is the one the suffix sums of Km ak take off again, so dw keeps no rounding of a
-        // large D (bf16 S_out) that cancels; what remains scales with e^{G_63}.
+        const int i = 32 * hh + 16 * tp + lr;
         float later = sm.Dv[i] + ((sm.Pk[0][i] + sm.Pk[1][i]) + (sm.Pk[2][i] + sm.Pk[3][i]));
         for (int W2 = W + 1; W2 < 4; ++W2) later += sm.red[W2][i];
         float g[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const int tt = 16 * W + 4 * lq + rr;
-            g[rr] = dwv[tp][rr] + later;
+            g[rr] = go.dwv[tp][rr] + later;
             // A floored token's gradient is 0: the derivative of the floored forward, within
             // e^W_MIN of the exact one (which carries the token's own decay factor).  The
             // sequence-first entry returns d decay = dw * w, w = -exp(decay).
-            if (SEQ && tt < nvalid) {
+            if (SEQ && t4 + rr < nvalid) {
                 const float wn = -ex2((float)wrw[tp][rr] * RW_L2E);
                 g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
             }
-            if (!SEQ && ((floored >> (4 * tp + rr)) & 1u)) g[rr] = 0.f;
+            if (!SEQ && ((go.floored >> (4 * tp + rr)) & 1u)) g[rr] = 0.f;
         }
-        const int t4 = 16 * W + 4 * lq;
-        *reinterpret_cast<uint2*>(&Ts[0][i][t4]) = make_uint2(pk2(drv[tp][0], drv[tp][1]), pk2(drv[tp][2], drv[tp][3]));
-        *reinterpret_cast<uint2*>(&Ts[1][i][t4]) = make_uint2(pk2(dkv[tp][0], dkv[tp][1]), pk2(dkv[tp][2], dkv[tp][3]));
-        *reinterpret_cast<uint2*>(&Ts[2][i][t4]) = make_uint2(pk2(av[tp][0], av[tp][1]), pk2(av[tp][2], av[tp][3]));
-        *reinterpret_cast<uint2*>(&Ts[3][i][t4]) = make_uint2(pk2(g[0], g[1]), pk2(g[2], g[3]));
+        *reinterpret_cast<bf16x4*>(&Ts[0][i][t4]) = go.drb[tp];
+        *reinterpret_cast<bf16x4*>(&Ts[1][i][t4]) = go.dkb[tp];
+        const float avf[4] = {go.av[tp][0], go.av[tp][1], go.av[tp][2], go.av[tp][3]};
+        st_ch4(&Ts[2][0][0], i, t4, avf);
+        st_ch4(&Ts[3][0][0], i, t4, g);
     }
     __syncthreads();
     {
