@@ -10,8 +10,9 @@ the C ABI, inputs already resident in HBM.  value = tokens (B*T) per second.
 Also reported:
   * per-phase kernel times, measured live with HIP events recorded by the
     library on the stream the kernels run on (rwkv6_wkv_*_ex);
-  * roofline of the dominant kernel (HBM-bound): algorithmic bytes per launch
-    (reads r,k,v,w,dO + writes dr,dk,dv,dw = 1152 B per token-head) over its
+  * roofline of the dominant kernel (the backward's gradient kernel, HBM-bound):
+    algorithmic bytes per launch (reads r,k,v,w,dO + writes dr,dk,dv,dw = 1152 B per
+    token-head) over its
     average event-timed duration, against 8 TB/s;
   * TFLOP/s of the whole op (fwd 32768 + bwd 65536 FLOP per token-head) and the
     fraction of the 2.5 PFLOP/s dense bf16 MFMA peak;
@@ -204,14 +205,27 @@ def config1_bench(pkg, gpu_steps, with_cpu):
     return out
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "wkv6_bwd_chunk_grads_traffic.json")
+def bwd_loop(BH, T):
+    """Whether the library's backward runs as one reverse walk per (b,h) (wkv6_bwd_loop): the
+    rule of walk_segments() in csrc/wkv6.hip with a 256-workgroup target."""
+    NT = -(-T // 64)
+    if NT <= 0:
+        return True
+    P = min(-(-256 // BH), max(1, NT // 8))
+    NC = -(-NT // P)
+    return -(-NT // NC) == 1
+
+
+def bwd_kernel(BH, T):
+    return "wkv6_bwd_loop" if bwd_loop(BH, T) else "wkv6_bwd_chunk_grads"
 
 
 def measured_traffic(B, H, T):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter runs
     (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter on a copy of known size)."""
+    path = os.path.join(ROOT, "profiles", bwd_kernel(B * H, T) + "_traffic.json")
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             d = json.load(f)
     except (OSError, ValueError):
         return None
@@ -223,8 +237,9 @@ def measured_traffic(B, H, T):
 def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
     """WKV6 fwd+bwd through the C ABI (the _ex entries) on synthetic inputs resident in HBM.
     with_state: h0 ~ N(0, 0.5^2), dhT ~ N(0,1), dh0 returned (config 5).
-    The timed region (ms_per_step) records HIP events only around the gradient kernel, the
-    roofline kernel, whose live average becomes bwd_phases[2]; a second loop of the same
+    The timed region (ms_per_step) records HIP events only around the gradient kernel (the
+    reverse walk or the chunk gradients), the roofline kernel, whose live average becomes
+    bwd_phases[2]; a second loop of the same
     length records an event around every phase for the rest of the breakdown (each event in
     the stream adds a few microseconds of gap, so they stay out of the timed region).
     Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases)."""
@@ -437,9 +452,11 @@ def main():
         "wkv6_pct_bf16_mfma_peak": 100.0 * tflops / BF16_PEAK_TFLOPS,
         "wkv6_alg_hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "phase_ms": {"fwd_segment_states": fwd_ph[0], "fwd_walk": fwd_ph[2],
-                     "bwd_chunk_dstate": bwd_ph[0], "bwd_dstate_walk_or_scan": bwd_ph[1],
-                     "bwd_chunk_grads": bwd_ph[2], "bwd_du_reduce": bwd_ph[3]},
-        "roofline": {"kernel": "wkv6_bwd_chunk_grads", "bound": "hbm", "achieved": achieved,
+                     "bwd_chunk_dstate": bwd_ph[0], "bwd_state_scan": bwd_ph[1],
+                     "bwd_grads": bwd_ph[2], "bwd_du_reduce": bwd_ph[3]},
+        "bwd_path": "reverse walk (wkv6_bwd_loop)" if bwd_loop(B * H, T) else
+                    "chunk-parallel (wkv6_bwd_chunk_dstate, wkv6_state_scan_bwd, wkv6_bwd_chunk_grads)",
+        "roofline": {"kernel": bwd_kernel(B * H, T), "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic(B, H, T)},
     }

@@ -71,15 +71,14 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // Transposed read of a token-major tile X (row stride TS): the lane receives
 // X[r0 + 4q + s][c0 + L], s = 0..3 -- one column, four consecutive rows.
-__device__ __forceinline__ bf16x4 ld_tr4(const uint16_t* X, int r0, int c0) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ bf16x4 ld_tr4(const uint16_t* X, int r0, int c0, int lane = threadIdx.x & 63) {
     const int L = lane & 15, q = lane >> 4;
     const uint16_t* p = X + (r0 + 4 * q + (L >> 2)) * TS + c0 + 4 * (L & 3);
     return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
 }
 // 32-row version for the 16x16x32 MFMA: slots 0-3 rows r0+4q+s, slots 4-7 rows r0+16+4q+s.
-__device__ __forceinline__ bf16x8 ld_tr8(const uint16_t* X, int r0, int c0) {
-    const bf16x4 a = ld_tr4(X, r0, c0), b = ld_tr4(X, r0 + 16, c0);
+__device__ __forceinline__ bf16x8 ld_tr8(const uint16_t* X, int r0, int c0, int lane = threadIdx.x & 63) {
+    const bf16x4 a = ld_tr4(X, r0, c0, lane), b = ld_tr4(X, r0 + 16, c0, lane);
     return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 // Lane l receives X[r0 + s][l], s = 0..3: 16-lane row group q reads columns 16q..16q+15 of
@@ -90,27 +89,40 @@ __device__ __forceinline__ bf16x4 ld_col4(const uint16_t* X, int r0) {
     const uint16_t* p = X + (r0 + (L >> 2)) * TS + 16 * q + 4 * (L & 3);
     return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
 }
+// Lane (q, L) receives X[r0 + 8q + s][c0 + L], s = 0..3: the 16 lanes of row group q read
+// rows r0 + 8q + (0..3) (lanes 4s..4s+3 read row s as 16 consecutive columns).
+__device__ __forceinline__ bf16x4 ld_tr4_g8(const uint16_t* X, int r0, int c0, int lane = threadIdx.x & 63) {
+    const int L = lane & 15, q = lane >> 4;
+    const uint16_t* p = X + (r0 + 8 * q + (L >> 2)) * TS + c0 + 4 * (L & 3);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
+// 8 consecutive rows r0 + 8q + (0..7) of column c0 + L.
+__device__ __forceinline__ bf16x8 ld_tr8_g8(const uint16_t* X, int r0, int c0, int lane = threadIdx.x & 63) {
+    const bf16x4 a = ld_tr4_g8(X, r0, c0, lane), b = ld_tr4_g8(X, r0 + 4, c0, lane);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // Direct read of row `row` with the slot order of ld_tr8: columns c0+4q+(0..3), c0+16+4q+(0..3).
-__device__ __forceinline__ bf16x8 ld_dir8(const uint16_t* X, int row, int c0) {
-    const int q = (threadIdx.x & 63) >> 4;
+__device__ __forceinline__ bf16x8 ld_dir8(const uint16_t* X, int row, int c0, int lane = threadIdx.x & 63) {
+    const int q = lane >> 4;
     const uint2 a = *reinterpret_cast<const uint2*>(X + row * TS + c0 + 4 * q);
     const uint2 b = *reinterpret_cast<const uint2*>(X + row * TS + c0 + 16 + 4 * q);
     return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
 }
 // Direct 16-byte read of row `row`, columns c0 + 8q .. +7 (products whose operands are both direct).
-__device__ __forceinline__ bf16x8 ld_row8(const uint16_t* X, int row, int c0) {
-    const int q = (threadIdx.x & 63) >> 4;
+__device__ __forceinline__ bf16x8 ld_row8(const uint16_t* X, int row, int c0, int lane = threadIdx.x & 63) {
+    const int q = lane >> 4;
     return ld_bf16x8(X + row * TS + c0 + 8 * q);
 }
 // Per-slot fp32 factors in ld_dir8 order from a 64-vector.
-__device__ __forceinline__ void dir8_vec(const float* v, int c0, float* f) {
-    const int q = (threadIdx.x & 63) >> 4;
+__device__ __forceinline__ void dir8_vec(const float* v, int c0, float* f, int lane = threadIdx.x & 63) {
+    const int q = lane >> 4;
     const float4 a = *reinterpret_cast<const float4*>(v + c0 + 4 * q);
     const float4 b = *reinterpret_cast<const float4*>(v + c0 + 16 + 4 * q);
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
 }
-__device__ __forceinline__ void row8_vec(const float* v, int c0, float* f) {
-    const int q = (threadIdx.x & 63) >> 4;
+__device__ __forceinline__ void row8_vec(const float* v, int c0, float* f, int lane = threadIdx.x & 63) {
+    const int q = lane >> 4;
     const float4 a = *reinterpret_cast<const float4*>(v + c0 + 8 * q);
     const float4 b = *reinterpret_cast<const float4*>(v + c0 + 8 * q + 4);
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
@@ -249,7 +261,7 @@ __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2
 #endif
 #define WALK_MIN_CHUNKS 8       // shortest segment worth a pre-pass
 #ifndef DSTATE_TARGET_ITEMS
-#define DSTATE_TARGET_ITEMS 256 // the same for the backward's reverse walk
+#define DSTATE_TARGET_ITEMS 256 // the same for the backward's walk
 #endif
 #ifndef WALK_WPE
 #define WALK_WPE 2              // waves per SIMD the walk is compiled for (1 block of 8 waves / CU)
@@ -335,9 +347,9 @@ inline int walk_segments(int64_t BH, int64_t NT, int64_t target = WALK_TARGET_IT
     return (int)((NT + NC - 1) / NC);                   // no empty segment
 }
 
-// The backward's state gradients walk each sequence in one workgroup when that fills the
-// device (a segmented reverse walk reads r, w, dO twice and loses to the chunk-parallel form).
-inline bool dstate_walk(int64_t BH, int64_t NT) { return walk_segments(BH, NT, DSTATE_TARGET_ITEMS) == 1; }
+// The backward walks each sequence in one workgroup (wkv6_bwd_loop) when that fills the device
+// or the sequences are short; otherwise the state gradients run chunk-parallel.
+inline bool bwd_loop(int64_t BH, int64_t NT) { return walk_segments(BH, NT, DSTATE_TARGET_ITEMS) == 1; }
 
 struct WalkPrefetch {
     uint4 r, k, v, w;
@@ -759,193 +771,6 @@ wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict_
     if (dh0) *reinterpret_cast<float2*>(dh0 + (size_t)bh * KD * KD + e) = dS;
 }
 
-// ---------------------------------------------------------------------------
-// backward: state gradients as a reverse walk (B*H large enough to fill the device)
-// ---------------------------------------------------------------------------
-// dS_out(c) is the gradient w.r.t. the state after chunk c: dS_out(NT-1) = dhT and
-//   dS_out(c-1) = diag(e^{G_63(c)}) dS_out(c) + s sum_{t in c} (r_t e^{G_{t-1}}) dO_t^T,
-// dh0 = dS_out(-1).  One workgroup per (b,h) walks its chunks from the last to the first
-// with dS in the accumulator registers and writes bf16 dS_out(c) per chunk, the gradient
-// kernel's input: r, w, dO are read once and no chunk-local state goes through HBM.
-//
-// Wave (cg, jh) owns state rows [16cg, 16cg+16) x columns [32jh, 32jh+32).  Its MFMA A
-// operand (s r e^{G_{t-1}})^T is built in registers: lane (q, L) holds channel 16cg + L for
-// the tokens 32ks + 8q + s, s = 0..7, ks = 0, 1 -- read from the token-major tiles with the
-// LDS transpose read, scanned along the tokens in registers (the 8-token runs of the four
-// lane rows combined by lane shuffles), exponentiated, and fed to the MFMA as is: no
-// cumulative-decay or operand tile goes through LDS, and one barrier per chunk suffices.
-struct DstateSmem {
-    tile_t Rw[2], Ww[2], Dw[2];       // raw r, w (or pre-activation decay), dO of chunk c in [c & 1]
-    uint16_t Ds[8][16][40];           // per-wave bf16 dS_out staging (16 rows x 32 columns)
-    float g63[8][16];                 // per-wave G_63 of its 16 channels
-};
-static_assert(sizeof(DstateSmem) <= 80 * 1024, "two dstate blocks per CU");
-
-// Lane (q, L) receives X[r0 + 8q + s][c0 + L], s = 0..3: the 16 lanes of row group q read
-// rows r0 + 8q + (0..3) (lanes 4s..4s+3 read row s as 16 consecutive columns).
-__device__ __forceinline__ bf16x4 ld_tr4_g8(const uint16_t* X, int r0, int c0) {
-    const int lane = threadIdx.x & 63;
-    const int L = lane & 15, q = lane >> 4;
-    const uint16_t* p = X + (r0 + 8 * q + (L >> 2)) * TS + c0 + 4 * (L & 3);
-    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
-}
-// 8 consecutive rows r0 + 8q + (0..7) of column c0 + L.
-__device__ __forceinline__ bf16x8 ld_tr8_g8(const uint16_t* X, int r0, int c0) {
-    const bf16x4 a = ld_tr4_g8(X, r0, c0), b = ld_tr4_g8(X, r0 + 4, c0);
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-struct DstatePrefetch {
-    uint4 r, w, d;
-};
-
-template <bool SEQ>
-__device__ __forceinline__ void dstate_issue(DstatePrefetch& f, const uint16_t* __restrict__ r,
-                                             const uint16_t* __restrict__ w,
-                                             const uint16_t* __restrict__ dO, int bh, int c,
-                                             int B, int H, int T) {
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
-    // unconditional loads (rows past the end read the last token; dstate_chunk zeroes them):
-    // a load under a branch makes the next wait a full one
-    const int row = min((int)(threadIdx.x >> 3), nvalid - 1), c8 = (threadIdx.x & 7) * 8;
-    f.r = *reinterpret_cast<const uint4*>(r + base + (size_t)row * rs + c8);
-    f.w = *reinterpret_cast<const uint4*>(w + base + (size_t)row * rs + c8);
-    f.d = *reinterpret_cast<const uint4*>(dO + ((size_t)bh * T + t0 + row) * KD + c8);
-}
-
-// One chunk of the reverse walk: stores the prefetched tiles, writes dS_out(c) and advances
-// D to dS_out(c - 1).
-template <bool SEQ>
-__device__ __forceinline__ void dstate_chunk(DstateSmem& sm, const DstatePrefetch& f, f32x4 (&D)[2],
-                                             uint16_t* __restrict__ dHs, int bh, int c, int T,
-                                             int NT, float scale) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int cg = wv >> 1, jh = wv & 1;
-    const int L = lane & 15, q = lane >> 4;
-    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
-    const int nvalid = min(CL, T - c * CL), b = c & 1;
-    const bool zero = nvalid < CL && row >= nvalid;
-    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-    sstore16(sm.Rw[b], row, c8, zero ? z : f.r);
-    sstore16(sm.Ww[b], row, c8, zero ? z : f.w);
-    sstore16(sm.Dw[b], row, c8, zero ? z : f.d);
-    __syncthreads();       // chunk c's tiles are in; buffer b ^ 1 was last read before this point
-    // cumulative log2-decay of channel 16cg + L at tokens 32ks + 8q + s (run-local)
-    float g[2][8], run[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 wx = ld_tr8_g8(&sm.Ww[b][0][0], 32 * ks, 16 * cg);
-        float a = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float x = (float)wx[s];
-            const float wn = SEQ ? ((32 * ks + 8 * q + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
-            a += fmaxf(wn, W_MIN) * RW_L2E;
-            g[ks][s] = a;
-        }
-        run[ks] = a;
-    }
-    // exclusive prefix of the run totals over the lane rows q (lanes L + 16q); the second
-    // half of the chunk starts after the whole first half
-    float e0, e1;
-    {
-        float x = run[0];
-        float y = __shfl_up(x, 16);
-        x += q >= 1 ? y : 0.f;
-        y = __shfl_up(x, 32);
-        x += q >= 2 ? y : 0.f;                                   // inclusive over q
-        const float tot0 = __shfl(x, 48 + L);
-        e0 = x - run[0];
-        float z = run[1];
-        y = __shfl_up(z, 16);
-        z += q >= 1 ? y : 0.f;
-        y = __shfl_up(z, 32);
-        z += q >= 2 ? y : 0.f;
-        e1 = tot0 + (z - run[1]);
-    }
-    const float g63 = __shfl(e1 + run[1], 48 + L);
-    if (q == 0) sm.g63[wv][L] = g63;
-    // A operand (s r_t e^{G_{t-1}})^T, slot s <-> token 32ks + 8q + s
-    bf16x8 aop[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 rx = ld_tr8_g8(&sm.Rw[b][0][0], 32 * ks, 16 * cg);
-        const float base = ks == 0 ? e0 : e1;
-        float y[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float gm1 = s == 0 ? base : base + g[ks][s - 1];
-            y[s] = scale * (float)rx[s] * ex2(gm1);
-        }
-        aop[ks] = __builtin_bit_cast(bf16x8, pack8(y));
-    }
-    {
-        // dS_out(c), bf16, staged per wave for 16-byte stores
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) sm.Ds[wv][4 * q + rr][16 * tp + L] = f2bf(D[tp][rr]);
-        const int sr = lane >> 2, sc = (lane & 3) * 8;
-        *reinterpret_cast<uint4*>(dHs + ((size_t)bh * NT + c) * KD * KD + (16 * cg + sr) * KD + 32 * jh + sc) =
-            *reinterpret_cast<const uint4*>(&sm.Ds[wv][sr][sc]);
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-        const float d = ex2(sm.g63[wv][4 * q + rr]);
-        D[0][rr] *= d;
-        D[1][rr] *= d;
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
-            D[tp] = mfma32(aop[ks], ld_tr8_g8(&sm.Dw[b][0][0], 32 * ks, 32 * jh + 16 * tp), D[tp]);
-}
-
-// One workgroup per (b,h), chunks NT-1 .. 0; writes dHs and dh0.  Loads run two chunks
-// ahead (two register sets, the loop unrolled by two).
-template <bool SEQ>
-__global__ void __launch_bounds__(NTHR_W)
-wkv6_bwd_dstate_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
-                     const uint16_t* __restrict__ dO, const float* __restrict__ dhT,
-                     uint16_t* __restrict__ dHs, float* __restrict__ dh0, float scale, int B,
-                     int H, int T, int NT) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    DstateSmem& sm = *reinterpret_cast<DstateSmem*>(smem_raw);
-    const int bh = blockIdx.x;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int cg = wv >> 1, jh = wv & 1;
-    const int L = lane & 15, q = lane >> 4;
-    const size_t sbase = (size_t)bh * KD * KD;
-
-    DstatePrefetch fa, fb;
-    if (NT >= 1) dstate_issue<SEQ>(fa, r, w, dO, bh, NT - 1, B, H, T);
-    if (NT >= 2) dstate_issue<SEQ>(fb, r, w, dO, bh, NT - 2, B, H, T);
-    f32x4 D[2];                            // dS_out(NT - 1) = dhT
-#pragma unroll
-    for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-            D[tp][rr] = dhT ? dhT[sbase + (16 * cg + 4 * q + rr) * KD + 32 * jh + 16 * tp + L] : 0.f;
-    // the prologue's loads complete here, so the loop's waits follow its own order; the
-    // issues are unconditional (past chunk 0 they reload chunk 0)
-    __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
-    for (int c = NT - 1; c >= 0; c -= 2) {
-        dstate_chunk<SEQ>(sm, fa, D, dHs, bh, c, T, NT, scale);
-        dstate_issue<SEQ>(fa, r, w, dO, bh, max(c - 2, 0), B, H, T);
-        if (c - 1 < 0) break;
-        dstate_chunk<SEQ>(sm, fb, D, dHs, bh, c - 1, T, NT, scale);
-        dstate_issue<SEQ>(fb, r, w, dO, bh, max(c - 3, 0), B, H, T);
-    }
-    if (dh0) {
-#pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                dh0[sbase + (16 * cg + 4 * q + rr) * KD + 32 * jh + 16 * tp + L] = D[tp][rr];
-    }
-}
 
 // ---------------------------------------------------------------------------
 // backward: gradients of one chunk
@@ -1008,20 +833,20 @@ struct GradOut {
     f32x4 av[2];                             // dv
 };
 
-// The products of token block W (wave-uniform, in a scalar register) for the two 16-channel
-// columns cb = 32hh + 16tp of the wave, with dr and dk finished as soon as their accumulators
-// are complete (their factors, raw r, k and dd are then dead while dv is formed).
-template <bool SEQ>
-__device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, float scale,
-                                               const GradLane& g, GradOut& out) {
+// The products of token block W (wave-uniform, in a scalar register) for the NTP 16-channel
+// columns c0 + 16tp of the wave, with dr and dk finished as soon as their accumulators are
+// complete (their factors, raw r, k and dd are then dead while dv is formed).
+template <bool SEQ, int NTP, class Smem>
+__device__ __forceinline__ void grads_products(Smem& sm, int W, int c0, float scale,
+                                               const GradLane& g, GradOut& out, int lane) {
     const int TW = 16 * W;
-    const int lane = threadIdx.x & 63, lr = lane & 15, lq = lane >> 4;
+    const int lr = lane & 15, lq = lane >> 4;
     const int rowW = TW + lr;
     const uint16_t* Vp = &sm.Vt[0][0];
     const uint16_t* Dp = &sm.Dt[0][0];
     const uint16_t* RTp = &sm.RT[0][0];
     const uint16_t* KTp = &sm.KT[0][0];
-    const int cbl[2] = {32 * hh + lr, 32 * hh + 16 + lr};      // the lane's channel of each tp
+    const int cbl[2] = {c0 + lr, c0 + 16 + lr};              // the lane's channel of each tp
     f32x4 ar[2], ak[2];
     float ddv[4], xr[2][4];
     // ---------------- dr (targets t in W) ----------------
@@ -1029,22 +854,22 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         f32x4 tmp[2] = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_row8(Dp, rowW, 32 * ks);
+            const bf16x8 a = ld_row8(Dp, rowW, 32 * ks, lane);
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                tmp[tp] = mfma32(a, ld_row8(&sm.Sin[0][0], cbl[tp], 32 * ks), tmp[tp]);
+            for (int tp = 0; tp < NTP; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&sm.Sin[0][0], cbl[tp], 32 * ks, lane), tmp[tp]);
         }
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) ar[tp] = tmp[tp] * sm.emu[W][cbl[tp]];
+        for (int tp = 0; tp < NTP; ++tp) ar[tp] = tmp[tp] * sm.emu[W][cbl[tp]];
     }
     for (int J = 0; J < W; ++J) {          // dA[t = 16W+lr][tau = 16J+4lq+rr], then x Km_J
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+            at = mfma32(ld_row8(Vp, 16 * J + lr, 32 * ks, lane), ld_row8(Dp, rowW, 32 * ks, lane), at);
         const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
+        for (int tp = 0; tp < NTP; ++tp) {
             const f32x4 t2 = mfma16(aop, ld_ch4(KTp, cbl[tp], 16 * J + 4 * lq), f32x4{});
             // the two halves of the cross factor one after the other (q_J p_WJ as one number can
             // underflow where the product with t2 is O(1))
@@ -1055,7 +880,7 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_row8(Vp, rowW, 32 * ks), ld_row8(Dp, rowW, 32 * ks), at);
+            at = mfma32(ld_row8(Vp, rowW, 32 * ks, lane), ld_row8(Dp, rowW, 32 * ks, lane), at);
         // the lane's tokens 16W + 4lq + rr take dd from lane (lq, 4lq + rr), element rr
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) ddv[rr] = __shfl(at[rr], 20 * lq + rr);
@@ -1064,11 +889,11 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr < lr ? at[rr] : 0.f;
         const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) ar[tp] = mfma16(aop, ld_ch4(KTp, cbl[tp], TW + 4 * lq), ar[tp]);
+        for (int tp = 0; tp < NTP; ++tp) ar[tp] = mfma16(aop, ld_ch4(KTp, cbl[tp], TW + 4 * lq), ar[tp]);
     }
     // dr = s Fm acc_r + s u k dd;  Rm s acc_r, the first half of x
 #pragma unroll
-    for (int tp = 0; tp < 2; ++tp) {
+    for (int tp = 0; tp < NTP; ++tp) {
         float d[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
@@ -1083,47 +908,53 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         f32x4 tmp[2] = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_row8(Vp, rowW, 32 * ks);
+            const bf16x8 a = ld_row8(Vp, rowW, 32 * ks, lane);
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                tmp[tp] = mfma32(a, ld_row8(&sm.dS[0][0], cbl[tp], 32 * ks), tmp[tp]);
+            for (int tp = 0; tp < NTP; ++tp)
+                tmp[tp] = mfma32(a, ld_row8(&sm.dS[0][0], cbl[tp], 32 * ks, lane), tmp[tp]);
         }
         float pk[2];
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) {
+        for (int tp = 0; tp < NTP; ++tp) {
             ak[tp] = tmp[tp] * sm.eg[W][cbl[tp]];
             // this wave's share of sum_tau Km acc_k^{inter}[tau] (the dk terms of D)
             pk[tp] = 0.f;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) pk[tp] += (float)g.kmb[tp][rr] * ak[tp][rr];
         }
-        // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
-        const bool up = lane & 16;
-        float p = (up ? pk[1] : pk[0]) + lane_xor_swz<16>(up ? pk[0] : pk[1]);
-        p += lane_xor32(p);
-        if (lq < 2) sm.Pk[W][32 * hh + 16 * lq + lr] = p;
+        if (NTP == 2) {
+            // sum over lq (lane bits 4, 5): lanes of odd lq keep tp = 1, even lq tp = 0
+            const bool up = lane & 16;
+            float p = (up ? pk[1] : pk[0]) + lane_xor_swz<16>(up ? pk[0] : pk[1]);
+            p += lane_xor32(p);
+            if (lq < 2) sm.Pk[W][c0 + 16 * lq + lr] = p;
+        } else {
+            float p = pk[0] + lane_xor_swz<16>(pk[0]);
+            p += lane_xor32(p);
+            if (lq == 0) sm.Pk[W][c0 + lr] = p;
+        }
     }
     {   // diagonal block: dA[t = 16W+4lq+rr][tau = 16W+lr], t > tau
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_row8(Dp, rowW, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+            at = mfma32(ld_row8(Dp, rowW, 32 * ks, lane), ld_row8(Vp, rowW, 32 * ks, lane), at);
         float xa[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) xa[rr] = 4 * lq + rr > lr ? at[rr] * scale : 0.f;
         const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) ak[tp] = mfma16(aop, ld_ch4(RTp, cbl[tp], TW + 4 * lq), ak[tp]);
+        for (int tp = 0; tp < NTP; ++tp) ak[tp] = mfma16(aop, ld_ch4(RTp, cbl[tp], TW + 4 * lq), ak[tp]);
     }
     {
         for (int I = W + 1; I < 4; ++I) {  // dA[t = 16I+4lq+rr][tau = 16W+lr], then x Rm_I
             f32x4 at = {};
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-                at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks), ld_row8(Vp, rowW, 32 * ks), at);
+                at = mfma32(ld_row8(Dp, 16 * I + lr, 32 * ks, lane), ld_row8(Vp, rowW, 32 * ks, lane), at);
             const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp) {
+            for (int tp = 0; tp < NTP; ++tp) {
                 const f32x4 t2 = mfma16(aop, ld_ch4(RTp, cbl[tp], 16 * I + 4 * lq), f32x4{});
                 ak[tp] += (t2 * sm.fp[(I * (I - 1)) / 2 + W][cbl[tp]]) * sm.kb[W][cbl[tp]];
             }
@@ -1133,7 +964,7 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
     // lane over the later tokens; du partial r k dd
     out.floored = 0u;
 #pragma unroll
-    for (int tp = 0; tp < 2; ++tp) {
+    for (int tp = 0; tp < NTP; ++tp) {
         float d[4], xv[4];
         out.dup[tp] = 0.f;
 #pragma unroll
@@ -1155,20 +986,20 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         out.dwv[tp][0] += (xv[3] + xv[2]) + xv[1];
         out.lt[tp] = ((xv[3] + xv[2]) + xv[1]) + xv[0];
     }
-    // ---------------- dv (sources tau in W, value columns 32hh..) ----------------
+    // ---------------- dv (sources tau in W, value columns c0..) ----------------
     f32x4 av[2] = {};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 a = ld_tr8(&sm.KtT[0][0], 32 * ks, TW);           // Kt[tau = 16W+lr][i]
+        const bf16x8 a = ld_tr8(&sm.KtT[0][0], 32 * ks, TW, lane);           // Kt[tau = 16W+lr][i]
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
-            av[tp] = mfma32(a, ld_tr8(&sm.dS[0][0], 32 * ks, 32 * hh + 16 * tp), av[tp]);
+        for (int tp = 0; tp < NTP; ++tp)
+            av[tp] = mfma32(a, ld_tr8(&sm.dS[0][0], 32 * ks, c0 + 16 * tp, lane), av[tp]);
     }
     {   // diagonal block: A[t = 16W+4lq+rr][tau = 16W+lr], t > tau, the u-bonus at t == tau
         f32x4 at = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_tr8_g8(RTp, 32 * ks, TW), ld_tr8_g8(KTp, 32 * ks, TW), at);
+            at = mfma32(ld_tr8_g8(RTp, 32 * ks, TW, lane), ld_tr8_g8(KTp, 32 * ks, TW, lane), at);
         const float bon = sm.bonus[rowW];
         float xa[4];
 #pragma unroll
@@ -1178,7 +1009,7 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
         }
         const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, TW, 32 * hh + 16 * tp), av[tp]);
+        for (int tp = 0; tp < NTP; ++tp) av[tp] = mfma16(aop, ld_tr4(Dp, TW, c0 + 16 * tp, lane), av[tp]);
     }
     {
         for (int I = W + 1; I < 4; ++I) {  // A[t = 16I+4lq+rr][tau = 16W+lr] = (Rm_I p_IW) Kq_W
@@ -1186,18 +1017,18 @@ __device__ __forceinline__ void grads_products(GradSmem& sm, int W, int hh, floa
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 float f[8];
-                row8_vec(sm.fp[(I * (I - 1)) / 2 + W], 32 * ks, f);
-                at = mfma32(scale8(ld_tr8_g8(RTp, 32 * ks, 16 * I), f),
-                            ld_tr8_g8(&sm.KqT[0][0], 32 * ks, TW), at);    // Kq[tau = 16W+lr][i]
+                row8_vec(sm.fp[(I * (I - 1)) / 2 + W], 32 * ks, f, lane);
+                at = mfma32(scale8(ld_tr8_g8(RTp, 32 * ks, 16 * I, lane), f),
+                            ld_tr8_g8(&sm.KqT[0][0], 32 * ks, TW, lane), at);    // Kq[tau = 16W+lr][i]
             }
             const bf16x4 aop = cvt4(at[0] * scale, at[1] * scale, at[2] * scale, at[3] * scale);
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, 32 * hh + 16 * tp), av[tp]);
+            for (int tp = 0; tp < NTP; ++tp)
+                av[tp] = mfma16(aop, ld_tr4(Dp, 16 * I, c0 + 16 * tp, lane), av[tp]);
         }
     }
-    out.av[0] = av[0];
-    out.av[1] = av[1];
+#pragma unroll
+    for (int tp = 0; tp < NTP; ++tp) out.av[tp] = av[tp];
 }
 
 // SEQ: r, k, v, the pre-activation decay and dr, dk, dv, d_decay are sequence-first (dO is
@@ -1364,7 +1195,7 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 
     // ---- P3: the products, dr and dk finished on the way ----
     GradOut go;
-    grads_products<SEQ>(sm, __builtin_amdgcn_readfirstlane(W), hh, scale, gl, go);
+    grads_products<SEQ, 2>(sm, __builtin_amdgcn_readfirstlane(W), 32 * hh, scale, gl, go, lane);
 
     // ---------------- epilogue ----------------
     // dw[t] = D + sum_{m > t} x[m] + y[t]: the suffix sums within the lane are in go.dwv; here
@@ -1441,6 +1272,559 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
             const uint4 x = __builtin_bit_cast(uint4, ld_tr8_g8(&Ts[n][0][0], 32 * (wv >> 2), 16 * (wv & 3)));
             if (tk < nvalid) *reinterpret_cast<uint4*>(outs[n] + base + (size_t)tk * rs + ch) = x;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward as one reverse walk per sequence (B*H large enough to fill the device)
+// ---------------------------------------------------------------------------
+// One 1024-thread workgroup per (b,h) walks the chunks from the last to the first.  It carries
+// the state gradient dS_out(c) (the gradient w.r.t. the state after chunk c, dS_out(NT-1) =
+// dhT) in fp32 MFMA accumulators and does, per chunk, what wkv6_bwd_chunk_grads does for one
+// chunk (the same factors and rounding points) followed by the state-gradient step
+//   dS_out(c-1) = diag(e^{G_63}) dS_out(c) + s sum_t (r_t e^{G_{t-1}})^T dO_t          [MFMA]
+// so no dstate pass runs, r, w, dO are read once and dS never goes through HBM; dh0 =
+// dS_out(-1) and du are summed over the whole sequence in registers.  The next chunk's raw
+// pieces are loaded into registers while the current one is computed.
+// 16 waves: wave (W, col) = (wv >> 2, wv & 3) owns tokens [16W, 16W+16) and the one channel
+// column [16col, 16col+16); lane (lq, lr) holds t = 16W + 4lq + rr (rr = 0..3), i = 16col + lr,
+// and, in the state-gradient accumulator, dS[i = 16col + lr][j = 16W + 4lq + rr].
+#define NTHR_L 1024
+
+struct LoopSmem {
+    tile_t Vt, Dt;                  // raw v, dO (token-major)
+    tile_t RT, KT;                  // raw r, k (token-major), then Rm^T, Km^T (channel-major)
+    tile_t KtT, KqT;                // raw w in KtT first; then Kt^T, Kq^T (channel-major)
+    tile_t Sin, dS;                 // S_in, dS_out (bf16 [i][j])
+    tile_t RiT;                     // (s r e^{G_{t-1}})^T, the state-gradient step's operand
+    tile_t RpT[2];                  // (s Rm_I p_IW)^T of the six cross pairs I > W (dv)
+    tile_t Out[4];                  // dr, dk, dv, dw staged channel-major
+    // the 16x16 blocks of the chunk, once per chunk for all four channel columns:
+    // dAb[W(W+1)/2 + J] = dA[t in W][tau in J] (W >= J; the diagonal block strictly lower),
+    // bf16 row-major [t][tau]; Ab[I(I+1)/2 + W] = s A[t in I][tau in W] (I >= W; the diagonal
+    // block with the u-bonus on its diagonal), bf16 in MFMA-operand order (8 bytes per lane)
+    uint16_t dAb[10][16][16];
+    uint16_t Ab[10][64][4];
+    float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD], eG63[KD];
+    float bonus[CL], Dv[KD], dd[CL];  // dd[t] = dO_t . v_t
+    float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
+    float red[8][KD];               // block totals and mu of the decay scan, then dw block
+                                    // totals [0..3] and du partials [4..7]
+};
+static_assert(sizeof(LoopSmem) <= 160 * 1024, "one loop workgroup per CU");
+
+// (J, W) of block b in the order b = W(W+1)/2 + J, J <= W (wave-uniform).
+__device__ __forceinline__ void tri_pair(int b, int& hi, int& lo) {
+    hi = (b >= 1) + (b >= 3) + (b >= 6);
+    lo = b - (hi * (hi + 1)) / 2;
+}
+
+// Lane (q, L) receives X[4q + s][L], s = 0..3, of a 16x16 row-major bf16 block.
+__device__ __forceinline__ bf16x4 ld_blk_tr(const uint16_t* X, int lane) {
+    const int L = lane & 15, q = lane >> 4;
+    const uint16_t* p = X + (4 * q + (L >> 2)) * 16 + 4 * (L & 3);
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
+__device__ __forceinline__ bf16x4 ld_b64(const uint16_t* p) {
+    return __builtin_bit_cast(bf16x4, *reinterpret_cast<const uint2*>(p));
+}
+
+// dA block b of the chunk (waves 0..9, after the raw tiles are in): the lane holds
+// dA[t = 16W + lr][tau = 16J + 4lq + rr] and stores it at row lr, columns 4lq .. +3.
+__device__ __forceinline__ void loop_dA_block(LoopSmem& sm, int b, int lane) {
+    int W, J;
+    tri_pair(b, W, J);
+    const int lr = lane & 15, lq = lane >> 4;
+    f32x4 at = {};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+        at = mfma32(ld_row8(&sm.Vt[0][0], 16 * J + lr, 32 * ks, lane),
+                    ld_row8(&sm.Dt[0][0], 16 * W + lr, 32 * ks, lane), at);
+    float x[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) x[rr] = (W > J || 4 * lq + rr < lr) ? at[rr] : 0.f;
+    *reinterpret_cast<uint2*>(&sm.dAb[b][lr][4 * lq]) = make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3]));
+}
+
+// A block b (waves 0..9, after the operand tiles are in): the lane holds
+// s A[t = 16I + 4lq + rr][tau = 16W + lr], the A operand of dv's 16x16x16 products.
+__device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, int lane) {
+    int I, W;
+    tri_pair(b, I, W);
+    const int lr = lane & 15, lq = lane >> 4;
+    f32x4 at = {};
+    float x[4];
+    if (I == W) {
+        // Rm_W Km_W^T over the channels, strictly causal, the u-bonus on the diagonal
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_tr8_g8(&sm.RT[0][0], 32 * ks, 16 * W, lane),
+                        ld_tr8_g8(&sm.KT[0][0], 32 * ks, 16 * W, lane), at);
+        const float bon = sm.bonus[16 * W + lr];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int tl = 4 * lq + rr;
+            x[rr] = (tl > lr ? at[rr] : (tl == lr ? bon : 0.f)) * scale;
+        }
+    } else {
+        // (s Rm_I p_IW) Kq_W^T, the pair tile pre-scaled
+        const int pi = (I * (I - 1)) / 2 + W;
+        const uint16_t* Rp = &sm.RpT[pi >> 2][0][0] + 16 * (pi & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            at = mfma32(ld_tr8_g8(Rp, 32 * ks, 0, lane), ld_tr8_g8(&sm.KqT[0][0], 32 * ks, 16 * W, lane), at);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) x[rr] = at[rr];
+    }
+    *reinterpret_cast<uint2*>(&sm.Ab[b][lane][0]) = make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3]));
+}
+
+// dr and dk of the wave's token block W and channel column ch = 16 col + lr (the factors and
+// operands as in grads_products, the 16x16 blocks read from dAb).
+template <bool SEQ>
+__device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, float scale,
+                                                 const GradLane& g, GradOut& out, int lane) {
+    const int TW = 16 * W, lr = lane & 15, lq = lane >> 4;
+    const int rowW = TW + lr, ch = 16 * col + lr;
+    const uint16_t* KTp = &sm.KT[0][0];
+    const uint16_t* RTp = &sm.RT[0][0];
+    float ddv[4];
+    {
+        const float4 d = *reinterpret_cast<const float4*>(&sm.dd[TW + 4 * lq]);
+        ddv[0] = d.x; ddv[1] = d.y; ddv[2] = d.z; ddv[3] = d.w;
+    }
+    // ---------------- dr ----------------
+    f32x4 ar;
+    {
+        f32x4 tmp = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            tmp = mfma32(ld_row8(&sm.Dt[0][0], rowW, 32 * ks, lane), ld_row8(&sm.Sin[0][0], ch, 32 * ks, lane), tmp);
+        ar = tmp * sm.emu[W][ch];
+    }
+    const int bW = (W * (W + 1)) / 2;
+    for (int J = 0; J < W; ++J) {
+        const f32x4 t2 = mfma16(ld_b64(&sm.dAb[bW + J][lr][4 * lq]), ld_ch4(KTp, ch, 16 * J + 4 * lq), f32x4{});
+        ar += (t2 * sm.kb[J][ch]) * sm.fp[(W * (W - 1)) / 2 + J][ch];
+    }
+    ar = mfma16(ld_b64(&sm.dAb[bW + W][lr][4 * lq]), ld_ch4(KTp, ch, TW + 4 * lq), ar);
+    float xr[4];
+    {
+        float d[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float sar = scale * ar[rr];
+            d[rr] = g.Fm[0][rr] * sar + (g.ulane[0] * ddv[rr]) * (float)g.krw[0][rr];
+            xr[rr] = (float)g.rmb[0][rr] * sar;
+        }
+        out.drb[0] = cvt4(d[0], d[1], d[2], d[3]);
+    }
+    // ---------------- dk ----------------
+    f32x4 ak, ak2;
+    {
+        f32x4 tmp = {};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            tmp = mfma32(ld_row8(&sm.Vt[0][0], rowW, 32 * ks, lane), ld_row8(&sm.dS[0][0], ch, 32 * ks, lane), tmp);
+        ak = tmp * sm.eg[W][ch];
+        float pk = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) pk += (float)g.kmb[0][rr] * ak[rr];
+        float p = pk + lane_xor_swz<16>(pk);
+        p += lane_xor32(p);
+        if (lq == 0) sm.Pk[W][ch] = p;
+    }
+    ak2 = mfma16(ld_blk_tr(&sm.dAb[bW + W][0][0], lane), ld_ch4(RTp, ch, TW + 4 * lq), f32x4{});
+    for (int I = W + 1; I < 4; ++I) {
+        const f32x4 t2 = mfma16(ld_blk_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], lane), ld_ch4(RTp, ch, 16 * I + 4 * lq), f32x4{});
+        ak2 += (t2 * sm.fp[(I * (I - 1)) / 2 + W][ch]) * sm.kb[W][ch];
+    }
+    out.floored = 0u;
+    {
+        float d[4], xv[4];
+        out.dup[0] = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float akr = ak[rr] + scale * ak2[rr];
+            const float rv = (float)g.rrw[0][rr], kv = (float)g.krw[0][rr];
+            d[rr] = g.Fk[0][rr] * akr + (g.ulane[0] * ddv[rr]) * rv;
+            out.dup[0] += (rv * kv) * ddv[rr];
+            const float y = -(float)g.kmb[0][rr] * akr;
+            xv[rr] = xr[rr] + y;
+            out.dwv[0][rr] = y;
+            if (!SEQ && g.Fm[0][rr] * g.Fk[0][rr] > FLOOR_FF) out.floored |= 1u << rr;
+        }
+        out.dkb[0] = cvt4(d[0], d[1], d[2], d[3]);
+        out.dwv[0][2] += xv[3];
+        out.dwv[0][1] += xv[3] + xv[2];
+        out.dwv[0][0] += (xv[3] + xv[2]) + xv[1];
+        out.lt[0] = ((xv[3] + xv[2]) + xv[1]) + xv[0];
+    }
+}
+
+// dv of the wave's token block W and value column ch (the A blocks read from Ab).
+__device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int W, int col, int lane) {
+    const int TW = 16 * W, c0 = 16 * col;
+    f32x4 av = {};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+        av = mfma32(ld_tr8(&sm.KtT[0][0], 32 * ks, TW, lane), ld_tr8(&sm.dS[0][0], 32 * ks, c0, lane), av);
+    av = mfma16(ld_b64(&sm.Ab[(W * (W + 1)) / 2 + W][lane][0]), ld_tr4(&sm.Dt[0][0], TW, c0, lane), av);
+    for (int I = W + 1; I < 4; ++I)
+        av = mfma16(ld_b64(&sm.Ab[(I * (I + 1)) / 2 + W][lane][0]), ld_tr4(&sm.Dt[0][0], 16 * I, c0, lane), av);
+    return av;
+}
+
+// The raw pieces of one chunk a thread moves into LDS: thread (row, c4) = (tid >> 4,
+// 4 (tid & 15)) holds token `row` of r, k, v, w, dO at channels c4 .. c4+3 and row i = row of
+// S_in.
+struct LoopPrefetch {
+    uint2 r, k, v, w, d, s;
+};
+
+// Part PART (0: r, k; 1: v, w; 2: dO, S_in) of the loads of chunk c.  The three parts go out
+// in three phases of the step before, so the vector-memory issue of the 16 waves does not
+// pile up in one phase.
+template <bool SEQ, int PART>
+__device__ __forceinline__ void loop_issue(LoopPrefetch& f, const uint16_t* __restrict__ r,
+                                           const uint16_t* __restrict__ k,
+                                           const uint16_t* __restrict__ v,
+                                           const uint16_t* __restrict__ w,
+                                           const uint16_t* __restrict__ dO,
+                                           const uint16_t* __restrict__ Hs, int bh, int c, int B,
+                                           int H, int T, int NT, int tid) {
+    const int row = tid >> 4, c4 = (tid & 15) * 4;
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    // unconditional loads (rows past a ragged end read the last token and are zeroed when
+    // stored): a load under a branch makes the next wait a full one
+    const int lrow = min(row, nvalid - 1);
+    const size_t off = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)lrow * tok_rs<SEQ>(B, H) + c4;
+    if (PART == 0) {
+        f.r = *reinterpret_cast<const uint2*>(r + off);
+        f.k = *reinterpret_cast<const uint2*>(k + off);
+    } else if (PART == 1) {
+        f.v = *reinterpret_cast<const uint2*>(v + off);
+        f.w = *reinterpret_cast<const uint2*>(w + off);
+    } else {
+        f.d = *reinterpret_cast<const uint2*>(dO + ((size_t)bh * T + t0 + lrow) * KD + c4);
+        f.s = *reinterpret_cast<const uint2*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c4);
+    }
+}
+
+// The staged gradients of chunk c to HBM: wave wv writes tensor wv >> 2 at tokens
+// 16 (wv & 3) + lr, channels 8 lq .. +7 and 32 + 8 lq .. +7.
+template <bool SEQ>
+__device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restrict__ dr,
+                                           uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
+                                           uint16_t* __restrict__ dw, int bh, int c, int B, int H,
+                                           int T, int tid) {
+    const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = wv >> 2, tk = 16 * (wv & 3) + (lane & 15);
+    const int t0 = c * CL, nvalid = min(CL, T - t0);
+    uint16_t* dst = n == 0 ? dr : n == 1 ? dk : n == 2 ? dv : dw;
+    const size_t o = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)tk * tok_rs<SEQ>(B, H) + 8 * (lane >> 4);
+    const uint4 x0 = __builtin_bit_cast(uint4, ld_tr8_g8(&sm.Out[n][0][0], 0, 16 * (wv & 3), lane));
+    const uint4 x1 = __builtin_bit_cast(uint4, ld_tr8_g8(&sm.Out[n][0][0], 32, 16 * (wv & 3), lane));
+    if (tk < nvalid) {
+        *reinterpret_cast<uint4*>(dst + o) = x0;
+        *reinterpret_cast<uint4*>(dst + o + 32) = x1;
+    }
+}
+
+// Sum over aligned groups of 16 lanes (a DPP row); all 16 lanes get the same bits.
+__device__ __forceinline__ float sum16lanes(float v) {
+    v = sum8lanes(v);
+    return v + dpp_mov<0x140>(v);                 // row_mirror: lane i <-> lane 15 - i
+}
+
+// SEQ as for wkv6_bwd_chunk_grads.  du_part gets one 64-vector per (b,h) ([h][b][i]).
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR_L)
+wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+              const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
+              const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ dO,
+              const float* __restrict__ dhT, const uint16_t* __restrict__ Hs,
+              uint16_t* __restrict__ dr, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
+              uint16_t* __restrict__ dw, float* __restrict__ du_part, float* __restrict__ dh0,
+              float scale, int B, int H, int T, int NT) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    LoopSmem& sm = *reinterpret_cast<LoopSmem*>(smem_raw);
+    const int bh = blockIdx.x, h = bh % H;
+    const size_t sbase = (size_t)bh * KD * KD;
+    // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
+    const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
+    const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
+
+    LoopPrefetch pf;
+    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
+    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
+    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
+    float ub[4];                                            // u at the thread's 4 channels (bonus)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ub[s] = load_u(u, u_dtype, h * KD + (threadIdx.x & 15) * 4 + s);
+    GradLane gl;
+    gl.ulane[0] = scale * load_u(u, u_dtype, h * KD + ch0);
+    f32x4 Dst = {};                                         // dS[ch][t4 + rr]
+    if (dhT) {
+        const float4 x = *reinterpret_cast<const float4*>(dhT + sbase + ch0 * KD + t40);
+        Dst[0] = x.x; Dst[1] = x.y; Dst[2] = x.z; Dst[3] = x.w;
+    }
+    float du_acc = 0.f;
+
+    for (int c = NT - 1; c >= 0; --c) {
+        // The lane indices come from an opaque copy of the thread id made in every iteration:
+        // the LDS addresses derived from them are then formed where they are used, instead of
+        // being hoisted out of the walk and held in (spilled) registers for its whole length.
+        int tid;
+        asm volatile("" : "=v"(tid) : "0"((int)threadIdx.x));
+        const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int W = wv >> 2, col = wv & 3, lr = lane & 15, lq = lane >> 4;
+        const int ch = 16 * col + lr, t4 = 16 * W + 4 * lq;
+        const int row = tid >> 4, c4 = (tid & 15) * 4;      // the thread's raw pieces
+        const int t0 = c * CL, nvalid = min(CL, T - t0);
+        // ---- S1: the raw pieces into LDS, the bonus, dS_out(c) as a bf16 tile ----
+        {
+            LoopPrefetch x = pf;
+            if (nvalid < CL && row >= nvalid) {
+                const uint2 z = make_uint2(0u, 0u);
+                x.r = x.k = x.v = x.w = x.d = z;
+            }
+            *reinterpret_cast<uint2*>(&sm.Vt[row][c4]) = x.v;
+            *reinterpret_cast<uint2*>(&sm.Dt[row][c4]) = x.d;
+            *reinterpret_cast<uint2*>(&sm.RT[row][c4]) = x.r;
+            *reinterpret_cast<uint2*>(&sm.KT[row][c4]) = x.k;
+            *reinterpret_cast<uint2*>(&sm.KtT[row][c4]) = x.w;          // w scratch
+            *reinterpret_cast<uint2*>(&sm.Sin[row][c4]) = x.s;
+            float rf[4], kf[4];
+            unpack4(x.r, rf);
+            unpack4(x.k, kf);
+            float b = (rf[0] * ub[0]) * kf[0];
+#pragma unroll
+            for (int s = 1; s < 4; ++s) b += (rf[s] * ub[s]) * kf[s];
+            b = sum16lanes(b);
+            float vf[4], df[4];
+            unpack4(x.v, vf);
+            unpack4(x.d, df);
+            float e = (df[0] * vf[0] + df[1] * vf[1]) + (df[2] * vf[2] + df[3] * vf[3]);
+            e = sum16lanes(e);
+            if ((tid & 15) == 0) {
+                sm.bonus[row] = b;
+                sm.dd[row] = e;
+            }
+            const float d4[4] = {Dst[0], Dst[1], Dst[2], Dst[3]};
+            st_ch4(&sm.dS[0][0], ch, t4, d4);
+        }
+        // the next chunk's loads (past chunk 0 they reload chunk 0) go out in S2, S3 and S4,
+        // the stores of the chunk before in S4
+        const int cn = max(c - 1, 0);
+        __syncthreads();
+
+        // ---- S2: dA blocks; raw r, k, w at the lane's positions; the decay scan; Fm, Fk; Rm,
+        // Km; Dv ----
+        loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        if (wv < 10) loop_dA_block(sm, wv, lane);
+        bf16x4 wrw;
+        float kmf[4], rmf[4], qloc, m7;
+        {
+            gl.rrw[0] = ld_tr4(&sm.RT[0][0], 16 * W, 16 * col, lane);      // x[16W + 4lq + s][ch]
+            gl.krw[0] = ld_tr4(&sm.KT[0][0], 16 * W, 16 * col, lane);
+            wrw = ld_tr4(&sm.KtT[0][0], 16 * W, 16 * col, lane);
+            float cs[4], run = 0.f;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                float x = (float)wrw[rr];
+                if (SEQ) x = t4 + rr < nvalid ? -ex2(x * RW_L2E) : 0.f;   // w = -exp(decay), :336
+                run += fmaxf(x, W_MIN) * RW_L2E;
+                cs[rr] = run;
+            }
+            float xi = run, y = __shfl_up(xi, 16);
+            xi += lq >= 1 ? y : 0.f;
+            y = __shfl_up(xi, 32);
+            xi += lq >= 2 ? y : 0.f;                            // inclusive over lq
+            const float excl = xi - run;
+            const float tot = __shfl(xi, 48 + lr);              // the block's total
+            m7 = __shfl(excl + cs[3], 16 + lr);                 // G at token 16W+7
+            qloc = tot - m7;                                    // b_W - mu_W
+            if (lq == 0) {
+                sm.red[W][ch] = tot;
+                sm.red[4 + W][ch] = m7;
+            }
+            float rm[4], km[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                gl.Fm[0][rr] = ex2(excl + (rr ? cs[rr - 1] : 0.f) - m7);
+                gl.Fk[0][rr] = ex2(m7 - (excl + cs[rr]));
+                rm[rr] = (float)gl.rrw[0][rr] * gl.Fm[0][rr];
+                km[rr] = (float)gl.krw[0][rr] * gl.Fk[0][rr];
+                kmf[rr] = km[rr];
+                rmf[rr] = rm[rr];
+            }
+            gl.rmb[0] = cvt4(rm[0], rm[1], rm[2], rm[3]);
+            gl.kmb[0] = cvt4(km[0], km[1], km[2], km[3]);
+        }
+        {   // Dv[i] = sum_j S_in[i][j] dS[i][j], i = row
+            float a[4], d[4];
+            unpack4(*reinterpret_cast<const uint2*>(&sm.Sin[row][c4]), a);
+            unpack4(*reinterpret_cast<const uint2*>(&sm.dS[row][c4]), d);
+            float x = (a[0] * d[0] + a[1] * d[1]) + (a[2] * d[2] + a[3] * d[3]);
+            x = sum16lanes(x);
+            if ((tid & 15) == 0) sm.Dv[row] = x;
+        }
+        __syncthreads();                   // raw r, k, w read; block totals and mu in `red`
+
+        // ---- S3: operand tiles (channel-major), the state-gradient operand, the tables ----
+        loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        {
+            *reinterpret_cast<bf16x4*>(&sm.RT[ch][t4]) = gl.rmb[0];
+            *reinterpret_cast<bf16x4*>(&sm.KT[ch][t4]) = gl.kmb[0];
+            float after = 0.f, before = 0.f;                    // G_63 - b_W, b_{W-1}
+#pragma unroll
+            for (int J = 0; J < 4; ++J) {
+                const float tJ = sm.red[J][ch];
+                after += J > W ? tJ : 0.f;
+                before += J < W ? tJ : 0.f;
+            }
+            const float eg = ex2(after + qloc), kq = ex2(qloc);
+            float x[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * eg;
+            st_ch4(&sm.KtT[0][0], ch, t4, x);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * kq;
+            st_ch4(&sm.KqT[0][0], ch, t4, x);
+            // s r e^{G_{t-1}} = s r Fm e^{mu_W}, mu_W = b_{W-1} + (G at 16W+7 within the block)
+            const float emw = scale * ex2(before + m7);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) x[rr] = (float)gl.rrw[0][rr] * (gl.Fm[0][rr] * emw);
+            st_ch4(&sm.RiT[0][0], ch, t4, x);
+            // the pair tiles of the block as the later one: s Rm_W p_WJ, p_WJ = e^{mu_W - b_J}
+            float bJ = 0.f;
+            for (int J = 0; J < W; ++J) {
+                bJ += sm.red[J][ch];
+                const float pf = scale * ex2(before + m7 - bJ);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) x[rr] = rmf[rr] * pf;
+                const int pi = (W * (W - 1)) / 2 + J;
+                st_ch4(&sm.RpT[pi >> 2][0][0] + 16 * (pi & 3), ch, 4 * lq, x);
+            }
+        }
+        {
+            // tables per channel i = lane from the block totals and mu: b_J = G[16J+15],
+            // mu_J = b_{J-1} + m7_J; each wave fills one or two rows (wave-uniform branches)
+            const int i = lane;
+            float bnd[4], mu[4], a = 0.f;
+#pragma unroll
+            for (int J = 0; J < 4; ++J) {
+                mu[J] = a + sm.red[4 + J][i];
+                a += sm.red[J][i];
+                bnd[J] = a;
+            }
+            if (wv < 4) {
+                sm.emu[wv][i] = ex2(wv == 0 ? mu[0] : wv == 1 ? mu[1] : wv == 2 ? mu[2] : mu[3]);
+            } else if (wv < 8) {
+                const int J = wv - 4;
+                sm.eg[J][i] = ex2(bnd[3] - (J == 0 ? mu[0] : J == 1 ? mu[1] : J == 2 ? mu[2] : mu[3]));
+            } else if (wv < 11) {
+                const int J = wv - 8;
+                sm.kb[J][i] = ex2(J == 0 ? bnd[0] - mu[0] : J == 1 ? bnd[1] - mu[1] : bnd[2] - mu[2]);
+            } else if (wv == 11) {
+                sm.fp[0][i] = ex2(mu[1] - bnd[0]);              // (1, 0)
+                sm.fp[1][i] = ex2(mu[2] - bnd[0]);              // (2, 0)
+            } else if (wv == 12) {
+                sm.fp[2][i] = ex2(mu[2] - bnd[1]);              // (2, 1)
+                sm.fp[3][i] = ex2(mu[3] - bnd[0]);              // (3, 0)
+            } else if (wv == 13) {
+                sm.fp[4][i] = ex2(mu[3] - bnd[1]);              // (3, 1)
+                sm.fp[5][i] = ex2(mu[3] - bnd[2]);              // (3, 2)
+            } else if (wv == 14) {
+                const float e = ex2(bnd[3]);
+                sm.eG63[i] = e;
+                sm.Dv[i] *= e;
+            }
+        }
+        __syncthreads();
+
+        // ---- S4: the products (dr, dk finished on the way), the state-gradient step ----
+        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, tid);
+        loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        if (wv < 10) loop_A_block(sm, wv, scale, lane);
+        GradOut go;
+        loop_products_rk<SEQ>(sm, W, col, scale, gl, go, lane);
+        {
+            const float e = sm.eG63[ch];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) Dst[rr] *= e;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                Dst = mfma32(ld_tr8(&sm.Dt[0][0], 32 * ks, 16 * W, lane), ld_dir8(&sm.RiT[0][0], ch, 32 * ks, lane), Dst);
+        }
+        du_acc += go.dup[0];
+        __syncthreads();                   // A blocks in
+        go.av[0] = loop_products_v(sm, W, col, lane);
+        // dw: the suffix sums across the four lane rows (shuffles on all lanes)
+        float later;
+        {
+            const float lt = go.lt[0];
+            const float d16 = __shfl_down(lt, 16);
+            float vsum = lt + (lq <= 2 ? d16 : 0.f);
+            const float d32 = __shfl_down(vsum, 32);
+            vsum += lq <= 1 ? d32 : 0.f;                        // sum over lq' >= lq
+            later = vsum - lt;
+            if (lq == 0) sm.red[W][ch] = vsum;                  // the wave's total
+        }
+        __syncthreads();                   // all products done; red, Pk in
+
+        // ---- S5: dw; dr, dk, dv, dw staged channel-major (stored during the next step) ----
+        {
+            later += sm.Dv[ch] + ((sm.Pk[0][ch] + sm.Pk[1][ch]) + (sm.Pk[2][ch] + sm.Pk[3][ch]));
+            for (int W2 = W + 1; W2 < 4; ++W2) later += sm.red[W2][ch];
+            float g[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                g[rr] = go.dwv[0][rr] + later;
+                // a floored token's gradient is 0 (the derivative of the floored forward)
+                if (SEQ && t4 + rr < nvalid) {
+                    const float wn = -ex2((float)wrw[rr] * RW_L2E);
+                    g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
+                }
+                if (!SEQ && ((go.floored >> rr) & 1u)) g[rr] = 0.f;
+            }
+            *reinterpret_cast<bf16x4*>(&sm.Out[0][ch][t4]) = go.drb[0];
+            *reinterpret_cast<bf16x4*>(&sm.Out[1][ch][t4]) = go.dkb[0];
+            const float avf[4] = {go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]};
+            st_ch4(&sm.Out[2][0][0], ch, t4, avf);
+            st_ch4(&sm.Out[3][0][0], ch, t4, g);
+        }
+        // no barrier here: the next step's S1 touches nothing S5 reads or writes, and its B1
+        // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
+    }
+    __syncthreads();
+    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, 0, B, H, T, threadIdx.x);
+    // du over the sequence: lanes of one channel (lq), then the four token blocks in order
+    {
+        float p = du_acc + lane_xor_swz<16>(du_acc);
+        p += lane_xor32(p);
+        if (((threadIdx.x >> 4) & 3) == 0) sm.red[4 + (threadIdx.x >> 8)][ch0] = p;
+    }
+    if (dh0) *reinterpret_cast<float4*>(dh0 + sbase + ch0 * KD + t40) = make_float4(Dst[0], Dst[1], Dst[2], Dst[3]);
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < KD) {
+        const float acc = (sm.red[4][tid] + sm.red[5][tid]) + (sm.red[6][tid] + sm.red[7][tid]);
+        du_part[((size_t)h * B + bh / H) * KD + tid] = scale * acc;
+    }
+}
+
+// T = 0: dh0 = dhT (zero without one), du = 0 (a kernel rather than a memset node, so the
+// call can be captured in a graph).
+__global__ void __launch_bounds__(256)
+wkv6_bwd_empty(const float* __restrict__ dhT, float* __restrict__ dh0, void* __restrict__ du,
+               int u_dtype, int n_state, int n_u) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (dh0 && i < n_state) dh0[i] = dhT ? dhT[i] : 0.f;
+    if (i < n_u) {
+        if (u_dtype == RWKV6_BF16) reinterpret_cast<uint16_t*>(du)[i] = 0;
+        else reinterpret_cast<float*>(du)[i] = 0.f;
     }
 }
 
@@ -1539,9 +1923,9 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
         const size_t P = (size_t)walk_segments((int64_t)BH, nchunks(T));
         return std::max<size_t>(256, round_up(BH * (P - 1) * KD * KD * 4) + round_up(BH * (P - 1) * KD * 4));
     }
-    const size_t base = round_up(BH * NT * KD * KD * 2) + round_up(BH * NT * KD * 4);   // dHs, du_part
-    if (dstate_walk((int64_t)BH, nchunks(T))) return base;
-    return base + round_up(BH * NT * KD * KD * 2) + round_up(BH * NT * KD * 4);         // dS_loc, dec
+    if (bwd_loop((int64_t)BH, nchunks(T))) return round_up(BH * KD * 4);   // du_part per (b,h)
+    // dHs, du_part per chunk, dS_loc, dec
+    return 2 * round_up(BH * NT * KD * KD * 2) + 2 * round_up(BH * NT * KD * 4);
 }
 
 }  // extern "C"
@@ -1634,52 +2018,61 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     float* du_part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                               round_up((size_t)BH * NTa * KD * KD * 2));
     mark(phase_events, 0, s);
-    if (dstate_walk(BH, NT)) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_dstate_walk<SEQ>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)sizeof(DstateSmem)) != hipSuccess)
-            return RWKV6_ERR_LAUNCH;
-        mark(phase_events, 1, s);
-        mark(phase_events, 2, s);
-        hipLaunchKernelGGL(wkv6_bwd_dstate_walk<SEQ>, dim3((unsigned)BH), dim3(NTHR_W),
-                           sizeof(DstateSmem), s, (const uint16_t*)r, (const uint16_t*)w,
-                           (const uint16_t*)dO, dhT, dHs, dh0, scale, (int)B, (int)H, (int)T,
-                           (int)NT);
-    } else {
-        uint16_t* dSloc = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(du_part) +
-                                                      round_up((size_t)BH * NTa * KD * 4));
-        float* dec = reinterpret_cast<float*>(reinterpret_cast<char*>(dSloc) +
-                                              round_up((size_t)BH * NTa * KD * KD * 2));
-        hipLaunchKernelGGL(wkv6_bwd_chunk_dstate<SEQ>, dim3((unsigned)NT, (unsigned)BH), dim3(NTHR), 0,
-                           s, (const uint16_t*)r, (const uint16_t*)dO, (const uint16_t*)w, dSloc, dec,
-                           scale, (int)B, (int)H, (int)T, (int)NT);
-        mark(phase_events, 1, s);
-        mark(phase_events, 2, s);
-        hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
-                           dec, dhT, dHs, dh0, (int)NT);
+    if (NT == 0) {                          // T = 0: dh0 = dhT, du = 0
+        const int n = std::max<int>(BH * KD * KD, (int)H * KD);
+        hipLaunchKernelGGL(wkv6_bwd_empty, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dhT,
+                           dh0, du, u_dtype, BH * KD * KD, (int)H * KD);
+        for (int i = 1; i <= 7; ++i) mark(phase_events, i, s);
+        return launch_status();
     }
-    mark(phase_events, 3, s);
-    if (NT > 0) {
-        dim3 grid((unsigned)NT, (unsigned)BH);
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<SEQ>),
+    if (bwd_loop(BH, NT)) {
+        // one reverse walk per sequence: gradients and state gradients in one pass
+        du_part = reinterpret_cast<float*>(workspace);
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_loop<SEQ>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)sizeof(GradSmem)) != hipSuccess)
+                                (int)sizeof(LoopSmem)) != hipSuccess)
             return RWKV6_ERR_LAUNCH;
-        mark(phase_events, 4, s);
-        hipLaunchKernelGGL(wkv6_bwd_chunk_grads<SEQ>, grid, dim3(NTHR_G), sizeof(GradSmem), s,
+        for (int i = 1; i <= 4; ++i) mark(phase_events, i, s);
+        hipLaunchKernelGGL(wkv6_bwd_loop<SEQ>, dim3((unsigned)BH), dim3(NTHR_L), sizeof(LoopSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
-                           (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, Hs,
-                           (const uint16_t*)dHs, (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv,
-                           (uint16_t*)dw, du_part, scale, (int)B, (int)H, (int)T, (int)NT);
+                           (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, dhT, Hs,
+                           (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv, (uint16_t*)dw, du_part, dh0,
+                           scale, (int)B, (int)H, (int)T, (int)NT);
         mark(phase_events, 5, s);
         mark(phase_events, 6, s);
         hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(DU_THR), 0, s, du_part, du, u_dtype,
-                           (int)B, (int)H, (int)NT);
+                           (int)B, (int)H, 1);
         mark(phase_events, 7, s);
-    } else {
-        if (hipMemsetAsync(du, 0, (size_t)H * KD * (u_dtype == RWKV6_BF16 ? 2 : 4), s) != hipSuccess)
-            return RWKV6_ERR_LAUNCH;
+        return launch_status();
     }
+    // chunk-parallel state gradients, then the gradient kernel over all (chunk, b,h)
+    uint16_t* dSloc = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(du_part) +
+                                                  round_up((size_t)BH * NTa * KD * 4));
+    float* dec = reinterpret_cast<float*>(reinterpret_cast<char*>(dSloc) +
+                                          round_up((size_t)BH * NTa * KD * KD * 2));
+    hipLaunchKernelGGL(wkv6_bwd_chunk_dstate<SEQ>, dim3((unsigned)NT, (unsigned)BH), dim3(NTHR), 0,
+                       s, (const uint16_t*)r, (const uint16_t*)dO, (const uint16_t*)w, dSloc, dec,
+                       scale, (int)B, (int)H, (int)T, (int)NT);
+    mark(phase_events, 1, s);
+    mark(phase_events, 2, s);
+    hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
+                       dec, dhT, dHs, dh0, (int)NT);
+    mark(phase_events, 3, s);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<SEQ>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(GradSmem)) != hipSuccess)
+        return RWKV6_ERR_LAUNCH;
+    mark(phase_events, 4, s);
+    hipLaunchKernelGGL(wkv6_bwd_chunk_grads<SEQ>, dim3((unsigned)NT, (unsigned)BH), dim3(NTHR_G),
+                       sizeof(GradSmem), s, (const uint16_t*)r, (const uint16_t*)k,
+                       (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, Hs,
+                       (const uint16_t*)dHs, (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv,
+                       (uint16_t*)dw, du_part, scale, (int)B, (int)H, (int)T, (int)NT);
+    mark(phase_events, 5, s);
+    mark(phase_events, 6, s);
+    hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(DU_THR), 0, s, du_part, du, u_dtype,
+                       (int)B, (int)H, (int)NT);
+    mark(phase_events, 7, s);
     return launch_status();
 }
 
