@@ -49,8 +49,9 @@ BYTES_FWD = 640           # per token-head: read r,k,v,w, write o
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=300,
+                    help="untimed steps first; the GPU's clocks take ~0.1 s of load to settle")
     ap.add_argument("--B", type=int, default=8)
     ap.add_argument("--H", type=int, default=32)
     ap.add_argument("--T", type=int, default=4096)
@@ -237,12 +238,14 @@ def measured_traffic(B, H, T):
 def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
     """WKV6 fwd+bwd through the C ABI (the _ex entries) on synthetic inputs resident in HBM.
     with_state: h0 ~ N(0, 0.5^2), dhT ~ N(0,1), dh0 returned (config 5).
-    The timed region (ms_per_step) records HIP events only around the gradient kernel (the
-    reverse walk or the chunk gradients), the roofline kernel, whose live average becomes
-    bwd_phases[2]; a second loop of the same
-    length records an event around every phase for the rest of the breakdown (each event in
-    the stream adds a few microseconds of gap, so they stay out of the timed region).
-    Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases)."""
+    Three loops of `steps` steps after the warm-up: the timed region proper (ms_per_step) with
+    no event inside it; the same steps with HIP events around the backward's gradient kernel,
+    the roofline kernel, recorded by the library on the kernels' stream (its live average
+    becomes bwd_phases[2]); and the same steps with an event around every phase for the rest
+    of the breakdown.  Each event recorded between two kernels adds a gap to the stream (a
+    few to tens of microseconds per step), which is why the step time comes from a loop
+    without them.
+    Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases, ms_per_step_with_events)."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -278,31 +281,38 @@ def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
                                           P(saved), P(dr), P(dk), P(dv), P(dw), P(du), P(dh0), P(ws_b),
                                           B, H, T, K, K, 1.0, sp, ba), "bwd")
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
     fevs = [[ev() for _ in range(6)] for _ in range(steps)]
     bevs = [[ev() for _ in range(8)] for _ in range(steps)]
     gevs = [[ev() for _ in range(8)] for _ in range(steps)]   # only [4], [5] recorded
-    t0 = ev()
-    t1 = ev()
-    for e in [x for evs in fevs + bevs + gevs for x in evs]:
+    t0, t1, t2, t3 = ev(), ev(), ev(), ev()
+    for e in [x for evs in fevs + bevs + gevs for x in evs] + [t0, t1, t2, t3]:
         e.record(stream)               # torch creates the hipEvent_t on first record
+    torch.cuda.synchronize()
+    # the warm-up runs right before the timed region: an idle GPU lowers its clocks within
+    # milliseconds and takes ~30 ms of load to raise them again
+    for _ in range(warmup):
+        step()
     torch.cuda.synchronize()
     t0.record(stream)
     for i in range(steps):
-        step(None, [None, None, None, None, gevs[i][4], gevs[i][5], None, None])
+        step()
     t1.record(stream)
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / steps
+    t2.record(stream)
+    for i in range(steps):
+        step(None, [None, None, None, None, gevs[i][4], gevs[i][5], None, None])
+    t3.record(stream)
+    torch.cuda.synchronize()
+    ms_step_ev = t2.elapsed_time(t3) / steps
     for i in range(steps):
         step(fevs[i], bevs[i])
     torch.cuda.synchronize()
     avg = lambda evs, a, b: sum(e[a].elapsed_time(e[b]) for e in evs) / len(evs)
     fwd_ph = [avg(fevs, 2 * p, 2 * p + 1) for p in range(3)]
     bwd_ph = [avg(bevs, 2 * p, 2 * p + 1) for p in range(4)]
-    bwd_ph[2] = avg(gevs, 4, 5)        # the roofline kernel, from the timed region
-    return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph
+    bwd_ph[2] = avg(gevs, 4, 5)        # the roofline kernel, from its own timed loop
+    return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph, ms_step_ev
 
 
 def train_step_bench(pkg, steps, warmup):
@@ -423,7 +433,7 @@ def main():
     B, H, T, K = args.B, args.H, args.T, 64
     N_th = B * H * T
 
-    ms_step, fwd_ms, bwd_ms, fwd_ph, bwd_ph = time_wkv(pkg, L, B, H, T, args.steps, args.warmup)
+    ms_step, fwd_ms, bwd_ms, fwd_ph, bwd_ph, ms_step_ev = time_wkv(pkg, L, B, H, T, args.steps, args.warmup)
 
     grads_ms = bwd_ph[2]
     achieved = N_th * BYTES_BWD_GRADS / (grads_ms * 1e-3) / 1e9
@@ -446,6 +456,7 @@ def main():
         "config": {"workload": "WKV6 fwd+bwd, BASELINE config 2 (chunk_rwkv6 via C ABI)",
                    "B": B, "H": H, "T": T, "K": K, "V": K, "h0": None, "output_final_state": True,
                    "parallelism": "single GPU"},
+        "ms_per_step_with_roofline_events": ms_step_ev,
         "wkv6_fwd_ms": fwd_ms,
         "wkv6_bwd_ms": bwd_ms,
         "wkv6_tflops": tflops,
@@ -463,7 +474,7 @@ def main():
     if not args.no_extra_configs:
         # the long-context one-GPU share with carried state (h0, dhT, dh0)
         B5, H5, T5 = 1, 32, 32768
-        c5 = time_wkv(pkg, L, B5, H5, T5, max(5, args.steps // 2), args.warmup, with_state=True)
+        c5 = time_wkv(pkg, L, B5, H5, T5, max(5, args.steps // 2), args.warmup // 2, with_state=True)
         out["config5"] = {"workload": "BASELINE config 5: WKV6 B=1, H=32, T=32768, h0 ~ N(0,0.5^2), "
                                       "dhT ~ N(0,1), final state and dh0 returned",
                           "ms_per_step": c5[0], "tokens_per_s": B5 * T5 / (c5[0] * 1e-3),

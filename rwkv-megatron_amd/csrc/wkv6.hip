@@ -1932,6 +1932,58 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
 
 namespace {
 
+constexpr int kMaxDevices = 64;
+
+// The device a call's kernels run on: the stream's, or the current one for the NULL stream.
+int stream_device(hipStream_t stream, int* dev, int* cur) {
+    if (hipGetDevice(cur) != hipSuccess) return RWKV6_ERR_LAUNCH;
+    *dev = *cur;
+    if (stream) {
+        hipDevice_t d = 0;
+        if (hipStreamGetDevice(stream, &d) != hipSuccess) return RWKV6_ERR_INVALID_ARG;
+        *dev = d;
+    }
+    return (*dev < 0 || *dev >= kMaxDevices) ? RWKV6_ERR_UNSUPPORTED : RWKV6_OK;
+}
+
+// The dynamic-LDS limit of every kernel here that takes more than 64 KB, raised once per
+// device (with that device current) instead of on every call.
+struct AttrSlot {
+    std::once_flag once;
+    int status = RWKV6_ERR_LAUNCH;
+};
+AttrSlot g_lds_attr[kMaxDevices];
+
+int lds_attributes(hipStream_t stream) {
+    int dev = 0, cur = 0;
+    int st = stream_device(stream, &dev, &cur);
+    if (st != RWKV6_OK) return st;
+    AttrSlot& slot = g_lds_attr[dev];
+    std::call_once(slot.once, [&slot, dev, cur] {
+        struct Lds {
+            const void* fn;
+            size_t bytes;
+        };
+        const Lds list[] = {
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<false, false>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<false, true>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<true, false>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<true, true>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_bwd_loop<false>), sizeof(LoopSmem)},
+            {reinterpret_cast<const void*>(wkv6_bwd_loop<true>), sizeof(LoopSmem)},
+            {reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<false>), sizeof(GradSmem)},
+            {reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<true>), sizeof(GradSmem)},
+        };
+        hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+        for (const Lds& x : list)
+            if (e == hipSuccess)
+                e = hipFuncSetAttribute(x.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.bytes);
+        if (dev != cur) (void)hipSetDevice(cur);
+        slot.status = e == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH;
+    });
+    return slot.status;
+}
+
 template <bool SEQ>
 int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, const void* u,
                  int u_dtype, const float* h0, void* o, float* hT, void* saved, void* workspace,
@@ -1961,11 +2013,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     float* Sseg = reinterpret_cast<float*>(workspace);
     float* Aseg = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                            round_up((size_t)BH * (P - 1) * KD * KD * 4));
-    for (const void* fn : {reinterpret_cast<const void*>(wkv6_fwd_walk<SEQ, false>),
-                           reinterpret_cast<const void*>(wkv6_fwd_walk<SEQ, true>)})
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)sizeof(WalkSmem)) != hipSuccess)
-            return RWKV6_ERR_LAUNCH;
+    if ((st = lds_attributes(s)) != RWKV6_OK) return st;
     mark(phase_events, 0, s);
     if (P > 1)
         hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, false>), dim3((unsigned)(BH * (P - 1))), dim3(NTHR_W),
@@ -2010,6 +2058,7 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
             return RWKV6_ERR_INVALID_ARG;
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if ((st = lds_attributes(s)) != RWKV6_OK) return st;
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);
     const uint16_t* Hs = reinterpret_cast<const uint16_t*>(saved);
@@ -2028,10 +2077,6 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     if (bwd_loop(BH, NT)) {
         // one reverse walk per sequence: gradients and state gradients in one pass
         du_part = reinterpret_cast<float*>(workspace);
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_loop<SEQ>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)sizeof(LoopSmem)) != hipSuccess)
-            return RWKV6_ERR_LAUNCH;
         for (int i = 1; i <= 4; ++i) mark(phase_events, i, s);
         hipLaunchKernelGGL(wkv6_bwd_loop<SEQ>, dim3((unsigned)BH), dim3(NTHR_L), sizeof(LoopSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
@@ -2058,10 +2103,6 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
     hipLaunchKernelGGL(wkv6_state_scan_bwd, dim3((unsigned)BH * SCAN_BLK), dim3(NTHR), 0, s, dSloc,
                        dec, dhT, dHs, dh0, (int)NT);
     mark(phase_events, 3, s);
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<SEQ>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(GradSmem)) != hipSuccess)
-        return RWKV6_ERR_LAUNCH;
     mark(phase_events, 4, s);
     hipLaunchKernelGGL(wkv6_bwd_chunk_grads<SEQ>, dim3((unsigned)NT, (unsigned)BH), dim3(NTHR_G),
                        sizeof(GradSmem), s, (const uint16_t*)r, (const uint16_t*)k,
@@ -2095,7 +2136,6 @@ static __device__ __align__(256) unsigned char scratch[WKV_SCRATCH_BYTES];
 
 namespace {
 
-constexpr int kMaxDevices = 64;
 struct ScratchSlot {
     std::once_flag once;
     int status = RWKV6_ERR_LAUNCH;
@@ -2107,15 +2147,9 @@ ScratchSlot g_scratch[kMaxDevices];
 // NULL stream).  Looked up once per device, with that device current; in host code the
 // array's name is only a stand-in, never a device address.
 int scratch_address(hipStream_t stream, void** out) {
-    int cur = 0;
-    if (hipGetDevice(&cur) != hipSuccess) return RWKV6_ERR_LAUNCH;
-    int dev = cur;
-    if (stream) {
-        hipDevice_t d = 0;
-        if (hipStreamGetDevice(stream, &d) != hipSuccess) return RWKV6_ERR_INVALID_ARG;
-        dev = d;
-    }
-    if (dev < 0 || dev >= kMaxDevices) return RWKV6_ERR_UNSUPPORTED;
+    int dev = 0, cur = 0;
+    const int st = stream_device(stream, &dev, &cur);
+    if (st != RWKV6_OK) return st;
     ScratchSlot& slot = g_scratch[dev];
     std::call_once(slot.once, [&slot, dev, cur] {
         hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
