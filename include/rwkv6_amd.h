@@ -141,6 +141,19 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
                           int param_dtype, const void* const* d_mixed, void* d_mexp,
                           float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
                           int64_t T, int64_t B, int64_t C, int64_t R, void* stream);
+/* Backward of the bottleneck's tanh (autograd of torch.tanh at rwkv6_layer_specs.py:195):
+ *   d_pre[n][e*R + r] = d_neck(e, n, r) * (1 - neck[n][e*R + r]^2)
+ * with d_neck(e, n, r) at d_neck + e*sE + n*sN + r (bf16; sE = N*R, sN = R for the batched
+ * [E,N,R] GEMM output, sE = R, sN = E*R for [N,E,R]), neck and d_pre [N, E*R] bf16.  R, sE,
+ * sN multiples of 8. */
+int rwkv6_lora_tanh_bwd(const void* d_neck, int64_t sE, int64_t sN, const void* neck, void* d_pre,
+                        int64_t N, int64_t E, int64_t R, void* stream);
+/* out[m] = sum_n x[n][m] for x [N, M] bf16 (M a multiple of 8), summed in fp32 in a fixed order
+ * and written in param_dtype: the bias gradient of a bottleneck (autograd of the `+ bias` at
+ * rwkv6_layer_specs.py:195), N = tokens, M = E*C. */
+size_t rwkv6_col_sum_workspace_bytes(int64_t N, int64_t M);
+int rwkv6_col_sum(const void* x, int64_t N, int64_t M, int param_dtype, void* out,
+                  void* workspace, void* stream);
 /* Input gradient of the time-mix token mixing given d_xxx [T,B,C] bf16 (the gradient of
  * xxx = x + (shift(x) - x) * maa, :443-444, from the LoRA down-projection) and the two sums of
  * rwkv6_ddlerp_lora_bwd:  d_delta = d_delta_part + d_xxx * maa,

@@ -48,6 +48,9 @@ SIGNATURES = {
     "rwkv6_ddlerp_lora_fwd": (_int, [_vp] * 4 + [_int, _vp] + [_i64] * 4 + [_vp]),
     "rwkv6_lora_bias_fwd": (_int, [_vp] * 3 + [_int, _vp] + [_i64] * 4 + [_vp]),
     "rwkv6_ddlerp_lora_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
+    "rwkv6_lora_tanh_bwd": (_int, [_vp, _i64, _i64, _vp, _vp] + [_i64] * 3 + [_vp]),
+    "rwkv6_col_sum_workspace_bytes": (ctypes.c_size_t, [_i64] * 2),
+    "rwkv6_col_sum": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp]),
     "rwkv6_ddlerp_lora_bwd": (_int, [_vp] * 4 + [_int] + [_vp] * 6 + [_i64] * 4 + [_vp]),
     "rwkv6_shift_lerp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 3),
     "rwkv6_shift_lerp_bwd": (_int, [_vp, _vp, _int] + [_vp] * 6 + [_i64] * 3 + [_vp]),

@@ -445,6 +445,63 @@ rwkv6_lora_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int
     }
 }
 
+// The backward of the bottleneck's tanh (rwkv6_layer_specs.py:177-195):
+//   d_pre[n][e*R + r] = d_neck(e, n, r) * (1 - neck[n][e*R + r]^2),
+// with d_neck(e, n, r) at d_neck + e*sE + n*sN + r (the up-projection's input gradient as the
+// batched or per-mix GEMM left it) and d_pre in the [N, E*R] layout of the down-projection's
+// GEMMs.  One thread per 8 consecutive r (16-byte accesses).
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_lora_tanh_bwd_kernel(const uint16_t* __restrict__ d_neck, int64_t sE, int64_t sN,
+                           const uint16_t* __restrict__ neck, uint16_t* __restrict__ d_pre,
+                           int64_t N, int E, int R) {
+    const int64_t R8 = R / 8, per_n = (int64_t)E * R8;
+    const int64_t i = (int64_t)blockIdx.x * LORA_THR + threadIdx.x;
+    if (i >= N * per_n) return;
+    const int64_t n = i / per_n, rem = i - n * per_n;
+    const int64_t e = rem / R8, r8 = rem - e * R8;
+    float d[8], t[8], y[8];
+    load8(d_neck + e * sE + n * sN + 8 * r8, d);
+    load8(neck + n * E * R + e * R + 8 * r8, t);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = d[j] * (1.f - t[j] * t[j]);
+    store8(d_pre + n * E * R + e * R + 8 * r8, y);
+}
+
+// Column sums of x [N, M] bf16 (the bias gradient of a bottleneck, summed over the tokens),
+// stage 1: block (rb, cb) sums rows [256 rb, 256 rb + 256) of columns [256 cb, 256 cb + 256);
+// thread (q, g) takes 8 columns and the rows q, q + 8, ...; the 8 partials of a column are
+// combined in LDS in a fixed order into part[rb][M] (rwkv6_lora_col_reduce finishes).
+#define CS_ROWS 256
+__global__ void __launch_bounds__(LORA_THR)
+rwkv6_col_sum_kernel(const uint16_t* __restrict__ x, int64_t N, int64_t M,
+                     float* __restrict__ part) {
+    __shared__ float acc[8][256 + 4];
+    const int q = threadIdx.x >> 5, g = threadIdx.x & 31;
+    const int64_t c0 = (int64_t)blockIdx.y * 256 + 8 * g;
+    const int64_t r0 = (int64_t)blockIdx.x * CS_ROWS;
+    float a[8] = {};
+    if (c0 < M) {
+        const int64_t r1 = min<int64_t>(N, r0 + CS_ROWS);
+        for (int64_t rw = r0 + q; rw < r1; rw += 8) {
+            float f[8];
+            load8(x + rw * M + c0, f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] += f[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[q][8 * g + j] = a[j];
+    __syncthreads();
+    const int cl = threadIdx.x;                     // 256 threads, one column each
+    const int64_t c = (int64_t)blockIdx.y * 256 + cl;
+    if (c < M) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t += acc[j][cl];
+        part[(int64_t)blockIdx.x * M + c] = t;
+    }
+}
+
 namespace {
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int launch_status() { return hipGetLastError() == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH; }
@@ -607,6 +664,52 @@ int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const 
                            d_sum, (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(LORA_THR), 0, s,
                        part, T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
+    return launch_status();
+}
+
+int rwkv6_lora_tanh_bwd(const void* d_neck, int64_t sE, int64_t sN, const void* neck, void* d_pre,
+                        int64_t N, int64_t E, int64_t R, void* stream) {
+    if (N < 0 || E < 1 || R < 1 || sE < 0 || sN < 0) return RWKV6_ERR_INVALID_ARG;
+    if (R % 8 || sE % 8 || sN % 8 || E > 64) return RWKV6_ERR_UNSUPPORTED;
+    if (N == 0) return RWKV6_OK;
+    if (!d_neck || !neck || !d_pre) return RWKV6_ERR_INVALID_ARG;
+    if (!al16(d_neck) || !al16(neck) || !al16(d_pre)) return RWKV6_ERR_ALIGNMENT;
+    const size_t nb = (size_t)(N * E * R) * 2;
+    const size_t dnb = (size_t)((E - 1) * sE + (N - 1) * sN + R) * 2;   // extent of d_neck
+    if (any_alias({{d_pre, nb}}, {{d_neck, dnb}, {neck, nb}})) return RWKV6_ERR_INVALID_ARG;
+    const int64_t items = N * E * (R / 8);
+    hipLaunchKernelGGL(rwkv6_lora_tanh_bwd_kernel, dim3((unsigned)((items + LORA_THR - 1) / LORA_THR)),
+                       dim3(LORA_THR), 0, reinterpret_cast<hipStream_t>(stream),
+                       (const uint16_t*)d_neck, sE, sN, (const uint16_t*)neck, (uint16_t*)d_pre, N,
+                       (int)E, (int)R);
+    return launch_status();
+}
+
+size_t rwkv6_col_sum_workspace_bytes(int64_t N, int64_t M) {
+    if (N < 0 || M < 1) return 0;
+    const int64_t nb = (N + CS_ROWS - 1) / CS_ROWS;
+    return (size_t)((nb > 0 ? nb : 1) * M) * sizeof(float);
+}
+
+int rwkv6_col_sum(const void* x, int64_t N, int64_t M, int param_dtype, void* out,
+                  void* workspace, void* stream) {
+    if (N < 0 || M < 1) return RWKV6_ERR_INVALID_ARG;
+    if (M % 8) return RWKV6_ERR_UNSUPPORTED;
+    if (param_dtype != RWKV6_F32 && param_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
+    if (!out || !workspace || (N > 0 && !x)) return RWKV6_ERR_INVALID_ARG;
+    if (!al16(x) || !al16(workspace)) return RWKV6_ERR_ALIGNMENT;
+    if (any_alias({{out, (size_t)M * param_bytes(param_dtype)},
+                   {workspace, rwkv6_col_sum_workspace_bytes(N, M)}},
+                  {{x, (size_t)(N * M) * 2}}))
+        return RWKV6_ERR_INVALID_ARG;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t nb = (N + CS_ROWS - 1) / CS_ROWS;
+    float* part = reinterpret_cast<float*>(workspace);
+    if (N > 0)
+        hipLaunchKernelGGL(rwkv6_col_sum_kernel, dim3((unsigned)nb, (unsigned)((M + 255) / 256)),
+                           dim3(LORA_THR), 0, s, (const uint16_t*)x, N, M, part);
+    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((M + 31) / 32)), dim3(LORA_THR), 0, s,
+                       part, N > 0 ? nb : (int64_t)0, M, param_dtype, out);
     return launch_status();
 }
 

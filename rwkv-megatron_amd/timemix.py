@@ -75,6 +75,29 @@ def shift_lerp(x: torch.Tensor, maa: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def tanh_bwd(d_neck, sE, sN, neck, N, E, R):
+    """d_pre [N, E*R] = d_neck * (1 - neck^2), the bottleneck's tanh backward (:195), with
+    d_neck(e, n, r) at element e*sE + n*sN + r of the contiguous bf16 tensor d_neck."""
+    d_neck = _c(d_neck.to(torch.bfloat16))
+    d_pre = torch.empty(N, E * R, dtype=torch.bfloat16, device=neck.device)
+    _lib.check(_lib.load().rwkv6_lora_tanh_bwd(_p(d_neck), sE, sN, _p(neck), _p(d_pre), N, E, R,
+                                               _stream(neck.device)), "rwkv6_lora_tanh_bwd")
+    return d_pre
+
+
+def col_sum(x, dtype):
+    """Sum over the rows of x [N, M] bf16 (fixed order, fp32 accumulation), as `dtype` (fp32 or
+    bf16): a bottleneck's bias gradient."""
+    L = _lib.load()
+    N, M = x.shape
+    x = _c(x)
+    pdt = _lib.RWKV6_BF16 if dtype == torch.bfloat16 else _lib.RWKV6_F32
+    out = torch.empty(M, dtype=torch.bfloat16 if pdt == _lib.RWKV6_BF16 else torch.float32, device=x.device)
+    ws = torch.empty(L.rwkv6_col_sum_workspace_bytes(N, M), dtype=torch.uint8, device=x.device)
+    _lib.check(L.rwkv6_col_sum(_p(x), N, M, pdt, _p(out), _p(ws), _stream(x.device)), "rwkv6_col_sum")
+    return out
+
+
 def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
     """GroupNorm over heads of 64 channels times silu(g_pre); g_pre None: GroupNorm alone."""
     if head_first:
@@ -164,8 +187,7 @@ class _TokenShiftMix(torch.autograd.Function):
                            d_mexp.view(NE * s, N // s, C),
                            out_dtype=torch.float32).view(NE, s, R, C).sum(1)    # [5, R, C]
         d_neck_t = torch.bmm(d_mexp, wut)                                       # [5, N, R]
-        d_pre = (d_neck_t.float() * (1.0 - neck_t.float() ** 2)).to(torch.bfloat16)
-        d_pre = d_pre.permute(1, 0, 2).reshape(N, NE * R)
+        d_pre = tanh_bwd(d_neck_t, N * R, R, neck, N, NE, R)                    # [N, 5R]
         wd = w_down.to(torch.bfloat16).reshape(C, NE * R)
         d_w_down = _wgrad(xxx.view(N, C), d_pre).view(C, NE, R)
         d_xxx = _c(d_pre @ wd.t())
@@ -209,11 +231,11 @@ class _Lora(torch.autograd.Function):
         E, R = w_down.shape[1], w_down.shape[2]
         N = T * B
         g = _c(d_out.to(torch.bfloat16)).view(N, E, C)
-        d_bias = g.float().sum(0)                                               # [E, C]
+        d_bias = col_sum(g.view(N, E * C), bias.dtype).view(E, C)              # [E, C]
         neck3 = neck.view(N, E, R)
         d_w_up = torch.stack([_wgrad(_c(neck3[:, e]), _c(g[:, e])) for e in range(E)])   # [E, R, C]
         d_neck = torch.stack([_c(g[:, e]) @ wut[e] for e in range(E)], 1)       # [N, E, R]
-        d_pre = (d_neck.float() * (1.0 - neck3.float() ** 2)).to(torch.bfloat16).view(N, E * R)
+        d_pre = tanh_bwd(d_neck, R, E * R, neck, N, E, R)                       # [N, E*R]
         d_w_down = _wgrad(x.view(N, C), d_pre).view(C, E, R)
         wd = w_down.to(torch.bfloat16).reshape(C, E * R)
         dx = (d_pre @ wd.t()).view(T, B, C)

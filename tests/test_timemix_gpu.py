@@ -220,3 +220,37 @@ def test_mix_and_gn_deterministic(pkg):
     a, b = run(), run()
     for ta, tb in zip(a, b):
         assert torch.equal(ta, tb)
+
+
+@pytest.mark.parametrize("layout", ["e_n_r", "n_e_r"])
+@pytest.mark.parametrize("N,E,R", [(1, 1, 8), (333, 5, 32), (4096, 1, 64)])
+def test_lora_tanh_bwd(pkg, layout, N, E, R):
+    """d_pre = d_neck * (1 - neck^2) in the down-projection's [N, E*R] layout, from d_neck laid
+    out [E,N,R] (the batched GEMM) or [N,E,R]; against fp64 on the same bf16 inputs."""
+    g = torch.Generator().manual_seed(N + E + R)
+    neck = _bf(torch.tanh(torch.randn(N, E * R, generator=g)))
+    d_ner = _bf(torch.randn(N, E, R, generator=g))
+    ref = (d_ner.double() * (1.0 - neck.double().view(N, E, R) ** 2)).reshape(N, E * R)
+    if layout == "e_n_r":
+        d_in, sE, sN = d_ner.permute(1, 0, 2).contiguous(), N * R, R
+    else:
+        d_in, sE, sN = d_ner.contiguous(), R, E * R
+    got = pkg.timemix.tanh_bwd(d_in.to(DEV), sE, sN, neck.to(DEV), N, E, R)
+    torch.cuda.synchronize()
+    _check("d_pre", _n(got), ref.numpy())
+
+
+@pytest.mark.parametrize("N,M", [(1, 8), (255, 360), (257, 64), (16384, 2048)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_col_sum(pkg, N, M, dtype):
+    """Column sums of a bf16 [N, M] (a bottleneck's bias gradient over the tokens), ragged N
+    and M, both parameter dtypes; bit-identical on a rerun (fixed reduction order)."""
+    g = torch.Generator().manual_seed(N + M)
+    x = _bf(torch.randn(N, M, generator=g))
+    ref = x.double().sum(0).numpy()
+    got = pkg.timemix.col_sum(x.to(DEV), dtype)
+    again = pkg.timemix.col_sum(x.to(DEV), dtype)
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and torch.equal(got, again)
+    # fp32 sums of N terms of magnitude ~1: error ~ N * 2^-24 * sqrt(N)-scale, well inside the bar
+    _check("col_sum", _n(got), ref)
