@@ -31,6 +31,13 @@ __device__ __forceinline__ bf16x4 cvt4(float a, float b, float c, float d) {
 }
 // 2^x with the hardware base-2 exponential (v_exp_f32).
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+// a.x*b.x + a.y*b.y + a.z*b.z + a.w*b.w of two packed bf16x4 (uint2), fp32 sums (v_dot2).
+__device__ __forceinline__ float dot4_bf16(uint2 a, uint2 b) {
+    const float lo = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x),
+                                                     __builtin_bit_cast(bf16x2, b.x), 0.f, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y),
+                                           __builtin_bit_cast(bf16x2, b.y), lo, false);
+}
 
 __device__ __forceinline__ f32x4 mfma32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

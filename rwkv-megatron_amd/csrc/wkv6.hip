@@ -1319,36 +1319,109 @@ __device__ __forceinline__ void tri_pair(int b, int& hi, int& lo) {
     lo = b - (hi * (hi + 1)) / 2;
 }
 
-// Lane (q, L) receives X[4q + s][L], s = 0..3, of a 16x16 row-major bf16 block.
-__device__ __forceinline__ bf16x4 ld_blk_tr(const uint16_t* X, int lane) {
+// Per-lane LDS byte offsets of the loop kernel's access patterns (lane = 16q + L).  They are
+// formed once per launch and passed through an empty asm at the top of every chunk, which
+// the compiler must assume changes them: an address of the chunk is then one add (its
+// wave-uniform part, or a constant folded into the instruction) from one of them.  Derived
+// from the thread id inside the chunk, the addresses cost several instructions each; hoisted
+// out of the walk, they do not fit the registers.
+struct LaneOfs {
+    int tr;      // ((4q + L/4) TS + 4 (L%4)) * 2: ds_read_b64_tr_b16 over rows r0 + 4q + s
+    int g8;      // ((8q + L/4) TS + 4 (L%4)) * 2: the same over rows r0 + 8q + s
+    int row;     // (L TS + 8q) * 2: 16-byte row pieces (row L, columns 8q..)
+    int ch;      // (L TS + 4q) * 2: 8-byte row pieces (row L, columns 4q..)
+    int blk;     // (16 L + 4q) * 2: a 16x16 row-major block, direct
+    int blktr;   // ((4q + L/4) 16 + 4 (L%4)) * 2: the same, transposed
+    int frag;    // 8 lane: 8 bytes per lane in MFMA-operand order
+    int tab;     // 4 L: a float per channel of a 16-channel column
+    int th;      // (q TS + 4 L) * 2: thread (row, c4) of a wave's four rows
+    int q16;     // 16 q: four floats per lane row
+};
+__device__ __forceinline__ LaneOfs lane_ofs(int lane) {
     const int L = lane & 15, q = lane >> 4;
-    const uint16_t* p = X + (4 * q + (L >> 2)) * 16 + 4 * (L & 3);
-    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+    LaneOfs o;
+    o.tr = ((4 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
+    o.g8 = ((8 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
+    o.row = (L * TS + 8 * q) * 2;
+    o.ch = (L * TS + 4 * q) * 2;
+    o.blk = (16 * L + 4 * q) * 2;
+    o.blktr = ((4 * q + (L >> 2)) * 16 + 4 * (L & 3)) * 2;
+    o.frag = 8 * lane;
+    o.tab = 4 * L;
+    o.th = (q * TS + 4 * L) * 2;
+    o.q16 = 16 * q;
+    return o;
 }
-__device__ __forceinline__ bf16x4 ld_b64(const uint16_t* p) {
-    return __builtin_bit_cast(bf16x4, *reinterpret_cast<const uint2*>(p));
+__device__ __forceinline__ void launder(LaneOfs& o) {
+    asm volatile("" : "+v"(o.tr), "+v"(o.g8), "+v"(o.row), "+v"(o.ch), "+v"(o.blk), "+v"(o.blktr),
+                 "+v"(o.frag), "+v"(o.tab), "+v"(o.th), "+v"(o.q16));
+}
+
+template <class T>
+__device__ __forceinline__ T lds_ld(const void* base, int bytes) {
+    return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + bytes);
+}
+template <class T>
+__device__ __forceinline__ void lds_st(void* base, int bytes, T v) {
+    *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + bytes) = v;
+}
+__device__ __forceinline__ bf16x4 lds_tr(const void* base, int bytes) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(reinterpret_cast<const char*>(base) + bytes)));
+}
+__device__ __forceinline__ bf16x8 cat8(bf16x4 a, bf16x4 b) {
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+// The tile readers of the loop with precomputed offsets (X a bf16 tile of row stride TS):
+//   tr8 (X, r0, c0): X[r0 + 4q + s][c0 + L], X[r0 + 16 + 4q + s][c0 + L]   (as ld_tr8)
+//   g8  (X, r0, c0): X[r0 + 8q + s][c0 + L], s = 0..7                       (as ld_tr8_g8)
+//   row8(X, r0, c0): X[r0 + L][c0 + 8q + s]                                 (as ld_row8)
+//   dir8(X, r0, c0): X[r0 + L][c0 + 4q + s], X[r0 + L][c0 + 16 + 4q + s]    (as ld_dir8)
+//   ch4 (X, r0, c0): X[r0 + L][c0 + 4q + s], s = 0..3                       (as ld_ch4)
+__device__ __forceinline__ int tb(int r0, int c0) { return (r0 * TS + c0) * 2; }
+__device__ __forceinline__ bf16x4 tr4o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    return lds_tr(X, o.tr + tb(r0, c0));
+}
+__device__ __forceinline__ bf16x8 tr8o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    return cat8(lds_tr(X, o.tr + tb(r0, c0)), lds_tr(X, o.tr + tb(r0 + 16, c0)));
+}
+__device__ __forceinline__ bf16x8 g8o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    return cat8(lds_tr(X, o.g8 + tb(r0, c0)), lds_tr(X, o.g8 + tb(r0 + 4, c0)));
+}
+__device__ __forceinline__ bf16x8 row8o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    return lds_ld<bf16x8>(X, o.row + tb(r0, c0));
+}
+__device__ __forceinline__ bf16x8 dir8o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    const uint2 a = lds_ld<uint2>(X, o.ch + tb(r0, c0)), b = lds_ld<uint2>(X, o.ch + tb(r0, c0 + 16));
+    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+__device__ __forceinline__ bf16x4 ch4o(const uint16_t* X, const LaneOfs& o, int r0, int c0) {
+    return lds_ld<bf16x4>(X, o.ch + tb(r0, c0));
+}
+__device__ __forceinline__ void st_ch4o(uint16_t* X, const LaneOfs& o, int r0, int c0, const float* f) {
+    lds_st<uint2>(X, o.ch + tb(r0, c0), make_uint2(pk2(f[0], f[1]), pk2(f[2], f[3])));
 }
 
 // dA block b of the chunk (waves 0..9, after the raw tiles are in): the lane holds
 // dA[t = 16W + lr][tau = 16J + 4lq + rr] and stores it at row lr, columns 4lq .. +3.
-__device__ __forceinline__ void loop_dA_block(LoopSmem& sm, int b, int lane) {
+__device__ __forceinline__ void loop_dA_block(LoopSmem& sm, int b, const LaneOfs& o, int lane) {
     int W, J;
     tri_pair(b, W, J);
     const int lr = lane & 15, lq = lane >> 4;
     f32x4 at = {};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-        at = mfma32(ld_row8(&sm.Vt[0][0], 16 * J + lr, 32 * ks, lane),
-                    ld_row8(&sm.Dt[0][0], 16 * W + lr, 32 * ks, lane), at);
+        at = mfma32(row8o(&sm.Vt[0][0], o, 16 * J, 32 * ks), row8o(&sm.Dt[0][0], o, 16 * W, 32 * ks), at);
     float x[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) x[rr] = (W > J || 4 * lq + rr < lr) ? at[rr] : 0.f;
-    *reinterpret_cast<uint2*>(&sm.dAb[b][lr][4 * lq]) = make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3]));
+    lds_st<uint2>(&sm.dAb[b][0][0], o.blk, make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3])));
 }
 
 // A block b (waves 0..9, after the operand tiles are in): the lane holds
 // s A[t = 16I + 4lq + rr][tau = 16W + lr], the A operand of dv's 16x16x16 products.
-__device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, int lane) {
+__device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, const LaneOfs& o,
+                                             int lane) {
     int I, W;
     tri_pair(b, I, W);
     const int lr = lane & 15, lq = lane >> 4;
@@ -1358,9 +1431,8 @@ __device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, i
         // Rm_W Km_W^T over the channels, strictly causal, the u-bonus on the diagonal
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_tr8_g8(&sm.RT[0][0], 32 * ks, 16 * W, lane),
-                        ld_tr8_g8(&sm.KT[0][0], 32 * ks, 16 * W, lane), at);
-        const float bon = sm.bonus[16 * W + lr];
+            at = mfma32(g8o(&sm.RT[0][0], o, 32 * ks, 16 * W), g8o(&sm.KT[0][0], o, 32 * ks, 16 * W), at);
+        const float bon = lds_ld<float>(&sm.bonus[16 * W], o.tab);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tl = 4 * lq + rr;
@@ -1372,25 +1444,25 @@ __device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, i
         const uint16_t* Rp = &sm.RpT[pi >> 2][0][0] + 16 * (pi & 3);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            at = mfma32(ld_tr8_g8(Rp, 32 * ks, 0, lane), ld_tr8_g8(&sm.KqT[0][0], 32 * ks, 16 * W, lane), at);
+            at = mfma32(g8o(Rp, o, 32 * ks, 0), g8o(&sm.KqT[0][0], o, 32 * ks, 16 * W), at);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) x[rr] = at[rr];
     }
-    *reinterpret_cast<uint2*>(&sm.Ab[b][lane][0]) = make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3]));
+    lds_st<uint2>(&sm.Ab[b][0][0], o.frag, make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3])));
 }
 
 // dr and dk of the wave's token block W and channel column ch = 16 col + lr (the factors and
 // operands as in grads_products, the 16x16 blocks read from dAb).
 template <bool SEQ>
 __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, float scale,
-                                                 const GradLane& g, GradOut& out, int lane) {
-    const int TW = 16 * W, lr = lane & 15, lq = lane >> 4;
-    const int rowW = TW + lr, ch = 16 * col + lr;
+                                                 const GradLane& g, GradOut& out,
+                                                 const LaneOfs& o) {
+    const int TW = 16 * W, c0 = 16 * col;
     const uint16_t* KTp = &sm.KT[0][0];
     const uint16_t* RTp = &sm.RT[0][0];
     float ddv[4];
     {
-        const float4 d = *reinterpret_cast<const float4*>(&sm.dd[TW + 4 * lq]);
+        const float4 d = lds_ld<float4>(&sm.dd[TW], o.q16);
         ddv[0] = d.x; ddv[1] = d.y; ddv[2] = d.z; ddv[3] = d.w;
     }
     // ---------------- dr ----------------
@@ -1399,15 +1471,15 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
         f32x4 tmp = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            tmp = mfma32(ld_row8(&sm.Dt[0][0], rowW, 32 * ks, lane), ld_row8(&sm.Sin[0][0], ch, 32 * ks, lane), tmp);
-        ar = tmp * sm.emu[W][ch];
+            tmp = mfma32(row8o(&sm.Dt[0][0], o, TW, 32 * ks), row8o(&sm.Sin[0][0], o, c0, 32 * ks), tmp);
+        ar = tmp * lds_ld<float>(&sm.emu[W][c0], o.tab);
     }
     const int bW = (W * (W + 1)) / 2;
     for (int J = 0; J < W; ++J) {
-        const f32x4 t2 = mfma16(ld_b64(&sm.dAb[bW + J][lr][4 * lq]), ld_ch4(KTp, ch, 16 * J + 4 * lq), f32x4{});
-        ar += (t2 * sm.kb[J][ch]) * sm.fp[(W * (W - 1)) / 2 + J][ch];
+        const f32x4 t2 = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + J][0][0], o.blk), ch4o(KTp, o, c0, 16 * J), f32x4{});
+        ar += (t2 * lds_ld<float>(&sm.kb[J][c0], o.tab)) * lds_ld<float>(&sm.fp[(W * (W - 1)) / 2 + J][c0], o.tab);
     }
-    ar = mfma16(ld_b64(&sm.dAb[bW + W][lr][4 * lq]), ld_ch4(KTp, ch, TW + 4 * lq), ar);
+    ar = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + W][0][0], o.blk), ch4o(KTp, o, c0, TW), ar);
     float xr[4];
     {
         float d[4];
@@ -1425,19 +1497,19 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
         f32x4 tmp = {};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
-            tmp = mfma32(ld_row8(&sm.Vt[0][0], rowW, 32 * ks, lane), ld_row8(&sm.dS[0][0], ch, 32 * ks, lane), tmp);
-        ak = tmp * sm.eg[W][ch];
+            tmp = mfma32(row8o(&sm.Vt[0][0], o, TW, 32 * ks), row8o(&sm.dS[0][0], o, c0, 32 * ks), tmp);
+        ak = tmp * lds_ld<float>(&sm.eg[W][c0], o.tab);
         float pk = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) pk += (float)g.kmb[0][rr] * ak[rr];
         float p = pk + lane_xor_swz<16>(pk);
         p += lane_xor32(p);
-        if (lq == 0) sm.Pk[W][ch] = p;
+        if (o.q16 == 0) lds_st<float>(&sm.Pk[W][c0], o.tab, p);
     }
-    ak2 = mfma16(ld_blk_tr(&sm.dAb[bW + W][0][0], lane), ld_ch4(RTp, ch, TW + 4 * lq), f32x4{});
+    ak2 = mfma16(lds_tr(&sm.dAb[bW + W][0][0], o.blktr), ch4o(RTp, o, c0, TW), f32x4{});
     for (int I = W + 1; I < 4; ++I) {
-        const f32x4 t2 = mfma16(ld_blk_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], lane), ld_ch4(RTp, ch, 16 * I + 4 * lq), f32x4{});
-        ak2 += (t2 * sm.fp[(I * (I - 1)) / 2 + W][ch]) * sm.kb[W][ch];
+        const f32x4 t2 = mfma16(lds_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], o.blktr), ch4o(RTp, o, c0, 16 * I), f32x4{});
+        ak2 += (t2 * lds_ld<float>(&sm.fp[(I * (I - 1)) / 2 + W][c0], o.tab)) * lds_ld<float>(&sm.kb[W][c0], o.tab);
     }
     out.floored = 0u;
     {
@@ -1462,16 +1534,16 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
     }
 }
 
-// dv of the wave's token block W and value column ch (the A blocks read from Ab).
-__device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int W, int col, int lane) {
+// dv of the wave's token block W and value column 16 col + lr (the A blocks read from Ab).
+__device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int W, int col, const LaneOfs& o) {
     const int TW = 16 * W, c0 = 16 * col;
     f32x4 av = {};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-        av = mfma32(ld_tr8(&sm.KtT[0][0], 32 * ks, TW, lane), ld_tr8(&sm.dS[0][0], 32 * ks, c0, lane), av);
-    av = mfma16(ld_b64(&sm.Ab[(W * (W + 1)) / 2 + W][lane][0]), ld_tr4(&sm.Dt[0][0], TW, c0, lane), av);
+        av = mfma32(tr8o(&sm.KtT[0][0], o, 32 * ks, TW), tr8o(&sm.dS[0][0], o, 32 * ks, c0), av);
+    av = mfma16(lds_ld<bf16x4>(&sm.Ab[(W * (W + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, TW, c0), av);
     for (int I = W + 1; I < 4; ++I)
-        av = mfma16(ld_b64(&sm.Ab[(I * (I + 1)) / 2 + W][lane][0]), ld_tr4(&sm.Dt[0][0], 16 * I, c0, lane), av);
+        av = mfma16(lds_ld<bf16x4>(&sm.Ab[(I * (I + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, 16 * I, c0), av);
     return av;
 }
 
@@ -1517,17 +1589,16 @@ template <bool SEQ>
 __device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restrict__ dr,
                                            uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
                                            uint16_t* __restrict__ dw, int bh, int c, int B, int H,
-                                           int T, int tid) {
-    const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+                                           int T, int wv, int lane, const LaneOfs& o) {
     const int n = wv >> 2, tk = 16 * (wv & 3) + (lane & 15);
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     uint16_t* dst = n == 0 ? dr : n == 1 ? dk : n == 2 ? dv : dw;
-    const size_t o = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)tk * tok_rs<SEQ>(B, H) + 8 * (lane >> 4);
-    const uint4 x0 = __builtin_bit_cast(uint4, ld_tr8_g8(&sm.Out[n][0][0], 0, 16 * (wv & 3), lane));
-    const uint4 x1 = __builtin_bit_cast(uint4, ld_tr8_g8(&sm.Out[n][0][0], 32, 16 * (wv & 3), lane));
+    const size_t off = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)tk * tok_rs<SEQ>(B, H) + 8 * (lane >> 4);
+    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 0, 16 * (wv & 3)));
+    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 32, 16 * (wv & 3)));
     if (tk < nvalid) {
-        *reinterpret_cast<uint4*>(dst + o) = x0;
-        *reinterpret_cast<uint4*>(dst + o + 32) = x1;
+        *reinterpret_cast<uint4*>(dst + off) = x0;
+        *reinterpret_cast<uint4*>(dst + off + 32) = x1;
     }
 }
 
@@ -1554,6 +1625,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
     const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
     const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
+    LaneOfs o = lane_ofs(threadIdx.x & 63);
 
     LoopPrefetch pf;
     loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
@@ -1572,29 +1644,30 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     float du_acc = 0.f;
 
     for (int c = NT - 1; c >= 0; --c) {
-        // The lane indices come from an opaque copy of the thread id made in every iteration:
-        // the LDS addresses derived from them are then formed where they are used, instead of
-        // being hoisted out of the walk and held in (spilled) registers for its whole length.
+        // The offsets and the lane indices come from opaque copies made in every iteration
+        // (see LaneOfs): nothing derived from them is hoisted out of the walk.
+        launder(o);
         int tid;
         asm volatile("" : "=v"(tid) : "0"((int)threadIdx.x));
         const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int W = wv >> 2, col = wv & 3, lr = lane & 15, lq = lane >> 4;
-        const int ch = 16 * col + lr, t4 = 16 * W + 4 * lq;
-        const int row = tid >> 4, c4 = (tid & 15) * 4;      // the thread's raw pieces
+        const int c0 = 16 * col, TW = 16 * W, t4 = TW + 4 * lq;
+        const int row = tid >> 4;                           // the thread's raw pieces: row,
+        const int tw = 4 * TS * 2 * wv;                     // at byte tw + o.th of a tile
         const int t0 = c * CL, nvalid = min(CL, T - t0);
-        // ---- S1: the raw pieces into LDS, the bonus, dS_out(c) as a bf16 tile ----
+        // ---- S1: the raw pieces into LDS, the bonus, dd, dS_out(c) as a bf16 tile ----
         {
             LoopPrefetch x = pf;
             if (nvalid < CL && row >= nvalid) {
                 const uint2 z = make_uint2(0u, 0u);
                 x.r = x.k = x.v = x.w = x.d = z;
             }
-            *reinterpret_cast<uint2*>(&sm.Vt[row][c4]) = x.v;
-            *reinterpret_cast<uint2*>(&sm.Dt[row][c4]) = x.d;
-            *reinterpret_cast<uint2*>(&sm.RT[row][c4]) = x.r;
-            *reinterpret_cast<uint2*>(&sm.KT[row][c4]) = x.k;
-            *reinterpret_cast<uint2*>(&sm.KtT[row][c4]) = x.w;          // w scratch
-            *reinterpret_cast<uint2*>(&sm.Sin[row][c4]) = x.s;
+            lds_st<uint2>(&sm.Vt[0][0], tw + o.th, x.v);
+            lds_st<uint2>(&sm.Dt[0][0], tw + o.th, x.d);
+            lds_st<uint2>(&sm.RT[0][0], tw + o.th, x.r);
+            lds_st<uint2>(&sm.KT[0][0], tw + o.th, x.k);
+            lds_st<uint2>(&sm.KtT[0][0], tw + o.th, x.w);          // w scratch
+            lds_st<uint2>(&sm.Sin[0][0], tw + o.th, x.s);
             float rf[4], kf[4];
             unpack4(x.r, rf);
             unpack4(x.k, kf);
@@ -1602,17 +1675,13 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 #pragma unroll
             for (int s = 1; s < 4; ++s) b += (rf[s] * ub[s]) * kf[s];
             b = sum16lanes(b);
-            float vf[4], df[4];
-            unpack4(x.v, vf);
-            unpack4(x.d, df);
-            float e = (df[0] * vf[0] + df[1] * vf[1]) + (df[2] * vf[2] + df[3] * vf[3]);
-            e = sum16lanes(e);
-            if ((tid & 15) == 0) {
+            const float e = sum16lanes(dot4_bf16(x.d, x.v));
+            if (lr == 0) {
                 sm.bonus[row] = b;
                 sm.dd[row] = e;
             }
             const float d4[4] = {Dst[0], Dst[1], Dst[2], Dst[3]};
-            st_ch4(&sm.dS[0][0], ch, t4, d4);
+            st_ch4o(&sm.dS[0][0], o, c0, t4 - 4 * lq, d4);
         }
         // the next chunk's loads (past chunk 0 they reload chunk 0) go out in S2, S3 and S4,
         // the stores of the chunk before in S4
@@ -1622,13 +1691,13 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // ---- S2: dA blocks; raw r, k, w at the lane's positions; the decay scan; Fm, Fk; Rm,
         // Km; Dv ----
         loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
-        if (wv < 10) loop_dA_block(sm, wv, lane);
+        if (wv < 10) loop_dA_block(sm, wv, o, lane);
         bf16x4 wrw;
         float kmf[4], rmf[4], qloc, m7;
         {
-            gl.rrw[0] = ld_tr4(&sm.RT[0][0], 16 * W, 16 * col, lane);      // x[16W + 4lq + s][ch]
-            gl.krw[0] = ld_tr4(&sm.KT[0][0], 16 * W, 16 * col, lane);
-            wrw = ld_tr4(&sm.KtT[0][0], 16 * W, 16 * col, lane);
+            gl.rrw[0] = tr4o(&sm.RT[0][0], o, TW, c0);         // x[16W + 4lq + s][ch]
+            gl.krw[0] = tr4o(&sm.KT[0][0], o, TW, c0);
+            wrw = tr4o(&sm.KtT[0][0], o, TW, c0);
             float cs[4], run = 0.f;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -1646,8 +1715,8 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             m7 = __shfl(excl + cs[3], 16 + lr);                 // G at token 16W+7
             qloc = tot - m7;                                    // b_W - mu_W
             if (lq == 0) {
-                sm.red[W][ch] = tot;
-                sm.red[4 + W][ch] = m7;
+                lds_st<float>(&sm.red[W][c0], o.tab, tot);
+                lds_st<float>(&sm.red[4 + W][c0], o.tab, m7);
             }
             float rm[4], km[4];
 #pragma unroll
@@ -1663,49 +1732,46 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             gl.kmb[0] = cvt4(km[0], km[1], km[2], km[3]);
         }
         {   // Dv[i] = sum_j S_in[i][j] dS[i][j], i = row
-            float a[4], d[4];
-            unpack4(*reinterpret_cast<const uint2*>(&sm.Sin[row][c4]), a);
-            unpack4(*reinterpret_cast<const uint2*>(&sm.dS[row][c4]), d);
-            float x = (a[0] * d[0] + a[1] * d[1]) + (a[2] * d[2] + a[3] * d[3]);
-            x = sum16lanes(x);
-            if ((tid & 15) == 0) sm.Dv[row] = x;
+            const float x = sum16lanes(dot4_bf16(lds_ld<uint2>(&sm.Sin[0][0], tw + o.th),
+                                                 lds_ld<uint2>(&sm.dS[0][0], tw + o.th)));
+            if (lr == 0) sm.Dv[row] = x;
         }
         __syncthreads();                   // raw r, k, w read; block totals and mu in `red`
 
         // ---- S3: operand tiles (channel-major), the state-gradient operand, the tables ----
         loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
         {
-            *reinterpret_cast<bf16x4*>(&sm.RT[ch][t4]) = gl.rmb[0];
-            *reinterpret_cast<bf16x4*>(&sm.KT[ch][t4]) = gl.kmb[0];
-            float after = 0.f, before = 0.f;                    // G_63 - b_W, b_{W-1}
+            lds_st<bf16x4>(&sm.RT[0][0], o.ch + tb(c0, TW), gl.rmb[0]);
+            lds_st<bf16x4>(&sm.KT[0][0], o.ch + tb(c0, TW), gl.kmb[0]);
+            float after = 0.f, before = 0.f, tJs[4];            // G_63 - b_W, b_{W-1}
 #pragma unroll
             for (int J = 0; J < 4; ++J) {
-                const float tJ = sm.red[J][ch];
-                after += J > W ? tJ : 0.f;
-                before += J < W ? tJ : 0.f;
+                tJs[J] = lds_ld<float>(&sm.red[J][c0], o.tab);
+                after += J > W ? tJs[J] : 0.f;
+                before += J < W ? tJs[J] : 0.f;
             }
             const float eg = ex2(after + qloc), kq = ex2(qloc);
             float x[4];
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * eg;
-            st_ch4(&sm.KtT[0][0], ch, t4, x);
+            st_ch4o(&sm.KtT[0][0], o, c0, TW, x);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * kq;
-            st_ch4(&sm.KqT[0][0], ch, t4, x);
+            st_ch4o(&sm.KqT[0][0], o, c0, TW, x);
             // s r e^{G_{t-1}} = s r Fm e^{mu_W}, mu_W = b_{W-1} + (G at 16W+7 within the block)
             const float emw = scale * ex2(before + m7);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = (float)gl.rrw[0][rr] * (gl.Fm[0][rr] * emw);
-            st_ch4(&sm.RiT[0][0], ch, t4, x);
+            st_ch4o(&sm.RiT[0][0], o, c0, TW, x);
             // the pair tiles of the block as the later one: s Rm_W p_WJ, p_WJ = e^{mu_W - b_J}
             float bJ = 0.f;
             for (int J = 0; J < W; ++J) {
-                bJ += sm.red[J][ch];
-                const float pf = scale * ex2(before + m7 - bJ);
+                bJ += tJs[J];
+                const float pfac = scale * ex2(before + m7 - bJ);
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) x[rr] = rmf[rr] * pf;
+                for (int rr = 0; rr < 4; ++rr) x[rr] = rmf[rr] * pfac;
                 const int pi = (W * (W - 1)) / 2 + J;
-                st_ch4(&sm.RpT[pi >> 2][0][0] + 16 * (pi & 3), ch, 4 * lq, x);
+                st_ch4o(&sm.RpT[pi >> 2][0][0], o, c0, 16 * (pi & 3), x);
             }
         }
         {
@@ -1745,22 +1811,22 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();
 
         // ---- S4: the products (dr, dk finished on the way), the state-gradient step ----
-        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, tid);
+        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o);
         loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
-        if (wv < 10) loop_A_block(sm, wv, scale, lane);
+        if (wv < 10) loop_A_block(sm, wv, scale, o, lane);
         GradOut go;
-        loop_products_rk<SEQ>(sm, W, col, scale, gl, go, lane);
+        loop_products_rk<SEQ>(sm, W, col, scale, gl, go, o);
         {
-            const float e = sm.eG63[ch];
+            const float e = lds_ld<float>(&sm.eG63[c0], o.tab);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) Dst[rr] *= e;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-                Dst = mfma32(ld_tr8(&sm.Dt[0][0], 32 * ks, 16 * W, lane), ld_dir8(&sm.RiT[0][0], ch, 32 * ks, lane), Dst);
+                Dst = mfma32(tr8o(&sm.Dt[0][0], o, 32 * ks, TW), dir8o(&sm.RiT[0][0], o, c0, 32 * ks), Dst);
         }
         du_acc += go.dup[0];
         __syncthreads();                   // A blocks in
-        go.av[0] = loop_products_v(sm, W, col, lane);
+        go.av[0] = loop_products_v(sm, W, col, o);
         // dw: the suffix sums across the four lane rows (shuffles on all lanes)
         float later;
         {
@@ -1770,14 +1836,16 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             const float d32 = __shfl_down(vsum, 32);
             vsum += lq <= 1 ? d32 : 0.f;                        // sum over lq' >= lq
             later = vsum - lt;
-            if (lq == 0) sm.red[W][ch] = vsum;                  // the wave's total
+            if (lq == 0) lds_st<float>(&sm.red[W][c0], o.tab, vsum);   // the wave's total
         }
         __syncthreads();                   // all products done; red, Pk in
 
         // ---- S5: dw; dr, dk, dv, dw staged channel-major (stored during the next step) ----
         {
-            later += sm.Dv[ch] + ((sm.Pk[0][ch] + sm.Pk[1][ch]) + (sm.Pk[2][ch] + sm.Pk[3][ch]));
-            for (int W2 = W + 1; W2 < 4; ++W2) later += sm.red[W2][ch];
+            later += lds_ld<float>(&sm.Dv[c0], o.tab) +
+                     ((lds_ld<float>(&sm.Pk[0][c0], o.tab) + lds_ld<float>(&sm.Pk[1][c0], o.tab)) +
+                      (lds_ld<float>(&sm.Pk[2][c0], o.tab) + lds_ld<float>(&sm.Pk[3][c0], o.tab)));
+            for (int W2 = W + 1; W2 < 4; ++W2) later += lds_ld<float>(&sm.red[W2][c0], o.tab);
             float g[4];
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -1789,17 +1857,18 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 }
                 if (!SEQ && ((go.floored >> rr) & 1u)) g[rr] = 0.f;
             }
-            *reinterpret_cast<bf16x4*>(&sm.Out[0][ch][t4]) = go.drb[0];
-            *reinterpret_cast<bf16x4*>(&sm.Out[1][ch][t4]) = go.dkb[0];
+            lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(c0, TW), go.drb[0]);
+            lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(c0, TW), go.dkb[0]);
             const float avf[4] = {go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]};
-            st_ch4(&sm.Out[2][0][0], ch, t4, avf);
-            st_ch4(&sm.Out[3][0][0], ch, t4, g);
+            st_ch4o(&sm.Out[2][0][0], o, c0, TW, avf);
+            st_ch4o(&sm.Out[3][0][0], o, c0, TW, g);
         }
         // no barrier here: the next step's S1 touches nothing S5 reads or writes, and its B1
         // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
     }
     __syncthreads();
-    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, 0, B, H, T, threadIdx.x);
+    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, 0, B, H, T, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                    threadIdx.x & 63, o);
     // du over the sequence: lanes of one channel (lq), then the four token blocks in order
     {
         float p = du_acc + lane_xor_swz<16>(du_acc);
