@@ -268,12 +268,8 @@ __device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2
 #endif
 
 struct WalkSmem {
-    tile_t Rm, Km;                    // diagonal-block operands (midpoint-referenced)
-    tile_t Ri, Rp;                    // r e^{G_{t-1}} (inter-chunk), r e^{G_{t-1} - b_{I-1}} (cross)
-    tile_t Kt, Vm, Ot;                // state-update operand k e^{G_63 - G}, v, o staging
-    tile_t Sin[2];                    // bf16 S_in of chunk c in Sin[c & 1]
-    uint16_t Kc[6 * 16][TS];          // cross-block sources k e^{b_{I-1} - G}, rows 16 pair(I, J)
-    float G[CL * GSG];                // cumulative log2-decay
+    // the small members and the decay view first: within the 16-bit offset of the LDS
+    // instructions
     float emu[4][KD];                 // e^{mu_I}
     float c1[4][KD];                  // e^{mu_I - b_{I-1}}            (I >= 1)
     float c3[4][KD];                  // e^{G_63 - mu_J}
@@ -282,6 +278,12 @@ struct WalkSmem {
     float tot[NTHR_W];                // build_G scratch
     float bonus[CL];
     float uh[KD];                     // u of this head
+    float G[CL * GSG];                // cumulative log2-decay
+    tile_t Rm, Km;                    // diagonal-block operands (midpoint-referenced)
+    tile_t Ri, Rp;                    // r e^{G_{t-1}} (inter-chunk), r e^{G_{t-1} - b_{I-1}} (cross)
+    tile_t Kt, Vm, Ot;                // state-update operand k e^{G_63 - G}, v, o staging
+    tile_t Sin[2];                    // bf16 S_in of chunk c in Sin[c & 1]
+    uint16_t Kc[6 * 16][TS];          // cross-block sources k e^{b_{I-1} - G}, rows 16 pair(I, J)
 };
 static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
 
@@ -554,7 +556,8 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();
         if (OUT) {
             const int t = 16 * W + lr;
-            f32x4 ao[2] = {};
+            // the 16x16x32 and the 16x16x16 products go to separate accumulators (ao, ab)
+            f32x4 ao[2] = {}, ab[2] = {};
             // inter-chunk: (r e^{G_{t-1}}) S_in
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
@@ -578,7 +581,7 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
-                    ao[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ao[tp]);
+                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ab[tp]);
             }
             // earlier blocks J < W, both operands referenced at b_{W-1}
             for (int J = 0; J < W; ++J) {
@@ -590,13 +593,13 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
-                    ao[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ao[tp]);
+                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ab[tp]);
             }
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr)
-                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * ao[tp][rr]);
+                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * (ao[tp][rr] + ab[tp][rr]));
         }
         // state update: S = diag(e^{G_63}) S + Kt^T V
 #pragma unroll
@@ -797,15 +800,16 @@ wkv6_state_scan_bwd(const uint16_t* __restrict__ dSloc, const float* __restrict_
 // Operand tiles Rm, Km, Kt and Kq = Km q_W are stored channel-major (X^T[i][t]): a lane writes
 // its 4 tokens of a channel with one 8-byte store and reads them back the same way.
 struct GradSmem {
-    tile_t Vt, Dt;                  // raw v, dO (token-major); output staging at the end
-    tile_t RT, KT;                  // raw r, k (token-major), then Rm^T, Km^T (channel-major)
-    tile_t KtT, KqT;                // Kt^T, Kq^T (channel-major)
-    tile_t Sin, dS;                 // raw w in Sin first, then S_in, dS (bf16 [i][j])
+    // the small, often-read members first: within the 16-bit offset of the LDS instructions
     float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD];
     float bonus[CL], Dv[KD];
     float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
     float red[8][KD];               // block totals and mu of the decay scan, then dw block totals
                                     // [0..3] and du partials [4..7]
+    tile_t Vt, Dt;                  // raw v, dO (token-major); output staging at the end
+    tile_t RT, KT;                  // raw r, k (token-major), then Rm^T, Km^T (channel-major)
+    tile_t KtT, KqT;                // Kt^T, Kq^T (channel-major)
+    tile_t Sin, dS;                 // raw w in Sin first, then S_in, dS (bf16 [i][j])
 };
 static_assert(2 * sizeof(GradSmem) <= 160 * 1024, "two gradient blocks must fit one CU's LDS");
 
@@ -994,6 +998,14 @@ __device__ __forceinline__ void grads_products(Smem& sm, int W, int c0, float sc
 #pragma unroll
         for (int tp = 0; tp < NTP; ++tp)
             av[tp] = mfma32(a, ld_tr8(&sm.dS[0][0], 32 * ks, c0 + 16 * tp, lane), av[tp]);
+    }
+    // the 16x16x16 products below accumulate onto a VALU copy of the 16x16x32 result, never
+    // onto the 16x16x32 result itself (no mixed-shape MFMA accumulation chain)
+    {
+        float one;
+        asm volatile("" : "=v"(one) : "0"(1.0f));
+#pragma unroll
+        for (int tp = 0; tp < NTP; ++tp) av[tp] = av[tp] * one;
     }
     {   // diagonal block: A[t = 16W+4lq+rr][tau = 16W+lr], t > tau, the u-bonus at t == tau
         f32x4 at = {};
@@ -1297,24 +1309,28 @@ wkv6_bwd_chunk_grads(const uint16_t* __restrict__ r, const uint16_t* __restrict_
 #define DAB_RS 20
 
 struct LoopSmem {
-    tile_t Vt, Dt;                  // raw v, dO (token-major)
-    tile_t RT, KT;                  // raw r, k (token-major), then Rm^T, Km^T (channel-major)
-    tile_t KtT, KqT;                // raw w in KtT first; then Kt^T, Kq^T (channel-major)
-    tile_t Sin, dS;                 // S_in, dS_out (bf16 [i][j])
-    tile_t RiT;                     // (s r e^{G_{t-1}})^T, the state-gradient step's operand
-    tile_t RpT[2];                  // (s Rm_I p_IW)^T of the six cross pairs I > W (dv)
-    tile_t Out[4];                  // dr, dk, dv, dw staged channel-major
+    // Members in the first 64 KB are reached with the 16-bit offset of the LDS instructions;
+    // past it every access costs an address add.  The small, often-read members come first,
+    // then the tiles in decreasing order of accesses per chunk.
+    float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD], eG63[KD];
+    float bonus[CL], Dv[KD], dd[CL];  // dd[t] = dO_t . v_t
+    float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
+    float red[8][KD];               // block totals and mu of the decay scan, then dw block
+                                    // totals [0..3] and du partials [4..7]
     // the 16x16 blocks of the chunk, once per chunk for all four channel columns:
     // dAb[W(W+1)/2 + J] = dA[t in W][tau in J] (W >= J; the diagonal block strictly lower),
     // bf16 row-major [t][tau]; Ab[I(I+1)/2 + W] = s A[t in I][tau in W] (I >= W; the diagonal
     // block with the u-bonus on its diagonal), bf16 in MFMA-operand order (8 bytes per lane)
     uint16_t dAb[10][16][DAB_RS];
     uint16_t Ab[10][64][4];
-    float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD], eG63[KD];
-    float bonus[CL], Dv[KD], dd[CL];  // dd[t] = dO_t . v_t
-    float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
-    float red[8][KD];               // block totals and mu of the decay scan, then dw block
-                                    // totals [0..3] and du partials [4..7]
+    tile_t Dt, dS;                  // raw dO (token-major); dS_out (bf16 [i][j])
+    tile_t KT, RT;                  // raw k, r (token-major), then Km^T, Rm^T (channel-major)
+    tile_t KtT;                     // raw w first; then Kt^T (channel-major)
+    tile_t Vt;                      // raw v (token-major)
+    tile_t KqT, RiT;                // Kq^T; (s r e^{G_{t-1}})^T, the state-gradient step's operand
+    tile_t RpT[2];                  // (s Rm_I p_IW)^T of the six cross pairs I > W (dv)
+    tile_t Sin;                     // S_in (bf16 [i][j])
+    tile_t Out[4];                  // dr, dk, dv, dw staged channel-major
 };
 static_assert(sizeof(LoopSmem) <= 160 * 1024, "one loop workgroup per CU");
 
@@ -1542,14 +1558,14 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
 // dv of the wave's token block W and value column 16 col + lr (the A blocks read from Ab).
 __device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int W, int col, const LaneOfs& o) {
     const int TW = 16 * W, c0 = 16 * col;
-    f32x4 av = {};
+    f32x4 av = {}, ab = {};          // 16x16x32 and 16x16x16 products in separate accumulators
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
         av = mfma32(tr8o(&sm.KtT[0][0], o, 32 * ks, TW), tr8o(&sm.dS[0][0], o, 32 * ks, c0), av);
-    av = mfma16(lds_ld<bf16x4>(&sm.Ab[(W * (W + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, TW, c0), av);
+    ab = mfma16(lds_ld<bf16x4>(&sm.Ab[(W * (W + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, TW, c0), ab);
     for (int I = W + 1; I < 4; ++I)
-        av = mfma16(lds_ld<bf16x4>(&sm.Ab[(I * (I + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, 16 * I, c0), av);
-    return av;
+        ab = mfma16(lds_ld<bf16x4>(&sm.Ab[(I * (I + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, 16 * I, c0), ab);
+    return av + ab;
 }
 
 // The raw pieces of one chunk a thread moves into LDS: thread (row, c4) = (tid >> 4,
