@@ -1575,6 +1575,35 @@ struct LoopPrefetch {
     uint2 r, k, v, w, d, s;
 };
 
+// Byte offsets of a thread's global pieces within a chunk, formed once per launch and passed
+// through an empty asm every chunk like LaneOfs: an address is then the chunk's wave-uniform
+// base (scalar registers) plus one of these, the base + 32-bit offset form of the vector
+// memory instructions, with no 64-bit address arithmetic per chunk.
+//   tok: token row `row` = tid >> 4 of r, k, v, w at channels c4 = 4 (tid & 15)
+//   hd:  the same row of a head-first tensor (dO) and of the S_in tile
+//   st:  token 16 (wv & 3) + lr, channels 8 lq of a gradient (the stores of loop_store)
+// With B*H <= 65535 (check_shape) a token row is at most 8 MB, so every offset fits an int.
+struct GlobOfs {
+    int tok, hd, st;
+};
+template <bool SEQ>
+__device__ __forceinline__ GlobOfs glob_ofs(int tid, int B, int H) {
+    const int row = tid >> 4, c4 = (tid & 15) * 4, rs = (int)tok_rs<SEQ>(B, H);
+    const int wv = tid >> 6, lane = tid & 63;
+    GlobOfs g;
+    g.tok = (row * rs + c4) * 2;
+    g.hd = (row * KD + c4) * 2;
+    g.st = ((16 * (wv & 3) + (lane & 15)) * rs + 8 * (lane >> 4)) * 2;
+    return g;
+}
+__device__ __forceinline__ void launder(GlobOfs& g) {
+    asm volatile("" : "+v"(g.tok), "+v"(g.hd), "+v"(g.st));
+}
+template <class T>
+__device__ __forceinline__ T gld(const void* base, int bytes) {
+    return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + (unsigned)bytes);
+}
+
 // Part PART (0: r, k; 1: v, w; 2: dO, S_in) of the loads of chunk c.  The three parts go out
 // in three phases of the step before, so the vector-memory issue of the 16 waves does not
 // pile up in one phase.
@@ -1585,22 +1614,26 @@ __device__ __forceinline__ void loop_issue(LoopPrefetch& f, const uint16_t* __re
                                            const uint16_t* __restrict__ w,
                                            const uint16_t* __restrict__ dO,
                                            const uint16_t* __restrict__ Hs, int bh, int c, int B,
-                                           int H, int T, int NT, int tid) {
-    const int row = tid >> 4, c4 = (tid & 15) * 4;
+                                           int H, int T, int NT, int tid, const GlobOfs& g) {
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     // unconditional loads (rows past a ragged end read the last token and are zeroed when
     // stored): a load under a branch makes the next wait a full one
-    const int lrow = min(row, nvalid - 1);
-    const size_t off = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)lrow * tok_rs<SEQ>(B, H) + c4;
+    int otok = g.tok, ohd = g.hd;
+    if (nvalid < CL) {
+        const int lrow = min(tid >> 4, nvalid - 1), c4 = (tid & 15) * 4;
+        otok = (lrow * (int)tok_rs<SEQ>(B, H) + c4) * 2;
+        ohd = (lrow * KD + c4) * 2;
+    }
+    const size_t base = tok_base<SEQ>(bh, t0, B, H, T);
     if (PART == 0) {
-        f.r = *reinterpret_cast<const uint2*>(r + off);
-        f.k = *reinterpret_cast<const uint2*>(k + off);
+        f.r = gld<uint2>(r + base, otok);
+        f.k = gld<uint2>(k + base, otok);
     } else if (PART == 1) {
-        f.v = *reinterpret_cast<const uint2*>(v + off);
-        f.w = *reinterpret_cast<const uint2*>(w + off);
+        f.v = gld<uint2>(v + base, otok);
+        f.w = gld<uint2>(w + base, otok);
     } else {
-        f.d = *reinterpret_cast<const uint2*>(dO + ((size_t)bh * T + t0 + lrow) * KD + c4);
-        f.s = *reinterpret_cast<const uint2*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c4);
+        f.d = gld<uint2>(dO + ((size_t)bh * T + t0) * KD, ohd);
+        f.s = gld<uint2>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD, g.hd);
     }
 }
 
@@ -1610,16 +1643,17 @@ template <bool SEQ>
 __device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restrict__ dr,
                                            uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
                                            uint16_t* __restrict__ dw, int bh, int c, int B, int H,
-                                           int T, int wv, int lane, const LaneOfs& o) {
+                                           int T, int wv, int lane, const LaneOfs& o,
+                                           const GlobOfs& g) {
     const int n = wv >> 2, tk = 16 * (wv & 3) + (lane & 15);
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    uint16_t* dst = n == 0 ? dr : n == 1 ? dk : n == 2 ? dv : dw;
-    const size_t off = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)tk * tok_rs<SEQ>(B, H) + 8 * (lane >> 4);
+    uint16_t* dst = (n == 0 ? dr : n == 1 ? dk : n == 2 ? dv : dw) + tok_base<SEQ>(bh, t0, B, H, T);
     const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 0, 16 * (wv & 3)));
     const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 32, 16 * (wv & 3)));
     if (tk < nvalid) {
-        *reinterpret_cast<uint4*>(dst + off) = x0;
-        *reinterpret_cast<uint4*>(dst + off + 32) = x1;
+        char* p = reinterpret_cast<char*>(dst) + (unsigned)g.st;
+        *reinterpret_cast<uint4*>(p) = x0;
+        *reinterpret_cast<uint4*>(p + 64) = x1;
     }
 }
 
@@ -1647,11 +1681,12 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
     const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
     LaneOfs o = lane_ofs(threadIdx.x & 63);
+    GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
 
     LoopPrefetch pf;
-    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
-    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
-    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x);
+    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
     float ub[4];                                            // u at the thread's 4 channels (bonus)
 #pragma unroll
     for (int s = 0; s < 4; ++s) ub[s] = load_u(u, u_dtype, h * KD + (threadIdx.x & 15) * 4 + s);
@@ -1668,6 +1703,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // The offsets and the lane indices come from opaque copies made in every iteration
         // (see LaneOfs): nothing derived from them is hoisted out of the walk.
         launder(o);
+        launder(go_);
         int tid;
         asm volatile("" : "=v"(tid) : "0"((int)threadIdx.x));
         const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1711,7 +1747,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 
         // ---- S2: dA blocks; raw r, k, w at the lane's positions; the decay scan; Fm, Fk; Rm,
         // Km; Dv ----
-        loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
         if (wv < 10) loop_dA_block(sm, wv, o, lane);
         bf16x4 wrw;
         float kmf[4], rmf[4], qloc, m7;
@@ -1760,7 +1796,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();                   // raw r, k, w read; block totals and mu in `red`
 
         // ---- S3: operand tiles (channel-major), the state-gradient operand, the tables ----
-        loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
         {
             lds_st<bf16x4>(&sm.RT[0][0], o.ch + tb(c0, TW), gl.rmb[0]);
             lds_st<bf16x4>(&sm.KT[0][0], o.ch + tb(c0, TW), gl.kmb[0]);
@@ -1832,8 +1868,8 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();
 
         // ---- S4: the products (dr, dk finished on the way), the state-gradient step ----
-        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o);
-        loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid);
+        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o, go_);
+        loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
         if (wv < 10) loop_A_block(sm, wv, scale, o, lane);
         GradOut go;
         loop_products_rk<SEQ>(sm, W, col, scale, gl, go, o);
@@ -1889,7 +1925,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     }
     __syncthreads();
     loop_store<SEQ>(sm, dr, dk, dv, dw, bh, 0, B, H, T, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
-                    threadIdx.x & 63, o);
+                    threadIdx.x & 63, o, go_);
     // du over the sequence: lanes of one channel (lq), then the four token blocks in order
     {
         float p = du_acc + lane_xor_swz<16>(du_acc);
