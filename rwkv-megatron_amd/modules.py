@@ -72,13 +72,14 @@ def _splitk_wgrad(dy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype) -> torc
     A projection's weight gradient has a small output (O x I, e.g. 2048 x 2048 = 64 tiles
     of 256 x 256) and a long reduction (16 K tokens): one GEMM occupies a quarter of the
     256 CUs.  The tokens are split into s chunks (s doubles while the tile count stays below
-    512), the chunks run as one batched GEMM with fp32 outputs, and the partials are summed
-    in a fixed order."""
+    512, at most 4: measured on MI355X at 16 K tokens, a 2048 x 2048 dW takes 155 us with
+    s = 4 against 170 us with s = 8, whose partial sum reads twice the bytes), the chunks run
+    as one batched GEMM with fp32 outputs, and the partials are summed in a fixed order."""
     N, O = dy.shape
     I = x.shape[1]
     tiles = -(-O // 256) * -(-I // 256)
     s = 1
-    while s < 8 and tiles * s < 512 and N % (2 * s) == 0:
+    while s < 4 and tiles * s < 512 and N % (2 * s) == 0:
         s *= 2
     if s == 1:
         return (dy.t() @ x).to(dtype)
