@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define RWKV6_ABI_VERSION 2
+#define RWKV6_ABI_VERSION 3
 
 enum rwkv6_status {
     RWKV6_OK = 0,
@@ -134,12 +134,13 @@ int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, 
                         void* out, int64_t N, int64_t E, int64_t C, int64_t R, void* stream);
 /* Backward of rwkv6_ddlerp_lora_fwd for d_mixed (5 device pointers, [T,B,C] bf16):
  *   d_mexp [5,N,C] bf16 = d_mixed * (shift(x) - x)   (the LoRA up-projection's output gradient)
- *   d_delta_part [N,C] f32 = sum_e d_mixed_e (m_e + bias_e),   d_sum [N,C] f32 = sum_e d_mixed_e
- *   d_bias [5,C] (param_dtype).  m is recomputed on MFMA from neck and w_up_t. */
+ *   d_delta_part [N,C] bf16 = sum_e d_mixed_e (m_e + bias_e),   d_sum [N,C] bf16 = sum_e d_mixed_e
+ *   (summed in fp32, rounded once), d_bias [5,C] (param_dtype).  m is recomputed on MFMA from
+ *   neck and w_up_t. */
 size_t rwkv6_ddlerp_lora_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
 int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
                           int param_dtype, const void* const* d_mixed, void* d_mexp,
-                          float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
+                          void* d_delta_part, void* d_sum, void* d_bias, void* workspace,
                           int64_t T, int64_t B, int64_t C, int64_t R, void* stream);
 /* Backward of the bottleneck's tanh (autograd of torch.tanh at rwkv6_layer_specs.py:195):
  *   d_pre[n][e*R + r] = d_neck(e, n, r) * (1 - neck[n][e*R + r]^2)
@@ -159,8 +160,8 @@ int rwkv6_col_sum(const void* x, int64_t N, int64_t M, int param_dtype, void* ou
  * rwkv6_ddlerp_lora_bwd:  d_delta = d_delta_part + d_xxx * maa,
  * dx = d_sum + d_xxx - d_delta + shift^T(d_delta) -> dx [T,B,C] bf16, d_maa [C] (param_dtype). */
 size_t rwkv6_shift_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C);
-int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const float* d_delta_part,
-                         const float* d_sum, const void* d_xxx, void* dx, void* d_maa,
+int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const void* d_delta_part,
+                         const void* d_sum, const void* d_xxx, void* dx, void* d_maa,
                          void* workspace, int64_t T, int64_t B, int64_t C, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -18,6 +18,7 @@ RWKV6_ERR_LAUNCH = 3
 RWKV6_ERR_ALIGNMENT = 4
 RWKV6_F32 = 0
 RWKV6_BF16 = 1
+ABI_VERSION = 3                # RWKV6_ABI_VERSION of the header these signatures mirror
 
 _vp = ctypes.c_void_p
 _fp = ctypes.c_void_p          # float* passed as an address
@@ -87,6 +88,10 @@ def load() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        if L.rwkv6_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} has ABI version {L.rwkv6_abi_version()}, these bindings expect "
+                f"{ABI_VERSION}: rebuild it with `python rwkv-megatron_amd/build.py`")
         _lib = L
     return _lib
 

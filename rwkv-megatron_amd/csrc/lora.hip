@@ -14,7 +14,8 @@
 //                          the decay of :454);
 //   rwkv6_ddlerp_lora_bwd  recomputes m and writes d_mexp = d_mixed * delta (the LoRA GEMMs'
 //                          input), d_delta_part = sum_e d_mixed_e (m_e + bias_e),
-//                          d_sum = sum_e d_mixed_e and d_bias partials;
+//                          d_sum = sum_e d_mixed_e (both summed in fp32, stored bf16) and
+//                          d_bias partials;
 //   rwkv6_shift_lerp_bwd   finishes dx and d_maa from those and d_xxx.
 //
 // Up-projection tile: a wave owns 16 tokens x 64 channels.  MFMA 16x16x32 with
@@ -204,8 +205,8 @@ __global__ void __launch_bounds__(LORA_THR)
 rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                              const void* __restrict__ bias, int pdt,
                              const uint16_t* __restrict__ x, InPtrs<LORA_NE> dmix,
-                             uint16_t* __restrict__ dmexp, float* __restrict__ dd_out,
-                             float* __restrict__ ds_out, float* __restrict__ part, int64_t N,
+                             uint16_t* __restrict__ dmexp, uint16_t* __restrict__ dd_out,
+                             uint16_t* __restrict__ ds_out, float* __restrict__ part, int64_t N,
                              int64_t B, int64_t C, int R, int64_t per) {
     __shared__ float red[LORA_NE][2][64];          // [mix][token half of a group][channel]
     __shared__ __attribute__((aligned(16))) float bsm[LORA_NE][64];   // bias of the block's channels
@@ -325,12 +326,8 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
 #pragma unroll
         for (int P = 0; P < 2; ++P)
             if (tv[P]) {
-                float* o1 = dd_out + tok[P] * C + cl;
-                float* o2 = ds_out + tok[P] * C + cl;
-                *reinterpret_cast<float4*>(o1) = make_float4(dd[P][0], dd[P][1], dd[P][2], dd[P][3]);
-                *reinterpret_cast<float4*>(o1 + 4) = make_float4(dd[P][4], dd[P][5], dd[P][6], dd[P][7]);
-                *reinterpret_cast<float4*>(o2) = make_float4(ds[P][0], ds[P][1], ds[P][2], ds[P][3]);
-                *reinterpret_cast<float4*>(o2 + 4) = make_float4(ds[P][4], ds[P][5], ds[P][6], ds[P][7]);
+                store8(dd_out + tok[P] * C + cl, dd[P]);
+                store8(ds_out + tok[P] * C + cl, ds[P]);
             }
     }
     __syncthreads();
@@ -349,7 +346,7 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
 #define SLB_SS 8
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa, int pdt,
-                            const float* __restrict__ dd, const float* __restrict__ ds,
+                            const uint16_t* __restrict__ dd, const uint16_t* __restrict__ ds,
                             const uint16_t* __restrict__ dxxx, uint16_t* __restrict__ dx,
                             float* __restrict__ part, int64_t T, int64_t B, int64_t C) {
     __shared__ float red[SLB_SS][32 * 8 + 4];
@@ -369,10 +366,7 @@ rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restri
             const int64_t off = (t_hi * B + b) * C + 8 * cg;
             float g[8], dxx[8];
             load8(dxxx + off, dxx);
-            const float4 d0 = *reinterpret_cast<const float4*>(dd + off);
-            const float4 d1 = *reinterpret_cast<const float4*>(dd + off + 4);
-            g[0] = d0.x; g[1] = d0.y; g[2] = d0.z; g[3] = d0.w;
-            g[4] = d1.x; g[5] = d1.y; g[6] = d1.z; g[7] = d1.w;
+            load8(dd + off, g);
 #pragma unroll
             for (int s = 0; s < 8; ++s) nd[s] = g[s] + dxx[s] * mv[s];
         } else {
@@ -386,16 +380,8 @@ rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restri
             if (t > 0) load8(x + off - B * C, xp);
             else for (int s = 0; s < 8; ++s) xp[s] = 0.f;
             load8(dxxx + off, dxx);
-            {
-                const float4 a0 = *reinterpret_cast<const float4*>(dd + off);
-                const float4 a1 = *reinterpret_cast<const float4*>(dd + off + 4);
-                const float4 b0 = *reinterpret_cast<const float4*>(ds + off);
-                const float4 b1 = *reinterpret_cast<const float4*>(ds + off + 4);
-                ddv[0] = a0.x; ddv[1] = a0.y; ddv[2] = a0.z; ddv[3] = a0.w;
-                ddv[4] = a1.x; ddv[5] = a1.y; ddv[6] = a1.z; ddv[7] = a1.w;
-                dsv[0] = b0.x; dsv[1] = b0.y; dsv[2] = b0.z; dsv[3] = b0.w;
-                dsv[4] = b1.x; dsv[5] = b1.y; dsv[6] = b1.z; dsv[7] = b1.w;
-            }
+            load8(dd + off, ddv);
+            load8(ds + off, dsv);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const float dlt = ddv[s] + dxx[s] * mv[s];
@@ -594,7 +580,7 @@ size_t rwkv6_ddlerp_lora_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
 
 int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, const void* bias,
                           int param_dtype, const void* const* d_mixed, void* d_mexp,
-                          float* d_delta_part, float* d_sum, void* d_bias, void* workspace,
+                          void* d_delta_part, void* d_sum, void* d_bias, void* workspace,
                           int64_t T, int64_t B, int64_t C, int64_t R, void* stream) {
     if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
     int st = lora_check(LORA_NE, T * B, C, R, param_dtype);
@@ -609,7 +595,7 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
         return RWKV6_ERR_ALIGNMENT;
     if (T > 0) {
         const size_t act = (size_t)(T * B * C) * 2, par = (size_t)(LORA_NE * C) * param_bytes(param_dtype);
-        if (any_alias({{d_mexp, LORA_NE * act}, {d_delta_part, 2 * act}, {d_sum, 2 * act}, {d_bias, par},
+        if (any_alias({{d_mexp, LORA_NE * act}, {d_delta_part, act}, {d_sum, act}, {d_bias, par},
                        {workspace, rwkv6_ddlerp_lora_bwd_workspace_bytes(T, B, C)}},
                       {{x, act}, {neck, (size_t)(T * B * LORA_NE * R) * 2},
                        {w_up_t, (size_t)(LORA_NE * C * R) * 2}, {bias, par}, {dm.p[0], act},
@@ -623,7 +609,8 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
         hipLaunchKernelGGL(rwkv6_ddlerp_lora_bwd_kernel, up_grid(N, C), dim3(LORA_THR),
                            lora_lds_bytes(LORA_NE, (int)R), s,
                            (const uint16_t*)neck, (const uint16_t*)w_up_t, bias, param_dtype,
-                           (const uint16_t*)x, dm, (uint16_t*)d_mexp, d_delta_part, d_sum, part, N,
+                           (const uint16_t*)x, dm, (uint16_t*)d_mexp, (uint16_t*)d_delta_part,
+                           (uint16_t*)d_sum, part, N,
                            B, C, (int)R, up_per(N));
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((LORA_NE * C + 31) / 32)),
                        dim3(LORA_THR), 0, s, part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias);
@@ -636,8 +623,8 @@ size_t rwkv6_shift_lerp_bwd_workspace_bytes(int64_t T, int64_t B, int64_t C) {
     return (size_t)((ntb > 0 ? ntb : 1) * B * C) * sizeof(float);
 }
 
-int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const float* d_delta_part,
-                         const float* d_sum, const void* d_xxx, void* dx, void* d_maa,
+int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const void* d_delta_part,
+                         const void* d_sum, const void* d_xxx, void* dx, void* d_maa,
                          void* workspace, int64_t T, int64_t B, int64_t C, void* stream) {
     if (T < 0 || B < 1 || C < 8) return RWKV6_ERR_INVALID_ARG;
     if (C % 8) return RWKV6_ERR_UNSUPPORTED;
@@ -651,7 +638,7 @@ int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const 
     {
         const size_t act = (size_t)(T * B * C) * 2, par = (size_t)C * param_bytes(param_dtype);
         if (any_alias({{dx, act}, {d_maa, par}, {workspace, rwkv6_shift_lerp_bwd_workspace_bytes(T, B, C)}},
-                      {{x, act}, {maa, par}, {d_delta_part, 2 * act}, {d_sum, 2 * act}, {d_xxx, act}}))
+                      {{x, act}, {maa, par}, {d_delta_part, act}, {d_sum, act}, {d_xxx, act}}))
             return RWKV6_ERR_INVALID_ARG;
     }
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -660,8 +647,9 @@ int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const 
     if (T > 0)
         hipLaunchKernelGGL(rwkv6_shift_lerp_bwd_kernel,
                            dim3((unsigned)ntb, (unsigned)((C / 8 + 31) / 32), (unsigned)B),
-                           dim3(LORA_THR), 0, s, (const uint16_t*)x, maa, param_dtype, d_delta_part,
-                           d_sum, (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
+                           dim3(LORA_THR), 0, s, (const uint16_t*)x, maa, param_dtype,
+                           (const uint16_t*)d_delta_part, (const uint16_t*)d_sum,
+                           (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(LORA_THR), 0, s,
                        part, T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
     return launch_status();

@@ -174,7 +174,7 @@ class _TokenShiftMix(torch.autograd.Function):
         d_mixed = [torch.zeros_like(x) if d is None else _c(d.to(torch.bfloat16)) for d in d_mixed]
         b, pdt = _param(bias)
         d_mexp = torch.empty(NE, N, C, dtype=torch.bfloat16, device=dev)
-        dd = torch.empty(N, C, dtype=torch.float32, device=dev)
+        dd = torch.empty(N, C, dtype=torch.bfloat16, device=dev)
         dsum = torch.empty_like(dd)
         d_bias = torch.empty(NE, C, dtype=b.dtype, device=dev)
         ws = torch.empty(L.rwkv6_ddlerp_lora_bwd_workspace_bytes(T, B, C), dtype=torch.uint8, device=dev)

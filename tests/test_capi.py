@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_version_and_strerror(pkg):
     L = pkg._lib.load()
-    assert L.rwkv6_abi_version() == 2
+    assert L.rwkv6_abi_version() == pkg._lib.ABI_VERSION == 3
     assert L.rwkv6_strerror(0) == b"ok"
     assert b"64" in L.rwkv6_strerror(2)
     assert L.rwkv6_strerror(12345) == b"unknown rwkv6 status code"
