@@ -340,61 +340,57 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
 // Backward of xxx = x + (shift(x) - x) * maa together with the rest of the input gradient:
 //   d_delta[t] = dd[t] + d_xxx[t] maa,   dx[t] = ds[t] + d_xxx[t] - d_delta[t] + d_delta[t+1]
 //   d_maa partial = sum_t d_xxx[t] (x[t-1] - x[t])  -> part[tblk * B + b][C]
-// Block = 8 token sub-segments x 32 channel groups (8 channels each) over 64 tokens of one
-// batch row; a thread walks its 8 tokens backwards carrying d_delta[t+1].
-#define SLB_TB 64
+// Block = 8 token slots x 32 channel groups (8 channels each) over SLB_TB tokens of one batch
+// row; thread (ts, cgl) takes the tokens ts + 8j.  Every token is independent: d_delta[t+1] is
+// formed again from the next token's dd and d_xxx (re-read, mostly from L2) rather than carried
+// along a walk, so all of a thread's loads can be in flight together.  Loads clamp the token
+// (no branch); a token past the end stores nothing and adds nothing.
+#define SLB_TB 32
 #define SLB_SS 8
+#define SLB_NJ (SLB_TB / SLB_SS)
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa, int pdt,
                             const uint16_t* __restrict__ dd, const uint16_t* __restrict__ ds,
                             const uint16_t* __restrict__ dxxx, uint16_t* __restrict__ dx,
                             float* __restrict__ part, int64_t T, int64_t B, int64_t C) {
     __shared__ float red[SLB_SS][32 * 8 + 4];
-    const int ss = threadIdx.x >> 5, cgl = threadIdx.x & 31;
+    const int ts = threadIdx.x >> 5, cgl = threadIdx.x & 31;
     const int64_t C8 = C / 8, cg = (int64_t)blockIdx.y * 32 + cgl;
     const int64_t b = blockIdx.z;
-    const int64_t t_lo = (int64_t)blockIdx.x * SLB_TB + SLB_SS * ss;
-    const int64_t t_hi = t_lo + SLB_SS < T ? t_lo + SLB_SS : T;
     float acc[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc[s] = 0.f;
-    if (cg < C8 && t_lo < T) {
-        float mv[8], nd[8], xv[8];
+    if (cg < C8) {
+        float mv[8];
         load_param8(maa, pdt, 8 * cg, mv);
-        // d_delta of the token after the segment
-        if (t_hi < T) {
-            const int64_t off = (t_hi * B + b) * C + 8 * cg;
-            float g[8], dxx[8];
-            load8(dxxx + off, dxx);
-            load8(dd + off, g);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) nd[s] = g[s] + dxx[s] * mv[s];
-        } else {
-#pragma unroll
-            for (int s = 0; s < 8; ++s) nd[s] = 0.f;
-        }
-        load8(x + ((t_hi - 1) * B + b) * C + 8 * cg, xv);
-        for (int64_t t = t_hi - 1; t >= t_lo; --t) {
-            const int64_t off = (t * B + b) * C + 8 * cg;
-            float xp[8], dxx[8], ddv[8], dsv[8], out[8];
-            if (t > 0) load8(x + off - B * C, xp);
-            else for (int s = 0; s < 8; ++s) xp[s] = 0.f;
+        for (int j = 0; j < SLB_NJ; ++j) {
+            const int64_t t = (int64_t)blockIdx.x * SLB_TB + ts + SLB_SS * j;
+            const int64_t tc = t < T ? t : T - 1;
+            const int64_t tp = tc > 0 ? tc - 1 : 0, tn = tc + 1 < T ? tc + 1 : tc;
+            const float kv = t < T ? 1.f : 0.f, kp = tc > 0 ? 1.f : 0.f, kn = tc + 1 < T ? 1.f : 0.f;
+            const int64_t off = (tc * B + b) * C + 8 * cg;
+            const int64_t offp = (tp * B + b) * C + 8 * cg, offn = (tn * B + b) * C + 8 * cg;
+            float xv[8], xp[8], dxx[8], ddv[8], dsv[8], dxn[8], ddn[8], out[8];
+            load8(x + off, xv);
+            load8(x + offp, xp);
             load8(dxxx + off, dxx);
             load8(dd + off, ddv);
             load8(ds + off, dsv);
+            load8(dxxx + offn, dxn);
+            load8(dd + offn, ddn);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const float dlt = ddv[s] + dxx[s] * mv[s];
-                out[s] = dsv[s] + dxx[s] - dlt + nd[s];
-                nd[s] = dlt;
-                acc[s] += dxx[s] * (xp[s] - xv[s]);
-                xv[s] = xp[s];
+                const float nd = kn * (ddn[s] + dxn[s] * mv[s]);
+                out[s] = dsv[s] + dxx[s] - dlt + nd;
+                acc[s] += kv * (dxx[s] * (kp * xp[s] - xv[s]));
             }
-            store8(dx + off, out);
+            if (t < T) store8(dx + off, out);
         }
     }
 #pragma unroll
-    for (int s = 0; s < 8; ++s) red[ss][8 * cgl + s] = acc[s];
+    for (int s = 0; s < 8; ++s) red[ts][8 * cgl + s] = acc[s];
     __syncthreads();
     const int64_t P_row = (int64_t)blockIdx.x * B + b;
     for (int c = threadIdx.x; c < 256; c += LORA_THR) {
