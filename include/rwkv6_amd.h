@@ -189,6 +189,14 @@ int rwkv6_sigmoid_gate_fwd(const void* out, const void* gate_pre, void* y, int64
 int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy, void* d_out,
                            void* d_gate_pre, int64_t n, void* stream);
 
+/* out[i] = sum_{j < S} part[j*n + i] in fp32, j in order, written in out_dtype (RWKV6_F32 or
+ * RWKV6_BF16); n a multiple of 8, 1 <= S <= 64.  No counterpart in the reference: the weight
+ * gradient of each projection (autograd of linear_proj / linear_up / ... in
+ * rwkv6_layer_specs.py) is computed here as S token-split partial GEMMs (to fill the device),
+ * and this sums them in one pass. */
+int rwkv6_sum_partials(const float* part, int64_t S, int64_t n, int out_dtype, void* out,
+                       void* stream);
+
 /* ------------------------------------------------------------------------
  * GroupNorm(per head) * silu(gate), fused with the head-first -> sequence-first
  * layout change of rwkv6_layer_specs.py:341 and :461-465.

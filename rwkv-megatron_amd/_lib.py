@@ -62,6 +62,7 @@ SIGNATURES = {
     "rwkv6_relu_sq_bwd": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "rwkv6_sigmoid_gate_fwd": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "rwkv6_sigmoid_gate_bwd": (_int, [_vp] * 5 + [_i64, _vp]),
+    "rwkv6_sum_partials": (_int, [_fp, _i64, _i64, _int, _vp, _vp]),
     "rwkv6_gn_gate_fwd": (_int, [_vp, _int, _vp, _vp, _vp, _int, _f32, _vp, _fp, _fp] + [_i64] * 4 + [_vp]),
     "rwkv6_gn_gate_bwd_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
     "rwkv6_gn_gate_bwd": (_int, [_vp, _int, _vp, _vp, _vp, _int, _fp, _fp] + [_vp] * 5 + [_vp]

@@ -210,6 +210,39 @@ rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restric
     }
 }
 
+// out[i] = sum_{j < S} part[j][i] (fp32, j in order), written bf16 or fp32: the partial
+// weight gradients of a token-split GEMM summed in one pass (instead of a reduction kernel
+// writing fp32 and a cast kernel).  Thread = 8 consecutive elements; all S partial loads are
+// issued before the sum.
+__global__ void __launch_bounds__(MIX_THR)
+rwkv6_sum_partials_kernel(const float* __restrict__ part, int S, int64_t n8, int64_t n, int pdt,
+                          void* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
+    if (i >= n8) return;
+    const float* p = part + 8 * i;
+    float acc[8];
+    {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        acc[0] = a.x; acc[1] = a.y; acc[2] = a.z; acc[3] = a.w;
+        acc[4] = b.x; acc[5] = b.y; acc[6] = b.z; acc[7] = b.w;
+    }
+#pragma unroll 4
+    for (int j = 1; j < S; ++j) {
+        const float4 a = *reinterpret_cast<const float4*>(p + (int64_t)j * n);
+        const float4 b = *reinterpret_cast<const float4*>(p + (int64_t)j * n + 4);
+        acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+        acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    }
+    if (pdt == RWKV6_BF16) {
+        store8(reinterpret_cast<uint16_t*>(out) + 8 * i, acc);
+    } else {
+        float* o = reinterpret_cast<float*>(out) + 8 * i;
+        *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4*>(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+}
+
 // Elementwise epilogues over n bf16 elements (n % 8 == 0); each thread owns two 16-byte
 // vectors, both loads issued before any arithmetic.
 #define EW_VEC 2          // 16-byte pieces per thread.  Loads and stores clamp the index
@@ -469,6 +502,20 @@ int rwkv6_sigmoid_gate_bwd(const void* out, const void* gate_pre, const void* dy
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)out,
                        (const uint16_t*)gate_pre, (const uint16_t*)dy, (uint16_t*)d_out,
                        (uint16_t*)d_gate_pre, n / 8);
+    return launch_status();
+}
+
+int rwkv6_sum_partials(const float* part, int64_t S, int64_t n, int out_dtype, void* out,
+                       void* stream) {
+    if (S < 1 || S > 64 || n < 0) return RWKV6_ERR_INVALID_ARG;
+    if (out_dtype != RWKV6_F32 && out_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
+    int st = ew_check(n, {part, out});
+    if (st || n == 0) return st;
+    if (any_alias({{out, (size_t)n * param_bytes(out_dtype)}}, {{part, (size_t)(S * n) * 4}}))
+        return RWKV6_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(rwkv6_sum_partials_kernel, dim3(nblocks(n / 8)), dim3(MIX_THR), 0,
+                       reinterpret_cast<hipStream_t>(stream), part, (int)S, n / 8, n, out_dtype,
+                       out);
     return launch_status();
 }
 

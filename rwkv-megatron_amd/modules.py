@@ -85,7 +85,7 @@ def _splitk_wgrad(dy: torch.Tensor, x: torch.Tensor, dtype: torch.dtype) -> torc
         return (dy.t() @ x).to(dtype)
     part = torch.bmm(dy.view(s, N // s, O).transpose(1, 2), x.view(s, N // s, I),
                      out_dtype=torch.float32)
-    return part.sum(0).to(dtype)
+    return timemix.sum_partials(part, dtype)
 
 
 class _LinearFn(torch.autograd.Function):

@@ -125,6 +125,20 @@ def gn_gate_fwd(o, head_first, g_pre, gamma, beta, eps):
 # autograd Functions
 # ---------------------------------------------------------------------------
 
+def sum_partials(part: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """part [S, ...] fp32 -> sum over S in a fixed order, in `dtype` (bf16, else fp32), by
+    rwkv6_sum_partials: one pass instead of a reduction and a cast."""
+    if part.dtype != torch.float32 or part.device.type != "cuda":
+        raise TypeError("sum_partials takes fp32 partials on the GPU")
+    part = _c(part)
+    bf = dtype == torch.bfloat16
+    out = torch.empty(part.shape[1:], dtype=torch.bfloat16 if bf else torch.float32, device=part.device)
+    _lib.check(_lib.load().rwkv6_sum_partials(_p(part), part.shape[0], out.numel(),
+                                              _lib.RWKV6_BF16 if bf else _lib.RWKV6_F32, _p(out),
+                                              _stream(part.device)), "rwkv6_sum_partials")
+    return out if bf else out.to(dtype)
+
+
 def _wgrad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """a^T @ b for a [N,P], b [N,Q] bf16 with fp32 accumulation, split over N into s batched
     products (a weight gradient has a small output and a long reduction: one GEMM leaves most
@@ -133,7 +147,7 @@ def _wgrad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     s = next(d for d in (8, 4, 2, 1) if N % d == 0)
     part = torch.bmm(a.reshape(s, N // s, a.shape[1]).transpose(1, 2),
                      b.reshape(s, N // s, b.shape[1]), out_dtype=torch.float32)
-    return part.sum(0)
+    return sum_partials(part, torch.float32)
 
 
 class _TokenShiftMix(torch.autograd.Function):

@@ -254,3 +254,32 @@ def test_col_sum(pkg, N, M, dtype):
     assert got.dtype == dtype and torch.equal(got, again)
     # fp32 sums of N terms of magnitude ~1: error ~ N * 2^-24 * sqrt(N)-scale, well inside the bar
     _check("col_sum", _n(got), ref)
+
+
+@pytest.mark.parametrize("S,n", [(1, 8), (2, 1000 * 8), (4, 2048 * 2048), (7, 2048 * 160), (64, 24)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sum_partials(pkg, S, n, dtype):
+    """rwkv6_sum_partials against a left-to-right fp32 sum on the host: bit-identical in fp32
+    (same additions in the same order), and the bf16 output is that fp32 sum rounded to nearest
+    even (torch's own fp32 -> bf16 conversion)."""
+    g = torch.Generator().manual_seed(S * 1000 + n)
+    part = torch.randn(S, n, generator=g)
+    acc = part[0].clone()
+    for j in range(1, S):
+        acc = acc + part[j]                       # fp32, left to right
+    got = pkg.timemix.sum_partials(part.to(DEV), dtype)
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and got.shape == (n,)
+    assert torch.equal(got.cpu(), acc.to(dtype))
+
+
+def test_sum_partials_rejects_bad_arguments(pkg):
+    L = pkg._lib.load()
+    x = torch.zeros(2, 16, device=DEV)
+    o = torch.empty(16, device=DEV)
+    p = lambda t: t.data_ptr()
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.rwkv6_sum_partials(p(x), 0, 16, 0, p(o), s) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_sum_partials(p(x), 2, 12, 0, p(o), s) == pkg._lib.RWKV6_ERR_UNSUPPORTED
+    assert L.rwkv6_sum_partials(p(x), 2, 16, 5, p(o), s) == pkg._lib.RWKV6_ERR_INVALID_ARG
+    assert L.rwkv6_sum_partials(p(x), 2, 16, 0, p(x), s) == pkg._lib.RWKV6_ERR_INVALID_ARG   # aliasing
