@@ -35,15 +35,6 @@ namespace {
 
 // A lane's 16 values are two runs of 8 channels: c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7),
 // so each 16-byte access instruction of a wave covers 64 contiguous bytes of every token row.
-__device__ __forceinline__ void load16(const uint16_t* row_c0, int q, bool valid, float* f) {
-    if (valid) {
-        load8(row_c0 + 8 * q, f);
-        load8(row_c0 + 32 + 8 * q, f + 8);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) f[j] = 0.f;
-    }
-}
 __device__ __forceinline__ void store16(uint16_t* row_c0, int q, const float* f) {
     store8(row_c0 + 8 * q, f);
     store8(row_c0 + 32 + 8 * q, f + 8);
@@ -140,17 +131,23 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
     // mix are in flight together
     {
         int64_t tc[2];
-        float xv[2][16], dl[2][16];
+        // x and x[t-B] of the lane's two channel runs stay packed bf16 (16 registers a token
+        // group instead of 32 as fp32: 124 registers in all, four waves per SIMD); delta is
+        // formed again for every mix
+        uint4 xr[2][2], pr[2][2];
+        float keep[2];
 #pragma unroll
         for (int P = 0; P < 2; ++P) {
             const int64_t tok = tb * LORA_TT + 64 * P + 16 * wv + L;
             tc[P] = tok < N ? tok : N - 1;
             if (LERP) {
-                const float keep_p = tc[P] >= B ? 1.f : 0.f;
-                load16(x + tc[P] * C + c0, q, true, xv[P]);
-                load16(x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + c0, q, true, dl[P]);
-#pragma unroll
-                for (int j = 0; j < 16; ++j) dl[P][j] = dl[P][j] * keep_p - xv[P][j];
+                keep[P] = tc[P] >= B ? 1.f : 0.f;
+                const uint16_t* x0 = x + tc[P] * C + c0;
+                const uint16_t* p0 = x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + c0;
+                xr[P][0] = *reinterpret_cast<const uint4*>(x0 + 8 * q);
+                xr[P][1] = *reinterpret_cast<const uint4*>(x0 + 32 + 8 * q);
+                pr[P][0] = *reinterpret_cast<const uint4*>(p0 + 8 * q);
+                pr[P][1] = *reinterpret_cast<const uint4*>(p0 + 32 + 8 * q);
             }
         }
 #pragma unroll 1
@@ -161,11 +158,23 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
             const float* bq = &bsm[e][0];
 #pragma unroll
             for (int P = 0; P < 2; ++P) {
-                float o[16];
+                float o[16], xv[16], xp[16];
+                if (LERP) {
+                    // opaque copies in every mix: the unpacked values are not hoisted out of
+                    // the mix loop (they would hold 64 registers through it)
+                    asm volatile("" : "+v"(xr[P][0].x), "+v"(xr[P][0].y), "+v"(xr[P][0].z), "+v"(xr[P][0].w),
+                                      "+v"(xr[P][1].x), "+v"(xr[P][1].y), "+v"(xr[P][1].z), "+v"(xr[P][1].w));
+                    asm volatile("" : "+v"(pr[P][0].x), "+v"(pr[P][0].y), "+v"(pr[P][0].z), "+v"(pr[P][0].w),
+                                      "+v"(pr[P][1].x), "+v"(pr[P][1].y), "+v"(pr[P][1].z), "+v"(pr[P][1].w));
+                    unpack8(xr[P][0], xv);
+                    unpack8(xr[P][1], xv + 8);
+                    unpack8(pr[P][0], xp);
+                    unpack8(pr[P][1], xp + 8);
+                }
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
-                    o[j] = LERP ? xv[P][j] + dl[P][j] * (m[P][j] + bb) : m[P][j] + bb;
+                    o[j] = LERP ? xv[j] + (xp[j] * keep[P] - xv[j]) * (m[P][j] + bb) : m[P][j] + bb;
                 }
                 store16(out.p[e] + tc[P] * ors + c0, q, o);
             }
