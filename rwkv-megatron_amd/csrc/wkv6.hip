@@ -349,6 +349,29 @@ inline int walk_segments(int64_t BH, int64_t NT, int64_t target = WALK_TARGET_IT
     return (int)((NT + NC - 1) / NC);                   // no empty segment
 }
 
+// Pieces of the forward pre-pass (wkv6_fwd_pieces): each of the P-1 earlier segments of a
+// sequence is cut into `sub` pieces of at most `ncs` chunks, `sub` the nearest integer to
+// PIECE_TARGET / (B*H*(P-1)) (about one piece per CU: with most CUs busy the pre-pass is bound
+// by HBM reads, and more, shorter pieces only add states to fold), no piece shorter than
+// PIECE_MIN_CHUNKS, and at most max_pieces pieces in all (the workspace they fill).
+#ifndef PIECE_TARGET
+#define PIECE_TARGET 256
+#endif
+#define PIECE_MIN_CHUNKS 4
+struct Pieces {
+    int sub, ncs;
+};
+inline Pieces prepass_pieces(int64_t BH, int64_t NT, int P, int64_t max_pieces) {
+    if (P <= 1 || NT <= 0) return {1, 1};
+    const int64_t NC = (NT + P - 1) / P, segs = BH * (P - 1);
+    int64_t sub = (2 * PIECE_TARGET + segs) / (2 * segs);          // nearest
+    sub = std::max<int64_t>(sub, 1);
+    sub = std::min<int64_t>(sub, std::max<int64_t>(1, NC / PIECE_MIN_CHUNKS));
+    sub = std::min<int64_t>(sub, std::max<int64_t>(1, max_pieces / segs));
+    const int64_t ncs = (NC + sub - 1) / sub;
+    return {(int)((NC + ncs - 1) / ncs), (int)ncs};      // no empty piece, sub only shrinks
+}
+
 // The backward walks each sequence in one workgroup (wkv6_bwd_loop) when that fills the device
 // or the sequences are short; otherwise the state gradients run chunk-parallel.
 inline bool bwd_loop(int64_t BH, int64_t NT) { return walk_segments(BH, NT, DSTATE_TARGET_ITEMS) == 1; }
@@ -398,22 +421,20 @@ __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restr
         *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8]);
 }
 
-// OUT = true : output walk over segment blockIdx.x % P of sequence blockIdx.x / P.
-// OUT = false: state pre-pass over segment blockIdx.x % (P-1) (segments 0..P-2): writes
-//              S_seg (fp32 [64][64]) and A_seg (total log2-decay [64]) to Sseg / Aseg.
+// Output walk over segment blockIdx.x % P of sequence blockIdx.x / P.  Segment 0 starts from
+// h0 (or zero), segment p >= 1 from Sstart[b,h][p-1] (wkv6_fwd_fold).
 // SEQ: r, k, v and the pre-activation decay are sequence-first; o is always head-first.
-template <bool SEQ, bool OUT>
+template <bool SEQ>
 __global__ void __launch_bounds__(NTHR_W) __attribute__((amdgpu_waves_per_eu(WALK_WPE)))
 wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
               const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
               const void* __restrict__ u, int u_dtype, const float* __restrict__ h0,
-              uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float* __restrict__ hT, float* __restrict__ Sseg, float* __restrict__ Aseg,
-              float scale, int B, int H, int T, int NT, int P) {
+              uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float* __restrict__ hT,
+              const float* __restrict__ Sstart, float scale, int B, int H, int T, int NT, int P) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     WalkSmem& sm = *reinterpret_cast<WalkSmem*>(smem_raw);
     float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
-    const int nseg = OUT ? P : P - 1;
-    const int bh = blockIdx.x / nseg, seg = blockIdx.x - bh * nseg, h = bh % H;
+    const int bh = blockIdx.x / P, seg = blockIdx.x - bh * P, h = bh % H;
     const int NC = (NT + P - 1) / P;
     const int c_begin = seg * NC, c_end = min(NT, c_begin + NC);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -426,32 +447,21 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     const size_t sbase = (size_t)bh * KD * KD;
 
     WalkPrefetch nx;
-    if (c_begin < c_end) walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, c_begin, B, H, T);
+    if (c_begin < c_end) walk_issue<SEQ, true>(nx, r, k, v, w, bh, c_begin, B, H, T);
 
-    // ---- starting state (a pre-pass segment starts from zero) ----
+    // ---- starting state ----
     f32x4 acc[2];
+    {
+        const float* s0 = seg > 0 ? Sstart + ((size_t)bh * (P - 1) + seg - 1) * KD * KD
+                                  : (h0 ? h0 + sbase : nullptr);
 #pragma unroll
-    for (int tp = 0; tp < 2; ++tp)
+        for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-            acc[tp][rr] = (OUT && h0) ? h0[sbase + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr]
-                                      : 0.f;
-    if (OUT) {
-        for (int q = 0; q < seg; ++q) {
-            const size_t sq = (size_t)bh * (P - 1) + q;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int i = 16 * W + 4 * lq + rr;
-                const float a = ex2(Aseg[sq * KD + i]);
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    acc[tp][rr] = a * acc[tp][rr] + Sseg[sq * KD * KD + i * KD + 32 * hh + 16 * tp + lr];
-            }
-        }
+            for (int rr = 0; rr < 4; ++rr)
+                acc[tp][rr] = s0 ? s0[(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] : 0.f;
         if (threadIdx.x < KD) sm.uh[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
         __syncthreads();
     }
-    float gsum = 0.f;                      // pre-pass: total log2-decay of channel threadIdx.x
 
     // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
     // loop's own order (the next chunk's loads, then this chunk's two stores) alone
@@ -464,7 +474,7 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         sstore16(sm.Vm, row, c8, nx.v);
         sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
         sstore16(sm.Km, row, c8, nx.k);
-        if (OUT) {
+        {
             sstore16(sm.Rm, row, c8, nx.r);
             float rf[8], kf[8], bsum = 0.f;
             unpack8(nx.r, rf);
@@ -485,9 +495,9 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         }
         // unconditional (the last iteration reloads its own chunk): loads under a branch
         // would cost the loop a full wait
-        walk_issue<SEQ, OUT>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
+        walk_issue<SEQ, true>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
         __syncthreads();
-        if (OUT) {
+        {
             walk_build_G<SEQ>(sm, nvalid, c & 1);
             // Operand tiles of this thread's piece (token t = row in block I; I is
             // wave-uniform).  Two exponentials per element; every other factor is a
@@ -535,26 +545,9 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
                 sstore16(reinterpret_cast<uint16_t (*)[TS]>(sm.Kc[16 * pi]), row & 15, c8, pack8(y));
             }
-        } else {
-            build_G<NTHR_W, SEQ>(sm.Kt, Gm, sm.tot, nvalid);
-            const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
-            if (part == 7) {
-                sm.dec[c & 1][i] = ex2(Gm[CL - 1][i]);
-                gsum += Gm[CL - 1][i];
-            }
-            float kf[8], e[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
-            {
-                float gl[8], gg[8];
-                g8(Gm, CL - 1, c8, gl);
-                g8(Gm, row, c8, gg);
-#pragma unroll
-                for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(gl[s] - gg[s]);
-            }
-            sstore16(sm.Kt, row, c8, pack8(e));
         }
         __syncthreads();
-        if (OUT) {
+        {
             const int t = 16 * W + lr;
             // the 16x16x32 and the 16x16x16 products go to separate accumulators (ao, ab)
             f32x4 ao[2] = {}, ab[2] = {};
@@ -619,28 +612,164 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
         // for those at the top of the next iteration leaves these stores in flight (vmcnt
         // counts loads and stores in issue order)
-        if (OUT) walk_store(sm, o, Hs, bh, c, T, NT);
+        walk_store(sm, o, Hs, bh, c, T, NT);
     }
 
-    // ---- end of the segment ----
-    if (!OUT) {
-        const size_t sq = (size_t)bh * (P - 1) + seg;
+    // ---- end of the sequence: the final state ----
+    if (seg == P - 1) {
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
-        if (threadIdx.x >= 7 * 64) Aseg[sq * KD + (threadIdx.x & 63)] = gsum;
-    } else {
-        if (seg == P - 1) {
+            for (int rr = 0; rr < 4; ++rr) {
+                const size_t e = (size_t)(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr;
+                Hs[(size_t)bh * (NT + 1) * KD * KD + (size_t)NT * KD * KD + e] = f2bf(acc[tp][rr]);
+                if (hT) hT[sbase + e] = acc[tp][rr];
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// forward pre-pass: the end states of runs of chunks ("pieces")
+// ---------------------------------------------------------------------------
+// Segment p of the output walk starts from the state entering its first chunk.  Each of the
+// segments 0..P-2 is cut into SUB pieces of at most NCS chunks; one workgroup per (b,h, piece)
+// walks its chunks from a zero state,
+//   S = diag(e^{G_63}) S + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T        [MFMA]
+// and writes the piece's end state S_q (fp32 [64][64]) and total log2-decay A_q ([64]).  Only
+// k, v and w are read.  Per chunk, thread (part, i) scans the log-decay of channel i over the
+// tokens 8 part .. 8 part + 7 and forms those tokens' k e^{G_63 - G} itself, written
+// channel-major (one 16-byte store) as the MFMA's A operand: no cumulative-decay tile, four
+// barriers a chunk, ~30 KB of LDS.
+struct PieceSmem {
+    float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
+    float tot[NTHR_W];                // per-part log2-decay sums
+    tile_t Km, Wt, Vm;                // raw k; raw w, then (k e^{G_63 - G})^T channel-major; v
+};
+
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR_W)
+wkv6_fwd_pieces(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                const uint16_t* __restrict__ w, float* __restrict__ Sseg, float* __restrict__ Aseg,
+                int B, int H, int T, int NT, int NC, int SUB, int NCS, int npieces) {
+    __shared__ __attribute__((aligned(16))) PieceSmem sm;
+    const int bh = blockIdx.x / npieces, q = blockIdx.x - bh * npieces;
+    const int sg = q / SUB, j = q - sg * SUB;
+    // never empty: SUB = ceil(NC / NCS) puts the last piece's start below the segment's end,
+    // and segments 0..P-2 hold NC chunks each
+    const int c_begin = sg * NC + j * NCS;
+    const int c_end = min(min(c_begin + NCS, (sg + 1) * NC), NT);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;   // state rows [16W, +16) x columns [32hh, +32)
+    const int lr = lane & 15, lq = lane >> 4;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    const int i = lane, part = wv;        // decay scan: channel i, tokens 8 part .. +7
+
+    WalkPrefetch nx;
+    walk_issue<SEQ, false>(nx, nullptr, k, v, w, bh, c_begin, B, H, T);
+    f32x4 acc[2] = {};
+    float gsum = 0.f;                      // total log2-decay of channel i (part 7)
+    for (int c = c_begin; c < c_end; ++c) {
+        const int nvalid = min(CL, T - c * CL);
+        if (nvalid < CL && row >= nvalid) nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
+        sstore16(sm.Vm, row, c8, nx.v);
+        sstore16(sm.Wt, row, c8, nx.w);
+        sstore16(sm.Km, row, c8, nx.k);
+        // unconditional (the last iteration reloads its own chunk)
+        walk_issue<SEQ, false>(nx, nullptr, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
+        __syncthreads();
+        // the part's running log2-decay (as build_G) and its raw k
+        float loc[8], run = 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; s4 += 4) {
+            const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 8 * part + s4);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int s = s4 + jj;
+                const float x = (float)x4[jj];
+                const float wn = SEQ ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+                run += fmaxf(wn, W_MIN) * RW_L2E;
+                loc[s] = run;
+            }
+        }
+        const bf16x4 ka = ld_col4(&sm.Km[0][0], 8 * part), kb = ld_col4(&sm.Km[0][0], 8 * part + 4);
+        sm.tot[part * 64 + i] = run;
+        __syncthreads();
+        {
+            // G_t = loc + (sum of the earlier parts), G_63 = run_7 + sum of parts 0..6, in the
+            // order build_G adds them
+            float off = 0.f, o7 = 0.f;
+#pragma unroll
+            for (int p = 0; p < 7; ++p) {
+                const float t = sm.tot[p * 64 + i];
+                off += p < part ? t : 0.f;
+                o7 += t;
+            }
+            const float g63 = sm.tot[7 * 64 + i] + o7;
+            const float kf[8] = {(float)ka[0], (float)ka[1], (float)ka[2], (float)ka[3],
+                                 (float)kb[0], (float)kb[1], (float)kb[2], (float)kb[3]};
+            float e[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(g63 - (loc[s] + off));
+            *reinterpret_cast<uint4*>(&sm.Wt[i][8 * part]) = pack8(e);
+            if (part == 7) {
+                sm.dec[c & 1][i] = ex2(g63);
+                gsum += g63;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
+            acc[0][rr] *= d;
+            acc[1][rr] *= d;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_dir8(&sm.Wt[0][0], 16 * W + lr, 32 * ks);
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
+                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+        }
+        __syncthreads();
+    }
+    const size_t sq = (size_t)bh * npieces + q;
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const size_t e = (size_t)(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr;
-                    Hs[(size_t)bh * (NT + 1) * KD * KD + (size_t)NT * KD * KD + e] = f2bf(acc[tp][rr]);
-                    if (hT) hT[sbase + e] = acc[tp][rr];
-                }
+    for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
+    if (part == 7) Aseg[sq * KD + i] = gsum;
+}
+
+// Start states of the output walk's segments 1..P-1: the pieces folded in order onto h0 (or
+// zero), S = 2^{A_q} S + S_q, and Sstart[b,h][p-1] = S after the pieces of segments 0..p-1.
+// One thread per state element (i, j) of one sequence, 16 blocks of 256 per sequence; the
+// pieces are loaded eight at a time (clamped, unconditional loads) ahead of the chain.
+#define FOLD_THR 256
+__global__ void __launch_bounds__(FOLD_THR)
+wkv6_fwd_fold(const float* __restrict__ Sseg, const float* __restrict__ Aseg,
+              const float* __restrict__ h0, float* __restrict__ Sstart, int npieces, int SUB,
+              int P) {
+    constexpr int BPS = KD * KD / FOLD_THR;            // blocks per sequence
+    const int bh = blockIdx.x / BPS, e = (blockIdx.x - bh * BPS) * FOLD_THR + threadIdx.x;
+    const int i = e / KD;
+    float s = h0 ? h0[(size_t)bh * KD * KD + e] : 0.f;
+    const size_t qb = (size_t)bh * npieces;
+    for (int q0 = 0; q0 < npieces; q0 += 8) {
+        float a[8], x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const size_t q = qb + min(q0 + t, npieces - 1);
+            a[t] = Aseg[q * KD + i];
+            x[t] = Sseg[q * KD * KD + e];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int q = q0 + t;
+            if (q < npieces) {
+                s = ex2(a[t]) * s + x[t];
+                if ((q + 1) % SUB == 0) Sstart[((size_t)bh * (P - 1) + (q + 1) / SUB - 1) * KD * KD + e] = s;
+            }
         }
     }
 }
@@ -2031,6 +2160,16 @@ inline void mark(void* const* ev, int i, hipStream_t s) {
     if (ev && ev[i]) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(ev[i]), s);
 }
 
+// The forward's workspace: the pre-pass pieces' end states S_q (fp32 [64][64]) and total
+// log2-decays A_q (fp32 [64]), at most max_pieces pieces, then the start states of segments
+// 1..P-1 (fp32 [64][64] each).
+inline size_t fwd_workspace_bytes(int64_t BH, int64_t NT, int64_t max_pieces) {
+    const int P = walk_segments(BH, NT);
+    const size_t n = (size_t)(BH * (P - 1) * prepass_pieces(BH, NT, P, max_pieces).sub);
+    const size_t starts = (size_t)(BH * (P - 1)) * KD * KD * 4;
+    return std::max<size_t>(256, round_up(n * KD * KD * 4) + round_up(n * KD * 4) + round_up(starts));
+}
+
 }  // namespace
 
 extern "C" {
@@ -2045,10 +2184,7 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
                                  int for_bwd) {
     if (check_shape(B, H, T, K, V) != RWKV6_OK) return 0;
     const size_t BH = (size_t)(B * H), NT = (size_t)(nchunks(T) > 0 ? nchunks(T) : 1);
-    if (!for_bwd) {                                                    // S_seg, A_seg (fp32)
-        const size_t P = (size_t)walk_segments((int64_t)BH, nchunks(T));
-        return std::max<size_t>(256, round_up(BH * (P - 1) * KD * KD * 4) + round_up(BH * (P - 1) * KD * 4));
-    }
+    if (!for_bwd) return fwd_workspace_bytes((int64_t)BH, nchunks(T), PIECE_TARGET);
     if (bwd_loop((int64_t)BH, nchunks(T))) return round_up(BH * KD * 4);   // du_part per (b,h)
     // dHs, du_part per chunk, dS_loc, dec
     return 2 * round_up(BH * NT * KD * KD * 2) + 2 * round_up(BH * NT * KD * 4);
@@ -2091,10 +2227,8 @@ int lds_attributes(hipStream_t stream) {
             size_t bytes;
         };
         const Lds list[] = {
-            {reinterpret_cast<const void*>(wkv6_fwd_walk<false, false>), sizeof(WalkSmem)},
-            {reinterpret_cast<const void*>(wkv6_fwd_walk<false, true>), sizeof(WalkSmem)},
-            {reinterpret_cast<const void*>(wkv6_fwd_walk<true, false>), sizeof(WalkSmem)},
-            {reinterpret_cast<const void*>(wkv6_fwd_walk<true, true>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<false>), sizeof(WalkSmem)},
+            {reinterpret_cast<const void*>(wkv6_fwd_walk<true>), sizeof(WalkSmem)},
             {reinterpret_cast<const void*>(wkv6_bwd_loop<false>), sizeof(LoopSmem)},
             {reinterpret_cast<const void*>(wkv6_bwd_loop<true>), sizeof(LoopSmem)},
             {reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<false>), sizeof(GradSmem)},
@@ -2110,11 +2244,13 @@ int lds_attributes(hipStream_t stream) {
     return slot.status;
 }
 
+// max_pieces bounds the pre-pass pieces (the workspace's capacity): PIECE_TARGET for a
+// workspace sized by rwkv6_wkv_workspace_bytes, the scratch array's capacity without one.
 template <bool SEQ>
 int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, const void* u,
                  int u_dtype, const float* h0, void* o, float* hT, void* saved, void* workspace,
                  int64_t B, int64_t H, int64_t T, int64_t K, int64_t V, float scale,
-                 void* stream, void* const* phase_events) {
+                 void* stream, void* const* phase_events, int64_t max_pieces = PIECE_TARGET) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
     if (u_dtype != RWKV6_F32 && u_dtype != RWKV6_BF16) return RWKV6_ERR_INVALID_ARG;
@@ -2127,7 +2263,7 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
         const size_t act = (size_t)(B * H * T) * KD * 2, st = (size_t)(B * H) * KD * KD * 4;
         const size_t ub = (size_t)H * KD * (u_dtype == RWKV6_BF16 ? 2 : 4);
         if (any_alias({{o, act}, {hT, st}, {saved, rwkv6_wkv_saved_bytes(B, H, T, K, V)},
-                       {workspace, rwkv6_wkv_workspace_bytes(B, H, T, K, V, 0)}},
+                       {workspace, fwd_workspace_bytes(B * H, nchunks(T), max_pieces)}},
                       {{r, act}, {k, act}, {v, act}, {w, act}, {u, ub}, {h0, st}}))
             return RWKV6_ERR_INVALID_ARG;
     }
@@ -2135,25 +2271,32 @@ int wkv_fwd_impl(const void* r, const void* k, const void* v, const void* w, con
     const int64_t NT = nchunks(T);
     const int BH = (int)(B * H);
     const int P = walk_segments(BH, NT);
+    const Pieces pc = prepass_pieces(BH, NT, P, max_pieces);
+    const int npieces = (P - 1) * pc.sub;                  // per sequence
     uint16_t* Hs = reinterpret_cast<uint16_t*>(saved);
     float* Sseg = reinterpret_cast<float*>(workspace);
-    float* Aseg = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
-                                           round_up((size_t)BH * (P - 1) * KD * KD * 4));
+    float* Aseg = reinterpret_cast<float*>(reinterpret_cast<char*>(Sseg) +
+                                           round_up((size_t)BH * npieces * KD * KD * 4));
+    float* Sstart = reinterpret_cast<float*>(reinterpret_cast<char*>(Aseg) +
+                                             round_up((size_t)BH * npieces * KD * 4));
     if ((st = lds_attributes(s)) != RWKV6_OK) return st;
     mark(phase_events, 0, s);
-    if (P > 1)
-        hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, false>), dim3((unsigned)(BH * (P - 1))), dim3(NTHR_W),
-                           sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
-                           (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
-                           hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
+    if (P > 1) {
+        hipLaunchKernelGGL((wkv6_fwd_pieces<SEQ>), dim3((unsigned)(BH * npieces)), dim3(NTHR_W), 0, s,
+                           (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)w, Sseg, Aseg,
+                           (int)B, (int)H, (int)T, (int)NT, (int)((NT + P - 1) / P), pc.sub, pc.ncs,
+                           npieces);
+        hipLaunchKernelGGL(wkv6_fwd_fold, dim3((unsigned)(BH * (KD * KD / FOLD_THR))), dim3(FOLD_THR), 0,
+                           s, Sseg, Aseg, h0, Sstart, npieces, pc.sub, P);
+    }
     mark(phase_events, 1, s);
     mark(phase_events, 2, s);
     mark(phase_events, 3, s);
     mark(phase_events, 4, s);
-    hipLaunchKernelGGL((wkv6_fwd_walk<SEQ, true>), dim3((unsigned)(BH * P)), dim3(NTHR_W),
+    hipLaunchKernelGGL((wkv6_fwd_walk<SEQ>), dim3((unsigned)(BH * P)), dim3(NTHR_W),
                        sizeof(WalkSmem), s, (const uint16_t*)r, (const uint16_t*)k,
                        (const uint16_t*)v, (const uint16_t*)w, u, u_dtype, h0, (uint16_t*)o, Hs,
-                       hT, Sseg, Aseg, scale, (int)B, (int)H, (int)T, (int)NT, P);
+                       hT, Sstart, scale, (int)B, (int)H, (int)T, (int)NT, P);
     mark(phase_events, 5, s);
     return launch_status();
 }
@@ -2249,15 +2392,17 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
 // forward without a workspace argument
 // ---------------------------------------------------------------------------
 // For callers that cannot allocate (code under HIP graph capture, tight serving loops): the
-// forward's only scratch, the segment states of its pre-pass (S_seg fp32 [64][64] and A_seg
-// fp32 [64] per segment), lives in this file-scope device array instead of the caller's
-// workspace.  walk_segments() gives P <= ceil(256 / (B*H)) segments per sequence, so a forward
-// never needs more than B*H*(P-1) < 256 segment states: WKV_SCRATCH_BYTES covers every shape.
+// forward's only scratch, the end states of its pre-pass pieces (S_q fp32 [64][64] and A_q
+// fp32 [64] per piece) and the segments' start states (fp32 [64][64] per segment after the
+// first), lives in this file-scope device array instead of the caller's workspace.
+// walk_segments() gives P <= ceil(256 / (B*H)) segments per sequence, so B*H*(P-1) < 256, and
+// this entry caps the pieces at WKV_SCRATCH_SEGS (fewer, longer pieces than with a workspace
+// when the cap binds): WKV_SCRATCH_BYTES covers every shape.
 // Each GPU holds its own copy for the life of the process; calls on one GPU share it (the
 // last call's contents stay), so such calls must not overlap in time on one GPU.  Nothing in
-// it has to start at zero: the pre-pass writes every segment state the output walk reads.
+// it has to start at zero: the pre-pass writes every piece state the output walk reads.
 #define WKV_SCRATCH_SEGS 256
-#define WKV_SCRATCH_BYTES ((size_t)WKV_SCRATCH_SEGS * (KD * KD * 4 + KD * 4))
+#define WKV_SCRATCH_BYTES ((size_t)WKV_SCRATCH_SEGS * (2 * KD * KD * 4 + KD * 4))
 static __device__ __align__(256) unsigned char scratch[WKV_SCRATCH_BYTES];
 
 namespace {
@@ -2297,11 +2442,12 @@ int rwkv6_wkv_fwd_noalloc(const void* r, const void* k, const void* v, const voi
                           float scale, void* stream) {
     int st = check_shape(B, H, T, K, V);
     if (st != RWKV6_OK) return st;
-    if (rwkv6_wkv_workspace_bytes(B, H, T, K, V, 0) > WKV_SCRATCH_BYTES) return RWKV6_ERR_UNSUPPORTED;
+    if (fwd_workspace_bytes(B * H, nchunks(T), WKV_SCRATCH_SEGS) > WKV_SCRATCH_BYTES)
+        return RWKV6_ERR_UNSUPPORTED;
     void* ws = nullptr;
     if ((st = scratch_address(reinterpret_cast<hipStream_t>(stream), &ws)) != RWKV6_OK) return st;
     return wkv_fwd_impl<false>(r, k, v, w, u, u_dtype, h0, o, hT, saved, ws, B, H, T, K, V, scale,
-                               stream, nullptr);
+                               stream, nullptr, WKV_SCRATCH_SEGS);
 }
 
 int rwkv6_wkv_fwd_ex(const void* r, const void* k, const void* v, const void* w, const void* u,
