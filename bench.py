@@ -206,19 +206,31 @@ def config1_bench(pkg, gpu_steps, with_cpu):
     return out
 
 
-def bwd_loop(BH, T):
-    """Whether the library's backward runs as one reverse walk per (b,h) (wkv6_bwd_loop): the
-    rule of walk_segments() in csrc/wkv6.hip with a 256-workgroup target."""
+def bwd_walk_segments(BH, T):
+    """Segments per sequence of the library's reverse walk (wkv6_bwd_loop), 0 when the backward
+    runs chunk-parallel: the rule of bwd_walk_segments() in csrc/wkv6.hip (walk_segments() with
+    a 256-workgroup target; the walk when it is one segment or the segments fill the device)."""
     NT = -(-T // 64)
     if NT <= 0:
-        return True
+        return 1
     P = min(-(-256 // BH), max(1, NT // 8))
     NC = -(-NT // P)
-    return -(-NT // NC) == 1
+    P = -(-NT // NC)
+    return P if P == 1 or BH * P >= 256 else 0
 
 
 def bwd_kernel(BH, T):
-    return "wkv6_bwd_loop" if bwd_loop(BH, T) else "wkv6_bwd_chunk_grads"
+    return "wkv6_bwd_loop" if bwd_walk_segments(BH, T) else "wkv6_bwd_chunk_grads"
+
+
+def bwd_path(BH, T):
+    P = bwd_walk_segments(BH, T)
+    if P == 1:
+        return "reverse walk (wkv6_bwd_loop)"
+    if P > 1:
+        return (f"segmented reverse walk ({P} segments: wkv6_bwd_pieces, wkv6_bwd_fold, "
+                "wkv6_bwd_loop)")
+    return "chunk-parallel (wkv6_bwd_chunk_dstate, wkv6_state_scan_bwd, wkv6_bwd_chunk_grads)"
 
 
 def measured_traffic(B, H, T):
@@ -462,11 +474,12 @@ def main():
         "wkv6_tflops": tflops,
         "wkv6_pct_bf16_mfma_peak": 100.0 * tflops / BF16_PEAK_TFLOPS,
         "wkv6_alg_hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        # bwd phases: state pre-pass (backward pieces, or chunk dS_loc), then their fold (or
+        # the chunk scan), then the gradients (the walk, or the chunk gradient kernel), du
         "phase_ms": {"fwd_segment_states": fwd_ph[0], "fwd_walk": fwd_ph[2],
-                     "bwd_chunk_dstate": bwd_ph[0], "bwd_state_scan": bwd_ph[1],
+                     "bwd_state_pre_pass": bwd_ph[0], "bwd_state_fold_or_scan": bwd_ph[1],
                      "bwd_grads": bwd_ph[2], "bwd_du_reduce": bwd_ph[3]},
-        "bwd_path": "reverse walk (wkv6_bwd_loop)" if bwd_loop(B * H, T) else
-                    "chunk-parallel (wkv6_bwd_chunk_dstate, wkv6_state_scan_bwd, wkv6_bwd_chunk_grads)",
+        "bwd_path": bwd_path(B * H, T),
         "roofline": {"kernel": bwd_kernel(B * H, T), "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": measured_traffic(B, H, T)},

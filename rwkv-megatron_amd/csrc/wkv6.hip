@@ -373,8 +373,14 @@ inline Pieces prepass_pieces(int64_t BH, int64_t NT, int P, int64_t max_pieces) 
 }
 
 // The backward walks each sequence in one workgroup (wkv6_bwd_loop) when that fills the device
-// or the sequences are short; otherwise the state gradients run chunk-parallel.
-inline bool bwd_loop(int64_t BH, int64_t NT) { return walk_segments(BH, NT, DSTATE_TARGET_ITEMS) == 1; }
+// or the sequences are short; with fewer sequences, each is cut into segments like the
+// forward's as long as the (b,h, segment) workgroups still fill the device (a segment walks at
+// ~6 us a chunk whatever the occupancy).  Otherwise (few, short segments) the state gradients
+// run chunk-parallel.  Returns the segment count of the walk, or 0 for the chunk-parallel form.
+inline int bwd_walk_segments(int64_t BH, int64_t NT) {
+    const int P = walk_segments(BH, NT, DSTATE_TARGET_ITEMS);
+    return (P == 1 || BH * P >= DSTATE_TARGET_ITEMS) ? P : 0;
+}
 
 struct WalkPrefetch {
     uint4 r, k, v, w;
@@ -769,6 +775,155 @@ wkv6_fwd_fold(const float* __restrict__ Sseg, const float* __restrict__ Aseg,
             if (q < npieces) {
                 s = ex2(a[t]) * s + x[t];
                 if ((q + 1) % SUB == 0) Sstart[((size_t)bh * (P - 1) + (q + 1) / SUB - 1) * KD * KD + e] = s;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward pre-pass: the state gradients runs of chunks ("pieces") hand to the left
+// ---------------------------------------------------------------------------
+// With the reverse walk cut into P segments, segment p starts at its last chunk from the
+// state gradient dS_end(p) the later segments hand it.  Each of the segments 1..P-1 is cut into
+// SUB pieces of at most NCS chunks (trailing pieces of a short last segment are empty); one
+// workgroup per (b,h, piece) walks its chunks from the last to the first from a zero state
+// gradient,
+//   dS = diag(e^{G_63}) dS + s sum_t (r_t e^{G_{t-1}}) dO_t^T                  [MFMA]
+// and writes the piece's dS_q (fp32 [64][64]) and total log2-decay A_q ([64]).  Reads r, w
+// (sequence-first for SEQ) and dO (head-first); the per-thread decay scan of wkv6_fwd_pieces
+// writes r e^{G_{t-1}} channel-major as the MFMA's A operand.
+struct BwdPieceSmem {
+    float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
+    float tot[NTHR_W];                // per-part log2-decay sums
+    tile_t Rm, Wt, Dm;                // raw r; raw w, then (r e^{G_{t-1}})^T channel-major; dO
+};
+
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR_W)
+wkv6_bwd_pieces(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
+                const uint16_t* __restrict__ dO, float* __restrict__ dSp, float* __restrict__ Ap,
+                float scale, int B, int H, int T, int NT, int NC, int SUB, int NCS, int npieces) {
+    __shared__ __attribute__((aligned(16))) BwdPieceSmem sm;
+    const int bh = blockIdx.x / npieces, q = blockIdx.x - bh * npieces;
+    const int sg = 1 + q / SUB, j = q - (sg - 1) * SUB;            // segments 1..P-1
+    const int c_begin = sg * NC + j * NCS;
+    const int c_end = min(min(c_begin + NCS, (sg + 1) * NC), NT);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;   // dS rows [16W, +16) x columns [32hh, +32)
+    const int lr = lane & 15, lq = lane >> 4;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    const int i = lane, part = wv;        // decay scan: channel i, tokens 8 part .. +7
+
+    // the 16-byte pieces of r, w, dO this thread stores (rows past a ragged end read the last
+    // token; they are zeroed before the store)
+    uint4 xr = make_uint4(0u, 0u, 0u, 0u), xw = xr, xd = xr;
+    auto issue = [&](int c) {
+        const int t0 = c * CL, nv = min(CL, T - t0), rrow = min(row, nv - 1);
+        const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+        const size_t dbase = tok_base<false>(bh, t0, B, H, T);
+        xr = *reinterpret_cast<const uint4*>(r + base + (size_t)rrow * rs + c8);
+        xw = *reinterpret_cast<const uint4*>(w + base + (size_t)rrow * rs + c8);
+        xd = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)rrow * KD + c8);
+    };
+    f32x4 acc[2] = {};
+    float gsum = 0.f;                      // total log2-decay of channel i (part 7)
+    if (c_begin < c_end) issue(c_end - 1);
+    for (int c = c_end - 1; c >= c_begin; --c) {
+        const int nvalid = min(CL, T - c * CL);
+        if (nvalid < CL && row >= nvalid) xr = xw = xd = make_uint4(0u, 0u, 0u, 0u);
+        sstore16(sm.Dm, row, c8, xd);
+        sstore16(sm.Wt, row, c8, xw);
+        sstore16(sm.Rm, row, c8, xr);
+        issue(max(c - 1, c_begin));        // unconditional: the first chunk reloads itself
+        __syncthreads();
+        float loc[8], run = 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; s4 += 4) {
+            const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 8 * part + s4);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int s = s4 + jj;
+                const float x = (float)x4[jj];
+                const float wn = SEQ ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+                run += fmaxf(wn, W_MIN) * RW_L2E;
+                loc[s] = run;
+            }
+        }
+        const bf16x4 ra = ld_col4(&sm.Rm[0][0], 8 * part), rb = ld_col4(&sm.Rm[0][0], 8 * part + 4);
+        sm.tot[part * 64 + i] = run;
+        __syncthreads();
+        {
+            // G_{t-1} = off (first token of the part) or loc[s-1] + off; G_63 = run_7 + parts 0..6
+            float off = 0.f, o7 = 0.f;
+#pragma unroll
+            for (int p = 0; p < 7; ++p) {
+                const float t = sm.tot[p * 64 + i];
+                off += p < part ? t : 0.f;
+                o7 += t;
+            }
+            const float g63 = sm.tot[7 * 64 + i] + o7;
+            const float rf[8] = {(float)ra[0], (float)ra[1], (float)ra[2], (float)ra[3],
+                                 (float)rb[0], (float)rb[1], (float)rb[2], (float)rb[3]};
+            float e[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) e[s] = rf[s] * ex2(s == 0 ? off : loc[s - 1] + off);
+            *reinterpret_cast<uint4*>(&sm.Wt[i][8 * part]) = pack8(e);
+            if (part == 7) {
+                sm.dec[c & 1][i] = ex2(g63);
+                gsum += g63;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
+            acc[0][rr] *= d;
+            acc[1][rr] *= d;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_dir8(&sm.Wt[0][0], 16 * W + lr, 32 * ks);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                acc[tp] = mfma32(a, ld_tr8(&sm.Dm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+        }
+        __syncthreads();
+    }
+    const size_t sq = (size_t)bh * npieces + q;
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            dSp[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = scale * acc[tp][rr];
+    if (part == 7) Ap[sq * KD + i] = gsum;
+}
+
+// dS_end[b,h][p], p = 0..P-2: the state gradient segment p starts from, the pieces folded from
+// the last to the first onto dhT (or zero), dS = 2^{A_q} dS + dS_q, recorded after the first
+// piece of each segment p+1.  Thread layout and load batching as wkv6_fwd_fold.
+__global__ void __launch_bounds__(FOLD_THR)
+wkv6_bwd_fold(const float* __restrict__ dSp, const float* __restrict__ Ap,
+              const float* __restrict__ dhT, float* __restrict__ dSend, int npieces, int SUB,
+              int P) {
+    constexpr int BPS = KD * KD / FOLD_THR;
+    const int bh = blockIdx.x / BPS, e = (blockIdx.x - bh * BPS) * FOLD_THR + threadIdx.x;
+    const int i = e / KD;
+    float s = dhT ? dhT[(size_t)bh * KD * KD + e] : 0.f;
+    const size_t qb = (size_t)bh * npieces;
+    for (int q0 = npieces - 1; q0 >= 0; q0 -= 8) {
+        float a[8], x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const size_t q = qb + max(q0 - t, 0);
+            a[t] = Ap[q * KD + i];
+            x[t] = dSp[q * KD * KD + e];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int q = q0 - t;
+            if (q >= 0) {
+                s = ex2(a[t]) * s + x[t];
+                if (q % SUB == 0) dSend[((size_t)bh * (P - 1) + q / SUB) * KD * KD + e] = s;
             }
         }
     }
@@ -1792,7 +1947,10 @@ __device__ __forceinline__ float sum16lanes(float v) {
     return v + dpp_mov<0x140>(v);                 // row_mirror: lane i <-> lane 15 - i
 }
 
-// SEQ as for wkv6_bwd_chunk_grads.  du_part gets one 64-vector per (b,h) ([h][b][i]).
+// SEQ as for wkv6_bwd_chunk_grads.  One workgroup per (b,h, segment) (P segments of ceil(NT/P)
+// chunks; P = 1 when B*H fills the device): segment p starts from dhT (p = P-1) or dSend[b,h][p]
+// (wkv6_bwd_fold) and writes dh0 if p = 0.  du_part gets one 64-vector per (b,h, segment)
+// ([h][b][p][i]).
 template <bool SEQ>
 __global__ void __launch_bounds__(NTHR_L)
 wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
@@ -1801,10 +1959,12 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
               const float* __restrict__ dhT, const uint16_t* __restrict__ Hs,
               uint16_t* __restrict__ dr, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
               uint16_t* __restrict__ dw, float* __restrict__ du_part, float* __restrict__ dh0,
-              float scale, int B, int H, int T, int NT) {
+              const float* __restrict__ dSend, float scale, int B, int H, int T, int NT, int P) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     LoopSmem& sm = *reinterpret_cast<LoopSmem*>(smem_raw);
-    const int bh = blockIdx.x, h = bh % H;
+    // workgroup = (b,h, segment): chunks [c_lo, c_hi) of the sequence, walked from the last
+    const int bh = blockIdx.x / P, seg = blockIdx.x - bh * P, h = bh % H;
+    const int NC = (NT + P - 1) / P, c_lo = seg * NC, c_hi = min(NT, c_lo + NC);
     const size_t sbase = (size_t)bh * KD * KD;
     // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
     const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
@@ -1813,22 +1973,27 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
 
     LoopPrefetch pf;
-    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
-    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
-    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, NT - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
     float ub[4];                                            // u at the thread's 4 channels (bonus)
 #pragma unroll
     for (int s = 0; s < 4; ++s) ub[s] = load_u(u, u_dtype, h * KD + (threadIdx.x & 15) * 4 + s);
     GradLane gl;
     gl.ulane[0] = scale * load_u(u, u_dtype, h * KD + ch0);
     f32x4 Dst = {};                                         // dS[ch][t4 + rr]
-    if (dhT) {
-        const float4 x = *reinterpret_cast<const float4*>(dhT + sbase + ch0 * KD + t40);
-        Dst[0] = x.x; Dst[1] = x.y; Dst[2] = x.z; Dst[3] = x.w;
+    {
+        // dhT for the last segment, else what the later segments hand this one
+        const float* d0 = seg + 1 < P ? dSend + ((size_t)bh * (P - 1) + seg) * KD * KD
+                                      : (dhT ? dhT + sbase : nullptr);
+        if (d0) {
+            const float4 x = *reinterpret_cast<const float4*>(d0 + ch0 * KD + t40);
+            Dst[0] = x.x; Dst[1] = x.y; Dst[2] = x.z; Dst[3] = x.w;
+        }
     }
     float du_acc = 0.f;
 
-    for (int c = NT - 1; c >= 0; --c) {
+    for (int c = c_hi - 1; c >= c_lo; --c) {
         // The offsets and the lane indices come from opaque copies made in every iteration
         // (see LaneOfs): nothing derived from them is hoisted out of the walk.
         launder(o);
@@ -1871,7 +2036,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         }
         // the next chunk's loads (past chunk 0 they reload chunk 0) go out in S2, S3 and S4,
         // the stores of the chunk before in S4
-        const int cn = max(c - 1, 0);
+        const int cn = max(c - 1, c_lo);
         __syncthreads();
 
         // ---- S2: dA blocks; raw r, k, w at the lane's positions; the decay scan; Fm, Fk; Rm,
@@ -1997,7 +2162,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();
 
         // ---- S4: the products (dr, dk finished on the way), the state-gradient step ----
-        if (c + 1 < NT) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o, go_);
+        if (c + 1 < c_hi) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o, go_);
         loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
         if (wv < 10) loop_A_block(sm, wv, scale, o, lane);
         GradOut go;
@@ -2053,7 +2218,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
     }
     __syncthreads();
-    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, 0, B, H, T, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c_lo, B, H, T, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
                     threadIdx.x & 63, o, go_);
     // du over the sequence: lanes of one channel (lq), then the four token blocks in order
     {
@@ -2061,12 +2226,13 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         p += lane_xor32(p);
         if (((threadIdx.x >> 4) & 3) == 0) sm.red[4 + (threadIdx.x >> 8)][ch0] = p;
     }
-    if (dh0) *reinterpret_cast<float4*>(dh0 + sbase + ch0 * KD + t40) = make_float4(Dst[0], Dst[1], Dst[2], Dst[3]);
+    if (dh0 && seg == 0)
+        *reinterpret_cast<float4*>(dh0 + sbase + ch0 * KD + t40) = make_float4(Dst[0], Dst[1], Dst[2], Dst[3]);
     __syncthreads();
     const int tid = threadIdx.x;
     if (tid < KD) {
         const float acc = (sm.red[4][tid] + sm.red[5][tid]) + (sm.red[6][tid] + sm.red[7][tid]);
-        du_part[((size_t)h * B + bh / H) * KD + tid] = scale * acc;
+        du_part[(((size_t)h * B + bh / H) * P + seg) * KD + tid] = scale * acc;
     }
 }
 
@@ -2163,6 +2329,17 @@ inline void mark(void* const* ev, int i, hipStream_t s) {
 // The forward's workspace: the pre-pass pieces' end states S_q (fp32 [64][64]) and total
 // log2-decays A_q (fp32 [64]), at most max_pieces pieces, then the start states of segments
 // 1..P-1 (fp32 [64][64] each).
+// The reverse walk's workspace: du partials per (b,h, segment), then (P > 1) the backward
+// pieces' dS_q and A_q and the segments' starting state gradients dS_end.
+inline size_t bwd_walk_workspace_bytes(int64_t BH, int64_t NT) {
+    const int P = bwd_walk_segments(BH, NT);
+    size_t n = round_up((size_t)(BH * P) * KD * 4);
+    if (P > 1) {
+        const size_t np = (size_t)(BH * (P - 1) * prepass_pieces(BH, NT, P, PIECE_TARGET).sub);
+        n += round_up(np * KD * KD * 4) + round_up(np * KD * 4) + round_up((size_t)(BH * (P - 1)) * KD * KD * 4);
+    }
+    return n;
+}
 inline size_t fwd_workspace_bytes(int64_t BH, int64_t NT, int64_t max_pieces) {
     const int P = walk_segments(BH, NT);
     const size_t n = (size_t)(BH * (P - 1) * prepass_pieces(BH, NT, P, max_pieces).sub);
@@ -2185,7 +2362,7 @@ size_t rwkv6_wkv_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t K, int
     if (check_shape(B, H, T, K, V) != RWKV6_OK) return 0;
     const size_t BH = (size_t)(B * H), NT = (size_t)(nchunks(T) > 0 ? nchunks(T) : 1);
     if (!for_bwd) return fwd_workspace_bytes((int64_t)BH, nchunks(T), PIECE_TARGET);
-    if (bwd_loop((int64_t)BH, nchunks(T))) return round_up(BH * KD * 4);   // du_part per (b,h)
+    if (bwd_walk_segments((int64_t)BH, nchunks(T))) return bwd_walk_workspace_bytes((int64_t)BH, nchunks(T));
     // dHs, du_part per chunk, dS_loc, dec
     return 2 * round_up(BH * NT * KD * KD * 2) + 2 * round_up(BH * NT * KD * 4);
 }
@@ -2343,19 +2520,45 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
         for (int i = 1; i <= 7; ++i) mark(phase_events, i, s);
         return launch_status();
     }
-    if (bwd_loop(BH, NT)) {
-        // one reverse walk per sequence: gradients and state gradients in one pass
+    if (const int P = bwd_walk_segments(BH, NT)) {
+        // one reverse walk per (b,h, segment): gradients and state gradients in one pass; with
+        // P > 1 segments the pieces of segments 1..P-1 and their fold first give each segment
+        // its starting state gradient
         du_part = reinterpret_cast<float*>(workspace);
-        for (int i = 1; i <= 4; ++i) mark(phase_events, i, s);
-        hipLaunchKernelGGL(wkv6_bwd_loop<SEQ>, dim3((unsigned)BH), dim3(NTHR_L), sizeof(LoopSmem), s,
+        const float* dSend = nullptr;
+        if (P > 1) {
+            const Pieces pc = prepass_pieces(BH, NT, P, PIECE_TARGET);
+            const int npieces = (P - 1) * pc.sub;
+            float* dSp = reinterpret_cast<float*>(reinterpret_cast<char*>(du_part) +
+                                                  round_up((size_t)BH * P * KD * 4));
+            float* Ap = reinterpret_cast<float*>(reinterpret_cast<char*>(dSp) +
+                                                 round_up((size_t)BH * npieces * KD * KD * 4));
+            float* dSe = reinterpret_cast<float*>(reinterpret_cast<char*>(Ap) +
+                                                  round_up((size_t)BH * npieces * KD * 4));
+            hipLaunchKernelGGL((wkv6_bwd_pieces<SEQ>), dim3((unsigned)(BH * npieces)), dim3(NTHR_W), 0,
+                               s, (const uint16_t*)r, (const uint16_t*)w, (const uint16_t*)dO, dSp, Ap,
+                               scale, (int)B, (int)H, (int)T, (int)NT, (int)((NT + P - 1) / P),
+                               pc.sub, pc.ncs, npieces);
+            mark(phase_events, 1, s);
+            mark(phase_events, 2, s);
+            hipLaunchKernelGGL(wkv6_bwd_fold, dim3((unsigned)(BH * (KD * KD / FOLD_THR))), dim3(FOLD_THR),
+                               0, s, dSp, Ap, dhT, dSe, npieces, pc.sub, P);
+            dSend = dSe;
+        } else {
+            mark(phase_events, 1, s);
+            mark(phase_events, 2, s);
+        }
+        mark(phase_events, 3, s);
+        mark(phase_events, 4, s);
+        hipLaunchKernelGGL(wkv6_bwd_loop<SEQ>, dim3((unsigned)(BH * P)), dim3(NTHR_L), sizeof(LoopSmem), s,
                            (const uint16_t*)r, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)w, u, u_dtype, (const uint16_t*)dO, dhT, Hs,
                            (uint16_t*)dr, (uint16_t*)dk, (uint16_t*)dv, (uint16_t*)dw, du_part, dh0,
-                           scale, (int)B, (int)H, (int)T, (int)NT);
+                           dSend, scale, (int)B, (int)H, (int)T, (int)NT, P);
         mark(phase_events, 5, s);
         mark(phase_events, 6, s);
         hipLaunchKernelGGL(wkv6_du_reduce, dim3((unsigned)H), dim3(DU_THR), 0, s, du_part, du, u_dtype,
-                           (int)B, (int)H, 1);
+                           (int)B, (int)H, P);
         mark(phase_events, 7, s);
         return launch_status();
     }

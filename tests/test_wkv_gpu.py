@@ -144,11 +144,15 @@ def test_wkv_empty_sequence(pkg):
     assert torch.equal(hT, h0)
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17)])
+@pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17), (2, 64, 64 * 17 + 5),
+                                   (1, 128, 64 * 30 + 9)])
 def test_wkv_parity_segmented(pkg, shape):
-    """Few sequences of many chunks: the forward cuts each sequence into segments (a state
-    pre-pass per segment, then output walks that start from the combined segment states),
-    here 2 segments of 9 chunks and 5 segments of 9 chunks with a ragged last chunk."""
+    """Few sequences of many chunks: the forward cuts each sequence into segments (pre-pass
+    pieces folded into each segment's start state, then output walks), here 2 segments of 9
+    chunks and 5 of 9 with a ragged last chunk; the backward runs chunk-parallel for those two
+    and as a segmented reverse walk (backward pieces folded into each segment's starting state
+    gradient) for the 128-sequence shapes: 2 segments of 9 chunks, and of 16 + 15 chunks with
+    a ragged last one."""
     B, H, T = shape
     x = _inputs(B, H, T, seed=T)
     got = run_gpu(pkg, x, 0.5, True, True)
