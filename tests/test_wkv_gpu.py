@@ -124,8 +124,11 @@ def test_wkv_extreme_decay_is_floored(pkg):
     _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
 
 
-def test_wkv_deterministic(pkg):
-    x = _inputs(2, 2, 200, seed=3)
+@pytest.mark.parametrize("shape", [(2, 2, 200), (2, 64, 64 * 17 + 5)])
+def test_wkv_deterministic(pkg, shape):
+    """Bit-identical reruns: the chunk-parallel backward and, at B*H = 128, the segmented
+    forward and reverse walks (their pieces and folds sum in a fixed order)."""
+    x = _inputs(*shape, seed=3)
     a = run_gpu(pkg, x, 1.0, True, True)
     b = run_gpu(pkg, x, 1.0, True, True)
     for n in a:
@@ -248,10 +251,11 @@ def test_wkv_decay_gradient_through_exp_past_the_floor(pkg):
     _compare(got, ref, ["o", "dr", "dk", "dv", "d_decay", "du"])
 
 
-@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64), (2, 1, 1300)])
+@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64), (2, 1, 1300), (2, 64, 1093)])
 def test_wkv_seqfirst_entry(pkg, shape):
     """The time-mix module's entry: r, k, v, decay in [T,B,H*64], w = -exp(decay) inside,
-    o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs."""
+    o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs.
+    (2, 64, 1093): B*H = 128, the segmented walks (2 segments of 9 chunks, ragged end)."""
     B, H, T = shape
     K = 64
     g = torch.Generator().manual_seed(T + B)
