@@ -101,15 +101,16 @@ __device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __re
 
 // LERP: out_e = x + (shift(x) - x) * (m_e + bias_e)  (E = 5);  else out_e = m_e + bias_e.
 // Token n of output e starts at out.p[e] + n * ors (ors = C for separate [N,C] tensors, E * C
-// for one [N,E,C] tensor).
-template <int E, bool LERP>
+// for one [N,E,C] tensor).  A block takes REP consecutive 128-token tiles of its channel block
+// (the single-mix decay output stages the block's W_up for four tiles instead of one).
+template <int E, bool LERP, int REP>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
                      OutPtrs<E> out, int64_t ors, int64_t N, int64_t B, int64_t C, int R,
                      int64_t per) {
     int64_t tb, cb;
-    if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
+    if (!lora_tile((N + LORA_TT * REP - 1) / (LORA_TT * REP), C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
     const int64_t c0 = cb * 64;
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
@@ -129,7 +130,9 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
     static_assert(LORA_TT == 128, "two 64-token groups per block");
     // both 64-token groups at a time (tokens g = 0, 1 of this lane): their neck loads of a
     // mix are in flight together
-    {
+#pragma unroll 1
+    for (int rp = 0; rp < REP; ++rp) {
+        const int64_t tt = tb * REP + rp;            // 128-token tile
         int64_t tc[2];
         // x and x[t-B] of the lane's two channel runs stay packed bf16 (16 registers a token
         // group instead of 32 as fp32: 124 registers in all, four waves per SIMD); delta is
@@ -138,7 +141,7 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
         float keep[2];
 #pragma unroll
         for (int P = 0; P < 2; ++P) {
-            const int64_t tok = tb * LORA_TT + 64 * P + 16 * wv + L;
+            const int64_t tok = tt * LORA_TT + 64 * P + 16 * wv + L;
             tc[P] = tok < N ? tok : N - 1;
             if (LERP) {
                 keep[P] = tc[P] >= B ? 1.f : 0.f;
@@ -472,12 +475,17 @@ rwkv6_col_sum_kernel(const uint16_t* __restrict__ x, int64_t N, int64_t M,
     const int64_t r0 = (int64_t)blockIdx.x * CS_ROWS;
     float a[8] = {};
     if (c0 < M) {
+        // rows q, q + 8, ... of the block in order; eight loads in flight (unconditional: a
+        // row past the end reads the last row and adds zero)
         const int64_t r1 = min<int64_t>(N, r0 + CS_ROWS);
-        for (int64_t rw = r0 + q; rw < r1; rw += 8) {
+#pragma unroll 8
+        for (int k = 0; k < CS_ROWS / 8; ++k) {
+            const int64_t rw = r0 + q + 8 * k;
+            const float keep = rw < r1 ? 1.f : 0.f;
             float f[8];
-            load8(x + rw * M + c0, f);
+            load8(x + (rw < r1 ? rw : r1 - 1) * M + c0, f);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a[j] += f[j];
+            for (int j = 0; j < 8; ++j) a[j] += keep * f[j];
         }
     }
 #pragma unroll
@@ -512,9 +520,13 @@ inline int gather(const void* const* src, P& dst) {
     }
     return RWKV6_OK;
 }
-// token blocks per XCD and the padded 1-D grid of lora_tile
-inline int64_t up_per(int64_t N) { return ((N + LORA_TT - 1) / LORA_TT + 7) / 8; }
-inline dim3 up_grid(int64_t N, int64_t C) { return dim3((unsigned)(8 * up_per(N) * (C / 64))); }
+// token blocks (of rep 128-token tiles) per XCD and the padded 1-D grid of lora_tile
+inline int64_t up_per(int64_t N, int64_t rep = 1) {
+    return ((N + LORA_TT * rep - 1) / (LORA_TT * rep) + 7) / 8;
+}
+inline dim3 up_grid(int64_t N, int64_t C, int64_t rep = 1) {
+    return dim3((unsigned)(8 * up_per(N, rep) * (C / 64)));
+}
 }  // namespace
 
 extern "C" {
@@ -538,7 +550,7 @@ int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, c
                        {bias, (size_t)(LORA_NE * C) * param_bytes(param_dtype)}}))
             return RWKV6_ERR_INVALID_ARG;
     }
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true>), up_grid(T * B, C), dim3(LORA_THR),
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true, 1>), up_grid(T * B, C), dim3(LORA_THR),
                        lora_lds_bytes(LORA_NE, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
                        (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, C,
@@ -562,14 +574,14 @@ int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, 
     if (E == 1) {
         OutPtrs<1> o;
         o.p[0] = (uint16_t*)out;
-        hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false>), up_grid(N, C), dim3(LORA_THR),
+        hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false, 4>), up_grid(N, C, 4), dim3(LORA_THR),
                            lora_lds_bytes(1, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
-                           C, N, (int64_t)1, C, (int)R, up_per(N));
+                           C, N, (int64_t)1, C, (int)R, up_per(N, 4));
     } else {
         OutPtrs<LORA_NE> o;
         for (int e = 0; e < LORA_NE; ++e) o.p[e] = (uint16_t*)out + (int64_t)e * C;
-        hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, false>), up_grid(N, C), dim3(LORA_THR),
+        hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, false, 1>), up_grid(N, C), dim3(LORA_THR),
                            lora_lds_bytes(LORA_NE, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
                            (int64_t)LORA_NE * C, N, (int64_t)1, C, (int)R, up_per(N));
