@@ -460,11 +460,20 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     {
         const float* s0 = seg > 0 ? Sstart + ((size_t)bh * (P - 1) + seg - 1) * KD * KD
                                   : (h0 ? h0 + sbase : nullptr);
+        // one branch around all eight loads (a conditional per element came out ~1 % slower
+        // over the whole walk: the register assignment of the loop differed)
+        if (s0) {
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
+            for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr)
-                acc[tp][rr] = s0 ? s0[(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] : 0.f;
+                for (int rr = 0; rr < 4; ++rr)
+                    acc[tp][rr] = s0[(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr];
+        } else {
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) acc[tp][rr] = 0.f;
+        }
         if (threadIdx.x < KD) sm.uh[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
         __syncthreads();
     }
