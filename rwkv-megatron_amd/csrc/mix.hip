@@ -25,23 +25,47 @@
 
 #define MIX_THR 256
 
-// xxx = x + (shift(x) - x) * maa
+// The static lerps, out_e[n] = x[n] + (shift(x)[n] - x[n]) * coef[e] (token rows n = t*B + b,
+// shift(x)[n] = x[n - B], zero for n < B): xxx = lerp with maa (NE = 1, rwkv6_shift_lerp_fwd),
+// or the channel mix's two mixes with mix_coeffs [2,C] (NE = 2, rwkv6_cmix_lerp_fwd).  Thread = 8 channels of
+// LERP_ROWS rows (grid.x over channel groups, grid.y over row blocks, striding when the rows
+// outnumber the grid): its coefficients are loaded once and all its row loads are in flight
+// together (clamped rows: no branch).
+#define LERP_ROWS 4
+template <int NE>
 __global__ void __launch_bounds__(MIX_THR)
-rwkv6_shift_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ maa, int pdt,
-                        uint16_t* __restrict__ xxx, int64_t T, int64_t B, int64_t C) {
-    const int64_t C8 = C / 8;
-    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    if (idx >= T * B * C8) return;
-    const int64_t cg = idx % C8, tb = idx / C8;
-    const int64_t off = tb * C + 8 * cg;
-    float xv[8], xp[8], m[8], out[8];
-    load8(x + off, xv);
-    if (tb >= B) load8(x + off - B * C, xp);
-    else for (int s = 0; s < 8; ++s) xp[s] = 0.f;
-    load_param8(maa, pdt, 8 * cg, m);
+rwkv6_lerp_rows_kernel(const uint16_t* __restrict__ x, const void* __restrict__ coef, int pdt,
+                       OutPtrs<NE> out, int64_t N, int64_t B, int64_t C) {
+    const int64_t C8 = C / 8, cg = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
+    if (cg >= C8) return;
+    float m[NE][8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) out[s] = xv[s] + (xp[s] - xv[s]) * m[s];
-    store8(xxx + off, out);
+    for (int e = 0; e < NE; ++e) load_param8(coef, pdt, e * C + 8 * cg, m[e]);
+    for (int64_t r0 = (int64_t)blockIdx.y * LERP_ROWS; r0 < N; r0 += (int64_t)gridDim.y * LERP_ROWS) {
+        float xv[LERP_ROWS][8], xp[LERP_ROWS][8];
+#pragma unroll
+        for (int j = 0; j < LERP_ROWS; ++j) {
+            const int64_t r = r0 + j < N ? r0 + j : N - 1;
+            load8(x + r * C + 8 * cg, xv[j]);
+            load8(x + (r >= B ? r - B : r) * C + 8 * cg, xp[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < LERP_ROWS; ++j) {
+            const int64_t r = r0 + j;
+            const float keep = (r < N ? r : N - 1) >= B ? 1.f : 0.f;
+#pragma unroll
+            for (int e = 0; e < NE; ++e) {
+                float o[8];
+#pragma unroll
+                for (int s = 0; s < 8; ++s) o[s] = xv[j][s] + (xp[j][s] * keep - xv[j][s]) * m[e][s];
+                if (r < N) store8(out.p[e] + r * C + 8 * cg, o);
+            }
+        }
+    }
+}
+inline dim3 lerp_grid(int64_t N, int64_t C) {
+    const int64_t rb = (N + LERP_ROWS - 1) / LERP_ROWS;
+    return dim3((unsigned)((C / 8 + MIX_THR - 1) / MIX_THR), (unsigned)(rb < 65535 ? rb : 65535));
 }
 
 // Backward kernel: block = 8 token sub-segments x 32 channel groups (256 threads); the
@@ -79,36 +103,6 @@ rwkv6_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
 // ---------------------------------------------------------------------------------------
 // Channel mix.
 #define CMIX_NE 2
-
-// mixed[e] = x + (shift(x) - x) * mix[e];  mix [2,C], mixed 2 x [T,B,C]
-__global__ void __launch_bounds__(MIX_THR)
-rwkv6_cmix_lerp_kernel(const uint16_t* __restrict__ x, const void* __restrict__ mix, int pdt,
-                       OutPtrs<CMIX_NE> mixed, int64_t T, int64_t B, int64_t C) {
-    const int64_t C8 = C / 8;
-    const int64_t idx = (int64_t)blockIdx.x * MIX_THR + threadIdx.x;
-    const int64_t N = T * B;
-    if (idx >= N * C8) return;
-    const int64_t cg = idx % C8, tb = idx / C8;
-    const int64_t off = tb * C + 8 * cg;
-    float xv[8], d[8];
-    load8(x + off, xv);
-    if (tb >= B) {
-        load8(x + off - B * C, d);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) d[s] -= xv[s];
-    } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) d[s] = -xv[s];
-    }
-#pragma unroll
-    for (int e = 0; e < CMIX_NE; ++e) {
-        float m[8], out[8];
-        load_param8(mix, pdt, e * C + 8 * cg, m);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) out[s] = xv[s] + d[s] * m[s];
-        store8(mixed.p[e] + off, out);
-    }
-}
 
 // Backward of the channel-mix lerp (walked forward with dx[t] emitted one token late; d_delta
 // of each sub-segment's first token is handed to the previous sub-segment through LDS):
@@ -379,10 +373,11 @@ int rwkv6_shift_lerp_fwd(const void* x, const void* maa, int param_dtype, void* 
     const size_t act = (size_t)(T * B * C) * 2;
     if (any_alias({{xxx, act}}, {{x, act}, {maa, (size_t)C * param_bytes(param_dtype)}}))
         return RWKV6_ERR_INVALID_ARG;
-    const int64_t n = T * B * (C / 8);
-    hipLaunchKernelGGL(rwkv6_shift_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
+    OutPtrs<1> out;
+    out.p[0] = (uint16_t*)xxx;
+    hipLaunchKernelGGL(rwkv6_lerp_rows_kernel<1>, lerp_grid(T * B, C), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, maa, param_dtype,
-                       (uint16_t*)xxx, T, B, C);
+                       out, T * B, B, C);
     return launch_status();
 }
 
@@ -402,10 +397,9 @@ int rwkv6_cmix_lerp_fwd(const void* x, const void* mix, int param_dtype, void* c
     if (any_alias({{out.p[0], act}, {out.p[1], act}},
                   {{x, act}, {mix, (size_t)CMIX_NE * C * param_bytes(param_dtype)}}))
         return RWKV6_ERR_INVALID_ARG;
-    const int64_t n = T * B * (C / 8);
-    hipLaunchKernelGGL(rwkv6_cmix_lerp_kernel, dim3(nblocks(n)), dim3(MIX_THR), 0,
+    hipLaunchKernelGGL(rwkv6_lerp_rows_kernel<CMIX_NE>, lerp_grid(T * B, C), dim3(MIX_THR), 0,
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)x, mix, param_dtype,
-                       out, T, B, C);
+                       out, T * B, B, C);
     return launch_status();
 }
 
