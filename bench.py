@@ -209,14 +209,14 @@ def config1_bench(pkg, gpu_steps, with_cpu):
 def bwd_walk_segments(BH, T):
     """Segments per sequence of the library's reverse walk (wkv6_bwd_loop), 0 when the backward
     runs chunk-parallel: the rule of bwd_walk_segments() in csrc/wkv6.hip (walk_segments() with
-    a 256-workgroup target; the walk when it is one segment or the segments fill the device)."""
+    a 256-workgroup target; the walk when it is one segment or the segments fill 7/8 of it)."""
     NT = -(-T // 64)
     if NT <= 0:
         return 1
-    P = min(-(-256 // BH), max(1, NT // 8))
+    P = min(max(1, 256 // BH), max(1, NT // 8))
     NC = -(-NT // P)
     P = -(-NT // NC)
-    return P if P == 1 or BH * P >= 256 else 0
+    return P if P == 1 or 8 * BH * P >= 7 * 256 else 0
 
 
 def bwd_kernel(BH, T):

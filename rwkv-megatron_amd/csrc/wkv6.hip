@@ -339,11 +339,13 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
     __syncthreads();
 }
 
-// Segments per sequence (shared by the workspace query and the launch): enough
-// (b,h, segment) workgroups to offer `target`, no segment shorter than WALK_MIN_CHUNKS.
+// Segments per sequence (shared by the workspace query and the launch): as many (b,h, segment)
+// workgroups as fit `target` (one walk per CU) without a second round, no segment shorter
+// than WALK_MIN_CHUNKS.  (Rounding up instead, e.g. 3 segments for 96 sequences, put the 288
+// walks into two rounds: 30 % slower at B*H = 96, T = 4096.)
 inline int walk_segments(int64_t BH, int64_t NT, int64_t target = WALK_TARGET_ITEMS) {
     if (NT <= 0) return 1;
-    int64_t P = (target + BH - 1) / BH;
+    int64_t P = target / BH > 1 ? target / BH : 1;
     P = std::min<int64_t>(P, std::max<int64_t>(1, NT / WALK_MIN_CHUNKS));
     const int64_t NC = (NT + P - 1) / P;               // chunks per segment
     return (int)((NT + NC - 1) / NC);                   // no empty segment
@@ -372,14 +374,14 @@ inline Pieces prepass_pieces(int64_t BH, int64_t NT, int P, int64_t max_pieces) 
     return {(int)((NC + ncs - 1) / ncs), (int)ncs};      // no empty piece, sub only shrinks
 }
 
-// The backward walks each sequence in one workgroup (wkv6_bwd_loop) when that fills the device
-// or the sequences are short; with fewer sequences, each is cut into segments like the
-// forward's as long as the (b,h, segment) workgroups still fill the device (a segment walks at
-// ~6 us a chunk whatever the occupancy).  Otherwise (few, short segments) the state gradients
-// run chunk-parallel.  Returns the segment count of the walk, or 0 for the chunk-parallel form.
+// The backward walks each sequence in one workgroup (wkv6_bwd_loop) when there is one segment;
+// with fewer sequences, each is cut into segments like the forward's as long as the (b,h,
+// segment) workgroups fill at least 7/8 of the device (a segment walks at ~6 us a chunk
+// whatever the occupancy).  Otherwise (few, short segments) the state gradients run
+// chunk-parallel.  Returns the segment count of the walk, or 0 for the chunk-parallel form.
 inline int bwd_walk_segments(int64_t BH, int64_t NT) {
     const int P = walk_segments(BH, NT, DSTATE_TARGET_ITEMS);
-    return (P == 1 || BH * P >= DSTATE_TARGET_ITEMS) ? P : 0;
+    return (P == 1 || 8 * BH * P >= 7 * DSTATE_TARGET_ITEMS) ? P : 0;
 }
 
 struct WalkPrefetch {
@@ -2607,7 +2609,7 @@ int wkv_bwd_impl(const void* r, const void* k, const void* v, const void* w, con
 // forward's only scratch, the end states of its pre-pass pieces (S_q fp32 [64][64] and A_q
 // fp32 [64] per piece) and the segments' start states (fp32 [64][64] per segment after the
 // first), lives in this file-scope device array instead of the caller's workspace.
-// walk_segments() gives P <= ceil(256 / (B*H)) segments per sequence, so B*H*(P-1) < 256, and
+// walk_segments() gives B*H*P <= 256 when P > 1, so B*H*(P-1) < 256, and
 // this entry caps the pieces at WKV_SCRATCH_SEGS (fewer, longer pieces than with a workspace
 // when the cap binds): WKV_SCRATCH_BYTES covers every shape.
 // Each GPU holds its own copy for the life of the process; calls on one GPU share it (the
