@@ -20,8 +20,9 @@ Also reported:
     fla's naive recurrent RWKV-6) timed on this host on the same workload;
   * config5 (WKV6 long context with carried state), slice_7b (config 4: four 7B-shape
     layers fwd+bwd), train_step (config 3: the 1.6B-shape training step) and config1 (the
-    tiny LM's fwd+bwd step on the GPU and, as its CPU baseline, the reference model restated
-    in torch fp32 on this host); the CPU baselines also give forward-only times, and
+    tiny LM's fwd+bwd step on the GPU, eager and replayed from a HIP graph, and, as its CPU
+    baseline, the reference model restated in torch fp32 on this host); the CPU baselines
+    also give forward-only times, and
     cpu_host names the CPU model and thread counts.
 """
 from __future__ import annotations
@@ -173,9 +174,43 @@ def config1_bench(pkg, gpu_steps, with_cpu):
     e1.record()
     torch.cuda.synchronize()
     gpu_ms = e0.elapsed_time(e1) / gpu_steps
+
+    # The same step captured once in a HIP graph and replayed: the step is launch-bound
+    # (~270 small kernels), which the graph's single submission removes.  Gradients land in
+    # the graph's own .grad tensors, overwritten by every replay.
+    def fwd_bwd():
+        logits = model(tok_d)
+        losses = F.cross_entropy(logits.float().transpose(0, 1).reshape(-1, V), tgt_d, reduction="none")
+        loss = (losses * mask_d).sum() / mask_d.sum()
+        loss.backward()
+        return loss
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            model.zero_grad(set_to_none=True)
+            fwd_bwd()
+    torch.cuda.current_stream().wait_stream(side)
+    model.zero_grad(set_to_none=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd_bwd()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(gpu_steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_ms = e0.elapsed_time(e1) / gpu_steps
+    del graph
+    model.zero_grad(set_to_none=True)
     out = {"workload": "BASELINE config 1: tiny RWKV-6 LM (2 layers, d_model 512, 8 heads, ffn 1792, "
                        "vocab 65536, fp32 weights), batch 2 x 512, fwd+bwd with next-token CE",
            "gpu_ms_per_step": gpu_ms, "gpu_tokens_per_s": B * T / (gpu_ms * 1e-3),
+           "gpu_graph_ms_per_step": graph_ms, "gpu_graph_tokens_per_s": B * T / (graph_ms * 1e-3),
            "gpu_steps": gpu_steps}
     if with_cpu:
         from oracle import lm

@@ -103,8 +103,10 @@ __device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __re
 // Token n of output e starts at out.p[e] + n * ors (ors = C for separate [N,C] tensors, E * C
 // for one [N,E,C] tensor).  A block takes REP consecutive 128-token tiles of its channel block
 // (the single-mix decay output stages the block's W_up for four tiles instead of one).
+// Four waves per SIMD: without the bound the ddlerp form takes 124 + 16 registers (three waves
+// per SIMD) and runs ~3 % slower at the config-3 shape.
 template <int E, bool LERP, int REP>
-__global__ void __launch_bounds__(LORA_THR)
+__global__ void __launch_bounds__(LORA_THR) __attribute__((amdgpu_waves_per_eu(4)))
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
                      OutPtrs<E> out, int64_t ors, int64_t N, int64_t B, int64_t C, int R,

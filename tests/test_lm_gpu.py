@@ -61,3 +61,58 @@ def test_config1_tiny_lm_forward_backward(pkg):
     got = {name: n(prm.grad) for name, prm in model.named_parameters()}
     want = {name: n(p[name].grad) for name in got}
     parity.check_all(got, want, sorted(got), **BARS)
+
+
+def test_config1_graph_replay_matches_eager(pkg):
+    """The config-1 forward + backward captured once in a HIP graph (torch.cuda.CUDAGraph, the
+    package's kernels launched on the capturing stream) and replayed: every replay, with eager
+    GPU work and synchronizations between replays, gives the eager step's loss and parameter
+    gradients (1e-6 relative bar; the kernels are deterministic)."""
+    M = pkg.modules
+    cfg = M.TransformerConfig(hidden_size=512, num_attention_heads=8, ffn_hidden_size=1792,
+                              num_layers=2, params_dtype=torch.float32, rwkv_lm_decay_init=True)
+    V = 65536
+    torch.manual_seed(0)
+    model = M.RWKV6Model(cfg, V, device=DEV)
+    tokens, targets, mask = config1_batch(V)
+    tok, tgt, m = tokens.to(DEV), targets.to(DEV).reshape(-1), mask.to(DEV).reshape(-1)
+
+    def step():
+        logits = model(tok)
+        losses = F.cross_entropy(logits.float().transpose(0, 1).reshape(-1, V), tgt, reduction="none")
+        loss = (losses * m).sum() / m.sum()
+        loss.backward()
+        return loss
+
+    model.zero_grad(set_to_none=True)
+    ref_loss = step().detach().clone()
+    ref_grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            model.zero_grad(set_to_none=True)
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    model.zero_grad(set_to_none=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_loss = step()
+    other = torch.randn(1024, 1024, device=DEV)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        rel = abs(static_loss.item() - ref_loss.item()) / abs(ref_loss.item())
+        worst = 0.0
+        for n, p in model.named_parameters():
+            d = (p.grad - ref_grads[n]).abs().max().item()
+            s = ref_grads[n].abs().max().item()
+            worst = max(worst, d / s if s > 0 else d)
+        print(f"replay {rep}: loss rel diff {rel:.2e}, worst grad max-rel diff {worst:.2e}", flush=True)
+        assert rel <= 1e-6 and worst <= 1e-6
+        # eager work between replays (its own kernels, outside the model's gradients)
+        with torch.no_grad():
+            model(tok)
+            other = other @ other.T / 1024
+        torch.cuda.synchronize()
