@@ -215,6 +215,9 @@ __device__ __forceinline__ void lora_up8(const uint16_t* sw, const uint16_t* __r
         for (int rr = 0; rr < 4; ++rr) m[4 * tc + rr] = acc[tc][rr];
 }
 
+// KS = R / 32 (1 or 2; the launch picks it): a compile-time count, because a loop with a
+// load inside makes the compiler wait for every outstanding load and store where it merges.
+template <int KS>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                              const void* __restrict__ bias, int pdt,
@@ -292,7 +295,8 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
                     for (int tcn = 0; tcn < 2; ++tcn)
                         acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 8 * q),
                                           __builtin_bit_cast(bf16x8, nk_e[P]), acc[tcn]);
-                    for (int ks = 1; ks < R / 32; ++ks) {
+#pragma unroll
+                    for (int ks = 1; ks < KS; ++ks) {
                         const int r0 = 32 * ks + 8 * q;
                         const bf16x8 bq = ld_bf16x8(nrow[P] + e * R + r0);
 #pragma unroll
@@ -624,13 +628,14 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t N = T * B, nb = (N + LORA_TT - 1) / LORA_TT;
     float* part = reinterpret_cast<float*>(workspace);
-    if (N > 0)
-        hipLaunchKernelGGL(rwkv6_ddlerp_lora_bwd_kernel, up_grid(N, C), dim3(LORA_THR),
-                           lora_lds_bytes(LORA_NE, (int)R), s,
+    if (N > 0) {
+        // lora_check admits R = 32 and 64 for five mixes (the LDS bound)
+        auto kern = R == 32 ? rwkv6_ddlerp_lora_bwd_kernel<1> : rwkv6_ddlerp_lora_bwd_kernel<2>;
+        hipLaunchKernelGGL(kern, up_grid(N, C), dim3(LORA_THR), lora_lds_bytes(LORA_NE, (int)R), s,
                            (const uint16_t*)neck, (const uint16_t*)w_up_t, bias, param_dtype,
                            (const uint16_t*)x, dm, (uint16_t*)d_mexp, (uint16_t*)d_delta_part,
-                           (uint16_t*)d_sum, part, N,
-                           B, C, (int)R, up_per(N));
+                           (uint16_t*)d_sum, part, N, B, C, (int)R, up_per(N));
+    }
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((LORA_NE * C + 31) / 32)),
                        dim3(LORA_THR), 0, s, part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias);
     return launch_status();
