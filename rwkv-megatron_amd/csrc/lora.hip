@@ -77,19 +77,27 @@ __device__ __forceinline__ void lora_stage(uint16_t* sw, const uint16_t* __restr
 }
 
 // m[j] = sum_r neck[tok][e*R + r] * W_up[e][r][c], c the lane's j-th channel (run layout).
+// KS = R / 32 when the launch knows it (0: from R at run time; a loop with a load inside makes
+// the compiler wait for every outstanding load and store where it merges).
+template <int KS>
 __device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __restrict__ neck_row,
-                                        bool tv, int R, int e, float* m) {
+                                        int R, int e, float* m) {
     const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
     const int rs = lds_rs(R);
     const uint16_t* swe = sw + e * 64 * rs;
     f32x4 acc[4] = {};
-    for (int ks = 0; ks < R / 32; ++ks) {
+    auto step = [&](int ks) {
         const int r0 = 32 * ks + 8 * q;
-        const bf16x8 b = tv ? ld_bf16x8(neck_row + e * R + r0)
-                            : __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+        const bf16x8 b = ld_bf16x8(neck_row + e * R + r0);
 #pragma unroll
         for (int tc = 0; tc < 4; ++tc)
             acc[tc] = mfma32(ld_bf16x8(swe + tile_channel(tc, L) * rs + r0), b, acc[tc]);
+    };
+    if constexpr (KS > 0) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) step(ks);
+    } else {
+        for (int ks = 0; ks < R / 32; ++ks) step(ks);
     }
 #pragma unroll
     for (int tc = 0; tc < 4; ++tc)
@@ -105,7 +113,7 @@ __device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __re
 // (the single-mix decay output stages the block's W_up for four tiles instead of one).
 // Four waves per SIMD: without the bound the ddlerp form takes 124 + 16 registers (three waves
 // per SIMD) and runs ~3 % slower at the config-3 shape.
-template <int E, bool LERP, int REP>
+template <int E, bool LERP, int REP, int KS>
 __global__ void __launch_bounds__(LORA_THR) __attribute__((amdgpu_waves_per_eu(4)))
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
@@ -159,7 +167,7 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
         for (int e = 0; e < E; ++e) {
             float m[2][16];
 #pragma unroll
-            for (int P = 0; P < 2; ++P) lora_up(lora_sm, neck + tc[P] * E * R, true, R, e, m[P]);
+            for (int P = 0; P < 2; ++P) lora_up<KS>(lora_sm, neck + tc[P] * E * R, R, e, m[P]);
             const float* bq = &bsm[e][0];
 #pragma unroll
             for (int P = 0; P < 2; ++P) {
@@ -193,28 +201,8 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
 // Wave wv takes the channel half h = wv & 1 (32 channels) of the 16 tokens 16 (wv >> 1) + L
 // of each 32-token group; a lane holds the one 16-byte run c0 + 32h + 8q + (0..7), so a load
 // instruction still covers 64 contiguous bytes of 16 token rows, and eight values per lane
-// (instead of sixteen) keep the registers low enough for four waves per SIMD: the kernel
-// is bound by how many loads are in flight.
-__device__ __forceinline__ void lora_up8(const uint16_t* sw, const uint16_t* __restrict__ neck_row,
-                                         bool tv, int R, int e, int h, float* m) {
-    const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
-    const int rs = lds_rs(R);
-    const uint16_t* swe = sw + (e * 64 + 32 * h) * rs;
-    f32x4 acc[2] = {};
-    for (int ks = 0; ks < R / 32; ++ks) {
-        const int r0 = 32 * ks + 8 * q;
-        const bf16x8 b = tv ? ld_bf16x8(neck_row + e * R + r0)
-                            : __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
-#pragma unroll
-        for (int tc = 0; tc < 2; ++tc)
-            acc[tc] = mfma32(ld_bf16x8(swe + tile_channel(tc, L) * rs + r0), b, acc[tc]);
-    }
-#pragma unroll
-    for (int tc = 0; tc < 2; ++tc)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) m[4 * tc + rr] = acc[tc][rr];
-}
-
+// (instead of sixteen) hold the registers to three waves per SIMD (a four-wave cap spills;
+// issuing all five mixes' loads at once, at half the waves, was no faster).
 // KS = R / 32 (1 or 2; the launch picks it): a compile-time count, because a loop with a
 // load inside makes the compiler wait for every outstanding load and store where it merges.
 template <int KS>
@@ -556,7 +544,9 @@ int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, c
                        {bias, (size_t)(LORA_NE * C) * param_bytes(param_dtype)}}))
             return RWKV6_ERR_INVALID_ARG;
     }
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true, 1>), up_grid(T * B, C), dim3(LORA_THR),
+    // the rank count from R at run time: the compile-time form measured 7 % slower here (136
+    // against 127 us at the config-3 shape, R = 32), while it is faster for the bias forms
+    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true, 1, 0>), up_grid(T * B, C), dim3(LORA_THR),
                        lora_lds_bytes(LORA_NE, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
                        (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, C,
@@ -580,14 +570,17 @@ int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, 
     if (E == 1) {
         OutPtrs<1> o;
         o.p[0] = (uint16_t*)out;
-        hipLaunchKernelGGL((rwkv6_lora_up_kernel<1, false, 4>), up_grid(N, C, 4), dim3(LORA_THR),
+        // the decay LoRA's rank 64 with a compile-time count, any other rank from R
+        auto kern = R == 64 ? rwkv6_lora_up_kernel<1, false, 4, 2> : rwkv6_lora_up_kernel<1, false, 4, 0>;
+        hipLaunchKernelGGL(kern, up_grid(N, C, 4), dim3(LORA_THR),
                            lora_lds_bytes(1, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
                            C, N, (int64_t)1, C, (int)R, up_per(N, 4));
     } else {
         OutPtrs<LORA_NE> o;
         for (int e = 0; e < LORA_NE; ++e) o.p[e] = (uint16_t*)out + (int64_t)e * C;
-        hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, false, 1>), up_grid(N, C), dim3(LORA_THR),
+        auto kern = R == 64 ? rwkv6_lora_up_kernel<LORA_NE, false, 1, 2> : rwkv6_lora_up_kernel<LORA_NE, false, 1, 0>;
+        hipLaunchKernelGGL(kern, up_grid(N, C), dim3(LORA_THR),
                            lora_lds_bytes(LORA_NE, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
                            (int64_t)LORA_NE * C, N, (int64_t)1, C, (int)R, up_per(N));
