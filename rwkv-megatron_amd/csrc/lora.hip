@@ -459,7 +459,11 @@ rwkv6_lora_tanh_bwd_kernel(const uint16_t* __restrict__ d_neck, int64_t sE, int6
 // stage 1: block (rb, cb) sums rows [256 rb, 256 rb + 256) of columns [256 cb, 256 cb + 256);
 // thread (q, g) takes 8 columns and the rows q, q + 8, ...; the 8 partials of a column are
 // combined in LDS in a fixed order into part[rb][M] (rwkv6_lora_col_reduce finishes).
+// BATCH rows' loads are issued together: 8 when the grid leaves few waves per CU (17.4 -> 13.0
+// us at N = 16384, M = 2048), 1 when it fills the device (M = 4096: 22.8 us, ~5.9 TB/s, where
+// batches of 8 measured 27 us).  Same summation order either way.
 #define CS_ROWS 256
+template <int BATCH>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_col_sum_kernel(const uint16_t* __restrict__ x, int64_t N, int64_t M,
                      float* __restrict__ part) {
@@ -472,14 +476,24 @@ rwkv6_col_sum_kernel(const uint16_t* __restrict__ x, int64_t N, int64_t M,
         // rows q, q + 8, ... of the block in order; eight loads in flight (unconditional: a
         // row past the end reads the last row and adds zero)
         const int64_t r1 = min<int64_t>(N, r0 + CS_ROWS);
-#pragma unroll 8
-        for (int k = 0; k < CS_ROWS / 8; ++k) {
-            const int64_t rw = r0 + q + 8 * k;
-            const float keep = rw < r1 ? 1.f : 0.f;
-            float f[8];
-            load8(x + (rw < r1 ? rw : r1 - 1) * M + c0, f);
+        static_assert(CS_ROWS % (8 * BATCH) == 0, "rows in whole batches per thread");
+        for (int k0 = 0; k0 < CS_ROWS / 8; k0 += BATCH) {
+            // the batch's 16-byte loads first, then the sums (left to itself the compiler
+            // waited for each load before issuing the next)
+            uint4 raw[BATCH];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a[j] += keep * f[j];
+            for (int k = 0; k < BATCH; ++k) {
+                const int64_t rw = r0 + q + 8 * (k0 + k);
+                raw[k] = *reinterpret_cast<const uint4*>(x + (rw < r1 ? rw : r1 - 1) * M + c0);
+            }
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const float keep = r0 + q + 8 * (k0 + k) < r1 ? 1.f : 0.f;
+                float f[8];
+                unpack8(raw[k], f);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a[j] += keep * f[j];
+            }
         }
     }
 #pragma unroll
@@ -710,9 +724,11 @@ int rwkv6_col_sum(const void* x, int64_t N, int64_t M, int param_dtype, void* ou
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t nb = (N + CS_ROWS - 1) / CS_ROWS;
     float* part = reinterpret_cast<float*>(workspace);
-    if (N > 0)
-        hipLaunchKernelGGL(rwkv6_col_sum_kernel, dim3((unsigned)nb, (unsigned)((M + 255) / 256)),
-                           dim3(LORA_THR), 0, s, (const uint16_t*)x, N, M, part);
+    if (N > 0) {
+        const dim3 grid((unsigned)nb, (unsigned)((M + 255) / 256));
+        auto kern = (int64_t)grid.x * grid.y >= 1024 ? rwkv6_col_sum_kernel<1> : rwkv6_col_sum_kernel<8>;
+        hipLaunchKernelGGL(kern, grid, dim3(LORA_THR), 0, s, (const uint16_t*)x, N, M, part);
+    }
     hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((M + 31) / 32)), dim3(LORA_THR), 0, s,
                        part, N > 0 ? nb : (int64_t)0, M, param_dtype, out);
     return launch_status();
