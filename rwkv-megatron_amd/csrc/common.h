@@ -155,3 +155,48 @@ inline bool any_alias(std::initializer_list<Span> outs, std::initializer_list<Sp
     }
     return false;
 }
+
+// Second stage of every fixed-order reduction over token blocks: out[n] = sum_p part[p][n]
+// for fp32 partials part[P][Nn], written bf16 or fp32 (pdt); columns n >= split go to
+// out2[n - split] (split = Nn: all to out).  Thread (q, nl) of a 256-thread block sums the
+// rows q, q + 8, ... of column 32 blockIdx.x + nl in order, eight loads in flight (clamped:
+// a row past the end reads the last row and adds zero), then the eight row-lane sums are
+// added in order: deterministic, and the same at every launch.  P = 0 writes zeros.
+#define PR_THR 256
+#define PR_BATCH 8
+namespace {
+__global__ void __launch_bounds__(PR_THR)
+partials_reduce_kernel(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
+                       void* __restrict__ out, void* __restrict__ out2, int64_t split) {
+    __shared__ float acc8[8][32];
+    const int q = threadIdx.x >> 5, nl = threadIdx.x & 31;
+    const int64_t n = (int64_t)blockIdx.x * 32 + nl, nc = n < Nn ? n : Nn - 1;
+    float acc = 0.f;
+    for (int64_t p0 = q; p0 < P; p0 += 8 * PR_BATCH) {
+        float v[PR_BATCH];
+#pragma unroll
+        for (int k = 0; k < PR_BATCH; ++k) {
+            const int64_t p = p0 + 8 * k;
+            v[k] = part[(p < P ? p : P - 1) * Nn + nc];
+        }
+#pragma unroll
+        for (int k = 0; k < PR_BATCH; ++k) acc += p0 + 8 * k < P ? v[k] : 0.f;
+    }
+    acc8[q][nl] = acc;
+    __syncthreads();
+    if (q == 0 && n < Nn) {
+        float tot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tot += acc8[j][nl];
+        void* dst = n < split ? out : out2;
+        const int64_t i = n < split ? n : n - split;
+        if (pdt == 1) reinterpret_cast<uint16_t*>(dst)[i] = f2bf(tot);   // RWKV6_BF16
+        else reinterpret_cast<float*>(dst)[i] = tot;
+    }
+}
+inline void launch_partials_reduce(const float* part, int64_t P, int64_t Nn, int pdt, void* out,
+                                   void* out2, int64_t split, hipStream_t s) {
+    hipLaunchKernelGGL(partials_reduce_kernel, dim3((unsigned)((Nn + 31) / 32)), dim3(PR_THR), 0, s,
+                       part, P, Nn, pdt, out, out2, split);
+}
+}  // namespace

@@ -140,31 +140,6 @@ rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
     }
 }
 
-// Column sums of part[P][2][C] (P = B * nTB rows, C = H * 64): dgamma = column sums of the
-// first C columns, dbeta of the last C.  Thread (q, nl): strided partial over rows p = q mod 8,
-// then a fixed-order combine of the 8 partials (deterministic); 64 columns per block.
-__global__ void __launch_bounds__(GN_THR)
-rwkv6_gn_param_reduce(const float* __restrict__ part, int64_t P, int64_t C, int pdt,
-                      void* __restrict__ dgamma, void* __restrict__ dbeta) {
-    __shared__ float acc4[4][64];
-    const int q = threadIdx.x >> 6, nl = threadIdx.x & 63;
-    const int64_t n = (int64_t)blockIdx.x * 64 + nl;
-    float acc = 0.f;
-    if (n < 2 * C) {
-#pragma unroll 4
-        for (int64_t p = q; p < P; p += 4) acc += part[p * 2 * C + n];
-    }
-    acc4[q][nl] = acc;
-    __syncthreads();
-    if (q == 0 && n < 2 * C) {
-        const float tot = (acc4[0][nl] + acc4[1][nl]) + (acc4[2][nl] + acc4[3][nl]);
-        void* dst = n < C ? dgamma : dbeta;
-        const int64_t i = n < C ? n : n - C;
-        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(dst)[i] = f2bf(tot);
-        else reinterpret_cast<float*>(dst)[i] = tot;
-    }
-}
-
 namespace {
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int gn_check(int64_t T, int64_t B, int64_t H, int64_t K, int pdt) {
@@ -239,9 +214,9 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
                            (const uint16_t*)dy, (uint16_t*)d_o, (uint16_t*)d_g_pre,
                            (float*)workspace, T, B, H);
     }
-    hipLaunchKernelGGL(rwkv6_gn_param_reduce, dim3((unsigned)((2 * H * GN_D + 63) / 64)),
-                       dim3(GN_THR), 0, s, (const float*)workspace, T > 0 ? B * nTB : (int64_t)0,
-                       H * GN_D, param_dtype, dgamma, dbeta);
+    // partials [P][2 C]: dgamma columns, then dbeta
+    launch_partials_reduce((const float*)workspace, T > 0 ? B * nTB : (int64_t)0, 2 * H * GN_D,
+                           param_dtype, dgamma, dbeta, H * GN_D, s);
     return launch_status();
 }
 

@@ -409,30 +409,6 @@ rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restri
     }
 }
 
-// out[n] = sum_p part[p][n] (n < Nn) in param dtype: thread (q, n) sums rows p = q mod 8, then
-// a fixed-order combine of the 8 partials (deterministic).
-__global__ void __launch_bounds__(LORA_THR)
-rwkv6_lora_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
-                      void* __restrict__ out) {
-    __shared__ float acc8[8][32];
-    const int q = threadIdx.x >> 5, nl = threadIdx.x & 31;
-    const int64_t n = (int64_t)blockIdx.x * 32 + nl;
-    float acc = 0.f;
-    if (n < Nn) {
-#pragma unroll 4
-        for (int64_t p = q; p < P; p += 8) acc += part[p * Nn + n];
-    }
-    acc8[q][nl] = acc;
-    __syncthreads();
-    if (q == 0 && n < Nn) {
-        float tot = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tot += acc8[j][nl];
-        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(out)[n] = f2bf(tot);
-        else reinterpret_cast<float*>(out)[n] = tot;
-    }
-}
-
 // The backward of the bottleneck's tanh (rwkv6_layer_specs.py:177-195):
 //   d_pre[n][e*R + r] = d_neck(e, n, r) * (1 - neck[n][e*R + r]^2),
 // with d_neck(e, n, r) at d_neck + e*sE + n*sN + r (the up-projection's input gradient as the
@@ -458,7 +434,7 @@ rwkv6_lora_tanh_bwd_kernel(const uint16_t* __restrict__ d_neck, int64_t sE, int6
 // Column sums of x [N, M] bf16 (the bias gradient of a bottleneck, summed over the tokens),
 // stage 1: block (rb, cb) sums rows [256 rb, 256 rb + 256) of columns [256 cb, 256 cb + 256);
 // thread (q, g) takes 8 columns and the rows q, q + 8, ...; the 8 partials of a column are
-// combined in LDS in a fixed order into part[rb][M] (rwkv6_lora_col_reduce finishes).
+// combined in LDS in a fixed order into part[rb][M] (partials_reduce_kernel of common.h finishes).
 // BATCH rows' loads are issued together: 8 when the grid leaves few waves per CU (17.4 -> 13.0
 // us at N = 16384, M = 2048), 1 when it fills the device (M = 4096: 22.8 us, ~5.9 TB/s, where
 // batches of 8 measured 27 us).  Same summation order either way.
@@ -643,8 +619,8 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
                            (const uint16_t*)x, dm, (uint16_t*)d_mexp, (uint16_t*)d_delta_part,
                            (uint16_t*)d_sum, part, N, B, C, (int)R, up_per(N));
     }
-    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((LORA_NE * C + 31) / 32)),
-                       dim3(LORA_THR), 0, s, part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias);
+    launch_partials_reduce(part, nb, (int64_t)LORA_NE * C, param_dtype, d_bias, nullptr,
+                           (int64_t)LORA_NE * C, s);
     return launch_status();
 }
 
@@ -681,8 +657,7 @@ int rwkv6_shift_lerp_bwd(const void* x, const void* maa, int param_dtype, const 
                            dim3(LORA_THR), 0, s, (const uint16_t*)x, maa, param_dtype,
                            (const uint16_t*)d_delta_part, (const uint16_t*)d_sum,
                            (const uint16_t*)d_xxx, (uint16_t*)dx, part, T, B, C);
-    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((C + 31) / 32)), dim3(LORA_THR), 0, s,
-                       part, T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa);
+    launch_partials_reduce(part, T > 0 ? ntb * B : (int64_t)0, C, param_dtype, d_maa, nullptr, C, s);
     return launch_status();
 }
 
@@ -729,8 +704,7 @@ int rwkv6_col_sum(const void* x, int64_t N, int64_t M, int param_dtype, void* ou
         auto kern = (int64_t)grid.x * grid.y >= 1024 ? rwkv6_col_sum_kernel<1> : rwkv6_col_sum_kernel<8>;
         hipLaunchKernelGGL(kern, grid, dim3(LORA_THR), 0, s, (const uint16_t*)x, N, M, part);
     }
-    hipLaunchKernelGGL(rwkv6_lora_col_reduce, dim3((unsigned)((M + 31) / 32)), dim3(LORA_THR), 0, s,
-                       part, N > 0 ? nb : (int64_t)0, M, param_dtype, out);
+    launch_partials_reduce(part, N > 0 ? nb : (int64_t)0, M, param_dtype, out, nullptr, M, s);
     return launch_status();
 }
 

@@ -76,30 +76,6 @@ inline dim3 lerp_grid(int64_t N, int64_t C) {
 #define MIX_TB 64          // tokens per block
 #define MIX_SS 8           // tokens per thread
 
-// out[n] = sum_p part[p][n] for n < Nn, in param dtype; thread (n, q): strided partial over
-// p = q mod 8, then a fixed-order combine (deterministic).
-__global__ void __launch_bounds__(MIX_THR)
-rwkv6_col_reduce(const float* __restrict__ part, int64_t P, int64_t Nn, int pdt,
-                 void* __restrict__ out) {
-    __shared__ float acc8[8][32];
-    const int q = threadIdx.x >> 5, nl = threadIdx.x & 31;
-    const int64_t n = (int64_t)blockIdx.x * 32 + nl;
-    float acc = 0.f;
-    if (n < Nn) {
-#pragma unroll 4
-        for (int64_t p = q; p < P; p += 8) acc += part[p * Nn + n];
-    }
-    acc8[q][nl] = acc;
-    __syncthreads();
-    if (q == 0 && n < Nn) {
-        float tot = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tot += acc8[j][nl];
-        if (pdt == RWKV6_BF16) reinterpret_cast<uint16_t*>(out)[n] = f2bf(tot);
-        else reinterpret_cast<float*>(out)[n] = tot;
-    }
-}
-
 // ---------------------------------------------------------------------------------------
 // Channel mix.
 #define CMIX_NE 2
@@ -432,9 +408,8 @@ int rwkv6_cmix_lerp_bwd(const void* x, const void* mix, int param_dtype,
         hipLaunchKernelGGL(rwkv6_cmix_lerp_bwd_kernel, bwd_grid(T, B, C), dim3(MIX_THR), 0, s,
                            (const uint16_t*)x, mix, param_dtype, dm, (uint16_t*)dx, part, T, B,
                            C);
-    hipLaunchKernelGGL(rwkv6_col_reduce, dim3((unsigned)((CMIX_NE * C + 31) / 32)), dim3(MIX_THR), 0,
-                       s, part, T > 0 ? ntb * B : (int64_t)0, (int64_t)CMIX_NE * C, param_dtype,
-                       d_mix);
+    launch_partials_reduce(part, T > 0 ? ntb * B : (int64_t)0, (int64_t)CMIX_NE * C, param_dtype,
+                           d_mix, nullptr, (int64_t)CMIX_NE * C, s);
     return launch_status();
 }
 
