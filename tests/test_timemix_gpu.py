@@ -46,7 +46,7 @@ def test_shift_lerp(pkg, shape, pdt):
     _check("xxx", _n(xxx), orc.shift_lerp_fwd(_n(x), _n(maa)))
 
 
-@pytest.mark.parametrize("E,R", [(5, 32), (1, 64)])
+@pytest.mark.parametrize("E,R", [(5, 32), (5, 64), (1, 64), (1, 96)])
 def test_bottleneck_module(pkg, E, R):
     """RWKV6Bottleneck.forward (:177-195) on its own, both expansions: [T,B,C] -> [T,B,E,C]
     through the HIP up-projection + bias, forward and every gradient, against the oracle."""
@@ -108,11 +108,13 @@ def test_group_norm_module(pkg, pdt):
         M.GroupNorm(cfg, 2 * H, C, device=DEV)(xg)          # 32-channel groups: no kernel
 
 
-# N = T*B = 10 (a partial 64-token tile), 210 and 520 (several tiles, C > 64)
-@pytest.mark.parametrize("T,B,C,pdt", [(5, 2, 64, torch.float32), (70, 3, 256, torch.float32),
-                                       (130, 4, 192, torch.bfloat16)])
-def test_token_shift_mix_forward_backward(pkg, T, B, C, pdt):
-    R = 32
+# N = T*B = 10 (a partial 64-token tile), 210 and 520 (several tiles, C > 64); rank 32 (the
+# reference's token-shift bottleneck) and 64 (the other rank the kernels take for five mixes,
+# compiled with its own step count)
+@pytest.mark.parametrize("T,B,C,pdt,R", [(5, 2, 64, torch.float32, 32), (70, 3, 256, torch.float32, 32),
+                                         (130, 4, 192, torch.bfloat16, 32),
+                                         (70, 3, 256, torch.float32, 64)])
+def test_token_shift_mix_forward_backward(pkg, T, B, C, pdt, R):
     g = torch.Generator().manual_seed(C)
     x = _bf(torch.randn(T, B, C, generator=g))
     maa = torch.rand(C, generator=g).to(pdt)
@@ -240,7 +242,8 @@ def test_lora_tanh_bwd(pkg, layout, N, E, R):
     _check("d_pre", _n(got), ref.numpy())
 
 
-@pytest.mark.parametrize("N,M", [(1, 8), (255, 360), (257, 64), (16384, 2048)])
+# (16384, 4096): 1024 blocks, the launch that issues one row at a time; the others eight
+@pytest.mark.parametrize("N,M", [(1, 8), (255, 360), (257, 64), (16384, 2048), (16384, 4096)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_col_sum(pkg, N, M, dtype):
     """Column sums of a bf16 [N, M] (a bottleneck's bias gradient over the tokens), ragged N
