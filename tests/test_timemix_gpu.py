@@ -6,6 +6,8 @@ elementwise kernels (their only rounding is the bf16 store); the LoRA weight
 gradients and the decay bottleneck's input gradient go through bf16 hipBLASLt GEMMs and
 use 2e-2.  The reference's elementwise metric is reported for every tensor (tests/parity.py).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -286,3 +288,47 @@ def test_sum_partials_rejects_bad_arguments(pkg):
     assert L.rwkv6_sum_partials(p(x), 2, 12, 0, p(o), s) == pkg._lib.RWKV6_ERR_UNSUPPORTED
     assert L.rwkv6_sum_partials(p(x), 2, 16, 5, p(o), s) == pkg._lib.RWKV6_ERR_INVALID_ARG
     assert L.rwkv6_sum_partials(p(x), 2, 16, 0, p(x), s) == pkg._lib.RWKV6_ERR_INVALID_ARG   # aliasing
+
+
+def test_empty_inputs_zero_parameter_gradients(pkg):
+    """No tokens: every backward that reduces a parameter gradient over the tokens writes zeros
+    (the fixed-order partial sum over zero blocks), and the column sum of an empty matrix is
+    zero.  Outputs start as NaN; the token tensors are never read."""
+    L = pkg._lib.load()
+    E = pkg._lib
+    C, H, K = 128, 2, 64
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    act = torch.zeros(64, C, dtype=torch.bfloat16, device=DEV)      # stand-in token tensors
+    par = torch.zeros(5, C, device=DEV)
+    nan = lambda n, dt=torch.float32: torch.full((n,), float("nan"), dtype=dt, device=DEV)
+    ws = lambda nbytes: torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=DEV)
+
+    out = nan(C)
+    assert L.rwkv6_col_sum(P(act), 0, C, E.RWKV6_F32, P(out), P(ws(L.rwkv6_col_sum_workspace_bytes(0, C))),
+                           sp) == E.RWKV6_OK
+    d_maa = nan(C)                                                   # fp32, as maa
+    assert L.rwkv6_shift_lerp_bwd(P(act), P(par), E.RWKV6_F32, P(act), P(act), P(act), P(act), P(d_maa),
+                                  P(ws(L.rwkv6_shift_lerp_bwd_workspace_bytes(0, 2, C))), 0, 2, C,
+                                  sp) == E.RWKV6_OK
+    d_mix = nan(2 * C)
+    dm2 = (ctypes.c_void_p * 2)(act.data_ptr(), act.data_ptr())
+    assert L.rwkv6_cmix_lerp_bwd(P(act), P(par), E.RWKV6_F32, ctypes.cast(dm2, ctypes.c_void_p), P(act),
+                                 P(d_mix), P(ws(L.rwkv6_cmix_lerp_bwd_workspace_bytes(0, 2, C))), 0, 2, C,
+                                 sp) == E.RWKV6_OK
+    dgamma, dbeta = nan(H * K), nan(H * K)
+    stats = torch.zeros(64, device=DEV)
+    assert L.rwkv6_gn_gate_bwd(P(act), 1, P(act), P(par), P(par), E.RWKV6_F32, P(stats), P(stats), P(act),
+                               P(act), P(act), P(dgamma), P(dbeta),
+                               P(ws(L.rwkv6_gn_gate_bwd_workspace_bytes(0, 2, H, K))), 0, 2, H, K,
+                               sp) == E.RWKV6_OK
+    d_bias = nan(5 * C)
+    dm5 = (ctypes.c_void_p * 5)(*[act.data_ptr()] * 5)
+    assert L.rwkv6_ddlerp_lora_bwd(P(act), P(act), P(act), P(par), E.RWKV6_F32,
+                                   ctypes.cast(dm5, ctypes.c_void_p), P(act), P(act), P(act), P(d_bias),
+                                   P(ws(L.rwkv6_ddlerp_lora_bwd_workspace_bytes(0, 2, C))), 0, 2, C, 32,
+                                   sp) == E.RWKV6_OK
+    torch.cuda.synchronize()
+    for name, t in (("col_sum", out), ("d_maa", d_maa), ("d_mix", d_mix), ("dgamma", dgamma),
+                    ("dbeta", dbeta), ("d_bias", d_bias)):
+        assert torch.equal(t, torch.zeros_like(t)), name
