@@ -30,8 +30,9 @@
 // or the channel mix's two mixes with mix_coeffs [2,C] (NE = 2, rwkv6_cmix_lerp_fwd).  Thread = 8 channels of
 // LERP_ROWS rows (grid.x over channel groups, grid.y over row blocks, striding when the rows
 // outnumber the grid): its coefficients are loaded once and all its row loads are in flight
-// together (clamped rows: no branch).
-#define LERP_ROWS 4
+// together (clamped rows: no branch).  8 rows measured 6-8 % faster than 4 at the config-3
+// shape (28.4 against 30.8 us for xxx, 38.8 against 40.8 for the two mixes); 16 was slower.
+#define LERP_ROWS 8
 template <int NE>
 __global__ void __launch_bounds__(MIX_THR)
 rwkv6_lerp_rows_kernel(const uint16_t* __restrict__ x, const void* __restrict__ coef, int pdt,
@@ -213,9 +214,12 @@ rwkv6_sum_partials_kernel(const float* __restrict__ part, int S, int64_t n8, int
     }
 }
 
-// Elementwise epilogues over n bf16 elements (n % 8 == 0); each thread owns two 16-byte
-// vectors, both loads issued before any arithmetic.
-#define EW_VEC 2          // 16-byte pieces per thread.  Loads and stores clamp the index
+// Elementwise epilogues over n bf16 elements (n % 8 == 0); each thread owns EW_VEC 16-byte
+// vectors, all loads issued before any arithmetic.  One vector per thread (more, smaller-
+// footprint waves) measured faster than two at the config-3 shapes: sigmoid gate backward 54
+// against 68 us, forward 36 against 40, relu^2 78 against 83, its backward 139 against 145;
+// four were slower still.
+#define EW_VEC 1          // 16-byte pieces per thread.  Loads and stores clamp the index
                           // (no branch, so all of a thread's loads are in flight together);
                           // a piece past the end repeats the last one, same value, same place
 __device__ __forceinline__ float sigmoid_(float z) { return 1.f / (1.f + __expf(-z)); }
