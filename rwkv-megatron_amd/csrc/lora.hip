@@ -591,6 +591,9 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
     if (T < 0 || B < 1) return RWKV6_ERR_INVALID_ARG;
     int st = lora_check(LORA_NE, T * B, C, R, param_dtype);
     if (st) return st;
+    // lora_check admits R = 32 and 64 for five mixes (the LDS bound); the kernel is compiled
+    // for exactly those two step counts
+    if (R != 32 && R != 64) return RWKV6_ERR_UNSUPPORTED;
     if (!bias || !d_bias || !workspace ||
         (T > 0 && (!x || !neck || !w_up_t || !d_mexp || !d_delta_part || !d_sum)))
         return RWKV6_ERR_INVALID_ARG;
@@ -612,7 +615,6 @@ int rwkv6_ddlerp_lora_bwd(const void* x, const void* neck, const void* w_up_t, c
     const int64_t N = T * B, nb = (N + LORA_TT - 1) / LORA_TT;
     float* part = reinterpret_cast<float*>(workspace);
     if (N > 0) {
-        // lora_check admits R = 32 and 64 for five mixes (the LDS bound)
         auto kern = R == 32 ? rwkv6_ddlerp_lora_bwd_kernel<1> : rwkv6_ddlerp_lora_bwd_kernel<2>;
         hipLaunchKernelGGL(kern, up_grid(N, C), dim3(LORA_THR), lora_lds_bytes(LORA_NE, (int)R), s,
                            (const uint16_t*)neck, (const uint16_t*)w_up_t, bias, param_dtype,
