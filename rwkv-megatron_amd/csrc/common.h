@@ -76,6 +76,15 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
 __device__ __forceinline__ void store8(uint16_t* p, const float* f) {
     *reinterpret_cast<uint4*>(p) = pack8(f);
 }
+// The same as a nontemporal (streaming) store: for large outputs written once and not read
+// back by the same kernel; it measured much faster for the LoRA up-projection's five mixes
+// and slower for some other outputs, so each call site chooses.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store8_nt(uint16_t* p, const float* f) {
+    const uint4 q = pack8(f);
+    const u32x4_t v = {q.x, q.y, q.z, q.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+}
 // 8 consecutive parameters (RWKV6_BF16 or RWKV6_F32, the codes of rwkv6_amd.h) as fp32.
 // Branch-free: both forms issue two 16-byte loads from in-bounds addresses (the bf16 form
 // reads its one piece twice) and select the converted values, so the caller's other loads
