@@ -400,7 +400,7 @@ rwkv6_shift_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restri
                 out[s] = dsv[s] + dxx[s] - dlt + nd;
                 acc[s] += kv * (dxx[s] * (kp * xp[s] - xv[s]));
             }
-            if (t < T) store8(dx + off, out);
+            if (t < T) store8_nt(dx + off, out);   // streaming: 70 -> 60 us at config 3
         }
     }
 #pragma unroll

@@ -423,10 +423,13 @@ __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restr
     // unconditional (a store under a branch costs the loop a full wait): rows past the end
     // store the last token's own values again
     const int ro = min(row, nvalid - 1);
-    *reinterpret_cast<uint4*>(o + ((size_t)bh * T + t0 + ro) * KD + c8) =
-        *reinterpret_cast<const uint4*>(&sm.Ot[ro][c8]);
-    *reinterpret_cast<uint4*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8) =
-        *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8]);
+    // streaming stores (o and the states are read back only by later kernels): 1 % off the
+    // walk and 8 us off the next call's pre-pass at config 5
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(&sm.Ot[ro][c8])),
+                                reinterpret_cast<u32x4_t*>(o + ((size_t)bh * T + t0 + ro) * KD + c8));
+    __builtin_nontemporal_store(
+        __builtin_bit_cast(u32x4_t, *reinterpret_cast<const uint4*>(&sm.Sin[c & 1][row][c8])),
+        reinterpret_cast<u32x4_t*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8));
 }
 
 // Output walk over segment blockIdx.x % P of sequence blockIdx.x / P.  Segment 0 starts from
