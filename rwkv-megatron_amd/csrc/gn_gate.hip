@@ -62,7 +62,7 @@ rwkv6_gn_gate_fwd_kernel(const uint16_t* __restrict__ o, int head_first,
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             out[i] = ((x[i] - mean) * rstd * ga[i] + be[i]) * (GATE ? z[i] * sigmoidf_(z[i]) : 1.f);
-        store8_nt(y + yo, out);          // streaming: 43.6 -> 40.5 us at the config-3 shape
+        store8(y + yo, out);
         if (l8 == 0) {
             mean_out[(t * B + b) * H + h] = mean;
             rstd_out[(t * B + b) * H + h] = rstd;
@@ -121,9 +121,8 @@ rwkv6_gn_gate_bwd_kernel(const uint16_t* __restrict__ o, int head_first,
         s2 = sum8lanes(s2) * (1.f / GN_D);
 #pragma unroll
         for (int i = 0; i < 8; ++i) outo[i] = rstd * (dxh[i] - s1 - xh[i] * s2);
-        // streaming stores: 67 -> 60 us at the config-3 shape
-        store8_nt(d_o + oo, outo);
-        if (GATE) store8_nt(d_g + yo, outg);
+        store8(d_o + oo, outo);
+        if (GATE) store8(d_g + yo, outg);
     }
     // reduce the 32 group slots of this block (fixed order)
 #pragma unroll
