@@ -51,8 +51,11 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=300,
-                    help="untimed steps first; the GPU's clocks take ~0.1 s of load to settle")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed steps first")
+    ap.add_argument("--settle-s", type=float, default=0.3,
+                    help="then untimed steps for this many seconds right before each timed WKV "
+                         "region: the GPU raises its clocks only after ~30 ms of sustained load "
+                         "and lowers them within milliseconds of idling (reported as settle_s)")
     ap.add_argument("--B", type=int, default=8)
     ap.add_argument("--H", type=int, default=32)
     ap.add_argument("--T", type=int, default=4096)
@@ -211,7 +214,10 @@ def config1_bench(pkg, gpu_steps, with_cpu):
                        "vocab 65536, fp32 weights), batch 2 x 512, fwd+bwd with next-token CE",
            "gpu_ms_per_step": gpu_ms, "gpu_tokens_per_s": B * T / (gpu_ms * 1e-3),
            "gpu_graph_ms_per_step": graph_ms, "gpu_graph_tokens_per_s": B * T / (graph_ms * 1e-3),
-           "gpu_steps": gpu_steps}
+           "gpu_steps": gpu_steps,
+           "gpu_precision": "fp32 parameters, bf16 activations: the GPU figures are a "
+                            "bf16-activation step (the HIP kernels take bf16 r/k/v/w and "
+                            "activations; the CPU baseline runs fp32 throughout)"}
     if with_cpu:
         from oracle import lm
 
@@ -282,7 +288,26 @@ def measured_traffic(B, H, T):
     return d.get("traffic_bytes")
 
 
-def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
+def settle(step, seconds):
+    """Runs untimed steps for `seconds` of wall clock (checked every 10 steps, synchronised):
+    the clocks of an idle GPU are low and rise under ~30 ms of sustained load.  Returns the
+    seconds actually spent and the steps run."""
+    import torch
+
+    if seconds <= 0:
+        return 0.0, 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            step()
+        n += 10
+        torch.cuda.synchronize()
+    return time.perf_counter() - t0, n
+
+
+def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False, settle_s=0.0):
     """WKV6 fwd+bwd through the C ABI (the _ex entries) on synthetic inputs resident in HBM.
     with_state: h0 ~ N(0, 0.5^2), dhT ~ N(0,1), dh0 returned (config 5).
     Three loops of `steps` steps after the warm-up: the timed region proper (ms_per_step) with
@@ -292,7 +317,10 @@ def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
     of the breakdown.  Each event recorded between two kernels adds a gap to the stream (a
     few to tens of microseconds per step), which is why the step time comes from a loop
     without them.
-    Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases, ms_per_step_with_events)."""
+    The warm-up steps and then `settle_s` seconds of steps (settle()) run right before the
+    timed region, untimed.
+    Returns (ms_per_step, fwd_ms, bwd_ms, fwd_phases, bwd_phases, ms_per_step_with_events,
+    settle seconds, settle steps)."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -335,10 +363,11 @@ def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
     for e in [x for evs in fevs + bevs + gevs for x in evs] + [t0, t1, t2, t3]:
         e.record(stream)               # torch creates the hipEvent_t on first record
     torch.cuda.synchronize()
-    # the warm-up runs right before the timed region: an idle GPU lowers its clocks within
-    # milliseconds and takes ~30 ms of load to raise them again
+    # the warm-up and the settle phase run right before the timed region: an idle GPU lowers
+    # its clocks within milliseconds and takes ~30 ms of load to raise them again
     for _ in range(warmup):
         step()
+    settled_s, settled_n = settle(step, settle_s)
     torch.cuda.synchronize()
     t0.record(stream)
     for i in range(steps):
@@ -359,7 +388,7 @@ def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False):
     fwd_ph = [avg(fevs, 2 * p, 2 * p + 1) for p in range(3)]
     bwd_ph = [avg(bevs, 2 * p, 2 * p + 1) for p in range(4)]
     bwd_ph[2] = avg(gevs, 4, 5)        # the roofline kernel, from its own timed loop
-    return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph, ms_step_ev
+    return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph, ms_step_ev, settled_s, settled_n
 
 
 def train_step_bench(pkg, steps, warmup):
@@ -480,7 +509,8 @@ def main():
     B, H, T, K = args.B, args.H, args.T, 64
     N_th = B * H * T
 
-    ms_step, fwd_ms, bwd_ms, fwd_ph, bwd_ph, ms_step_ev = time_wkv(pkg, L, B, H, T, args.steps, args.warmup)
+    ms_step, fwd_ms, bwd_ms, fwd_ph, bwd_ph, ms_step_ev, settle_s, settle_n = time_wkv(
+        pkg, L, B, H, T, args.steps, args.warmup, settle_s=args.settle_s)
 
     grads_ms = bwd_ph[2]
     achieved = N_th * BYTES_BWD_GRADS / (grads_ms * 1e-3) / 1e9
@@ -503,6 +533,8 @@ def main():
         "config": {"workload": "WKV6 fwd+bwd, BASELINE config 2 (chunk_rwkv6 via C ABI)",
                    "B": B, "H": H, "T": T, "K": K, "V": K, "h0": None, "output_final_state": True,
                    "parallelism": "single GPU"},
+        "settle_s": settle_s,
+        "settle_steps": settle_n,
         "ms_per_step_with_roofline_events": ms_step_ev,
         "wkv6_fwd_ms": fwd_ms,
         "wkv6_bwd_ms": bwd_ms,
@@ -522,11 +554,18 @@ def main():
     if not args.no_extra_configs:
         # the long-context one-GPU share with carried state (h0, dhT, dh0)
         B5, H5, T5 = 1, 32, 32768
-        c5 = time_wkv(pkg, L, B5, H5, T5, max(5, args.steps // 2), args.warmup // 2, with_state=True)
+        c5 = time_wkv(pkg, L, B5, H5, T5, args.steps, args.warmup, with_state=True,
+                      settle_s=args.settle_s)
         out["config5"] = {"workload": "BASELINE config 5: WKV6 B=1, H=32, T=32768, h0 ~ N(0,0.5^2), "
                                       "dhT ~ N(0,1), final state and dh0 returned",
                           "ms_per_step": c5[0], "tokens_per_s": B5 * T5 / (c5[0] * 1e-3),
-                          "fwd_ms": c5[1], "bwd_ms": c5[2],
+                          "steps": args.steps, "warmup": args.warmup, "settle_s": c5[6],
+                          "settle_steps": c5[7], "fwd_ms": c5[1], "bwd_ms": c5[2],
+                          "phase_ms": {"fwd_segment_states": c5[3][0], "fwd_segment_fold": c5[3][1],
+                                       "fwd_walk": c5[3][2], "bwd_state_pre_pass": c5[4][0],
+                                       "bwd_state_fold_or_scan": c5[4][1], "bwd_grads": c5[4][2],
+                                       "bwd_du_reduce": c5[4][3]},
+                          "bwd_path": bwd_path(B5 * H5, T5),
                           "tflops": B5 * H5 * T5 * (FLOP_FWD + FLOP_BWD) / (c5[0] * 1e-3) / 1e12}
         if not args.no_cpu_baseline:
             out["config5"]["cpu_baseline"] = cpu_baseline(B5, H5, T5, 0, with_state=True)

@@ -225,9 +225,12 @@ int rwkv6_gn_gate_bwd(const void* o, int head_first, const void* g_pre, const vo
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  Same arguments and results as rwkv6_wkv_fwd minus `workspace`:
  * the forward's scratch (the pre-pass pieces' states, at most 256, and the segments' start
- * states) lives in a library-owned device array of 8.25 MiB per GPU (enough for every shape;
- * larger needs return RWKV6_ERR_UNSUPPORTED).  The call allocates nothing; the first call on a GPU looks the
- * array's address up once.  Calls on one GPU share the array: they must not overlap in time
+ * states) lives in a library-owned device array of 8,454,144 bytes (8.06 MiB: 256 x (two fp32
+ * 64x64 states + one fp32 64-vector)) per GPU (enough for every shape; larger needs return
+ * RWKV6_ERR_UNSUPPORTED).  The call allocates nothing.  The first call on a GPU looks the
+ * array's address up and raises the kernels' LDS limits (host API calls, once per GPU): make
+ * that first call eagerly, before capturing later calls into a HIP graph.  A failed look-up is
+ * retried by the next call.  Calls on one GPU share the array: they must not overlap in time
  * (concurrent calls on two streams of one GPU race).  The caller still provides o, hT and
  * `saved` (rwkv6_wkv_saved_bytes), which rwkv6_wkv_bwd consumes as after rwkv6_wkv_fwd.
  * ---------------------------------------------------------------------- */

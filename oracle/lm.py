@@ -64,33 +64,43 @@ def bottleneck(p, pre, z):
     return torch.einsum("tber,erd->tbed", neck, p[pre + ".weight_up"]) + p[pre + ".bias"]
 
 
+def linear(p, name, x):
+    """Column/RowParallelLinear at TP = 1: x W^T, plus the bias when the layer has one
+    (add_bias_linear / add_qkv_bias, :393, :416, :484-505)."""
+    y = x @ p[name + ".weight"].t()
+    b = p.get(name + ".bias")
+    return y if b is None else y + b
+
+
 def time_mix(p, x, H, eps):
-    """RWKV6TimeMix.forward (:440-466); p maps the module's parameter names to tensors."""
+    """RWKV6TimeMix.forward (:440-466); p maps the module's parameter names to tensors.  The
+    output projection's bias, which the reference hands back separately (skip_bias_add, :418)
+    for the layer's bias-dropout-add, is included in the returned output."""
     delta = token_shift(x) - x
     mixed_input = x + delta * p["mix_coeff_input"]
     mix = bottleneck(p, "bottleneck_token_shift", mixed_input)
     m_w, m_k, m_v, m_r, m_g = (x.unsqueeze(-2) + delta.unsqueeze(-2) * mix).unbind(-2)
     decay = bottleneck(p, "bottleneck_decay", m_w).squeeze(-2)
-    key = m_k @ p["linear_key.weight"].t()
-    value = m_v @ p["linear_value.weight"].t()
-    rec = m_r @ p["linear_receptance.weight"].t()
-    gate = F.silu(m_g @ p["linear_gate.weight"].t())
+    key = linear(p, "linear_key", m_k)
+    value = linear(p, "linear_value", m_v)
+    rec = linear(p, "linear_receptance", m_r)
+    gate = F.silu(linear(p, "linear_gate", m_g))
     T, B, C = x.shape
     hf = lambda t: t.reshape(T, B, H, C // H).permute(1, 2, 0, 3).contiguous()   # :333-336
     o = OracleWKV.apply(hf(rec), hf(key), hf(value), -torch.exp(hf(decay)),
                         p["core_attention.time_first"].reshape(H, -1))
     o = o.permute(2, 0, 1, 3).reshape(T * B, C)                                    # :341, :462
     y = F.group_norm(o, H, p["group_norm.weight"], p["group_norm.bias"], eps=eps).reshape(T, B, C)
-    return (y * gate) @ p["linear_proj.weight"].t()
+    return linear(p, "linear_proj", y * gate)
 
 
 def channel_mix(p, x):
     """RWKV6ChannelMix.forward (:512-536)."""
     delta = token_shift(x) - x
     mixed_up, mixed_gate = (x.unsqueeze(-2) + delta.unsqueeze(-2) * p["mix_coeffs"]).unbind(-2)
-    h = torch.square(torch.relu(mixed_up @ p["linear_up.weight"].t()))
-    out = h @ p["linear_down.weight"].t()
-    return out * torch.sigmoid(mixed_gate @ p["linear_gate.weight"].t())
+    h = torch.square(torch.relu(linear(p, "linear_up", mixed_up)))
+    out = linear(p, "linear_down", h)
+    return out * torch.sigmoid(linear(p, "linear_gate", mixed_gate))
 
 
 def _sub(p, prefix):

@@ -84,17 +84,31 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} not found: build it with `python rwkv-megatron_amd/build.py` "
                 "(or __graft_entry__.build()); there is no fallback implementation")
-        L = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in SIGNATURES.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
-        if L.rwkv6_abi_version() != ABI_VERSION:
-            raise RuntimeError(
-                f"{LIB_PATH} has ABI version {L.rwkv6_abi_version()}, these bindings expect "
-                f"{ABI_VERSION}: rebuild it with `python rwkv-megatron_amd/build.py`")
-        _lib = L
+        _lib = bind(ctypes.CDLL(LIB_PATH), LIB_PATH)
     return _lib
+
+
+def bind(L: ctypes.CDLL, path: str) -> ctypes.CDLL:
+    """Checks the library's ABI version first (a stale build lacks newer symbols, and
+    binding them would fail with a bare AttributeError), then sets every signature."""
+    ver = getattr(L, "rwkv6_abi_version", None)
+    if ver is None:
+        raise RuntimeError(f"{path} exports no rwkv6_abi_version: not this library, or a "
+                           "broken build; rebuild it with `python rwkv-megatron_amd/build.py`")
+    ver.restype, ver.argtypes = SIGNATURES["rwkv6_abi_version"]
+    if ver() != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} has ABI version {ver()}, these bindings expect {ABI_VERSION}: "
+            "rebuild it with `python rwkv-megatron_amd/build.py`")
+    missing = [n for n in SIGNATURES if not hasattr(L, n)]
+    if missing:
+        raise RuntimeError(f"{path} (ABI version {ABI_VERSION}) lacks {missing}: rebuild it "
+                           "with `python rwkv-megatron_amd/build.py`")
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
 
 
 def check(status: int, what: str) -> None:

@@ -101,19 +101,6 @@ __device__ __forceinline__ void load_param8(const void* p, int dtype, int64_t of
     for (int s = 0; s < 8; ++s) f[s] = h ? hf[s] : __builtin_bit_cast(float, w[s]);
 }
 
-// Splits fp32 values into bf16 hi + lo parts (hi + lo carries ~16 mantissa bits):
-// an MFMA against both parts keeps operand rounding out of cancelling sums.
-template <int N>
-__device__ __forceinline__ void split_bf16(const float* f,
-                                           __bf16 __attribute__((ext_vector_type(N))) & hi,
-                                           __bf16 __attribute__((ext_vector_type(N))) & lo) {
-#pragma unroll
-    for (int s = 0; s < N; ++s) {
-        hi[s] = (__bf16)f[s];
-        lo[s] = (__bf16)(f[s] - (float)hi[s]);
-    }
-}
-
 // Lane exchanges without an address operand: DPP (a modifier of the consuming VALU op)
 // within rows of 16 lanes, ds_swizzle within 32 lanes; only the exchange across the two
 // 32-lane halves goes through ds_bpermute.

@@ -32,10 +32,12 @@
 //
 // Operands that reduce over tokens are read from the same token-major LDS tile with
 // the gfx950 LDS transpose read (ds_read_b64_tr_b16), so no tile is stored twice.
-// Every MFMA accumulates in fp32 and the carried states are fp32.  In the dr / dk
-// contractions Rm / Km are bf16 hi + lo pairs: dw is a cancelling suffix sum of
-// r*dr - k*dk, and single-bf16 operands there would dominate its error.
+// Every MFMA accumulates in fp32 and the carried states are fp32.  dw is a cancelling suffix
+// sum of Rm*acc_r - Km*acc_k: its terms cancel exactly only if the epilogue multiplies the
+// accumulators by the very bf16 Rm, Km the products used, so it does (single bf16 operands,
+// no hi + lo split).
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -132,15 +134,6 @@ __device__ __forceinline__ bf16x8 scale8(bf16x8 x, const float* f) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) y[s] = (float)x[s] * f[s];
     return __builtin_bit_cast(bf16x8, pack8(y));
-}
-// hi / lo split of 8 fp32 values, packed
-__device__ __forceinline__ void pack8_split(const float* f, uint4& hi, uint4& lo) {
-    float h[8], l[8];
-    hi = pack8(f);
-    unpack8(hi, h);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) l[s] = f[s] - h[s];
-    lo = pack8(l);
 }
 
 // ---------------------------------------------------------------------------
@@ -2399,20 +2392,37 @@ int stream_device(hipStream_t stream, int* dev, int* cur) {
     return (*dev < 0 || *dev >= kMaxDevices) ? RWKV6_ERR_UNSUPPORTED : RWKV6_OK;
 }
 
-// The dynamic-LDS limit of every kernel here that takes more than 64 KB, raised once per
-// device (with that device current) instead of on every call.
-struct AttrSlot {
-    std::once_flag once;
-    int status = RWKV6_ERR_LAUNCH;
+// Per-device set-up that is done once it has succeeded, with that device current: a failed
+// attempt is not cached, the next call tries again.  After the first success a call costs one
+// atomic load.  Set-up runs host API calls (attribute and symbol queries, no allocation); a
+// caller that captures the library's launches into a HIP graph makes one eager call on the
+// device first, so that none of it runs under capture.
+struct DeviceOnce {
+    std::mutex m;
+    std::atomic<bool> done{false};
 };
-AttrSlot g_lds_attr[kMaxDevices];
+template <class F>
+int device_once(DeviceOnce& slot, int dev, int cur, F&& body) {
+    if (slot.done.load(std::memory_order_acquire)) return RWKV6_OK;
+    std::lock_guard<std::mutex> lock(slot.m);
+    if (slot.done.load(std::memory_order_relaxed)) return RWKV6_OK;
+    hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+    if (e == hipSuccess) e = body();
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return RWKV6_ERR_LAUNCH;
+    slot.done.store(true, std::memory_order_release);
+    return RWKV6_OK;
+}
+
+// The dynamic-LDS limit of every kernel here that takes more than 64 KB, raised once per
+// device instead of on every call.
+DeviceOnce g_lds_attr[kMaxDevices];
 
 int lds_attributes(hipStream_t stream) {
     int dev = 0, cur = 0;
     int st = stream_device(stream, &dev, &cur);
     if (st != RWKV6_OK) return st;
-    AttrSlot& slot = g_lds_attr[dev];
-    std::call_once(slot.once, [&slot, dev, cur] {
+    return device_once(g_lds_attr[dev], dev, cur, [] {
         struct Lds {
             const void* fn;
             size_t bytes;
@@ -2425,14 +2435,12 @@ int lds_attributes(hipStream_t stream) {
             {reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<false>), sizeof(GradSmem)},
             {reinterpret_cast<const void*>(wkv6_bwd_chunk_grads<true>), sizeof(GradSmem)},
         };
-        hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+        hipError_t e = hipSuccess;
         for (const Lds& x : list)
             if (e == hipSuccess)
                 e = hipFuncSetAttribute(x.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)x.bytes);
-        if (dev != cur) (void)hipSetDevice(cur);
-        slot.status = e == hipSuccess ? RWKV6_OK : RWKV6_ERR_LAUNCH;
+        return e;
     });
-    return slot.status;
 }
 
 // max_pieces bounds the pre-pass pieces (the workspace's capacity): PIECE_TARGET for a
@@ -2624,29 +2632,25 @@ static __device__ __align__(256) unsigned char scratch[WKV_SCRATCH_BYTES];
 
 namespace {
 
-struct ScratchSlot {
-    std::once_flag once;
-    int status = RWKV6_ERR_LAUNCH;
-    void* ptr = nullptr;
-};
-ScratchSlot g_scratch[kMaxDevices];
+DeviceOnce g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
 
 // Device address of `scratch` on the GPU that runs `stream` (the current device for the
-// NULL stream).  Looked up once per device, with that device current; in host code the
-// array's name is only a stand-in, never a device address.
+// NULL stream).  Looked up once per device, with that device current (device_once); in host
+// code the array's name is only a stand-in, never a device address.
 int scratch_address(hipStream_t stream, void** out) {
     int dev = 0, cur = 0;
-    const int st = stream_device(stream, &dev, &cur);
+    int st = stream_device(stream, &dev, &cur);
     if (st != RWKV6_OK) return st;
-    ScratchSlot& slot = g_scratch[dev];
-    std::call_once(slot.once, [&slot, dev, cur] {
-        hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
-        if (e == hipSuccess) e = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch));
-        if (dev != cur) (void)hipSetDevice(cur);
-        slot.status = (e == hipSuccess && slot.ptr) ? RWKV6_OK : RWKV6_ERR_LAUNCH;
+    st = device_once(g_scratch_once[dev], dev, cur, [dev] {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess && !p) e = hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+        return e;
     });
-    *out = slot.ptr;
-    return slot.status;
+    *out = st == RWKV6_OK ? g_scratch_ptr[dev] : nullptr;
+    return st;
 }
 
 }  // namespace

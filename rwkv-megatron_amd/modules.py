@@ -17,14 +17,25 @@ way (Megatron's module prefix aside).  The hot path runs on the HIP kernels:
     relu^2, sigmoid(gate) * out          -> channelmix.relu_sq / sigmoid_gate (HIP)
     up / gate / down projections         -> torch.matmul
 
+Construction from Megatron's own TransformerConfig.  The layer spec (:539-550) builds
+``RWKV6TimeMix(config, layer_number)`` and ``RWKV6ChannelMix(config)``; the config then carries
+Megatron's fields plus the two bottleneck sizes pretrain_rwkv6.py:61-69 adds.  Every field
+read here is one of those, or is read with getattr and a default:
+  hidden_size, num_attention_heads, ffn_hidden_size, num_layers, layernorm_epsilon,
+  params_dtype, perform_initialization, init_method_std, token_shift_bottleneck_size,
+  decay_bottleneck_size; optional: init_method / output_layer_init_method (callables, as
+  Megatron's config sets them; else normal(0, std) and normal(0, std / sqrt(2 L))),
+  add_bias_linear / add_qkv_bias (default False), sequence_parallel (must be False: one
+  GPU, no token-shift halo), rwkv_lm_decay_init (this package's own switch, default False).
+
 Deliberate differences, all documented in the reference's own terms:
   * ``mix_coeff_input`` and ``RWKV6ChannelMix.mix_coeffs`` are left uninitialised by
     the reference (torch.empty, :377-385, :475-477); here they get the RWKV-6 ramp
-    ``1 - (c / C) ** (1 - l / L)`` so a freshly built model is finite.
+    ``1 - (c / C) ** (1 - l / L)`` so a freshly built model is finite.  Megatron builds the
+    channel mix without a layer number (:547); it then gets the first layer's ramp
+    (l = 0) in every layer, and a checkpoint (from_rwkv_lm) sets the real values.
   * The decay bias keeps the reference's uniform(-1, 1) (:173-175) unless
-    ``TransformerConfig.rwkv_lm_decay_init`` asks for RWKV-LM's ramp.
-  * Biases on the linear layers are absent (config ``add_bias_linear = False``,
-    the reference's example config), matching ``bias=...add_bias_linear`` (:393, :416).
+    ``rwkv_lm_decay_init`` asks for RWKV-LM's ramp.
   * LayerNorms and the output head cast their parameters to the activations' dtype, so fp32
     parameters train with bf16 activations (the HIP kernels take bf16 activations).
 """
@@ -54,10 +65,21 @@ class TransformerConfig:
     init_method_std: float = 0.02                # example_config.yaml:31
     params_dtype: torch.dtype = torch.bfloat16
     perform_initialization: bool = True
+    add_bias_linear: bool = False                # example_config.yaml:20
+    add_qkv_bias: bool = False                   # example_config.yaml:22
+    sequence_parallel: bool = False              # one GPU: no sequence-parallel token shift
     # The reference initialises the decay bottleneck's bias uniform(-1, 1) (:173-175).  True
     # selects RWKV-LM's per-channel ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1)) instead (the
-    # tiny-LM benchmark configuration asks for it).
+    # tiny-LM benchmark configuration asks for it).  Not a Megatron field: read with getattr.
     rwkv_lm_decay_init: bool = False
+
+
+def _check_config(config):
+    """Megatron options this one-GPU mirror does not implement raise here, at construction."""
+    if getattr(config, "sequence_parallel", False):
+        raise NotImplementedError(
+            "sequence_parallel: the token-shift halo exchange (rwkv6_layer_specs.py:213-287) is "
+            "multi-GPU and not built here")
 
 
 def _ramp(C, layer_id, n_layers, device):
@@ -110,16 +132,34 @@ class _LinearFn(torch.autograd.Function):
 
 
 class _Linear(nn.Module):
-    """Column/RowParallelLinear at TP=1: weight [out, in], y = x @ W^T (no bias)."""
+    """Column/RowParallelLinear at TP=1: weight [out, in], y = x @ W^T, optional bias.
 
-    def __init__(self, cfg, n_in, n_out, std, device):
+    The weight is initialised by the config's Megatron init callable (``init_attr``:
+    ``init_method`` or ``output_layer_init_method``) when it has one, else normal(0, std);
+    the bias, as Megatron's, with zeros.  forward returns (y + bias, None), or (y, bias) with
+    ``skip_bias_add`` (RowParallelLinear of the time mix's output projection, :411-421)."""
+
+    def __init__(self, cfg, n_in, n_out, std, device, init_attr="init_method", bias=False,
+                 skip_bias_add=False):
         super().__init__()
         self.weight = nn.Parameter(torch.empty(n_out, n_in, device=device, dtype=cfg.params_dtype))
+        self.bias = (nn.Parameter(torch.zeros(n_out, device=device, dtype=cfg.params_dtype))
+                     if bias else None)
+        self.skip_bias_add = skip_bias_add
         if cfg.perform_initialization:
-            nn.init.normal_(self.weight, 0.0, std)
+            init = getattr(cfg, init_attr, None)
+            with torch.no_grad():
+                if callable(init):
+                    init(self.weight)
+                else:
+                    nn.init.normal_(self.weight, 0.0, std)
 
     def forward(self, x):
-        return _LinearFn.apply(x, self.weight), None
+        y = _LinearFn.apply(x, self.weight)
+        if self.bias is None:
+            return y, None
+        b = self.bias.to(y.dtype)
+        return (y, b) if self.skip_bias_add else (y + b, None)
 
 
 class LayerNorm(nn.LayerNorm):
@@ -215,6 +255,7 @@ class RWKV6TimeMix(nn.Module):
 
     def __init__(self, config, layer_number=1, device=None):
         super().__init__()
+        _check_config(config)
         self.config = config
         C = config.hidden_size
         self.layer_number = layer_number
@@ -224,19 +265,23 @@ class RWKV6TimeMix(nn.Module):
         self.mix_coeff_input = nn.Parameter(torch.empty(C, device=device, dtype=config.params_dtype))
         std = config.init_method_std
         out_std = std / math.sqrt(2.0 * config.num_layers)
-        self.linear_receptance = _Linear(config, C, C, std, device)
-        self.linear_key = _Linear(config, C, C, std, device)
-        self.linear_value = _Linear(config, C, C, std, device)
-        self.linear_gate = _Linear(config, C, C, std, device)
+        bias_lin = getattr(config, "add_bias_linear", False)
+        bias_qkv = bias_lin or getattr(config, "add_qkv_bias", False)       # :393
+        col = lambda: _Linear(config, C, C, std, device, bias=bias_qkv)
+        self.linear_receptance = col()
+        self.linear_key = col()
+        self.linear_value = col()
+        self.linear_gate = col()
         self.core_attention = WKV6(config, layer_number, device)
         self.group_norm = GroupNorm(config, config.num_attention_heads, C, config.layernorm_epsilon, device)
-        self.linear_proj = _Linear(config, C, C, out_std, device)
+        self.linear_proj = _Linear(config, C, C, out_std, device, "output_layer_init_method",
+                                   bias=bias_lin, skip_bias_add=True)       # :411-421
         self.num_heads_per_partition = config.num_attention_heads
         self.head_size = C // config.num_attention_heads
         if config.perform_initialization:
             with torch.no_grad():
                 self.mix_coeff_input.copy_(_ramp(C, layer_number - 1, config.num_layers, device))
-                if config.rwkv_lm_decay_init:
+                if getattr(config, "rwkv_lm_decay_init", False):
                     # RWKV-LM's decay ramp -6 + 5 (c/(C-1))^(0.7 + 1.3 l/(L-1))
                     L = max(config.num_layers - 1, 1)
                     c = torch.arange(C, dtype=torch.float32, device=device) / max(C - 1, 1)
@@ -270,18 +315,23 @@ class RWKV6TimeMix(nn.Module):
 class RWKV6ChannelMix(nn.Module):
     """rwkv6_layer_specs.py:471-536 (TP = 1)."""
 
-    def __init__(self, config, layer_number=1, device=None):
+    def __init__(self, config, layer_number=None, device=None):
+        """Megatron builds this module as ``RWKV6ChannelMix(config)`` (:471-473, :547): with no
+        layer number the mix coefficients get the first layer's ramp."""
         super().__init__()
+        _check_config(config)
         self.config = config
         C, Fh = config.hidden_size, config.ffn_hidden_size
         self.mix_coeffs = nn.Parameter(torch.empty(2, C, device=device, dtype=config.params_dtype))
         std = config.init_method_std
-        self.linear_up = _Linear(config, C, Fh, std, device)
-        self.linear_gate = _Linear(config, C, C, std, device)
-        self.linear_down = _Linear(config, Fh, C, std / math.sqrt(2.0 * config.num_layers), device)
+        bias = getattr(config, "add_bias_linear", False)                     # :484, :495, :505
+        self.linear_up = _Linear(config, C, Fh, std, device, bias=bias)
+        self.linear_gate = _Linear(config, C, C, std, device, bias=bias)
+        self.linear_down = _Linear(config, Fh, C, std / math.sqrt(2.0 * config.num_layers), device,
+                                   "output_layer_init_method", bias=bias)
         if config.perform_initialization:
             with torch.no_grad():
-                ramp = _ramp(C, layer_number - 1, config.num_layers, device)
+                ramp = _ramp(C, (layer_number or 1) - 1, config.num_layers, device)
                 self.mix_coeffs.copy_(torch.stack([ramp, ramp]))
 
     def forward(self, hidden_states):
@@ -307,8 +357,8 @@ class RWKV6Layer(nn.Module):
         self.mlp = RWKV6ChannelMix(config, layer_number, device)
 
     def forward(self, x):
-        a, _ = self.self_attention(self.input_layernorm(x), None)
-        x = x + a
+        a, a_bias = self.self_attention(self.input_layernorm(x), None)
+        x = x + a if a_bias is None else x + (a + a_bias)    # bias-dropout-add, dropout 0
         m, _ = self.mlp(self.pre_mlp_layernorm(x))
         return x + m
 

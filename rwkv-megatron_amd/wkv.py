@@ -13,7 +13,9 @@ same contract (4th argument named ``g``).  Both names are provided here:
 * scale None or -1 means K**-0.5 (fla's convention); any other float is used as is.
 * initial_state: [B,H,K,V] (computed in fp32); final_state is fp32 or None.
 * o has r's dtype.  Arithmetic: bf16 operands on MFMA, fp32 accumulation and fp32
-  carried state; fp32 / fp16 inputs are rounded to bf16 on entry.
+  carried state.  bf16 r, k, v, g are used as they are; fp32 / fp16 ones are rounded to
+  bf16 on entry (one rounding each, 2^-9 relative), so an fp32 caller gets bf16-operand
+  arithmetic, not fp32 arithmetic.  u is used in its own dtype (fp32 or bf16).
 * Backward returns gradients for r, k, v, g, u and initial_state, and accepts a
   gradient on final_state.
 """

@@ -134,3 +134,23 @@ def test_wrapper_rejects_cpu_tensors(pkg):
         pkg.chunk_rwkv6(x, x, x, x, torch.zeros(1, 64))
     with pytest.raises(NotImplementedError):
         pkg.chunk_rwkv6(x, x, x, x, torch.zeros(1, 64), cu_seqlens=torch.tensor([0, 4]))
+
+
+@pytest.mark.parametrize("version,msg", [(2, "ABI version 2"), (None, "lacks")])
+def test_stale_library_gets_the_rebuild_message(pkg, tmp_path, version, msg):
+    """A stub library built here with gcc: an older ABI version, or the current version with
+    symbols missing, must fail with the rebuild hint, not a ctypes AttributeError."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    v = pkg._lib.ABI_VERSION if version is None else version
+    src = tmp_path / "stub.c"
+    src.write_text(f"int rwkv6_abi_version(void) {{ return {v}; }}\n"
+                   "const char* rwkv6_strerror(int c) { (void)c; return \"ok\"; }\n")
+    so = tmp_path / "libstub.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", "-o", str(so), str(src)], check=True)
+    with pytest.raises(RuntimeError, match="rebuild") as e:
+        pkg._lib.bind(ctypes.CDLL(str(so)), str(so))
+    assert msg in str(e.value)

@@ -71,3 +71,51 @@ def test_state_dict_contract(pkg):
     assert {n: tuple(t.shape) for n, t in cm.state_dict().items()} == {
         "mix_coeffs": (2, C), "linear_up.weight": (448, C), "linear_gate.weight": (C, C),
         "linear_down.weight": (C, 448)}
+
+
+@pytest.mark.parametrize("add_bias_linear", [False, True])
+def test_megatron_built_modules_match_reference(pkg, add_bias_linear):
+    """The Megatron route: RWKV6TimeMix(config, layer_number) and RWKV6ChannelMix(config) built
+    from a config with Megatron's field names only (test_module_config.megatron_config), on the
+    CPU, then moved to the GPU as Megatron's get_model does; forward and every gradient against
+    the reference's forward restated in oracle/lm.py (at the block bars)."""
+    from test_module_config import megatron_config
+
+    M = pkg.modules
+    cfg = megatron_config(C=256, H=4, F=896, L=2, params_dtype=torch.bfloat16,
+                          add_bias_linear=add_bias_linear)
+    torch.manual_seed(3)
+    tm = M.RWKV6TimeMix(cfg, 2)
+    cm = M.RWKV6ChannelMix(cfg)
+    with torch.no_grad():
+        for bn in (tm.bottleneck_token_shift, tm.bottleneck_decay):
+            bn.weight_down.uniform_(-0.1, 0.1)
+            bn.weight_up.uniform_(-0.1, 0.1)
+        for mod in (tm, cm):
+            for n, prm in mod.named_parameters():
+                if n.startswith("linear_") and n.endswith(".bias"):
+                    prm.normal_(0.0, 0.1)
+    tm, cm = tm.to("cuda:0"), cm.to("cuda:0")
+    T, B, C = 80, 2, 256
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(T, B, C, generator=g).to(torch.bfloat16)
+    dy = torch.randn(T, B, C, generator=g).to(torch.bfloat16)
+    n = lambda t: t.detach().double().cpu().numpy()
+    bars = parity.BLOCK_BARS
+    for name, mod, ref_fn in (("time_mix", tm, lambda p, z: lm.time_mix(p, z, 4, cfg.layernorm_epsilon)),
+                              ("channel_mix", cm, lm.channel_mix)):
+        xg = x.to("cuda:0").requires_grad_(True)
+        out, bias = mod(xg, None) if name == "time_mix" else mod(xg)
+        if bias is not None:
+            assert name == "time_mix" and add_bias_linear
+            out = out + bias
+        (out.float() * dy.to("cuda:0").float()).sum().backward()
+        torch.cuda.synchronize()
+        p = {k: t.detach().float().cpu().requires_grad_(True) for k, t in mod.named_parameters()}
+        xc = x.float().requires_grad_(True)
+        ref = ref_fn(p, xc)
+        (ref * dy.float()).sum().backward()
+        parity.check(f"{name} out", n(out), n(ref), **bars)
+        parity.check(f"{name} dx", n(xg.grad), n(xc.grad), **bars)
+        got = {k: n(prm.grad) for k, prm in mod.named_parameters()}
+        parity.check_all(got, {k: n(p[k].grad) for k in got}, sorted(got), **bars)

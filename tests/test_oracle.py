@@ -359,3 +359,17 @@ def test_lm_loss_is_masked_mean_cross_entropy():
     want = torch.nn.functional.cross_entropy(logits[:-1].transpose(0, 1).reshape(-1, V),
                                              tgt[:, :-1].reshape(-1))
     assert abs(float(got) - float(want)) < 1e-12
+
+
+def test_lm_linear_with_and_without_bias_is_f_linear():
+    """oracle/lm.py's linear (the TP = 1 Column/RowParallelLinear, bias when the layer has one)
+    against torch.nn.functional.linear, the library routine."""
+    from oracle import lm
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 3, 16, generator=g, dtype=torch.float64)
+    w = torch.randn(8, 16, generator=g, dtype=torch.float64)
+    b = torch.randn(8, generator=g, dtype=torch.float64)
+    assert torch.allclose(lm.linear({"l.weight": w}, "l", x), torch.nn.functional.linear(x, w))
+    assert torch.allclose(lm.linear({"l.weight": w, "l.bias": b}, "l", x),
+                          torch.nn.functional.linear(x, w, b))

@@ -67,6 +67,56 @@ def test_noalloc_forward_matches_workspace_forward(pkg):
         parity.check(f"call {i} hT", n(got[1]), hT_ref, elem_mean=parity.ELEM_MEAN_WKV)
 
 
+def _noalloc_args(pkg, r, k, v, w, u, h0, o, hT, saved):
+    B, H, T, K = r.shape
+    P = lambda t: ctypes.c_void_p(0 if t is None else t.data_ptr())
+    return (P(r), P(k), P(v), P(w), P(u), pkg._lib.RWKV6_F32, P(h0), P(o), P(hT), P(saved),
+            B, H, T, K, K, 1.0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def test_noalloc_forward_replays_from_a_hip_graph(pkg):
+    """The no-alloc forward captured in a HIP graph (torch.cuda.CUDAGraph) after one eager call
+    on the device, replayed three times with eager no-alloc calls of another shape in between
+    (they overwrite the shared scratch array): every replay is bit-identical to rwkv6_wkv_fwd."""
+    L = pkg._lib.load()
+    (B, H, T, _), (B2, H2, T2, _) = CALLS
+    print(f"graph: B={B} H={H} T={T}, between replays B={B2} H={H2} T={T2}", flush=True)
+    r, k, v, w, u, h0 = (t.to(DEV) for t in _inputs(B, H, T, seed=7))
+    want = _forward(pkg, False, r, k, v, w, u, h0)
+    o = torch.empty_like(v)
+    hT = torch.empty(B, H, 64, 64, dtype=torch.float32, device=DEV)
+    saved = torch.empty(L.rwkv6_wkv_saved_bytes(B, H, T, 64, 64), dtype=torch.uint8, device=DEV)
+    other = [t.to(DEV) for t in _inputs(B2, H2, T2, seed=8)]
+    o2 = torch.empty_like(other[2])
+    hT2 = torch.empty(B2, H2, 64, 64, dtype=torch.float32, device=DEV)
+    saved2 = torch.empty(L.rwkv6_wkv_saved_bytes(B2, H2, T2, 64, 64), dtype=torch.uint8, device=DEV)
+    # the eager first call on the device (documented: set-up must not run under capture)
+    pkg._lib.check(L.rwkv6_wkv_fwd_noalloc(*_noalloc_args(pkg, r, k, v, w, u, h0, o, hT, saved)),
+                   "eager no-alloc forward")
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            st = L.rwkv6_wkv_fwd_noalloc(*_noalloc_args(pkg, r, k, v, w, u, h0, o, hT, saved))
+    torch.cuda.current_stream().wait_stream(side)
+    pkg._lib.check(st, "captured no-alloc forward")
+    for rep in range(3):
+        o.zero_()
+        hT.zero_()
+        saved.zero_()
+        pkg._lib.check(L.rwkv6_wkv_fwd_noalloc(*_noalloc_args(pkg, *other[:5], None, o2, hT2, saved2)),
+                       "eager no-alloc forward, other shape")
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("o", "hT", "saved"), (o.cpu(), hT.cpu(), saved.cpu()), want):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from rwkv6_wkv_fwd"
+        print(f"replay {rep}: bit-identical", flush=True)
+    del graph
+
+
 def test_noalloc_rejects_bad_shapes_before_launch(pkg):
     L = pkg._lib.load()
     p = ctypes.c_void_p(0x100000)
