@@ -1605,6 +1605,7 @@ struct LoopSmem {
     // then the tiles in decreasing order of accesses per chunk.
     float emu[4][KD], eg[4][KD], kb[3][KD], fp[6][KD], eG63[KD];
     float bonus[CL], Dv[KD], dd[CL];  // dd[t] = dO_t . v_t
+    float uh[KD];                   // u of the head (fp32), for the bonus
     float Pk[4][KD];                // per-wave sums of Km acc_k^{inter}, for D
     float red[8][KD];               // block totals and mu of the decay scan, then dw block
                                     // totals [0..3] and du partials [4..7]
@@ -1763,10 +1764,10 @@ __device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, c
     lds_st<uint2>(&sm.Ab[b][0][0], o.frag, make_uint2(pk2(x[0], x[1]), pk2(x[2], x[3])));
 }
 
-// dr and dk of the wave's token block W and channel column ch = 16 col + lr (the factors and
-// operands as in grads_products, the 16x16 blocks read from dAb).
-template <bool SEQ>
-__device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, float scale,
+// dr and dk of the wave's token block W (compile-time) and channel column ch = 16 col + lr (the
+// factors and operands as in grads_products, the 16x16 blocks read from dAb).
+template <bool SEQ, int W>
+__device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float scale,
                                                  const GradLane& g, GradOut& out,
                                                  const LaneOfs& o) {
     const int TW = 16 * W, c0 = 16 * col;
@@ -1786,7 +1787,8 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
             tmp = mfma32(row8o(&sm.Dt[0][0], o, TW, 32 * ks), row8o(&sm.Sin[0][0], o, c0, 32 * ks), tmp);
         ar = tmp * lds_ld<float>(&sm.emu[W][c0], o.tab);
     }
-    const int bW = (W * (W + 1)) / 2;
+    constexpr int bW = (W * (W + 1)) / 2;
+#pragma unroll
     for (int J = 0; J < W; ++J) {
         const f32x4 t2 = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + J][0][0], o.blk), ch4o(KTp, o, c0, 16 * J), f32x4{});
         ar += (t2 * lds_ld<float>(&sm.kb[J][c0], o.tab)) * lds_ld<float>(&sm.fp[(W * (W - 1)) / 2 + J][c0], o.tab);
@@ -1819,6 +1821,7 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
         if (o.q16 == 0) lds_st<float>(&sm.Pk[W][c0], o.tab, p);
     }
     ak2 = mfma16(lds_tr(&sm.dAb[bW + W][0][0], o.blktr), ch4o(RTp, o, c0, TW), f32x4{});
+#pragma unroll
     for (int I = W + 1; I < 4; ++I) {
         const f32x4 t2 = mfma16(lds_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], o.blktr), ch4o(RTp, o, c0, 16 * I), f32x4{});
         ak2 += (t2 * lds_ld<float>(&sm.fp[(I * (I - 1)) / 2 + W][c0], o.tab)) * lds_ld<float>(&sm.kb[W][c0], o.tab);
@@ -1846,14 +1849,17 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int W, int col, f
     }
 }
 
-// dv of the wave's token block W and value column 16 col + lr (the A blocks read from Ab).
-__device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int W, int col, const LaneOfs& o) {
+// dv of the wave's token block W (compile-time) and value column 16 col + lr (the A blocks read
+// from Ab).
+template <int W>
+__device__ __forceinline__ f32x4 loop_products_v(LoopSmem& sm, int col, const LaneOfs& o) {
     const int TW = 16 * W, c0 = 16 * col;
     f32x4 av = {}, ab = {};          // 16x16x32 and 16x16x16 products in separate accumulators
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
         av = mfma32(tr8o(&sm.KtT[0][0], o, 32 * ks, TW), tr8o(&sm.dS[0][0], o, 32 * ks, c0), av);
     ab = mfma16(lds_ld<bf16x4>(&sm.Ab[(W * (W + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, TW, c0), ab);
+#pragma unroll
     for (int I = W + 1; I < 4; ++I)
         ab = mfma16(lds_ld<bf16x4>(&sm.Ab[(I * (I + 1)) / 2 + W][0][0], o.frag), tr4o(&sm.Dt[0][0], o, 16 * I, c0), ab);
     return av + ab;
@@ -1928,19 +1934,20 @@ __device__ __forceinline__ void loop_issue(LoopPrefetch& f, const uint16_t* __re
     }
 }
 
-// The staged gradients of chunk c to HBM: wave wv writes tensor wv >> 2 at tokens
-// 16 (wv & 3) + lr, channels 8 lq .. +7 and 32 + 8 lq .. +7.
-template <bool SEQ>
+// The staged gradients of chunk c to HBM: the waves of token block N (N = W of wave 4W + col)
+// write tensor N (dr, dk, dv, dw); wave col writes tokens 16 col + lr, channels 8 lq .. +7 and
+// 32 + 8 lq .. +7.
+template <bool SEQ, int N>
 __device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restrict__ dr,
                                            uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
                                            uint16_t* __restrict__ dw, int bh, int c, int B, int H,
-                                           int T, int wv, int lane, const LaneOfs& o,
+                                           int T, int col, int lane, const LaneOfs& o,
                                            const GlobOfs& g) {
-    const int n = wv >> 2, tk = 16 * (wv & 3) + (lane & 15);
+    const int tk = 16 * col + (lane & 15);
     const int t0 = c * CL, nvalid = min(CL, T - t0);
-    uint16_t* dst = (n == 0 ? dr : n == 1 ? dk : n == 2 ? dv : dw) + tok_base<SEQ>(bh, t0, B, H, T);
-    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 0, 16 * (wv & 3)));
-    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[n][0][0], o, 32, 16 * (wv & 3)));
+    uint16_t* dst = (N == 0 ? dr : N == 1 ? dk : N == 2 ? dv : dw) + tok_base<SEQ>(bh, t0, B, H, T);
+    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 0, 16 * col));
+    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 32, 16 * col));
     if (tk < nvalid) {
         char* p = reinterpret_cast<char*>(dst) + (unsigned)g.st;
         *reinterpret_cast<uint4*>(p) = x0;
@@ -1954,52 +1961,20 @@ __device__ __forceinline__ float sum16lanes(float v) {
     return v + dpp_mov<0x140>(v);                 // row_mirror: lane i <-> lane 15 - i
 }
 
-// SEQ as for wkv6_bwd_chunk_grads.  One workgroup per (b,h, segment) (P segments of ceil(NT/P)
-// chunks; P = 1 when B*H fills the device): segment p starts from dhT (p = P-1) or dSend[b,h][p]
-// (wkv6_bwd_fold) and writes dh0 if p = 0.  du_part gets one 64-vector per (b,h, segment)
-// ([h][b][p][i]).
-template <bool SEQ>
-__global__ void __launch_bounds__(NTHR_L)
-wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
-              const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
-              const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ dO,
-              const float* __restrict__ dhT, const uint16_t* __restrict__ Hs,
-              uint16_t* __restrict__ dr, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
-              uint16_t* __restrict__ dw, float* __restrict__ du_part, float* __restrict__ dh0,
-              const float* __restrict__ dSend, float scale, int B, int H, int T, int NT, int P) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    LoopSmem& sm = *reinterpret_cast<LoopSmem*>(smem_raw);
-    // workgroup = (b,h, segment): chunks [c_lo, c_hi) of the sequence, walked from the last
-    const int bh = blockIdx.x / P, seg = blockIdx.x - bh * P, h = bh % H;
-    const int NC = (NT + P - 1) / P, c_lo = seg * NC, c_hi = min(NT, c_lo + NC);
-    const size_t sbase = (size_t)bh * KD * KD;
-    // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
-    const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
-    const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
-    LaneOfs o = lane_ofs(threadIdx.x & 63);
-    GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
-
-    LoopPrefetch pf;
-    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
-    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
-    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
-    float ub[4];                                            // u at the thread's 4 channels (bonus)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) ub[s] = load_u(u, u_dtype, h * KD + (threadIdx.x & 15) * 4 + s);
-    GradLane gl;
-    gl.ulane[0] = scale * load_u(u, u_dtype, h * KD + ch0);
-    f32x4 Dst = {};                                         // dS[ch][t4 + rr]
-    {
-        // dhT for the last segment, else what the later segments hand this one
-        const float* d0 = seg + 1 < P ? dSend + ((size_t)bh * (P - 1) + seg) * KD * KD
-                                      : (dhT ? dhT + sbase : nullptr);
-        if (d0) {
-            const float4 x = *reinterpret_cast<const float4*>(d0 + ch0 * KD + t40);
-            Dst[0] = x.x; Dst[1] = x.y; Dst[2] = x.z; Dst[3] = x.w;
-        }
-    }
-    float du_acc = 0.f;
-
+// The chunk walk of one wave of wkv6_bwd_loop, for its token block W (a compile-time constant:
+// the cross-block loops, the block-dependent tables and every offset that depends on W are
+// resolved at compile time; the wave runs this one instantiation for the whole launch, and all
+// four have the same barriers).  col = the wave's channel column.
+template <bool SEQ, int W>
+__device__ __forceinline__ void bwd_loop_walk(
+        LoopSmem& sm, const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+        const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
+        const uint16_t* __restrict__ dO, const uint16_t* __restrict__ Hs,
+        uint16_t* __restrict__ dr, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
+        uint16_t* __restrict__ dw, float scale, int B, int H, int T, int NT, int bh, int c_lo,
+        int c_hi, LaneOfs o, GlobOfs go_, LoopPrefetch& pf, GradLane& gl, f32x4& Dst,
+        float& du_acc) {
+    constexpr int TW = 16 * W;
     for (int c = c_hi - 1; c >= c_lo; --c) {
         // The offsets and the lane indices come from opaque copies made in every iteration
         // (see LaneOfs): nothing derived from them is hoisted out of the walk.
@@ -2008,8 +1983,8 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         int tid;
         asm volatile("" : "=v"(tid) : "0"((int)threadIdx.x));
         const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int W = wv >> 2, col = wv & 3, lr = lane & 15, lq = lane >> 4;
-        const int c0 = 16 * col, TW = 16 * W, t4 = TW + 4 * lq;
+        const int col = wv & 3, lr = lane & 15, lq = lane >> 4;
+        const int c0 = 16 * col, t4 = TW + 4 * lq;
         const int row = tid >> 4;                           // the thread's raw pieces: row,
         const int tw = 4 * TS * 2 * wv;                     // at byte tw + o.th of a tile
         const int t0 = c * CL, nvalid = min(CL, T - t0);
@@ -2026,9 +2001,13 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             lds_st<uint2>(&sm.KT[0][0], tw + o.th, x.k);
             lds_st<uint2>(&sm.KtT[0][0], tw + o.th, x.w);          // w scratch
             lds_st<uint2>(&sm.Sin[0][0], tw + o.th, x.s);
-            float rf[4], kf[4];
+            float rf[4], kf[4], ub[4];
             unpack4(x.r, rf);
             unpack4(x.k, kf);
+            {
+                const float4 uu = lds_ld<float4>(&sm.uh[0], 4 * o.tab);   // u[4 L .. 4 L + 3]
+                ub[0] = uu.x; ub[1] = uu.y; ub[2] = uu.z; ub[3] = uu.w;
+            }
             float b = (rf[0] * ub[0]) * kf[0];
 #pragma unroll
             for (int s = 1; s < 4; ++s) b += (rf[s] * ub[s]) * kf[s];
@@ -2049,7 +2028,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // ---- S2: dA blocks; raw r, k, w at the lane's positions; the decay scan; Fm, Fk; Rm,
         // Km; Dv ----
         loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
-        if (wv < 10) loop_dA_block(sm, wv, o, lane);
+        if (W < 2 || (W == 2 && col < 2)) loop_dA_block(sm, wv, o, lane);
         bf16x4 wrw;
         float kmf[4], rmf[4], qloc, m7;
         {
@@ -2105,8 +2084,8 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 #pragma unroll
             for (int J = 0; J < 4; ++J) {
                 tJs[J] = lds_ld<float>(&sm.red[J][c0], o.tab);
-                after += J > W ? tJs[J] : 0.f;
-                before += J < W ? tJs[J] : 0.f;
+                if (J > W) after += tJs[J];
+                if (J < W) before += tJs[J];
             }
             const float eg = ex2(after + qloc), kq = ex2(qloc);
             float x[4];
@@ -2123,18 +2102,20 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             st_ch4o(&sm.RiT[0][0], o, c0, TW, x);
             // the pair tiles of the block as the later one: s Rm_W p_WJ, p_WJ = e^{mu_W - b_J}
             float bJ = 0.f;
+#pragma unroll
             for (int J = 0; J < W; ++J) {
                 bJ += tJs[J];
                 const float pfac = scale * ex2(before + m7 - bJ);
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) x[rr] = rmf[rr] * pfac;
-                const int pi = (W * (W - 1)) / 2 + J;
+                constexpr int pbase = (W * (W - 1)) / 2;
+                const int pi = pbase + J;
                 st_ch4o(&sm.RpT[pi >> 2][0][0], o, c0, 16 * (pi & 3), x);
             }
         }
         {
             // tables per channel i = lane from the block totals and mu: b_J = G[16J+15],
-            // mu_J = b_{J-1} + m7_J; each wave fills one or two rows (wave-uniform branches)
+            // mu_J = b_{J-1} + m7_J; each wave fills one or two rows
             const int i = lane;
             float bnd[4], mu[4], a = 0.f;
 #pragma unroll
@@ -2143,37 +2124,39 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 a += sm.red[J][i];
                 bnd[J] = a;
             }
-            if (wv < 4) {
-                sm.emu[wv][i] = ex2(wv == 0 ? mu[0] : wv == 1 ? mu[1] : wv == 2 ? mu[2] : mu[3]);
-            } else if (wv < 8) {
-                const int J = wv - 4;
-                sm.eg[J][i] = ex2(bnd[3] - (J == 0 ? mu[0] : J == 1 ? mu[1] : J == 2 ? mu[2] : mu[3]));
-            } else if (wv < 11) {
-                const int J = wv - 8;
-                sm.kb[J][i] = ex2(J == 0 ? bnd[0] - mu[0] : J == 1 ? bnd[1] - mu[1] : bnd[2] - mu[2]);
-            } else if (wv == 11) {
-                sm.fp[0][i] = ex2(mu[1] - bnd[0]);              // (1, 0)
-                sm.fp[1][i] = ex2(mu[2] - bnd[0]);              // (2, 0)
-            } else if (wv == 12) {
-                sm.fp[2][i] = ex2(mu[2] - bnd[1]);              // (2, 1)
-                sm.fp[3][i] = ex2(mu[3] - bnd[0]);              // (3, 0)
-            } else if (wv == 13) {
-                sm.fp[4][i] = ex2(mu[3] - bnd[1]);              // (3, 1)
-                sm.fp[5][i] = ex2(mu[3] - bnd[2]);              // (3, 2)
-            } else if (wv == 14) {
-                const float e = ex2(bnd[3]);
-                sm.eG63[i] = e;
-                sm.Dv[i] *= e;
+            if (W == 0) {
+                sm.emu[col][i] = ex2(col == 0 ? mu[0] : col == 1 ? mu[1] : col == 2 ? mu[2] : mu[3]);
+            } else if (W == 1) {
+                sm.eg[col][i] = ex2(bnd[3] - (col == 0 ? mu[0] : col == 1 ? mu[1] : col == 2 ? mu[2] : mu[3]));
+            } else if (W == 2) {
+                if (col < 3) {
+                    sm.kb[col][i] = ex2(col == 0 ? bnd[0] - mu[0] : col == 1 ? bnd[1] - mu[1] : bnd[2] - mu[2]);
+                } else {
+                    sm.fp[0][i] = ex2(mu[1] - bnd[0]);          // (1, 0)
+                    sm.fp[1][i] = ex2(mu[2] - bnd[0]);          // (2, 0)
+                }
+            } else {
+                if (col == 0) {
+                    sm.fp[2][i] = ex2(mu[2] - bnd[1]);          // (2, 1)
+                    sm.fp[3][i] = ex2(mu[3] - bnd[0]);          // (3, 0)
+                } else if (col == 1) {
+                    sm.fp[4][i] = ex2(mu[3] - bnd[1]);          // (3, 1)
+                    sm.fp[5][i] = ex2(mu[3] - bnd[2]);          // (3, 2)
+                } else if (col == 2) {
+                    const float e = ex2(bnd[3]);
+                    sm.eG63[i] = e;
+                    sm.Dv[i] *= e;
+                }
             }
         }
         __syncthreads();
 
         // ---- S4: the products (dr, dk finished on the way), the state-gradient step ----
-        if (c + 1 < c_hi) loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, wv, lane, o, go_);
+        if (c + 1 < c_hi) loop_store<SEQ, W>(sm, dr, dk, dv, dw, bh, c + 1, B, H, T, col, lane, o, go_);
         loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
-        if (wv < 10) loop_A_block(sm, wv, scale, o, lane);
+        if (W < 2 || (W == 2 && col < 2)) loop_A_block(sm, wv, scale, o, lane);
         GradOut go;
-        loop_products_rk<SEQ>(sm, W, col, scale, gl, go, o);
+        loop_products_rk<SEQ, W>(sm, col, scale, gl, go, o);
         {
             const float e = lds_ld<float>(&sm.eG63[c0], o.tab);
 #pragma unroll
@@ -2184,7 +2167,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         }
         du_acc += go.dup[0];
         __syncthreads();                   // A blocks in
-        go.av[0] = loop_products_v(sm, W, col, o);
+        go.av[0] = loop_products_v<W>(sm, col, o);
         // dw: the suffix sums across the four lane rows (shuffles on all lanes)
         float later;
         {
@@ -2203,6 +2186,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
             later += lds_ld<float>(&sm.Dv[c0], o.tab) +
                      ((lds_ld<float>(&sm.Pk[0][c0], o.tab) + lds_ld<float>(&sm.Pk[1][c0], o.tab)) +
                       (lds_ld<float>(&sm.Pk[2][c0], o.tab) + lds_ld<float>(&sm.Pk[3][c0], o.tab)));
+#pragma unroll
             for (int W2 = W + 1; W2 < 4; ++W2) later += lds_ld<float>(&sm.red[W2][c0], o.tab);
             float g[4];
 #pragma unroll
@@ -2225,8 +2209,74 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
     }
     __syncthreads();
-    loop_store<SEQ>(sm, dr, dk, dv, dw, bh, c_lo, B, H, T, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
-                    threadIdx.x & 63, o, go_);
+    {
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        loop_store<SEQ, W>(sm, dr, dk, dv, dw, bh, c_lo, B, H, T, wv & 3, threadIdx.x & 63, o, go_);
+    }
+}
+
+// SEQ as for wkv6_bwd_chunk_grads.  One workgroup per (b,h, segment) (P segments of ceil(NT/P)
+// chunks; P = 1 when B*H fills the device): segment p starts from dhT (p = P-1) or dSend[b,h][p]
+// (wkv6_bwd_fold) and writes dh0 if p = 0.  du_part gets one 64-vector per (b,h, segment)
+// ([h][b][p][i]).  The 16 waves: wave 4W + col owns token block W and channel column col.
+template <bool SEQ>
+__global__ void __launch_bounds__(NTHR_L)
+wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+              const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
+              const void* __restrict__ u, int u_dtype, const uint16_t* __restrict__ dO,
+              const float* __restrict__ dhT, const uint16_t* __restrict__ Hs,
+              uint16_t* __restrict__ dr, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
+              uint16_t* __restrict__ dw, float* __restrict__ du_part, float* __restrict__ dh0,
+              const float* __restrict__ dSend, float scale, int B, int H, int T, int NT, int P) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    LoopSmem& sm = *reinterpret_cast<LoopSmem*>(smem_raw);
+    // workgroup = (b,h, segment): chunks [c_lo, c_hi) of the sequence, walked from the last
+    const int bh = blockIdx.x / P, seg = blockIdx.x - bh * P, h = bh % H;
+    const int NC = (NT + P - 1) / P, c_lo = seg * NC, c_hi = min(NT, c_lo + NC);
+    const size_t sbase = (size_t)bh * KD * KD;
+    // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
+    const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
+    const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
+    LaneOfs o = lane_ofs(threadIdx.x & 63);
+    GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
+
+    LoopPrefetch pf;
+    loop_issue<SEQ, 0>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
+    loop_issue<SEQ, 2>(pf, r, k, v, w, dO, Hs, bh, c_hi - 1, B, H, T, NT, threadIdx.x, go_);
+    if (threadIdx.x < KD) sm.uh[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
+    __syncthreads();
+    GradLane gl;
+    gl.ulane[0] = scale * load_u(u, u_dtype, h * KD + ch0);
+    f32x4 Dst = {};                                         // dS[ch][t4 + rr]
+    {
+        // dhT for the last segment, else what the later segments hand this one
+        const float* d0 = seg + 1 < P ? dSend + ((size_t)bh * (P - 1) + seg) * KD * KD
+                                      : (dhT ? dhT + sbase : nullptr);
+        if (d0) {
+            const float4 x = *reinterpret_cast<const float4*>(d0 + ch0 * KD + t40);
+            Dst[0] = x.x; Dst[1] = x.y; Dst[2] = x.z; Dst[3] = x.w;
+        }
+    }
+    float du_acc = 0.f;
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 8)) {
+    case 0:
+        bwd_loop_walk<SEQ, 0>(sm, r, k, v, w, dO, Hs, dr, dk, dv, dw, scale, B, H, T, NT, bh, c_lo,
+                              c_hi, o, go_, pf, gl, Dst, du_acc);
+        break;
+    case 1:
+        bwd_loop_walk<SEQ, 1>(sm, r, k, v, w, dO, Hs, dr, dk, dv, dw, scale, B, H, T, NT, bh, c_lo,
+                              c_hi, o, go_, pf, gl, Dst, du_acc);
+        break;
+    case 2:
+        bwd_loop_walk<SEQ, 2>(sm, r, k, v, w, dO, Hs, dr, dk, dv, dw, scale, B, H, T, NT, bh, c_lo,
+                              c_hi, o, go_, pf, gl, Dst, du_acc);
+        break;
+    default:
+        bwd_loop_walk<SEQ, 3>(sm, r, k, v, w, dO, Hs, dr, dk, dv, dw, scale, B, H, T, NT, bh, c_lo,
+                              c_hi, o, go_, pf, gl, Dst, du_acc);
+        break;
+    }
     // du over the sequence: lanes of one channel (lq), then the four token blocks in order
     {
         float p = du_acc + lane_xor_swz<16>(du_acc);
