@@ -231,7 +231,7 @@ __device__ __forceinline__ float load_u(const void* u, int u_dtype, int idx) {
 }
 
 // Index of the cross-block pair (I, J), I > J, in the 6-entry tables.
-__device__ __forceinline__ int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }
+__host__ __device__ constexpr int pair_index(int I, int J) { return I * (I - 1) / 2 + J; }
 
 // ---------------------------------------------------------------------------
 // forward as a walk: one workgroup per (b,h, segment) carries the fp32 state in registers
@@ -425,6 +425,177 @@ __device__ __forceinline__ void walk_store(const WalkSmem& sm, uint16_t* __restr
         reinterpret_cast<u32x4_t*>(Hs + ((size_t)bh * (NT + 1) + c) * KD * KD + row * KD + c8));
 }
 
+// The chunk loop of one wave of wkv6_fwd_walk.  Wave wv works on token block I = wv >> 1 of
+// the operand tiles and, in the products, on token block W = (0, 0, 1, 1, 3, 3, 2, 2)[wv]:
+// both are compile-time here (PB = wv >> 1), so the cross-block loops, the table choices and
+// their offsets are resolved statically; all four instantiations pass the same barriers.
+template <bool SEQ, int PB>
+__device__ __forceinline__ void fwd_walk_chunks(
+        WalkSmem& sm, const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
+        const uint16_t* __restrict__ v, const uint16_t* __restrict__ w,
+        uint16_t* __restrict__ o, uint16_t* __restrict__ Hs, float scale, int B, int H, int T,
+        int NT, int bh, int c_begin, int c_end, int hh, WalkPrefetch& nx, f32x4* acc) {
+    constexpr int I = PB;                          // token block of the thread's tile pieces
+    constexpr int W = PB < 2 ? PB : 5 - PB;        // token block of the wave's products
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
+    const int lane = threadIdx.x & 63;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
+    // loop's own order (the next chunk's loads, then this chunk's two stores) alone
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    for (int c = c_begin; c < c_end; ++c) {
+        const int nvalid = min(CL, T - c * CL);
+        // Every tile written here was last read before the previous chunk's final barrier
+        // (Sin[c & 1] two chunks ago).  Raw r and k wait in Rm and Km.
+        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
+        sstore16(sm.Vm, row, c8, nx.v);
+        sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
+        sstore16(sm.Km, row, c8, nx.k);
+        {
+            sstore16(sm.Rm, row, c8, nx.r);
+            float rf[8], kf[8], bsum = 0.f;
+            unpack8(nx.r, rf);
+            unpack8(nx.k, kf);
+            const float4 ua = *reinterpret_cast<const float4*>(&sm.uh[c8]);
+            const float4 ub = *reinterpret_cast<const float4*>(&sm.uh[c8 + 4]);
+            const float uf[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) bsum += rf[s] * uf[s] * kf[s];
+            bsum = sum8lanes(bsum);
+            if ((threadIdx.x & 7) == 0) sm.bonus[row] = bsum;
+            // S_in of this chunk, bf16, for the inter-chunk product and the backward
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
+        }
+        // unconditional (the last iteration reloads its own chunk): loads under a branch
+        // would cost the loop a full wait
+        walk_issue<SEQ, true>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
+        __syncthreads();
+        {
+            walk_build_G<SEQ>(sm, nvalid, c & 1);
+            // Operand tiles of this thread's piece (token t = row in block I; I is
+            // wave-uniform).  Two exponentials per element; every other factor is a
+            // per-(block, channel) table entry <= 1 applied to the fp32 value:
+            //   Rm = r e^{G_{t-1} - mu_I}     Ri = Rm e^{mu_I}          Rp = Rm e^{mu_I - b_{I-1}}
+            //   Km = k e^{mu_I - G_t}         Kt = Km e^{G_63 - mu_I}   Kc(I2) = Km e^{b_{I2-1} - mu_I}
+            float rf[8], kf[8], rm[8], km[8], y[8], f[8];
+            unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
+            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+            float gm[8], gg[8], gp[8];
+            g8(Gm, 16 * I + 7, c8, gm);
+            g8(Gm, row, c8, gg);
+            g8m1(Gm, row, c8, gp);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                rm[s] = rf[s] * ex2(gp[s] - gm[s]);
+                km[s] = kf[s] * ex2(gm[s] - gg[s]);
+            }
+            sstore16(sm.Rm, row, c8, pack8(rm));
+            sstore16(sm.Km, row, c8, pack8(km));
+            auto tab8 = [&](const float* tb) {
+                const float4 a = *reinterpret_cast<const float4*>(tb + c8);
+                const float4 b = *reinterpret_cast<const float4*>(tb + c8 + 4);
+                f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+            };
+            tab8(sm.emu[I]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
+            sstore16(sm.Ri, row, c8, pack8(y));
+            if constexpr (I > 0) {
+                tab8(sm.c1[I]);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
+                sstore16(sm.Rp, row, c8, pack8(y));
+            }
+            tab8(sm.c3[I]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
+            sstore16(sm.Kt, row, c8, pack8(y));
+#pragma unroll
+            for (int I2 = I + 1; I2 < 4; ++I2) {
+                const int pi = pair_index(I2, I);
+                tab8(sm.c6[pi]);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
+                sstore16(reinterpret_cast<uint16_t (*)[TS]>(sm.Kc[16 * pi]), row & 15, c8, pack8(y));
+            }
+        }
+        __syncthreads();
+        {
+            const int t = 16 * W + lr;
+            // the 16x16x32 and the 16x16x16 products go to separate accumulators (ao, ab)
+            f32x4 ao[2] = {}, ab[2] = {};
+            // inter-chunk: (r e^{G_{t-1}}) S_in
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const bf16x8 a = ld_dir8(&sm.Ri[0][0], t, 32 * ks);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    ao[tp] = mfma32(a, ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), ao[tp]);
+            }
+            // diagonal block: strictly causal part plus the u-bonus diagonal
+            {
+                f32x4 at = {};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    at = mfma32(ld_row8(&sm.Km[0][0], 16 * W + lr, 32 * ks), ld_row8(&sm.Rm[0][0], t, 32 * ks), at);
+                float xa[4];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int tl = 4 * lq + rr;
+                    xa[rr] = tl < lr ? at[rr] : (tl == lr ? sm.bonus[t] : 0.f);
+                }
+                const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ab[tp]);
+            }
+            // earlier blocks J < W, both operands referenced at b_{W-1}
+#pragma unroll
+            for (int J = 0; J < W; ++J) {
+                f32x4 at = {};
+                const int pr = 16 * pair_index(W, J) + lr;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+                    at = mfma32(ld_row8(&sm.Kc[0][0], pr, 32 * ks), ld_row8(&sm.Rp[0][0], t, 32 * ks), at);
+                const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp)
+                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ab[tp]);
+            }
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * (ao[tp][rr] + ab[tp][rr]));
+        }
+        // state update: S = diag(e^{G_63}) S + Kt^T V
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
+            acc[0][rr] *= d;
+            acc[1][rr] *= d;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+        }
+        __syncthreads();
+        // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
+        // for those at the top of the next iteration leaves these stores in flight (vmcnt
+        // counts loads and stores in issue order)
+        walk_store(sm, o, Hs, bh, c, T, NT);
+    }
+
+}
+
 // Output walk over segment blockIdx.x % P of sequence blockIdx.x / P.  Segment 0 starts from
 // h0 (or zero), segment p >= 1 from Sstart[b,h][p-1] (wkv6_fwd_fold).
 // SEQ: r, k, v and the pre-activation decay are sequence-first; o is always head-first.
@@ -476,156 +647,19 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         __syncthreads();
     }
 
-    // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
-    // loop's own order (the next chunk's loads, then this chunk's two stores) alone
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    for (int c = c_begin; c < c_end; ++c) {
-        const int nvalid = min(CL, T - c * CL);
-        // Every tile written here was last read before the previous chunk's final barrier
-        // (Sin[c & 1] two chunks ago).  Raw r and k wait in Rm and Km.
-        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
-        sstore16(sm.Vm, row, c8, nx.v);
-        sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
-        sstore16(sm.Km, row, c8, nx.k);
-        {
-            sstore16(sm.Rm, row, c8, nx.r);
-            float rf[8], kf[8], bsum = 0.f;
-            unpack8(nx.r, rf);
-            unpack8(nx.k, kf);
-            const float4 ua = *reinterpret_cast<const float4*>(&sm.uh[c8]);
-            const float4 ub = *reinterpret_cast<const float4*>(&sm.uh[c8 + 4]);
-            const float uf[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
-#pragma unroll
-            for (int s = 0; s < 8; ++s) bsum += rf[s] * uf[s] * kf[s];
-            bsum = sum8lanes(bsum);
-            if ((threadIdx.x & 7) == 0) sm.bonus[row] = bsum;
-            // S_in of this chunk, bf16, for the inter-chunk product and the backward
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
-        }
-        // unconditional (the last iteration reloads its own chunk): loads under a branch
-        // would cost the loop a full wait
-        walk_issue<SEQ, true>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
-        __syncthreads();
-        {
-            walk_build_G<SEQ>(sm, nvalid, c & 1);
-            // Operand tiles of this thread's piece (token t = row in block I; I is
-            // wave-uniform).  Two exponentials per element; every other factor is a
-            // per-(block, channel) table entry <= 1 applied to the fp32 value:
-            //   Rm = r e^{G_{t-1} - mu_I}     Ri = Rm e^{mu_I}          Rp = Rm e^{mu_I - b_{I-1}}
-            //   Km = k e^{mu_I - G_t}         Kt = Km e^{G_63 - mu_I}   Kc(I2) = Km e^{b_{I2-1} - mu_I}
-            const int I = row >> 4;
-            float rf[8], kf[8], rm[8], km[8], y[8], f[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
-            float gm[8], gg[8], gp[8];
-            g8(Gm, 16 * I + 7, c8, gm);
-            g8(Gm, row, c8, gg);
-            g8m1(Gm, row, c8, gp);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                rm[s] = rf[s] * ex2(gp[s] - gm[s]);
-                km[s] = kf[s] * ex2(gm[s] - gg[s]);
-            }
-            sstore16(sm.Rm, row, c8, pack8(rm));
-            sstore16(sm.Km, row, c8, pack8(km));
-            auto tab8 = [&](const float* tb) {
-                const float4 a = *reinterpret_cast<const float4*>(tb + c8);
-                const float4 b = *reinterpret_cast<const float4*>(tb + c8 + 4);
-                f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-            };
-            tab8(sm.emu[I]);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
-            sstore16(sm.Ri, row, c8, pack8(y));
-            if (I > 0) {
-                tab8(sm.c1[I]);
-#pragma unroll
-                for (int s = 0; s < 8; ++s) y[s] = rm[s] * f[s];
-                sstore16(sm.Rp, row, c8, pack8(y));
-            }
-            tab8(sm.c3[I]);
-#pragma unroll
-            for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
-            sstore16(sm.Kt, row, c8, pack8(y));
-            for (int I2 = I + 1; I2 < 4; ++I2) {
-                const int pi = pair_index(I2, I);
-                tab8(sm.c6[pi]);
-#pragma unroll
-                for (int s = 0; s < 8; ++s) y[s] = km[s] * f[s];
-                sstore16(reinterpret_cast<uint16_t (*)[TS]>(sm.Kc[16 * pi]), row & 15, c8, pack8(y));
-            }
-        }
-        __syncthreads();
-        {
-            const int t = 16 * W + lr;
-            // the 16x16x32 and the 16x16x16 products go to separate accumulators (ao, ab)
-            f32x4 ao[2] = {}, ab[2] = {};
-            // inter-chunk: (r e^{G_{t-1}}) S_in
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const bf16x8 a = ld_dir8(&sm.Ri[0][0], t, 32 * ks);
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    ao[tp] = mfma32(a, ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), ao[tp]);
-            }
-            // diagonal block: strictly causal part plus the u-bonus diagonal
-            {
-                f32x4 at = {};
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    at = mfma32(ld_row8(&sm.Km[0][0], 16 * W + lr, 32 * ks), ld_row8(&sm.Rm[0][0], t, 32 * ks), at);
-                float xa[4];
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    const int tl = 4 * lq + rr;
-                    xa[rr] = tl < lr ? at[rr] : (tl == lr ? sm.bonus[t] : 0.f);
-                }
-                const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ab[tp]);
-            }
-            // earlier blocks J < W, both operands referenced at b_{W-1}
-            for (int J = 0; J < W; ++J) {
-                f32x4 at = {};
-                const int pr = 16 * pair_index(W, J) + lr;
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    at = mfma32(ld_row8(&sm.Kc[0][0], pr, 32 * ks), ld_row8(&sm.Rp[0][0], t, 32 * ks), at);
-                const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
-#pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ab[tp]);
-            }
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * (ao[tp][rr] + ab[tp][rr]));
-        }
-        // state update: S = diag(e^{G_63}) S + Kt^T V
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
-            acc[0][rr] *= d;
-            acc[1][rr] *= d;
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
-        }
-        __syncthreads();
-        // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
-        // for those at the top of the next iteration leaves these stores in flight (vmcnt
-        // counts loads and stores in issue order)
-        walk_store(sm, o, Hs, bh, c, T, NT);
+    switch (__builtin_amdgcn_readfirstlane(wv >> 1)) {
+    case 0:
+        fwd_walk_chunks<SEQ, 0>(sm, r, k, v, w, o, Hs, scale, B, H, T, NT, bh, c_begin, c_end, hh, nx, acc);
+        break;
+    case 1:
+        fwd_walk_chunks<SEQ, 1>(sm, r, k, v, w, o, Hs, scale, B, H, T, NT, bh, c_begin, c_end, hh, nx, acc);
+        break;
+    case 2:
+        fwd_walk_chunks<SEQ, 2>(sm, r, k, v, w, o, Hs, scale, B, H, T, NT, bh, c_begin, c_end, hh, nx, acc);
+        break;
+    default:
+        fwd_walk_chunks<SEQ, 3>(sm, r, k, v, w, o, Hs, scale, B, H, T, NT, bh, c_begin, c_end, hh, nx, acc);
+        break;
     }
 
     // ---- end of the sequence: the final state ----
