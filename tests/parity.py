@@ -21,8 +21,10 @@ TOL_L2 = 1e-2
 # tensors of fewer than MIN_ELEMS entries, where one near-zero reference entry decides it.
 ELEM_MEAN = 5e-3         # elementwise kernels: one bf16 rounding of an fp32 result (<= 2.1e-3)
 ELEM_MEAN_LORA = 8e-2    # kernels around bf16 hipBLASLt GEMMs (LoRA, channel-mix block; <= 3.8e-2)
-ELEM_MEAN_WKV = 6e-2     # WKV o, final state and gradients other than dw (<= 3.3e-2)
-ELEM_MEAN_WKV_DW = 2e-1  # WKV dw / d decay: a cancelling suffix sum, many near-zero entries (<= 8.7e-2)
+# WKV o, final state and every gradient, dw and d_decay included (largest measured on MI355X:
+# dw / d_decay 4.3e-2 in a sequence-first test, dv 3.6e-2, o 2.1e-2; at BASELINE config 2 dw is
+# at 1.7e-2).  Its relative L2 error (<= 3.3e-3) is the same as every other WKV tensor's.
+ELEM_MEAN_WKV = 6e-2
 ELEM_MEAN_BLOCK = 3e-1   # whole blocks / layers / models, bf16 activations (<= 1.6e-1)
 MIN_ELEMS = 4096
 # Whole blocks / layers / models keep bf16 activations between the bf16 hipBLASLt GEMMs (as
