@@ -68,6 +68,8 @@ def parse():
                     help="skip the config-5 WKV and config-4 7B-slice measurements")
     ap.add_argument("--train-only", action="store_true",
                     help="run only the config-3 training step (for kernel profiles)")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="run only the config-5 WKV measurement (for kernel profiles)")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--train-warmup", type=int, default=2)
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -391,6 +393,25 @@ def time_wkv(pkg, L, B, H, T, steps, warmup, with_state=False, settle_s=0.0):
     return ms_step, avg(fevs, 0, 5), avg(bevs, 0, 7), fwd_ph, bwd_ph, ms_step_ev, settled_s, settled_n
 
 
+def config5_bench(pkg, L, args):
+    """the long-context one-GPU share with carried state (h0, dhT, dh0):
+    WKV6 fwd+bwd at B=1, H=32, T=32768 through the C ABI, timed as config 2 (time_wkv)."""
+    B5, H5, T5 = 1, 32, 32768
+    c5 = time_wkv(pkg, L, B5, H5, T5, args.steps, args.warmup, with_state=True,
+                  settle_s=args.settle_s)
+    return {"workload": "BASELINE config 5: WKV6 B=1, H=32, T=32768, h0 ~ N(0,0.5^2), "
+                        "dhT ~ N(0,1), final state and dh0 returned",
+            "ms_per_step": c5[0], "tokens_per_s": B5 * T5 / (c5[0] * 1e-3),
+            "steps": args.steps, "warmup": args.warmup, "settle_s": c5[6],
+            "settle_steps": c5[7], "fwd_ms": c5[1], "bwd_ms": c5[2],
+            "phase_ms": {"fwd_segment_states": c5[3][0], "fwd_segment_fold": c5[3][1],
+                         "fwd_walk": c5[3][2], "bwd_state_pre_pass": c5[4][0],
+                         "bwd_state_fold_or_scan": c5[4][1], "bwd_grads": c5[4][2],
+                         "bwd_du_reduce": c5[4][3]},
+            "bwd_path": bwd_path(B5 * H5, T5),
+            "tflops": B5 * H5 * T5 * (FLOP_FWD + FLOP_BWD) / (c5[0] * 1e-3) / 1e12}
+
+
 def train_step_bench(pkg, steps, warmup):
     """RWKV-6 1.6B shape (24 layers, C=2048, 32 heads, ffn 7168, vocab 65536),
     batch 4 x 4096 random tokens, bf16 weights, full forward + backward + grad clip + AdamW.
@@ -505,6 +526,9 @@ def main():
         print(json.dumps({"train_step": train_step_bench(pkg, args.train_steps, args.train_warmup)}),
               flush=True)
         return
+    if args.config5_only:
+        print(json.dumps({"config5": config5_bench(pkg, L, args)}), flush=True)
+        return
     dev = torch.device("cuda:0")
     B, H, T, K = args.B, args.H, args.T, 64
     N_th = B * H * T
@@ -552,23 +576,9 @@ def main():
                      "traffic": measured_traffic(B, H, T)},
     }
     if not args.no_extra_configs:
-        # the long-context one-GPU share with carried state (h0, dhT, dh0)
-        B5, H5, T5 = 1, 32, 32768
-        c5 = time_wkv(pkg, L, B5, H5, T5, args.steps, args.warmup, with_state=True,
-                      settle_s=args.settle_s)
-        out["config5"] = {"workload": "BASELINE config 5: WKV6 B=1, H=32, T=32768, h0 ~ N(0,0.5^2), "
-                                      "dhT ~ N(0,1), final state and dh0 returned",
-                          "ms_per_step": c5[0], "tokens_per_s": B5 * T5 / (c5[0] * 1e-3),
-                          "steps": args.steps, "warmup": args.warmup, "settle_s": c5[6],
-                          "settle_steps": c5[7], "fwd_ms": c5[1], "bwd_ms": c5[2],
-                          "phase_ms": {"fwd_segment_states": c5[3][0], "fwd_segment_fold": c5[3][1],
-                                       "fwd_walk": c5[3][2], "bwd_state_pre_pass": c5[4][0],
-                                       "bwd_state_fold_or_scan": c5[4][1], "bwd_grads": c5[4][2],
-                                       "bwd_du_reduce": c5[4][3]},
-                          "bwd_path": bwd_path(B5 * H5, T5),
-                          "tflops": B5 * H5 * T5 * (FLOP_FWD + FLOP_BWD) / (c5[0] * 1e-3) / 1e12}
+        out["config5"] = config5_bench(pkg, L, args)
         if not args.no_cpu_baseline:
-            out["config5"]["cpu_baseline"] = cpu_baseline(B5, H5, T5, 0, with_state=True)
+            out["config5"]["cpu_baseline"] = cpu_baseline(1, 32, 32768, 0, with_state=True)
         out["slice_7b"] = slice_7b_bench(pkg, args.train_steps, args.train_warmup)
     if args.copy_calibration_mb > 0:
         n = args.copy_calibration_mb * (1 << 20) // 2
