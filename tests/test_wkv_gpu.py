@@ -143,15 +143,17 @@ def test_wkv_empty_sequence(pkg):
     assert torch.equal(hT, h0)
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17), (2, 64, 64 * 17 + 5),
-                                   (1, 128, 64 * 30 + 9)])
+@pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17), (2, 24, 64 * 32 + 11),
+                                   (3, 32, 64 * 20), (2, 64, 64 * 17 + 5), (1, 128, 64 * 30 + 9)])
 def test_wkv_parity_segmented(pkg, shape):
     """Few sequences of many chunks: the forward cuts each sequence into segments (pre-pass
     pieces folded into each segment's start state, then output walks), here 2 segments of 9
-    chunks and 5 of 9 with a ragged last chunk; the backward runs chunk-parallel for those two
-    and as a segmented reverse walk (backward pieces folded into each segment's starting state
-    gradient) for the 128-sequence shapes: 2 segments of 9 chunks, and of 16 + 15 chunks with
-    a ragged last one."""
+    chunks, 5 of 9 with a ragged last chunk, 4 of 9 (48 sequences) and 2 of 10 (96
+    sequences).  The backward runs chunk-parallel for those four (the (b,h, segment) walks
+    would fill less than 7/8 of the device: 2, 5, 192 and 192 of 256) and as a segmented
+    reverse walk (backward pieces folded into each segment's starting state gradient) for the
+    128-sequence shapes: 2 segments of 9 chunks, and of 16 + 15 chunks with a ragged last
+    one."""
     B, H, T = shape
     x = _inputs(B, H, T, seed=T)
     got = run_gpu(pkg, x, 0.5, True, True)
@@ -247,10 +249,12 @@ def test_wkv_decay_gradient_through_exp_past_the_floor(pkg):
     _compare(got, ref, ["o", "dr", "dk", "dv", "d_decay", "du"])
 
 
-@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64), (2, 1, 1300), (2, 64, 1093)])
+@pytest.mark.parametrize("shape", [(2, 2, 63), (3, 2, 130), (1, 3, 64), (2, 1, 1300), (2, 24, 2059),
+                                   (2, 64, 1093)])
 def test_wkv_seqfirst_entry(pkg, shape):
     """The time-mix module's entry: r, k, v, decay in [T,B,H*64], w = -exp(decay) inside,
     o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs.
+    (2, 24, 2059): B*H = 48, 4 forward segments of 9 chunks and the chunk-parallel backward;
     (2, 64, 1093): B*H = 128, the segmented walks (2 segments of 9 chunks, ragged end)."""
     B, H, T = shape
     K = 64
