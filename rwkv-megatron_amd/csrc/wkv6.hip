@@ -5,16 +5,26 @@
 //   o_t = s * r_t^T (S_{t-1} + diag(u) k_t v_t^T),   S_t = diag(exp(w_t)) S_{t-1} + k_t v_t^T.
 //
 // Decomposition (all deterministic):
-//   fwd_walk<pre>    per (b,h,segment), segments 0..P-2 only when B*H is small: the segment's
-//                    local end state and total decay (k, v, w read once)
-//   fwd_walk<out>    per (b,h,segment): walks the chunks in order with the fp32 state in
+//   wkv6_fwd_pieces  only when B*H gives fewer than 256 workgroups: per (b,h, piece of segments
+//                    0..P-2), the piece's end state from a zero start and its total decay
+//                    (k, v, w read once more)
+//   wkv6_fwd_fold    chains the pieces from h0 into each segment's start state
+//   wkv6_fwd_walk    per (b,h, segment): walks the chunks in order with the fp32 state in
 //                    registers: o = (r e^{G_{t-1}}) S_in + intra-chunk attention, then
 //                    S_out = e^{G_63} S_in + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T  [MFMA];
-//                    writes o, bf16 S_in per chunk and the chunk decays for the backward
-//   chunk_local<bwd> per (b,h,chunk): dS_loc = s * sum_t (r_t e^{G_{t-1}}) dO_t^T        [MFMA]
-//   state_scan_bwd   per (b,h,elem) : dS_out(c-1) = e^{G_63(c)} dS_out(c) + dS_loc(c)
-//   bwd_chunk_grads  per (b,h,chunk): dr, dk, dv, dw, du-partials                        [MFMA]
-//   du_reduce        per (h, channel): fixed-order sum of the du partials
+//                    writes o and the bf16 S_in of every chunk for the backward
+//   wkv6_bwd_pieces  segmented backward only: per (b,h, piece of segments 1..P-1), the state
+//                    gradient the piece hands to the left from a zero one, and its decay
+//   wkv6_bwd_fold    chains them from dhT into each segment's starting state gradient
+//   wkv6_bwd_loop    per (b,h, segment): the reverse walk, all gradients of each chunk with
+//                    dS_out(c-1) = e^{G_63} dS_out(c) + s sum_t (r_t e^{G_{t-1}}) dO_t^T  [MFMA]
+//                    carried in registers; dh0 and the du partials
+//   chunk-parallel backward, when even the segments cannot fill the device (few, short
+//   sequences):
+//     wkv6_bwd_chunk_dstate  per (b,h, chunk): dS_loc and the chunk decay                [MFMA]
+//     wkv6_state_scan_bwd    per (b,h, element): dS_out(c-1) = e^{G_63(c)} dS_out(c) + dS_loc(c)
+//     wkv6_bwd_chunk_grads   per (b,h, chunk): dr, dk, dv, dw, du partials               [MFMA]
+//   wkv6_du_reduce   per (h, channel): fixed-order sum of the du partials
 //
 // Inside a 64-token chunk G is the inclusive cumulative log-decay (base-2 units, so
 // every exponential is one v_exp_f32) and a chunk is four 16-token sub-blocks with
@@ -237,13 +247,13 @@ __host__ __device__ constexpr int pair_index(int I, int J) { return I * (I - 1) 
 // forward as a walk: one workgroup per (b,h, segment) carries the fp32 state in registers
 // ---------------------------------------------------------------------------
 // A segment is a run of consecutive chunks of one sequence.  Per chunk the workgroup reads
-// r, k, v, w once (prefetched into registers one chunk ahead), writes o, the bf16 S_in the
-// backward consumes and the chunk decay, and advances its state
+// r, k, v, w once (prefetched into registers one chunk ahead), writes o and the bf16 S_in the
+// backward consumes, and advances its state
 //   S_out = diag(e^{G_63}) S_in + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T      [MFMA]
 // in the accumulator registers.  When B*H alone gives too few workgroups for the device,
-// each sequence is cut into P segments: wkv6_fwd_walk<.., false> first walks segments
-// 0..P-2 for their local end state and total log-decay only (reading k, v, w), and each
-// output walk starts from
+// each sequence is cut into P segments: the pre-pass pieces (wkv6_fwd_pieces) give each of
+// segments 0..P-2 its local end state and total log-decay (reading k, v, w), wkv6_fwd_fold
+// chains them, and each output walk starts from
 //   S_start(p) = A(p-1) S_start(p-1) + S_seg(p-1),  S_start(0) = h0.
 // 8 waves: wave (W, hh) owns target tokens [16W, 16W+16) x value columns [32hh, 32hh+32)
 // of o, and state rows [16W, 16W+16) x columns [32hh, 32hh+32): lane (lq, lr) holds
