@@ -23,6 +23,14 @@ Pinned in tests/test_oracle.py: the model forward against tests/rwkv_lm_referenc
 numpy forward written against RWKV-LM's own parameter names, from the numpy oracle pieces),
 the WKV autograd wrapper against the C oracle's forward and backward, and the loss against
 torch.nn.functional.cross_entropy.
+
+``bf16_storage()`` turns the same functions into an emulation of the reference as it runs in
+bf16 on a GPU: every op computes in the tensors' own (higher) precision and its output is
+rounded to bf16 once, and so is the gradient reaching each op's output in the backward (the
+storage points of bf16 autograd; fla's WKV computes in fp32 and returns bf16).  Its error
+against the plain fp64 run is the rounding error the reference itself carries in bf16, which
+the block tests use as the scale of an acceptable error.  (torch's own bf16 CPU kernels are
+not that reference: some accumulate in bf16.)
 """
 from __future__ import annotations
 
@@ -31,6 +39,36 @@ import torch
 import torch.nn.functional as F
 
 from . import oracle as orc
+
+_ROUND = [False]
+
+
+class _RoundBF16(torch.autograd.Function):
+    """Rounds a tensor to bf16 (keeping its dtype) and the gradient flowing back through it."""
+
+    @staticmethod
+    def forward(ctx, t):
+        return t.to(torch.bfloat16).to(t.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+def rb(t):
+    """A bf16 storage point: identity unless inside bf16_storage()."""
+    return _RoundBF16.apply(t) if _ROUND[0] else t
+
+
+class bf16_storage:
+    """Context manager: the functions of this module round at every op boundary (above)."""
+
+    def __enter__(self):
+        _ROUND[0] = True
+        return self
+
+    def __exit__(self, *exc):
+        _ROUND[0] = False
 
 
 class OracleWKV(torch.autograd.Function):
@@ -60,47 +98,47 @@ def token_shift(x):
 
 def bottleneck(p, pre, z):
     """RWKV6Bottleneck.forward (:177-195, TP = 1): [T,B,C] -> [T,B,E,C]."""
-    neck = torch.einsum("tbd,der->tber", z, p[pre + ".weight_down"]).tanh()
-    return torch.einsum("tber,erd->tbed", neck, p[pre + ".weight_up"]) + p[pre + ".bias"]
+    neck = rb(rb(torch.einsum("tbd,der->tber", z, p[pre + ".weight_down"])).tanh())
+    return rb(rb(torch.einsum("tber,erd->tbed", neck, p[pre + ".weight_up"])) + p[pre + ".bias"])
 
 
 def linear(p, name, x):
     """Column/RowParallelLinear at TP = 1: x W^T, plus the bias when the layer has one
     (add_bias_linear / add_qkv_bias, :393, :416, :484-505)."""
-    y = x @ p[name + ".weight"].t()
+    y = rb(x @ p[name + ".weight"].t())
     b = p.get(name + ".bias")
-    return y if b is None else y + b
+    return y if b is None else rb(y + b)
 
 
 def time_mix(p, x, H, eps):
     """RWKV6TimeMix.forward (:440-466); p maps the module's parameter names to tensors.  The
     output projection's bias, which the reference hands back separately (skip_bias_add, :418)
     for the layer's bias-dropout-add, is included in the returned output."""
-    delta = token_shift(x) - x
-    mixed_input = x + delta * p["mix_coeff_input"]
+    delta = rb(token_shift(x) - x)
+    mixed_input = rb(x + rb(delta * p["mix_coeff_input"]))
     mix = bottleneck(p, "bottleneck_token_shift", mixed_input)
-    m_w, m_k, m_v, m_r, m_g = (x.unsqueeze(-2) + delta.unsqueeze(-2) * mix).unbind(-2)
+    m_w, m_k, m_v, m_r, m_g = rb(x.unsqueeze(-2) + rb(delta.unsqueeze(-2) * mix)).unbind(-2)
     decay = bottleneck(p, "bottleneck_decay", m_w).squeeze(-2)
     key = linear(p, "linear_key", m_k)
     value = linear(p, "linear_value", m_v)
     rec = linear(p, "linear_receptance", m_r)
-    gate = F.silu(linear(p, "linear_gate", m_g))
+    gate = rb(F.silu(linear(p, "linear_gate", m_g)))
     T, B, C = x.shape
     hf = lambda t: t.reshape(T, B, H, C // H).permute(1, 2, 0, 3).contiguous()   # :333-336
-    o = OracleWKV.apply(hf(rec), hf(key), hf(value), -torch.exp(hf(decay)),
-                        p["core_attention.time_first"].reshape(H, -1))
+    o = rb(OracleWKV.apply(hf(rec), hf(key), hf(value), -rb(torch.exp(hf(decay))),
+                           p["core_attention.time_first"].reshape(H, -1)))
     o = o.permute(2, 0, 1, 3).reshape(T * B, C)                                    # :341, :462
-    y = F.group_norm(o, H, p["group_norm.weight"], p["group_norm.bias"], eps=eps).reshape(T, B, C)
-    return linear(p, "linear_proj", y * gate)
+    y = rb(F.group_norm(o, H, p["group_norm.weight"], p["group_norm.bias"], eps=eps)).reshape(T, B, C)
+    return linear(p, "linear_proj", rb(y * gate))
 
 
 def channel_mix(p, x):
     """RWKV6ChannelMix.forward (:512-536)."""
-    delta = token_shift(x) - x
-    mixed_up, mixed_gate = (x.unsqueeze(-2) + delta.unsqueeze(-2) * p["mix_coeffs"]).unbind(-2)
-    h = torch.square(torch.relu(linear(p, "linear_up", mixed_up)))
+    delta = rb(token_shift(x) - x)
+    mixed_up, mixed_gate = rb(x.unsqueeze(-2) + rb(delta.unsqueeze(-2) * p["mix_coeffs"])).unbind(-2)
+    h = rb(torch.square(torch.relu(linear(p, "linear_up", mixed_up))))
     out = linear(p, "linear_down", h)
-    return out * torch.sigmoid(linear(p, "linear_gate", mixed_gate))
+    return rb(out * rb(torch.sigmoid(linear(p, "linear_gate", mixed_gate))))
 
 
 def _sub(p, prefix):
@@ -110,19 +148,19 @@ def _sub(p, prefix):
 def layer(p, x, H, eps):
     """The TransformerLayer of get_rwkv6_layer_spec() (:539-550): pre-LN residual blocks."""
     C = x.shape[-1]
-    ln = lambda z, n: F.layer_norm(z, (C,), p[n + ".weight"], p[n + ".bias"], eps)
-    x = x + time_mix(_sub(p, "self_attention."), ln(x, "input_layernorm"), H, eps)
-    return x + channel_mix(_sub(p, "mlp."), ln(x, "pre_mlp_layernorm"))
+    ln = lambda z, n: rb(F.layer_norm(z, (C,), p[n + ".weight"], p[n + ".bias"], eps))
+    x = rb(x + time_mix(_sub(p, "self_attention."), ln(x, "input_layernorm"), H, eps))
+    return rb(x + channel_mix(_sub(p, "mlp."), ln(x, "pre_mlp_layernorm")))
 
 
 def model_forward(p, tokens, n_layers, H, eps=1e-5):
     """RWKV6Model (rwkv6_model.py:28-37, :108-112): tokens [B,T] -> logits [T,B,V]."""
     C = p["embedding.weight"].shape[1]
-    ln = lambda z, n: F.layer_norm(z, (C,), p[n + ".weight"], p[n + ".bias"], eps)
-    x = ln(p["embedding.weight"][tokens.t()], "pre_norm")
+    ln = lambda z, n: rb(F.layer_norm(z, (C,), p[n + ".weight"], p[n + ".bias"], eps))
+    x = ln(rb(p["embedding.weight"][tokens.t()]), "pre_norm")
     for i in range(n_layers):
         x = layer(_sub(p, f"layers.{i}."), x, H, eps)
-    return ln(x, "final_layernorm") @ p["output_layer.weight"].t()
+    return rb(ln(x, "final_layernorm") @ p["output_layer.weight"].t())
 
 
 def lm_loss(logits, targets, loss_mask):

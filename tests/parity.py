@@ -35,6 +35,14 @@ MIN_ELEMS = 4096
 BLOCK_TOL_MAX = 1e-1
 BLOCK_TOL_L2 = 3e-2
 BLOCK_BARS = dict(tol_max=BLOCK_TOL_MAX, tol_l2=BLOCK_TOL_L2, elem_mean=ELEM_MEAN_BLOCK)
+# A second bar for blocks, set by the reference rather than by measurement: the same block
+# restated in oracle/lm.py and run under lm.bf16_storage() (fp64 compute, every op's output
+# and every activation gradient rounded to bf16 once: the reference as it runs in bf16) has
+# an error against the plain fp64 run; the GPU path's relative L2 error may be at most
+# BF16_RATIO times that, plus BF16_L2_FLOOR for tensors the emulation happens to get almost
+# exactly (a sum over many tokens whose roundings cancel).
+BF16_RATIO = 1.5
+BF16_L2_FLOOR = 2e-3
 
 
 def metrics(got, ref) -> dict:
@@ -76,6 +84,31 @@ def check_all(got: dict, ref: dict, names, elem_mean_of=None, **bars) -> dict:
             b["elem_mean"] = elem_mean_of(n)
         try:
             out[n] = check(n, got[n], ref[n], **b)
+        except AssertionError as e:
+            bad.append(str(e))
+    assert not bad, "\n".join(bad)
+    return out
+
+
+def check_block(name, got, ref, emu, **bars) -> dict:
+    """check() at the block bars, then the bar relative to the reference in bf16 storage:
+    l2_rel(got, ref) <= BF16_RATIO * l2_rel(emu, ref) + BF16_L2_FLOOR."""
+    m = check(name, got, ref, **bars)
+    me = metrics(emu, ref)
+    bound = BF16_RATIO * me["l2_rel"] + BF16_L2_FLOOR
+    print(f"    {name}: reference in bf16 storage l2_rel {me['l2_rel']:.1e} -> bound {bound:.1e} "
+          f"(ratio {m['l2_rel'] / max(me['l2_rel'], 1e-30):.2f})", flush=True)
+    assert m["l2_rel"] <= bound, f"{name}: l2_rel {m['l2_rel']:.2e} above {bound:.2e} " \
+                                 f"({BF16_RATIO} x the bf16-storage reference's {me['l2_rel']:.2e})"
+    return m
+
+
+def check_all_block(got: dict, ref: dict, emu: dict, names, **bars) -> dict:
+    """check_block() over several tensors; reports every one before failing."""
+    out, bad = {}, []
+    for n in names:
+        try:
+            out[n] = check_block(n, got[n], ref[n], emu[n], **bars)
         except AssertionError as e:
             bad.append(str(e))
     assert not bad, "\n".join(bad)

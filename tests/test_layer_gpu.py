@@ -9,7 +9,8 @@ B=2 x T=8192).
   y - x and the input gradient's non-identity part dx - dy are compared.  Bars for a block
   that keeps bf16 activations between hipBLASLt GEMMs (as bf16 training does; every kernel
   on it is pinned separately at 1e-2): parity.BLOCK_BARS (max_rel 1e-1, l2_rel 3e-2,
-  reference-metric mean 3e-1).
+  reference-metric mean 3e-1), and a relative L2 error at most 1.5x that of the same layer
+  restated in bf16 storage (lm.bf16_storage(): the reference as it runs in bf16) plus 2e-3.
 * Full shape: the same layer over the config's whole T x B: finite, bit-identical on a
   second run, and a gradient for every parameter.
 """
@@ -61,20 +62,32 @@ def test_full_width_layer_parity(pkg, cfg_name):
     out.backward(dy.to(DEV))
     torch.cuda.synchronize()
 
-    p = lm.params_from_state_dict(layer.state_dict())
-    xr = x.double().requires_grad_(True)
-    ref = lm.layer(p, xr, H, cfg.layernorm_epsilon)
-    ref.backward(dy.double())
+    def reference(storage):
+        p = lm.params_from_state_dict(layer.state_dict())
+        xr = x.double().requires_grad_(True)
+        if storage:
+            with lm.bf16_storage():
+                y = lm.layer(p, xr, H, cfg.layernorm_epsilon)
+                y.backward(dy.double())
+        else:
+            y = lm.layer(p, xr, H, cfg.layernorm_epsilon)
+            y.backward(dy.double())
+        # parameter gradients are stored in the parameters' dtype (bf16) by both
+        grads = {k: t.grad.to(torch.bfloat16) if storage else t.grad for k, t in p.items()}
+        return y, xr.grad, grads
+
+    ref, ref_dx, ref_g = reference(False)
+    emu, emu_dx, emu_g = reference(True)
 
     n = lambda t: t.detach().double().cpu().numpy()
     # out and dx are stored in bf16, rounded at the scale of x and dy (2^-9 of it), while the
     # block's own parts y - x and dx - dy are several times smaller: their errors carry that
     # storage rounding on top of the block's own
-    parity.check("y - x", n(out) - n(x), n(ref) - n(x), **BARS)
-    parity.check("dx - dy", n(xg.grad) - n(dy), n(xr.grad) - n(dy), **BARS)
+    parity.check_block("y - x", n(out) - n(x), n(ref) - n(x), n(emu) - n(x), **BARS)
+    parity.check_block("dx - dy", n(xg.grad) - n(dy), n(ref_dx) - n(dy), n(emu_dx) - n(dy), **BARS)
     got = {name: n(prm.grad) for name, prm in layer.named_parameters()}
-    want = {name: n(p[name].grad) for name in got}
-    parity.check_all(got, want, sorted(got), **BARS)
+    parity.check_all_block(got, {k: n(ref_g[k]) for k in got}, {k: n(emu_g[k]) for k in got},
+                           sorted(got), **BARS)
 
 
 @pytest.mark.parametrize("cfg_name", list(WIDTHS))

@@ -1,11 +1,12 @@
 """End-to-end drop-in check of RWKV6TimeMix on the GPU against the CPU restatement of
-the reference's forward (rwkv6_layer_specs.py:431-468, oracle/lm.py) in torch fp32, with
+the reference's forward (rwkv6_layer_specs.py:431-468, oracle/lm.py) in torch fp64, with
 the WKV of :339 provided by the CPU oracle through its autograd wrapper.
 
 Block-level tolerance (parity.BLOCK_BARS): relative L2 <= 3e-2 and max|err|/max|ref| <= 1e-1
 — the GPU path keeps activations in bf16 between the GEMMs (as bf16 training does); every
-kernel on it is pinned separately at 1e-2.  The reference's elementwise metric is printed
-(tests/parity.py).
+kernel on it is pinned separately at 1e-2 — and a relative L2 error at most 1.5x that of the
+same block run in bf16 storage (lm.bf16_storage(): the reference as it runs in bf16) plus
+2e-3.  The reference's elementwise metric is printed (tests/parity.py).
 """
 import pytest
 import torch
@@ -39,17 +40,36 @@ def test_timemix_module_matches_reference_forward(pkg, params_dtype):
     (out.float() * dy.to("cuda:0").float()).sum().backward()
     torch.cuda.synchronize()
 
-    p = {n: t.detach().float().cpu().requires_grad_(True) for n, t in mod.named_parameters()}
-    xc = x.float().requires_grad_(True)
-    ref = lm.time_mix(p, xc, cfg.num_attention_heads, cfg.layernorm_epsilon)
-    (ref * dy.float()).sum().backward()
+    ref, ref_dx, ref_g = _reference(mod, lambda p, z: lm.time_mix(
+        p, z, cfg.num_attention_heads, cfg.layernorm_epsilon), x, dy, False)
+    emu, emu_dx, emu_g = _reference(mod, lambda p, z: lm.time_mix(
+        p, z, cfg.num_attention_heads, cfg.layernorm_epsilon), x, dy, True)
 
     n = lambda t: t.detach().double().cpu().numpy()
     bars = parity.BLOCK_BARS
-    parity.check("out", n(out), n(ref), **bars)
-    parity.check("dx", n(xg.grad), n(xc.grad), **bars)
+    parity.check_block("out", n(out), n(ref), n(emu), **bars)
+    parity.check_block("dx", n(xg.grad), n(ref_dx), n(emu_dx), **bars)
     got = {name: n(prm.grad) for name, prm in mod.named_parameters()}
-    parity.check_all(got, {name: n(p[name].grad) for name in got}, sorted(got), **bars)
+    parity.check_all_block(got, {k: n(ref_g[k]) for k in got}, {k: n(emu_g[k]) for k in got},
+                           sorted(got), **bars)
+
+
+def _reference(mod, fn, x, dy, storage):
+    """fn (a block of oracle/lm.py) in fp64 on the module's parameters, forward and backward
+    of sum(out * dy); storage: under lm.bf16_storage(), with the parameter gradients stored in
+    the parameters' own dtype."""
+    p = {k: t.detach().double().cpu().requires_grad_(True) for k, t in mod.named_parameters()}
+    dt = {k: t.dtype for k, t in mod.named_parameters()}
+    xc = x.double().requires_grad_(True)
+    if storage:
+        with lm.bf16_storage():
+            ref = fn(p, xc)
+            (ref * dy.double()).sum().backward()
+    else:
+        ref = fn(p, xc)
+        (ref * dy.double()).sum().backward()
+    grads = {k: t.grad.to(dt[k]) if storage else t.grad for k, t in p.items()}
+    return ref, xc.grad, grads
 
 
 def test_state_dict_contract(pkg):
@@ -111,11 +131,10 @@ def test_megatron_built_modules_match_reference(pkg, add_bias_linear):
             out = out + bias
         (out.float() * dy.to("cuda:0").float()).sum().backward()
         torch.cuda.synchronize()
-        p = {k: t.detach().float().cpu().requires_grad_(True) for k, t in mod.named_parameters()}
-        xc = x.float().requires_grad_(True)
-        ref = ref_fn(p, xc)
-        (ref * dy.float()).sum().backward()
-        parity.check(f"{name} out", n(out), n(ref), **bars)
-        parity.check(f"{name} dx", n(xg.grad), n(xc.grad), **bars)
+        ref, ref_dx, ref_g = _reference(mod, ref_fn, x, dy, False)
+        emu, emu_dx, emu_g = _reference(mod, ref_fn, x, dy, True)
+        parity.check_block(f"{name} out", n(out), n(ref), n(emu), **bars)
+        parity.check_block(f"{name} dx", n(xg.grad), n(ref_dx), n(emu_dx), **bars)
         got = {k: n(prm.grad) for k, prm in mod.named_parameters()}
-        parity.check_all(got, {k: n(p[k].grad) for k in got}, sorted(got), **bars)
+        parity.check_all_block(got, {k: n(ref_g[k]) for k in got}, {k: n(emu_g[k]) for k in got},
+                               sorted(got), **bars)
