@@ -27,7 +27,8 @@ torch.nn.functional.cross_entropy.
 ``bf16_storage()`` turns the same functions into an emulation of the reference as it runs in
 bf16 on a GPU: every op computes in the tensors' own (higher) precision and its output is
 rounded to bf16 once, and so is the gradient reaching each op's output in the backward (the
-storage points of bf16 autograd; fla's WKV computes in fp32 and returns bf16).  Its error
+storage points of bf16 autograd; fla's WKV computes in fp32 and returns bf16; the gradients of
+a tensor that several ops read are summed unrounded where they meet).  Its error
 against the plain fp64 run is the rounding error the reference itself carries in bf16, which
 the block tests use as the scale of an acceptable error.  (torch's own bf16 CPU kernels are
 not that reference: some accumulate in bf16.)

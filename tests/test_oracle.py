@@ -373,3 +373,47 @@ def test_lm_linear_with_and_without_bias_is_f_linear():
     assert torch.allclose(lm.linear({"l.weight": w}, "l", x), torch.nn.functional.linear(x, w))
     assert torch.allclose(lm.linear({"l.weight": w, "l.bias": b}, "l", x),
                           torch.nn.functional.linear(x, w, b))
+
+
+def test_lm_bf16_storage_rounds_outputs_and_gradients():
+    """lm.bf16_storage(): a storage point rounds its value and the gradient through it to bf16
+    (torch's own bf16 conversion, round to nearest even) and is the identity outside; the
+    channel mix run under it returns bf16-representable values, and it and its input gradient
+    differ from the plain fp64 run by about bf16 rounding (2^-9 relative).  (The gradients of
+    a tensor that several ops read are summed unrounded where they meet.)"""
+    from oracle import lm
+
+    g = torch.Generator().manual_seed(3)
+    t = torch.randn(64, generator=g, dtype=torch.float64, requires_grad=True)
+    gr = torch.randn(64, generator=g, dtype=torch.float64)
+    assert lm.rb(t) is t
+    with lm.bf16_storage():
+        y = lm.rb(t)
+    y.backward(gr)
+    assert torch.equal(y.detach(), t.detach().to(torch.bfloat16).double())
+    assert torch.equal(t.grad, gr.to(torch.bfloat16).double())
+    assert lm.rb(t) is t                                   # the context is closed again
+
+    C, F, T, B = 64, 128, 7, 2
+    p = {"mix_coeffs": torch.rand(2, C, generator=g, dtype=torch.float64),
+         "linear_up.weight": 0.1 * torch.randn(F, C, generator=g, dtype=torch.float64),
+         "linear_down.weight": 0.1 * torch.randn(C, F, generator=g, dtype=torch.float64),
+         "linear_gate.weight": 0.1 * torch.randn(C, C, generator=g, dtype=torch.float64)}
+    x = torch.randn(T, B, C, generator=g, dtype=torch.float64)
+    dy = torch.randn(T, B, C, generator=g, dtype=torch.float64)
+    outs = []
+    for storage in (False, True):
+        xx = x.clone().requires_grad_(True)
+        if storage:
+            with lm.bf16_storage():
+                y = lm.channel_mix(p, xx)
+                y.backward(dy)
+        else:
+            y = lm.channel_mix(p, xx)
+            y.backward(dy)
+        outs.append((y.detach(), xx.grad))
+    (y64, dx64), (yb, dxb) = outs
+    assert torch.equal(yb, yb.to(torch.bfloat16).double())
+    for a, b in ((yb, y64), (dxb, dx64)):
+        rel = float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+        assert 2.0 ** -12 < rel < 2.0 ** -5, rel
