@@ -1169,6 +1169,10 @@ struct GradOut {
     float lt[2];                             // the lane's sum of x = Rm s acc_r - Km acc_k
     float dup[2];                            // du partial: sum over the lane's tokens of r k dd
     unsigned floored;                        // head-first: bit 4tp + rr for a floored token
+    bool fl[4];                              // the reverse walk's: token rr floored (head-first);
+                                             // per-lane flags the compiler keeps as lane masks
+                                             // in scalar registers (a bit field costs 3 VALU a
+                                             // token to build and test)
     f32x4 av[2];                             // dv
 };
 
@@ -1870,7 +1874,6 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float sc
         const f32x4 t2 = mfma16(lds_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], o.blktr), ch4o(RTp, o, c0, 16 * I), f32x4{});
         ak2 += (t2 * lds_ld<float>(&sm.fp[(I * (I - 1)) / 2 + W][c0], o.tab)) * lds_ld<float>(&sm.kb[W][c0], o.tab);
     }
-    out.floored = 0u;
     {
         float d[4], xv[4];
         out.dup[0] = 0.f;
@@ -1883,7 +1886,7 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float sc
             const float y = -(float)g.kmb[0][rr] * akr;
             xv[rr] = xr[rr] + y;
             out.dwv[0][rr] = y;
-            if (!SEQ && g.Fm[0][rr] * g.Fk[0][rr] > FLOOR_FF) out.floored |= 1u << rr;
+            out.fl[rr] = !SEQ && g.Fm[0][rr] * g.Fk[0][rr] > FLOOR_FF;
         }
         out.dkb[0] = cvt4(d[0], d[1], d[2], d[3]);
         out.dwv[0][2] += xv[3];
@@ -2241,7 +2244,7 @@ __device__ __forceinline__ void bwd_loop_walk(
                     const float wn = -ex2((float)wrw[rr] * RW_L2E);
                     g[rr] = wn < W_MIN ? 0.f : g[rr] * wn;
                 }
-                if (!SEQ && ((go.floored >> rr) & 1u)) g[rr] = 0.f;
+                if (!SEQ && go.fl[rr]) g[rr] = 0.f;
             }
             lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(c0, TW), go.drb[0]);
             lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(c0, TW), go.dkb[0]);
