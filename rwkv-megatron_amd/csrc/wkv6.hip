@@ -281,7 +281,8 @@ struct WalkSmem {
     float tot[NTHR_W];                // build_G scratch
     float bonus[CL];
     float uh[KD];                     // u of this head
-    float G[CL * GSG];                // cumulative log2-decay
+    float G[(CL + 1) * GSG];          // row 0 zero (G before the chunk), row t + 1 = G_t:
+                                      // cumulative log2-decay
     tile_t Rm, Km;                    // diagonal-block operands (midpoint-referenced)
     tile_t Ri, Rp;                    // r e^{G_{t-1}} (inter-chunk), r e^{G_{t-1} - b_{I-1}} (cross)
     tile_t Kt, Vm, Ot;                // state-update operand k e^{G_63 - G}, v, o staging
@@ -295,7 +296,7 @@ static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
 // ge[2I - 1], G_63 = ge[7]).  `part` is wave-uniform, so the table branches are scalar.
 template <bool DEC>
 __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar) {
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G + GSG);
     const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
     float loc[8];
     float run = 0.f;
@@ -447,7 +448,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
         int NT, int bh, int c_begin, int c_end, int hh, WalkPrefetch& nx, f32x4* acc) {
     constexpr int I = PB;                          // token block of the thread's tile pieces
     constexpr int W = PB < 2 ? PB : 5 - PB;        // token block of the wave's products
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G + GSG);   // Gm[-1] is the zero row
     const int lane = threadIdx.x & 63;
     const int lr = lane & 15, lq = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
@@ -498,7 +499,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
             float gm[8], gg[8], gp[8];
             g8(Gm, 16 * I + 7, c8, gm);
             g8(Gm, row, c8, gg);
-            g8m1(Gm, row, c8, gp);
+            g8(Gm, row - 1, c8, gp);                           // the zero row for row 0
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 rm[s] = rf[s] * ex2(gp[s] - gm[s]);
@@ -618,7 +619,6 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
               const float* __restrict__ Sstart, float scale, int B, int H, int T, int NT, int P) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     WalkSmem& sm = *reinterpret_cast<WalkSmem*>(smem_raw);
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G);
     const int bh = blockIdx.x / P, seg = blockIdx.x - bh * P, h = bh % H;
     const int NC = (NT + P - 1) / P;
     const int c_begin = seg * NC, c_end = min(NT, c_begin + NC);
@@ -654,6 +654,7 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
                 for (int rr = 0; rr < 4; ++rr) acc[tp][rr] = 0.f;
         }
         if (threadIdx.x < KD) sm.uh[threadIdx.x] = load_u(u, u_dtype, h * KD + threadIdx.x);
+        if (threadIdx.x < GSG) sm.G[threadIdx.x] = 0.f;       // G before the chunk: 0
         __syncthreads();
     }
 
