@@ -257,7 +257,8 @@ __host__ __device__ constexpr int pair_index(int I, int J) { return I * (I - 1) 
 //   S_start(p) = A(p-1) S_start(p-1) + S_seg(p-1),  S_start(0) = h0.
 // 8 waves: wave (W, hh) owns target tokens [16W, 16W+16) x value columns [32hh, 32hh+32)
 // of o, and state rows [16W, 16W+16) x columns [32hh, 32hh+32): lane (lq, lr) holds
-// S[16W + 4lq + rr][32hh + 16tp + lr] in acc[tp][rr].
+// S[16W + lr][32hh + 16tp + 4lq + rr] in acc[tp][rr] (the products are computed transposed,
+// value side as the A operand, so a lane's four values are adjacent columns of one row).
 #define NTHR_W 512
 #ifndef WALK_TARGET_ITEMS
 #define WALK_TARGET_ITEMS 256   // workgroups a forward should offer (one per CU of an MI355X)
@@ -475,12 +476,12 @@ __device__ __forceinline__ void fwd_walk_chunks(
             for (int s = 0; s < 8; ++s) bsum += rf[s] * uf[s] * kf[s];
             bsum = sum8lanes(bsum);
             if ((threadIdx.x & 7) == 0) sm.bonus[row] = bsum;
-            // S_in of this chunk, bf16, for the inter-chunk product and the backward
+            // S_in of this chunk, bf16, for the inter-chunk product and the backward: the lane's
+            // four values of a state row are adjacent, one 8-byte write per 16 columns
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    sm.Sin[c & 1][16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(acc[tp][rr]);
+                *reinterpret_cast<uint2*>(&sm.Sin[c & 1][16 * W + lr][32 * hh + 16 * tp + 4 * lq]) =
+                    make_uint2(pk2(acc[tp][0], acc[tp][1]), pk2(acc[tp][2], acc[tp][3]));
         }
         // unconditional (the last iteration reloads its own chunk): loads under a branch
         // would cost the loop a full wait
@@ -538,15 +539,18 @@ __device__ __forceinline__ void fwd_walk_chunks(
         __syncthreads();
         {
             const int t = 16 * W + lr;
-            // the 16x16x32 and the 16x16x16 products go to separate accumulators (ao, ab)
+            // o transposed: every product takes the value side as its A operand and the token
+            // side as its B operand, so lane (lq, lr) ends up with o[t = 16W + lr][j0 + 4 lq +
+            // rr], four adjacent columns of one token (one 8-byte write into Ot).  The 16x16x32
+            // and the 16x16x16 products go to separate accumulators (ao, ab).
             f32x4 ao[2] = {}, ab[2] = {};
             // inter-chunk: (r e^{G_{t-1}}) S_in
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const bf16x8 a = ld_dir8(&sm.Ri[0][0], t, 32 * ks);
+                const bf16x8 b = ld_dir8(&sm.Ri[0][0], t, 32 * ks);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
-                    ao[tp] = mfma32(a, ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), ao[tp]);
+                    ao[tp] = mfma32(ld_tr8(&sm.Sin[c & 1][0][0], 32 * ks, 32 * hh + 16 * tp), b, ao[tp]);
             }
             // diagonal block: strictly causal part plus the u-bonus diagonal
             {
@@ -563,7 +567,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
                 const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), ab[tp]);
+                    ab[tp] = mfma16(ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), aop, ab[tp]);
             }
             // earlier blocks J < W, both operands referenced at b_{W-1}
 #pragma unroll
@@ -576,27 +580,33 @@ __device__ __forceinline__ void fwd_walk_chunks(
                 const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
 #pragma unroll
                 for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(aop, ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), ab[tp]);
+                    ab[tp] = mfma16(ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), aop, ab[tp]);
             }
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
+            for (int tp = 0; tp < 2; ++tp) {
+                float y[4];
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    sm.Ot[16 * W + 4 * lq + rr][32 * hh + 16 * tp + lr] = f2bf(scale * (ao[tp][rr] + ab[tp][rr]));
+                for (int rr = 0; rr < 4; ++rr) y[rr] = scale * (ao[tp][rr] + ab[tp][rr]);
+                *reinterpret_cast<uint2*>(&sm.Ot[t][32 * hh + 16 * tp + 4 * lq]) =
+                    make_uint2(pk2(y[0], y[1]), pk2(y[2], y[3]));
+            }
         }
-        // state update: S = diag(e^{G_63}) S + Kt^T V
+        // state update: S = diag(e^{G_63}) S + Kt^T V, computed transposed like o (V^T as the A
+        // operand): lane (lq, lr) holds S[16W + lr][j0 + 4 lq + rr], so its row factor is one
+        {
+            const float d = sm.dec[c & 1][16 * W + lr];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
-            acc[0][rr] *= d;
-            acc[1][rr] *= d;
+            for (int rr = 0; rr < 4; ++rr) {
+                acc[0][rr] *= d;
+                acc[1][rr] *= d;
+            }
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
+            const bf16x8 b = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
-                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+                acc[tp] = mfma32(ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), b, acc[tp]);
         }
         __syncthreads();
         // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
@@ -643,10 +653,11 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
         // over the whole walk: the register assignment of the loop differed)
         if (s0) {
 #pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr)
-                    acc[tp][rr] = s0[(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr];
+            for (int tp = 0; tp < 2; ++tp) {
+                const float4 x = *reinterpret_cast<const float4*>(
+                    s0 + (16 * W + lr) * KD + 32 * hh + 16 * tp + 4 * lq);
+                acc[tp][0] = x.x; acc[tp][1] = x.y; acc[tp][2] = x.z; acc[tp][3] = x.w;
+            }
         } else {
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
@@ -676,13 +687,14 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     // ---- end of the sequence: the final state ----
     if (seg == P - 1) {
 #pragma unroll
-        for (int tp = 0; tp < 2; ++tp)
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const size_t e = (size_t)(16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr;
-                Hs[(size_t)bh * (NT + 1) * KD * KD + (size_t)NT * KD * KD + e] = f2bf(acc[tp][rr]);
-                if (hT) hT[sbase + e] = acc[tp][rr];
-            }
+        for (int tp = 0; tp < 2; ++tp) {
+            const size_t e = (size_t)(16 * W + lr) * KD + 32 * hh + 16 * tp + 4 * lq;
+            *reinterpret_cast<uint2*>(Hs + (size_t)bh * (NT + 1) * KD * KD + (size_t)NT * KD * KD + e) =
+                make_uint2(pk2(acc[tp][0], acc[tp][1]), pk2(acc[tp][2], acc[tp][3]));
+            if (hT)
+                *reinterpret_cast<float4*>(hT + sbase + e) =
+                    make_float4(acc[tp][0], acc[tp][1], acc[tp][2], acc[tp][3]);
+        }
     }
 }
 
