@@ -537,6 +537,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
             }
         }
         __syncthreads();
+        bf16x4 vt[4][2];
         {
             const int t = 16 * W + lr;
             // o transposed: every product takes the value side as its A operand and the token
@@ -544,6 +545,13 @@ __device__ __forceinline__ void fwd_walk_chunks(
             // rr], four adjacent columns of one token (one 8-byte write into Ot).  The 16x16x32
             // and the 16x16x16 products go to separate accumulators (ao, ab).
             f32x4 ao[2] = {}, ab[2] = {};
+            // V^T operands of the wave's 32 columns, token block J in vt[J]: the products below
+            // take the blocks they need, and the state update takes all four (ld_tr8 is two
+            // ld_tr4 of consecutive blocks), so each is read from LDS once
+#pragma unroll
+            for (int J = 0; J < 4; ++J)
+#pragma unroll
+                for (int tp = 0; tp < 2; ++tp) vt[J][tp] = ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp);
             // inter-chunk: (r e^{G_{t-1}}) S_in
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
@@ -559,15 +567,15 @@ __device__ __forceinline__ void fwd_walk_chunks(
                 for (int ks = 0; ks < 2; ++ks)
                     at = mfma32(ld_row8(&sm.Km[0][0], 16 * W + lr, 32 * ks), ld_row8(&sm.Rm[0][0], t, 32 * ks), at);
                 float xa[4];
+                const float bon = sm.bonus[t];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int tl = 4 * lq + rr;
-                    xa[rr] = tl < lr ? at[rr] : (tl == lr ? sm.bonus[t] : 0.f);
+                    xa[rr] = tl < lr ? at[rr] : (tl == lr ? bon : 0.f);
                 }
                 const bf16x4 aop = cvt4(xa[0], xa[1], xa[2], xa[3]);
 #pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(ld_tr4(&sm.Vm[0][0], 16 * W, 32 * hh + 16 * tp), aop, ab[tp]);
+                for (int tp = 0; tp < 2; ++tp) ab[tp] = mfma16(vt[W][tp], aop, ab[tp]);
             }
             // earlier blocks J < W, both operands referenced at b_{W-1}
 #pragma unroll
@@ -579,8 +587,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
                     at = mfma32(ld_row8(&sm.Kc[0][0], pr, 32 * ks), ld_row8(&sm.Rp[0][0], t, 32 * ks), at);
                 const bf16x4 aop = cvt4(at[0], at[1], at[2], at[3]);
 #pragma unroll
-                for (int tp = 0; tp < 2; ++tp)
-                    ab[tp] = mfma16(ld_tr4(&sm.Vm[0][0], 16 * J, 32 * hh + 16 * tp), aop, ab[tp]);
+                for (int tp = 0; tp < 2; ++tp) ab[tp] = mfma16(vt[J][tp], aop, ab[tp]);
             }
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp) {
@@ -606,7 +613,8 @@ __device__ __forceinline__ void fwd_walk_chunks(
             const bf16x8 b = ld_tr8(&sm.Kt[0][0], 32 * ks, 16 * W);
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp)
-                acc[tp] = mfma32(ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), b, acc[tp]);
+                acc[tp] = mfma32(__builtin_shufflevector(vt[2 * ks][tp], vt[2 * ks + 1][tp], 0, 1, 2, 3, 4, 5, 6, 7),
+                                 b, acc[tp]);
         }
         __syncthreads();
         // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
