@@ -459,13 +459,13 @@ __device__ __forceinline__ void fwd_walk_chunks(
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(CL, T - c * CL);
         // Every tile written here was last read before the previous chunk's final barrier
-        // (Sin[c & 1] two chunks ago).  Raw r and k wait in Rm and Km.
+        // (Sin[c & 1] two chunks ago).  The thread's raw r and k stay in registers (rq, kq)
+        // for its own operand tiles below.
         if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
         sstore16(sm.Vm, row, c8, nx.v);
         sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
-        sstore16(sm.Km, row, c8, nx.k);
+        const uint4 rq = nx.r, kq = nx.k;
         {
-            sstore16(sm.Rm, row, c8, nx.r);
             float rf[8], kf[8], bsum = 0.f;
             unpack8(nx.r, rf);
             unpack8(nx.k, kf);
@@ -495,8 +495,8 @@ __device__ __forceinline__ void fwd_walk_chunks(
             //   Rm = r e^{G_{t-1} - mu_I}     Ri = Rm e^{mu_I}          Rp = Rm e^{mu_I - b_{I-1}}
             //   Km = k e^{mu_I - G_t}         Kt = Km e^{G_63 - mu_I}   Kc(I2) = Km e^{b_{I2-1} - mu_I}
             float rf[8], kf[8], rm[8], km[8], y[8], f[8];
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Rm[row][c8]), rf);
-            unpack8(*reinterpret_cast<const uint4*>(&sm.Km[row][c8]), kf);
+            unpack8(rq, rf);
+            unpack8(kq, kf);
             float gm[8], gg[8], gp[8];
             g8(Gm, 16 * I + 7, c8, gm);
             g8(Gm, row, c8, gg);
