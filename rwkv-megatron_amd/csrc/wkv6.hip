@@ -453,6 +453,14 @@ __device__ __forceinline__ void fwd_walk_chunks(
     const int lane = threadIdx.x & 63;
     const int lr = lane & 15, lq = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+    // u at the thread's 8 channels, for the bonus of every chunk (constant over the walk)
+    float uf[8];
+    {
+        const float4 ua = *reinterpret_cast<const float4*>(&sm.uh[c8]);
+        const float4 ub = *reinterpret_cast<const float4*>(&sm.uh[c8 + 4]);
+        uf[0] = ua.x; uf[1] = ua.y; uf[2] = ua.z; uf[3] = ua.w;
+        uf[4] = ub.x; uf[5] = ub.y; uf[6] = ub.z; uf[7] = ub.w;
+    }
     // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
     // loop's own order (the next chunk's loads, then this chunk's two stores) alone
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -469,9 +477,6 @@ __device__ __forceinline__ void fwd_walk_chunks(
             float rf[8], kf[8], bsum = 0.f;
             unpack8(nx.r, rf);
             unpack8(nx.k, kf);
-            const float4 ua = *reinterpret_cast<const float4*>(&sm.uh[c8]);
-            const float4 ub = *reinterpret_cast<const float4*>(&sm.uh[c8 + 4]);
-            const float uf[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
 #pragma unroll
             for (int s = 0; s < 8; ++s) bsum += rf[s] * uf[s] * kf[s];
             bsum = sum8lanes(bsum);
