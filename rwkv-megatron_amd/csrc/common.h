@@ -116,6 +116,27 @@ template <int M> __device__ __forceinline__ float lane_xor_swz(float v) {       
                                                                  0x1F | (M << 10)));
 }
 __device__ __forceinline__ float lane_xor32(float v) { return __shfl_xor(v, 32); }
+// Sums across the four 16-lane rows of a wave (lane = 16 lq + lr) on the VALU, with gfx950's
+// row swaps instead of LDS-pipe shuffles.  With both operands x, v_permlane16_swap leaves the
+// even row of each row pair in the first result and the odd row in the second (rows 0,1 ->
+// x_0, x_1; rows 2,3 -> x_2, x_3, in every lane of the pair), and v_permlane32_swap leaves
+// rows {0,1} in the first and rows {2,3} in the second (probed on the device).
+struct RowSums {
+    float pair;        // x_0 + x_1 in rows 0 and 1, x_2 + x_3 in rows 2 and 3
+    float lo, hi;      // x_0 + x_1 and x_2 + x_3, in every lane
+};
+__device__ __forceinline__ RowSums row_sums(float x) {
+    const unsigned b = __float_as_uint(x);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    RowSums r;
+    r.pair = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const unsigned pb = __float_as_uint(r.pair);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(pb, pb, false, false);
+    r.lo = __uint_as_float(r32[0]);
+    r.hi = __uint_as_float(r32[1]);
+    return r;
+}
+
 // Sum over aligned groups of 8 lanes; all 8 lanes get the same bits.  The last step adds
 // the other quad through row_half_mirror (lane i <-> lane 7 - i of the group).
 __device__ __forceinline__ float sum8lanes(float v) {

@@ -1890,9 +1890,8 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float sc
         float pk = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) pk += (float)g.kmb[0][rr] * ak[rr];
-        float p = pk + lane_xor_swz<16>(pk);
-        p += lane_xor32(p);
-        if (o.q16 == 0) lds_st<float>(&sm.Pk[W][c0], o.tab, p);
+        const RowSums rs = row_sums(pk);                  // the column's sum over the 4 rows
+        if (o.q16 == 0) lds_st<float>(&sm.Pk[W][c0], o.tab, rs.lo + rs.hi);
     }
     ak2 = mfma16(lds_tr(&sm.dAb[bW + W][0][0], o.blktr), ch4o(RTp, o, c0, TW), f32x4{});
 #pragma unroll
@@ -2116,13 +2115,13 @@ __device__ __forceinline__ void bwd_loop_walk(
                 run += fmaxf(x, W_MIN) * RW_L2E;
                 cs[rr] = run;
             }
-            float xi = run, y = __shfl_up(xi, 16);
-            xi += lq >= 1 ? y : 0.f;
-            y = __shfl_up(xi, 32);
-            xi += lq >= 2 ? y : 0.f;                            // inclusive over lq
+            // prefix over the four lane rows: row 0 run_0, row 1 run_0 + run_1, row 2 (run_0 +
+            // run_1) + run_2, row 3 (run_0 + run_1) + (run_2 + run_3)
+            const RowSums rs = row_sums(run);
+            const float xi = ((lq & 1) ? rs.pair : run) + (lq >= 2 ? rs.lo : 0.f);
             const float excl = xi - run;
-            const float tot = __shfl(xi, 48 + lr);              // the block's total
-            m7 = __shfl(excl + cs[3], 16 + lr);                 // G at token 16W+7
+            const float tot = rs.lo + rs.hi;                    // the block's total
+            m7 = rs.lo;                                         // G at token 16W+7
             qloc = tot - m7;                                    // b_W - mu_W
             if (lq == 0) {
                 lds_st<float>(&sm.red[W][c0], o.tab, tot);
@@ -2245,10 +2244,8 @@ __device__ __forceinline__ void bwd_loop_walk(
         float later;
         {
             const float lt = go.lt[0];
-            const float d16 = __shfl_down(lt, 16);
-            float vsum = lt + (lq <= 2 ? d16 : 0.f);
-            const float d32 = __shfl_down(vsum, 32);
-            vsum += lq <= 1 ? d32 : 0.f;                        // sum over lq' >= lq
+            const RowSums rs = row_sums(lt);                    // sum over lq' >= lq:
+            const float vsum = ((lq & 1) ? lt : rs.pair) + (lq < 2 ? rs.hi : 0.f);
             later = vsum - lt;
             if (lq == 0) lds_st<float>(&sm.red[W][c0], o.tab, vsum);   // the wave's total
         }
@@ -2352,9 +2349,8 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     }
     // du over the sequence: lanes of one channel (lq), then the four token blocks in order
     {
-        float p = du_acc + lane_xor_swz<16>(du_acc);
-        p += lane_xor32(p);
-        if (((threadIdx.x >> 4) & 3) == 0) sm.red[4 + (threadIdx.x >> 8)][ch0] = p;
+        const RowSums rs = row_sums(du_acc);
+        if (((threadIdx.x >> 4) & 3) == 0) sm.red[4 + (threadIdx.x >> 8)][ch0] = rs.lo + rs.hi;
     }
     if (dh0 && seg == 0)
         *reinterpret_cast<float4*>(dh0 + sbase + ch0 * KD + t40) = make_float4(Dst[0], Dst[1], Dst[2], Dst[3]);
