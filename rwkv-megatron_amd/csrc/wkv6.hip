@@ -1716,25 +1716,26 @@ struct LaneOfs {
     int tr;      // ((4q + L/4) TS + 4 (L%4)) * 2: ds_read_b64_tr_b16 over rows r0 + 4q + s
     int g8;      // ((8q + L/4) TS + 4 (L%4)) * 2: the same over rows r0 + 8q + s
     int row;     // (L TS + 8q) * 2: 16-byte row pieces (row L, columns 8q..)
-    int ch;      // (L TS + 4q) * 2: 8-byte row pieces (row L, columns 4q..)
+    int ch;      // ((c0 + L) TS + 4q) * 2: 8-byte row pieces (row c0 + L, columns 4q..), c0 =
+                 // the wave's channel column 16 col: every use is in the wave's own rows
     int blk;     // (DAB_RS L + 4q) * 2: a 16x16 row-major dA block, direct
     int blktr;   // ((4q + L/4) DAB_RS + 4 (L%4)) * 2: the same, transposed
     int frag;    // 8 lane: 8 bytes per lane in MFMA-operand order
-    int tab;     // 4 L: a float per channel of a 16-channel column
+    int tab;     // 4 (c0 + L): a float per channel of the wave's 16-channel column
     int th;      // (q TS + 4 L) * 2: thread (row, c4) of a wave's four rows
     int q16;     // 16 q: four floats per lane row
 };
-__device__ __forceinline__ LaneOfs lane_ofs(int lane) {
+__device__ __forceinline__ LaneOfs lane_ofs(int lane, int c0) {
     const int L = lane & 15, q = lane >> 4;
     LaneOfs o;
     o.tr = ((4 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
     o.g8 = ((8 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
     o.row = (L * TS + 8 * q) * 2;
-    o.ch = (L * TS + 4 * q) * 2;
+    o.ch = ((c0 + L) * TS + 4 * q) * 2;
     o.blk = (DAB_RS * L + 4 * q) * 2;
     o.blktr = ((4 * q + (L >> 2)) * DAB_RS + 4 * (L & 3)) * 2;
     o.frag = 8 * lane;
-    o.tab = 4 * L;
+    o.tab = 4 * (c0 + L);
     o.th = (q * TS + 4 * L) * 2;
     o.q16 = 16 * q;
     return o;
@@ -1819,7 +1820,7 @@ __device__ __forceinline__ void loop_A_block(LoopSmem& sm, int b, float scale, c
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)     // channel slots in tr8 order on both operands
             at = mfma32(tr8o(&sm.RT[0][0], o, 32 * ks, 16 * W), tr8o(&sm.KT[0][0], o, 32 * ks, 16 * W), at);
-        const float bon = lds_ld<float>(&sm.bonus[16 * W], o.tab);
+        const float bon = lds_ld<float>(&sm.bonus[16 * W], o.tab - 64 * (b & 3));   // o.tab holds c0
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int tl = 4 * lq + rr;
@@ -1859,15 +1860,15 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float sc
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
             tmp = mfma32(row8o(&sm.Dt[0][0], o, TW, 32 * ks), row8o(&sm.Sin[0][0], o, c0, 32 * ks), tmp);
-        ar = tmp * lds_ld<float>(&sm.emu[W][c0], o.tab);
+        ar = tmp * lds_ld<float>(&sm.emu[W][0], o.tab);
     }
     constexpr int bW = (W * (W + 1)) / 2;
 #pragma unroll
     for (int J = 0; J < W; ++J) {
-        const f32x4 t2 = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + J][0][0], o.blk), ch4o(KTp, o, c0, 16 * J), f32x4{});
-        ar += (t2 * lds_ld<float>(&sm.kb[J][c0], o.tab)) * lds_ld<float>(&sm.fp[(W * (W - 1)) / 2 + J][c0], o.tab);
+        const f32x4 t2 = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + J][0][0], o.blk), ch4o(KTp, o, 0, 16 * J), f32x4{});
+        ar += (t2 * lds_ld<float>(&sm.kb[J][0], o.tab)) * lds_ld<float>(&sm.fp[(W * (W - 1)) / 2 + J][0], o.tab);
     }
-    ar = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + W][0][0], o.blk), ch4o(KTp, o, c0, TW), ar);
+    ar = mfma16(lds_ld<bf16x4>(&sm.dAb[bW + W][0][0], o.blk), ch4o(KTp, o, 0, TW), ar);
     float xr[4];
     {
         float d[4];
@@ -1886,18 +1887,18 @@ __device__ __forceinline__ void loop_products_rk(LoopSmem& sm, int col, float sc
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
             tmp = mfma32(row8o(&sm.Vt[0][0], o, TW, 32 * ks), row8o(&sm.dS[0][0], o, c0, 32 * ks), tmp);
-        ak = tmp * lds_ld<float>(&sm.eg[W][c0], o.tab);
+        ak = tmp * lds_ld<float>(&sm.eg[W][0], o.tab);
         float pk = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) pk += (float)g.kmb[0][rr] * ak[rr];
         const RowSums rs = row_sums(pk);                  // the column's sum over the 4 rows
-        if (o.q16 == 0) lds_st<float>(&sm.Pk[W][c0], o.tab, rs.lo + rs.hi);
+        if (o.q16 == 0) lds_st<float>(&sm.Pk[W][0], o.tab, rs.lo + rs.hi);
     }
-    ak2 = mfma16(lds_tr(&sm.dAb[bW + W][0][0], o.blktr), ch4o(RTp, o, c0, TW), f32x4{});
+    ak2 = mfma16(lds_tr(&sm.dAb[bW + W][0][0], o.blktr), ch4o(RTp, o, 0, TW), f32x4{});
 #pragma unroll
     for (int I = W + 1; I < 4; ++I) {
-        const f32x4 t2 = mfma16(lds_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], o.blktr), ch4o(RTp, o, c0, 16 * I), f32x4{});
-        ak2 += (t2 * lds_ld<float>(&sm.fp[(I * (I - 1)) / 2 + W][c0], o.tab)) * lds_ld<float>(&sm.kb[W][c0], o.tab);
+        const f32x4 t2 = mfma16(lds_tr(&sm.dAb[(I * (I + 1)) / 2 + W][0][0], o.blktr), ch4o(RTp, o, 0, 16 * I), f32x4{});
+        ak2 += (t2 * lds_ld<float>(&sm.fp[(I * (I - 1)) / 2 + W][0], o.tab)) * lds_ld<float>(&sm.kb[W][0], o.tab);
     }
     {
         float d[4], xv[4];
@@ -2077,7 +2078,7 @@ __device__ __forceinline__ void bwd_loop_walk(
             unpack4(x.r, rf);
             unpack4(x.k, kf);
             {
-                const float4 uu = lds_ld<float4>(&sm.uh[0], 4 * o.tab);   // u[4 L .. 4 L + 3]
+                const float4 uu = lds_ld<float4>(&sm.uh[0], 4 * (o.tab - 4 * c0));   // u[4 L .. 4 L + 3]
                 ub[0] = uu.x; ub[1] = uu.y; ub[2] = uu.z; ub[3] = uu.w;
             }
             float b = (rf[0] * ub[0]) * kf[0];
@@ -2090,7 +2091,7 @@ __device__ __forceinline__ void bwd_loop_walk(
                 sm.dd[row] = e;
             }
             const float d4[4] = {Dst[0], Dst[1], Dst[2], Dst[3]};
-            st_ch4o(&sm.dS[0][0], o, c0, t4 - 4 * lq, d4);
+            st_ch4o(&sm.dS[0][0], o, 0, t4 - 4 * lq, d4);
         }
         // the next chunk's loads (past chunk 0 they reload chunk 0) go out in S2, S3 and S4,
         // the stores of the chunk before in S4
@@ -2124,8 +2125,8 @@ __device__ __forceinline__ void bwd_loop_walk(
             m7 = rs.lo;                                         // G at token 16W+7
             qloc = tot - m7;                                    // b_W - mu_W
             if (lq == 0) {
-                lds_st<float>(&sm.red[W][c0], o.tab, tot);
-                lds_st<float>(&sm.red[4 + W][c0], o.tab, m7);
+                lds_st<float>(&sm.red[W][0], o.tab, tot);
+                lds_st<float>(&sm.red[4 + W][0], o.tab, m7);
             }
             float rm[4], km[4];
 #pragma unroll
@@ -2150,12 +2151,12 @@ __device__ __forceinline__ void bwd_loop_walk(
         // ---- S3: operand tiles (channel-major), the state-gradient operand, the tables ----
         loop_issue<SEQ, 1>(pf, r, k, v, w, dO, Hs, bh, cn, B, H, T, NT, tid, go_);
         {
-            lds_st<bf16x4>(&sm.RT[0][0], o.ch + tb(c0, TW), gl.rmb[0]);
-            lds_st<bf16x4>(&sm.KT[0][0], o.ch + tb(c0, TW), gl.kmb[0]);
+            lds_st<bf16x4>(&sm.RT[0][0], o.ch + tb(0, TW), gl.rmb[0]);
+            lds_st<bf16x4>(&sm.KT[0][0], o.ch + tb(0, TW), gl.kmb[0]);
             float after = 0.f, before = 0.f, tJs[4];            // G_63 - b_W, b_{W-1}
 #pragma unroll
             for (int J = 0; J < 4; ++J) {
-                tJs[J] = lds_ld<float>(&sm.red[J][c0], o.tab);
+                tJs[J] = lds_ld<float>(&sm.red[J][0], o.tab);
                 if (J > W) after += tJs[J];
                 if (J < W) before += tJs[J];
             }
@@ -2163,15 +2164,15 @@ __device__ __forceinline__ void bwd_loop_walk(
             float x[4];
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * eg;
-            st_ch4o(&sm.KtT[0][0], o, c0, TW, x);
+            st_ch4o(&sm.KtT[0][0], o, 0, TW, x);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = kmf[rr] * kq;
-            st_ch4o(&sm.KqT[0][0], o, c0, TW, x);
+            st_ch4o(&sm.KqT[0][0], o, 0, TW, x);
             // s r e^{G_{t-1}} = s r Fm e^{mu_W}, mu_W = b_{W-1} + (G at 16W+7 within the block)
             const float emw = scale * ex2(before + m7);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) x[rr] = (float)gl.rrw[0][rr] * (gl.Fm[0][rr] * emw);
-            st_ch4o(&sm.RiT[0][0], o, c0, TW, x);
+            st_ch4o(&sm.RiT[0][0], o, 0, TW, x);
             // the pair tiles of the block as the later one: s Rm_W p_WJ, p_WJ = e^{mu_W - b_J}
             float bJ = 0.f;
 #pragma unroll
@@ -2182,7 +2183,7 @@ __device__ __forceinline__ void bwd_loop_walk(
                 for (int rr = 0; rr < 4; ++rr) x[rr] = rmf[rr] * pfac;
                 constexpr int pbase = (W * (W - 1)) / 2;
                 const int pi = pbase + J;
-                st_ch4o(&sm.RpT[pi >> 2][0][0], o, c0, 16 * (pi & 3), x);
+                st_ch4o(&sm.RpT[pi >> 2][0][0], o, 0, 16 * (pi & 3), x);
             }
         }
         {
@@ -2230,12 +2231,12 @@ __device__ __forceinline__ void bwd_loop_walk(
         GradOut go;
         loop_products_rk<SEQ, W>(sm, col, scale, gl, go, o);
         {
-            const float e = lds_ld<float>(&sm.eG63[c0], o.tab);
+            const float e = lds_ld<float>(&sm.eG63[0], o.tab);
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) Dst[rr] *= e;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks)
-                Dst = mfma32(tr8o(&sm.Dt[0][0], o, 32 * ks, TW), dir8o(&sm.RiT[0][0], o, c0, 32 * ks), Dst);
+                Dst = mfma32(tr8o(&sm.Dt[0][0], o, 32 * ks, TW), dir8o(&sm.RiT[0][0], o, 0, 32 * ks), Dst);
         }
         du_acc += go.dup[0];
         __syncthreads();                   // A blocks in
@@ -2247,17 +2248,17 @@ __device__ __forceinline__ void bwd_loop_walk(
             const RowSums rs = row_sums(lt);                    // sum over lq' >= lq:
             const float vsum = ((lq & 1) ? lt : rs.pair) + (lq < 2 ? rs.hi : 0.f);
             later = vsum - lt;
-            if (lq == 0) lds_st<float>(&sm.red[W][c0], o.tab, vsum);   // the wave's total
+            if (lq == 0) lds_st<float>(&sm.red[W][0], o.tab, vsum);   // the wave's total
         }
         __syncthreads();                   // all products done; red, Pk in
 
         // ---- S5: dw; dr, dk, dv, dw staged channel-major (stored during the next step) ----
         {
-            later += lds_ld<float>(&sm.Dv[c0], o.tab) +
-                     ((lds_ld<float>(&sm.Pk[0][c0], o.tab) + lds_ld<float>(&sm.Pk[1][c0], o.tab)) +
-                      (lds_ld<float>(&sm.Pk[2][c0], o.tab) + lds_ld<float>(&sm.Pk[3][c0], o.tab)));
+            later += lds_ld<float>(&sm.Dv[0], o.tab) +
+                     ((lds_ld<float>(&sm.Pk[0][0], o.tab) + lds_ld<float>(&sm.Pk[1][0], o.tab)) +
+                      (lds_ld<float>(&sm.Pk[2][0], o.tab) + lds_ld<float>(&sm.Pk[3][0], o.tab)));
 #pragma unroll
-            for (int W2 = W + 1; W2 < 4; ++W2) later += lds_ld<float>(&sm.red[W2][c0], o.tab);
+            for (int W2 = W + 1; W2 < 4; ++W2) later += lds_ld<float>(&sm.red[W2][0], o.tab);
             float g[4];
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
@@ -2269,11 +2270,11 @@ __device__ __forceinline__ void bwd_loop_walk(
                 }
                 if (!SEQ && go.fl[rr]) g[rr] = 0.f;
             }
-            lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(c0, TW), go.drb[0]);
-            lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(c0, TW), go.dkb[0]);
+            lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(0, TW), go.drb[0]);
+            lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(0, TW), go.dkb[0]);
             const float avf[4] = {go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]};
-            st_ch4o(&sm.Out[2][0][0], o, c0, TW, avf);
-            st_ch4o(&sm.Out[3][0][0], o, c0, TW, g);
+            st_ch4o(&sm.Out[2][0][0], o, 0, TW, avf);
+            st_ch4o(&sm.Out[3][0][0], o, 0, TW, g);
         }
         // no barrier here: the next step's S1 touches nothing S5 reads or writes, and its B1
         // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
@@ -2307,7 +2308,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
     const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
     const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
-    LaneOfs o = lane_ofs(threadIdx.x & 63);
+    LaneOfs o = lane_ofs(threadIdx.x & 63, 16 * ((threadIdx.x >> 6) & 3));
     GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
 
     LoopPrefetch pf;
