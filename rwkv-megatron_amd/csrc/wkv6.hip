@@ -1714,7 +1714,8 @@ __device__ __forceinline__ void tri_pair(int b, int& hi, int& lo) {
 // out of the walk, they do not fit the registers.
 struct LaneOfs {
     int tr;      // ((4q + L/4) TS + 4 (L%4)) * 2: ds_read_b64_tr_b16 over rows r0 + 4q + s
-    int g8;      // ((8q + L/4) TS + 4 (L%4)) * 2: the same over rows r0 + 8q + s
+    int g8;      // ((8q + L/4) TS + 4 (L%4) + c0) * 2: the same over rows r0 + 8q + s, in the
+                 // wave's column c0 (its only use)
     int row;     // (L TS + 8q) * 2: 16-byte row pieces (row L, columns 8q..)
     int ch;      // ((c0 + L) TS + 4q) * 2: 8-byte row pieces (row c0 + L, columns 4q..), c0 =
                  // the wave's channel column 16 col: every use is in the wave's own rows
@@ -1722,21 +1723,22 @@ struct LaneOfs {
     int blktr;   // ((4q + L/4) DAB_RS + 4 (L%4)) * 2: the same, transposed
     int frag;    // 8 lane: 8 bytes per lane in MFMA-operand order
     int tab;     // 4 (c0 + L): a float per channel of the wave's 16-channel column
-    int th;      // (q TS + 4 L) * 2: thread (row, c4) of a wave's four rows
+    int th;      // ((4 wv + q) TS + 4 L) * 2: thread (row, c4) = (tid >> 4, 4 (tid & 15))
     int q16;     // 16 q: four floats per lane row
 };
-__device__ __forceinline__ LaneOfs lane_ofs(int lane, int c0) {
+__device__ __forceinline__ LaneOfs lane_ofs(int lane, int wv) {
+    const int c0 = 16 * (wv & 3);
     const int L = lane & 15, q = lane >> 4;
     LaneOfs o;
     o.tr = ((4 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
-    o.g8 = ((8 * q + (L >> 2)) * TS + 4 * (L & 3)) * 2;
+    o.g8 = ((8 * q + (L >> 2)) * TS + 4 * (L & 3) + c0) * 2;
     o.row = (L * TS + 8 * q) * 2;
     o.ch = ((c0 + L) * TS + 4 * q) * 2;
     o.blk = (DAB_RS * L + 4 * q) * 2;
     o.blktr = ((4 * q + (L >> 2)) * DAB_RS + 4 * (L & 3)) * 2;
     o.frag = 8 * lane;
     o.tab = 4 * (c0 + L);
-    o.th = (q * TS + 4 * L) * 2;
+    o.th = ((4 * wv + q) * TS + 4 * L) * 2;
     o.q16 = 16 * q;
     return o;
 }
@@ -2019,8 +2021,8 @@ __device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restr
     const int tk = 16 * col + (lane & 15);
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     uint16_t* dst = (N == 0 ? dr : N == 1 ? dk : N == 2 ? dv : dw) + tok_base<SEQ>(bh, t0, B, H, T);
-    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 0, 16 * col));
-    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 32, 16 * col));
+    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 0, 0));   // o.g8 holds c0
+    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 32, 0));
     if (tk < nvalid) {
         char* p = reinterpret_cast<char*>(dst) + (unsigned)g.st;
         *reinterpret_cast<uint4*>(p) = x0;
@@ -2058,8 +2060,8 @@ __device__ __forceinline__ void bwd_loop_walk(
         const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int col = wv & 3, lr = lane & 15, lq = lane >> 4;
         const int c0 = 16 * col, t4 = TW + 4 * lq;
-        const int row = tid >> 4;                           // the thread's raw pieces: row,
-        const int tw = 4 * TS * 2 * wv;                     // at byte tw + o.th of a tile
+        const int row = tid >> 4;                           // the thread's raw pieces: row
+                                                            // (at byte o.th of a tile)
         const int t0 = c * CL, nvalid = min(CL, T - t0);
         // ---- S1: the raw pieces into LDS, the bonus, dd, dS_out(c) as a bf16 tile ----
         {
@@ -2068,12 +2070,12 @@ __device__ __forceinline__ void bwd_loop_walk(
                 const uint2 z = make_uint2(0u, 0u);
                 x.r = x.k = x.v = x.w = x.d = z;
             }
-            lds_st<uint2>(&sm.Vt[0][0], tw + o.th, x.v);
-            lds_st<uint2>(&sm.Dt[0][0], tw + o.th, x.d);
-            lds_st<uint2>(&sm.RT[0][0], tw + o.th, x.r);
-            lds_st<uint2>(&sm.KT[0][0], tw + o.th, x.k);
-            lds_st<uint2>(&sm.KtT[0][0], tw + o.th, x.w);          // w scratch
-            lds_st<uint2>(&sm.Sin[0][0], tw + o.th, x.s);
+            lds_st<uint2>(&sm.Vt[0][0], o.th, x.v);
+            lds_st<uint2>(&sm.Dt[0][0], o.th, x.d);
+            lds_st<uint2>(&sm.RT[0][0], o.th, x.r);
+            lds_st<uint2>(&sm.KT[0][0], o.th, x.k);
+            lds_st<uint2>(&sm.KtT[0][0], o.th, x.w);          // w scratch
+            lds_st<uint2>(&sm.Sin[0][0], o.th, x.s);
             float rf[4], kf[4], ub[4];
             unpack4(x.r, rf);
             unpack4(x.k, kf);
@@ -2142,8 +2144,8 @@ __device__ __forceinline__ void bwd_loop_walk(
             gl.kmb[0] = cvt4(km[0], km[1], km[2], km[3]);
         }
         {   // Dv[i] = sum_j S_in[i][j] dS[i][j], i = row
-            const float x = sum16lanes(dot4_bf16(lds_ld<uint2>(&sm.Sin[0][0], tw + o.th),
-                                                 lds_ld<uint2>(&sm.dS[0][0], tw + o.th)));
+            const float x = sum16lanes(dot4_bf16(lds_ld<uint2>(&sm.Sin[0][0], o.th),
+                                                 lds_ld<uint2>(&sm.dS[0][0], o.th)));
             if (lr == 0) sm.Dv[row] = x;
         }
         __syncthreads();                   // raw r, k, w read; block totals and mu in `red`
@@ -2308,7 +2310,7 @@ wkv6_bwd_loop(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     // the lane's channel ch0 = 16 col + lr and first token t40 = 16 W + 4 lq
     const int ch0 = 16 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 15);
     const int t40 = 16 * (threadIdx.x >> 8) + 4 * ((threadIdx.x >> 4) & 3);
-    LaneOfs o = lane_ofs(threadIdx.x & 63, 16 * ((threadIdx.x >> 6) & 3));
+    LaneOfs o = lane_ofs(threadIdx.x & 63, threadIdx.x >> 6);
     GlobOfs go_ = glob_ofs<SEQ>(threadIdx.x, B, H);
 
     LoopPrefetch pf;
