@@ -295,10 +295,11 @@ static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
 // build_G for the output walk (512 threads, part = 8-token run): also fills the per-channel
 // tables, all from the part-end values ge[p] = G[8p + 7] (mu_I = ge[2I], b_{I-1} =
 // ge[2I - 1], G_63 = ge[7]).  `part` is wave-uniform, so the table branches are scalar.
-template <bool DEC>
+template <bool DEC, int PB>
 __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar) {
+    // the wave's 8-token part is 2 PB + hh (PB the wave pair, compile-time; hh wave-uniform)
     float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G + GSG);
-    const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+    const int i = threadIdx.x & 63, hh = (threadIdx.x >> 6) & 1, part = 2 * PB + hh;
     float loc[8];
     float run = 0.f;
 #pragma unroll
@@ -315,31 +316,37 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
     }
     sm.tot[part * 64 + i] = run;
     __syncthreads();
-    float ge[8], a = 0.f, off = 0.f;
+    float ge[8], a = 0.f;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
         a += sm.tot[p * 64 + i];
         ge[p] = a;
-        off = p < part ? a : off;
     }
+    // G before the part: the sum of parts 0 .. part-1
+    const float off = hh ? ge[2 * PB] : (PB > 0 ? ge[2 * PB - 1] : 0.f);
 #pragma unroll
     for (int s = 0; s < 8; ++s) Gm[8 * part + s][i] = loc[s] + off;
-    if (part < 4) {
-        const float mu = part == 0 ? ge[0] : part == 1 ? ge[2] : part == 2 ? ge[4] : ge[6];
+    if constexpr (PB < 2) {
+        // parts 0..3: emu, c3 of block `part`, and the c6 pairs (1,0), (2,0), (2,1), (3,0)
+        const float mu = hh ? ge[4 * PB + 2] : ge[4 * PB];
         sm.emu[part][i] = ex2(mu);
         sm.c3[part][i] = ex2(ge[7] - mu);
-        // c6 pairs (1,0), (2,0), (2,1), (3,0)
-        const float b = part == 0 ? ge[1] : part == 1 ? ge[3] : part == 2 ? ge[3] : ge[5];
-        const float mj = part == 0 ? ge[0] : part == 1 ? ge[0] : part == 2 ? ge[2] : ge[0];
+        const float b = PB == 0 ? (hh ? ge[3] : ge[1]) : (hh ? ge[5] : ge[3]);
+        const float mj = PB == 0 ? ge[0] : (hh ? ge[0] : ge[2]);
         sm.c6[part][i] = ex2(b - mj);
-    } else if (part < 7) {
-        const int I = part - 3;                                  // 1..3
-        const float mu = I == 1 ? ge[2] : I == 2 ? ge[4] : ge[6];
-        const float bp = I == 1 ? ge[1] : I == 2 ? ge[3] : ge[5];
-        sm.c1[I][i] = ex2(mu - bp);
-        if (part < 6) sm.c6[part][i] = ex2(ge[5] - (part == 4 ? ge[2] : ge[4]));   // (3,1), (3,2)
+    } else if constexpr (PB == 2) {
+        // parts 4, 5: c1 of blocks I = 1, 2 and the c6 pairs (3,1), (3,2)
+        const float mu = hh ? ge[4] : ge[2];
+        const float bp = hh ? ge[3] : ge[1];
+        sm.c1[1 + hh][i] = ex2(mu - bp);
+        sm.c6[part][i] = ex2(ge[5] - (hh ? ge[4] : ge[2]));
     } else {
-        sm.dec[cpar][i] = ex2(ge[7]);
+        // part 6: c1 of block 3; part 7: the chunk decay
+        if (hh == 0) {
+            sm.c1[3][i] = ex2(ge[6] - ge[5]);
+        } else {
+            sm.dec[cpar][i] = ex2(ge[7]);
+        }
     }
     __syncthreads();
 }
@@ -493,7 +500,7 @@ __device__ __forceinline__ void fwd_walk_chunks(
         walk_issue<SEQ, true>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
         __syncthreads();
         {
-            walk_build_G<SEQ>(sm, nvalid, c & 1);
+            walk_build_G<SEQ, PB>(sm, nvalid, c & 1);
             // Operand tiles of this thread's piece (token t = row in block I; I is
             // wave-uniform).  Two exponentials per element; every other factor is a
             // per-(block, channel) table entry <= 1 applied to the fp32 value:
