@@ -30,6 +30,9 @@
 #define LORA_THR 256      // 4 waves, each 16 tokens x 64 channels at a time
 #define LORA_TT 128       // tokens per block (64-token groups walked in turn)
 #define LORA_NE 5
+#ifndef LORA_BWD_AHEAD
+#define LORA_BWD_AHEAD 2
+#endif
 
 namespace {
 
@@ -206,13 +209,21 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
 // Backward of the token-shift LoRA's up-projection + ddlerp (E = 5), per token:
 //   d_mexp_e = d_mixed_e * delta;  dd = sum_e d_mixed_e (m_e + bias_e);  ds = sum_e d_mixed_e
 // and the d_bias partial of this block's tokens: part[blockIdx.x][e][C].
-// Wave wv takes the channel half h = wv & 1 (32 channels) of the 16 tokens 16 (wv >> 1) + L
-// of each 32-token group; a lane holds the one 16-byte run c0 + 32h + 8q + (0..7), so a load
-// instruction still covers 64 contiguous bytes of 16 token rows, and eight values per lane
-// (instead of sixteen) hold the registers to three waves per SIMD (a four-wave cap spills;
-// issuing all five mixes' loads at once, at half the waves, was no faster).
-// KS = R / 32 (1 or 2; the launch picks it): a compile-time count, because a loop with a
-// load inside makes the compiler wait for every outstanding load and store where it merges.
+// Wave wv takes the 32 tokens 32 wv + (0..31) of the block, 16 at a time (pass P), all 64
+// channels.  m comes out of the MFMA one token per lane column (lane (q, L): channel runs
+// 8q + (0..7) and 32 + 8q + (0..7) of token L) and goes through a wave-private LDS tile to
+// the row layout every global access uses: lane (rw, cg) = (lane >> 3, lane & 7) holds
+// channels 8 cg + (0..7) of tokens rw and rw + 8, so a load or store instruction covers
+// 128 contiguous bytes of 8 token rows.  (An instruction spanning 16 rows at 64 bytes each
+// streams ~1.35x slower on MI355X, measured with the same loads and stores and no
+// arithmetic: 276 against 201 us at N = 16384, C = 2048.)
+// The wave's ten stages s = 5 P + e (pass P, mix e) are one straight run; each stage issues
+// the loads of stage s + LORA_BWD_AHEAD before its own stores (the vector-memory counter
+// retires loads and stores in issue order).  No load or store sits under a branch: a token
+// past the end works on the last token and stores its values again (same values, same
+// place), and only its d_bias contribution is masked.
+// KS = R / 32 (1 or 2; the launch picks it).
+#define LORA_MT_RS 68                  // row stride (floats) of the wave's m tile
 template <int KS>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
@@ -221,133 +232,179 @@ rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* 
                              uint16_t* __restrict__ dmexp, uint16_t* __restrict__ dd_out,
                              uint16_t* __restrict__ ds_out, float* __restrict__ part, int64_t N,
                              int64_t B, int64_t C, int R, int64_t per) {
-    __shared__ float red[LORA_NE][2][64];          // [mix][token half of a group][channel]
+    __shared__ __attribute__((aligned(16))) float mt[4][16 * LORA_MT_RS];   // per wave: m [token][channel]
+    __shared__ float red[LORA_NE][4][64];          // [mix][wave][channel]
     __shared__ __attribute__((aligned(16))) float bsm[LORA_NE][64];   // bias of the block's channels
     int64_t tb, cb;
     if (!lora_tile((N + LORA_TT - 1) / LORA_TT, C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
-    const int h = wv & 1, tw = wv >> 1, cw = 32 * h + 8 * q;   // cw: first channel (rel. c0)
-    const int64_t cl = cb * 64 + cw;
+    const int rw = lane >> 3, cg = lane & 7;
+    const int64_t c0 = cb * 64, cl = c0 + 8 * cg;
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
-    lora_stage(lora_sm, wut, LORA_NE, C, R, cb * 64);
-    for (int j = threadIdx.x; j < LORA_NE * 2 * 64; j += LORA_THR) (&red[0][0][0])[j] = 0.f;
+    lora_stage(lora_sm, wut, LORA_NE, C, R, c0);
     if (threadIdx.x < LORA_NE * 8) {
         const int e = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
         float bb[8];
-        load_param8(bias, pdt, (int64_t)e * C + cb * 64 + c8, bb);
+        load_param8(bias, pdt, (int64_t)e * C + c0 + c8, bb);
 #pragma unroll
         for (int j = 0; j < 8; ++j) bsm[e][c8 + j] = bb[j];
     }
-    __syncthreads();
-    // Loads are unconditional (a token past the end reads the last token; its d_mixed is
-    // multiplied by 0 for the d_bias sums and nothing of it is stored): a load under a branch
-    // makes the merge wait for every outstanding load.
-    // two 32-token groups at a time (tokens g and g + 32 of this lane): four 16-byte loads
-    // in flight per mix, and one d_bias butterfly over their sum
-    for (int g = 0; g < LORA_TT / 32; g += 2) {
-        int64_t tok[2], tc[2];
-        bool tv[2];
-        float keep[2], dl[2][8], dd[2][8], ds[2][8];
-        const uint16_t* nrow[2];
+    static_assert(LORA_TT == 128, "four waves of 32 tokens per block");
+    // pass P: the MFMA column token (L) and the lane's two row tokens (rw, rw + 8), clamped
+    int64_t tm[2], tr[2][2];
+    float keep[2][2];
 #pragma unroll
-        for (int P = 0; P < 2; ++P) {
-            tok[P] = tb * LORA_TT + 32 * (g + P) + 16 * tw + L;
-            tv[P] = tok[P] < N;
-            tc[P] = tv[P] ? tok[P] : N - 1;
-            keep[P] = tv[P] ? 1.f : 0.f;
-            nrow[P] = neck + tc[P] * LORA_NE * R;
-            const float keep_p = tc[P] >= B ? 1.f : 0.f;
-            float xv[8];
-            load8(x + tc[P] * C + cl, xv);
-            load8(x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + cl, dl[P]);
+    for (int P = 0; P < 2; ++P) {
+        const int64_t t0 = tb * LORA_TT + 32 * wv + 16 * P;
+        tm[P] = t0 + L < N ? t0 + L : N - 1;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                dl[P][j] = dl[P][j] * keep_p - xv[j];
-                dd[P][j] = ds[P][j] = 0.f;
-            }
+        for (int k = 0; k < 2; ++k) {
+            const int64_t t = t0 + rw + 8 * k;
+            tr[P][k] = t < N ? t : N - 1;
+            keep[P][k] = t < N ? 1.f : 0.f;
         }
-#pragma unroll 1
-        for (int e = 0; e < LORA_NE; ++e) {
-            // this mix's neck pieces and d_mixed of both tokens, issued together
-            uint4 nk_e[2], dq_e[2];
+    }
+    // stage loads: the neck piece (MFMA layout) and d_mixed (row layout), LORA_BWD_AHEAD
+    // stages ahead in a ring; x and x[t-B] of a pass (packed) with its first stage's loads
+    uint4 xr[2], pr[2], nkb[LORA_BWD_AHEAD][KS], dqb[LORA_BWD_AHEAD][2];
+    auto load_x = [&](int P) {
 #pragma unroll
-            for (int P = 0; P < 2; ++P) {
-                nk_e[P] = *reinterpret_cast<const uint4*>(nrow[P] + e * R + 8 * q);
-                dq_e[P] = *reinterpret_cast<const uint4*>(dmix.p[e] + tc[P] * C + cl);
+        for (int k = 0; k < 2; ++k) {
+            const int64_t t = tr[P][k];
+            xr[k] = *reinterpret_cast<const uint4*>(x + t * C + cl);
+            pr[k] = *reinterpret_cast<const uint4*>(x + (t >= B ? t - B : t) * C + cl);
+        }
+    };
+    auto load_stage = [&](int st) {
+        const int P = st / LORA_NE, e = st - P * LORA_NE;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            nkb[st % LORA_BWD_AHEAD][ks] =
+                *reinterpret_cast<const uint4*>(neck + tm[P] * LORA_NE * R + e * R + 32 * ks + 8 * q);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            dqb[st % LORA_BWD_AHEAD][k] = *reinterpret_cast<const uint4*>(dmix.p[e] + tr[P][k] * C + cl);
+    };
+    load_x(0);
+#pragma unroll
+    for (int st = 0; st < LORA_BWD_AHEAD; ++st) load_stage(st);
+    __syncthreads();
+    const int rs = lds_rs(R);
+    float* mtw = mt[wv];
+    float bsum[LORA_NE];                           // d_bias of channel 8 cg + 4 b3 + 2 b4 + b5
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+        const uint4 xc[2] = {xr[0], xr[1]}, pc[2] = {pr[0], pr[1]};
+        float dd[2][8], ds[2][8];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dd[k][j] = ds[k][j] = 0.f;
+#pragma unroll
+        for (int e = 0; e < LORA_NE; ++e) {
+            const int st = LORA_NE * P + e;
+            const uint16_t* swe = lora_sm + e * 64 * rs;
+            // m = neck_e W_up_e, 16 tokens x 64 channels, to the wave's tile
+            f32x4 acc[4] = {};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const bf16x8 bq = __builtin_bit_cast(bf16x8, nkb[st % LORA_BWD_AHEAD][ks]);
+#pragma unroll
+                for (int tcn = 0; tcn < 4; ++tcn)
+                    acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 32 * ks + 8 * q), bq,
+                                      acc[tcn]);
             }
-            const int rs = lds_rs(R);
-            const uint16_t* swe = lora_sm + (e * 64 + 32 * h) * rs;
-            const float4 b0 = *reinterpret_cast<const float4*>(&bsm[e][cw]);
-            const float4 b1 = *reinterpret_cast<const float4*>(&bsm[e][cw + 4]);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float* d = mtw + L * LORA_MT_RS + 32 * hh + 8 * q;
+                *reinterpret_cast<float4*>(d) = make_float4(acc[2 * hh][0], acc[2 * hh][1], acc[2 * hh][2], acc[2 * hh][3]);
+                *reinterpret_cast<float4*>(d + 4) =
+                    make_float4(acc[2 * hh + 1][0], acc[2 * hh + 1][1], acc[2 * hh + 1][2], acc[2 * hh + 1][3]);
+            }
+            // the wave's own LDS writes and reads run in issue order; the compiler must not
+            // move the reads above the writes
+            asm volatile("" ::: "memory");
+            float m[2][8];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const float* sp = mtw + (rw + 8 * k) * LORA_MT_RS + 8 * cg;
+                const float4 m0 = *reinterpret_cast<const float4*>(sp);
+                const float4 m1 = *reinterpret_cast<const float4*>(sp + 4);
+                m[k][0] = m0.x; m[k][1] = m0.y; m[k][2] = m0.z; m[k][3] = m0.w;
+                m[k][4] = m1.x; m[k][5] = m1.y; m[k][6] = m1.z; m[k][7] = m1.w;
+            }
+            asm volatile("" ::: "memory");
+            float v[2][8];
+            unpack8(dqb[st % LORA_BWD_AHEAD][0], v[0]);
+            unpack8(dqb[st % LORA_BWD_AHEAD][1], v[1]);
+            // later stages' loads go out before this stage's stores (the scheduling barriers
+            // keep them here: hoisted to the top, the ten stages' loads would hold far more
+            // registers)
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + LORA_BWD_AHEAD < 2 * LORA_NE) {
+                if (st + LORA_BWD_AHEAD == LORA_NE) load_x(1);
+                load_stage(st + LORA_BWD_AHEAD);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const float4 b0 = *reinterpret_cast<const float4*>(&bsm[e][8 * cg]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&bsm[e][8 * cg + 4]);
             const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
             float vs[8];
 #pragma unroll
-            for (int P = 0; P < 2; ++P) {
-                float m[8], v[8];
-                {
-                    // m = neck_e W_up_e at the lane's 8 channels (ranks 0..31 from nk_e)
-                    f32x4 acc[2] = {};
-#pragma unroll
-                    for (int tcn = 0; tcn < 2; ++tcn)
-                        acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 8 * q),
-                                          __builtin_bit_cast(bf16x8, nk_e[P]), acc[tcn]);
-#pragma unroll
-                    for (int ks = 1; ks < KS; ++ks) {
-                        const int r0 = 32 * ks + 8 * q;
-                        const bf16x8 bq = ld_bf16x8(nrow[P] + e * R + r0);
-#pragma unroll
-                        for (int tcn = 0; tcn < 2; ++tcn)
-                            acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + r0), bq, acc[tcn]);
-                    }
-#pragma unroll
-                    for (int tcn = 0; tcn < 2; ++tcn)
-#pragma unroll
-                        for (int rr = 0; rr < 4; ++rr) m[4 * tcn + rr] = acc[tcn][rr];
-                }
-                unpack8(dq_e[P], v);
+            for (int k = 0; k < 2; ++k) {
+                float xv[8], dl[8];
+                unpack8(xc[k], xv);
+                unpack8(pc[k], dl);
+                const float keep_p = tr[P][k] >= B ? 1.f : 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    v[j] *= keep[P];
-                    dd[P][j] += v[j] * (m[j] + bb[j]);
-                    ds[P][j] += v[j];
-                    v[j] *= dl[P][j];                               // d_mexp
-                    vs[j] = P == 0 ? v[j] : vs[j] + v[j];
+                    dl[j] = dl[j] * keep_p - xv[j];
+                    dd[k][j] += v[k][j] * (m[k][j] + bb[j]);
+                    ds[k][j] += v[k][j];
+                    v[k][j] *= dl[j];                               // d_mexp
+                    vs[j] = k == 0 ? keep[P][0] * v[0][j] : vs[j] + keep[P][1] * v[1][j];
                 }
-                if (tv[P]) store8(dmexp + ((int64_t)e * N + tok[P]) * C + cl, v);
+                store8(dmexp + ((int64_t)e * N + tr[P][k]) * C + cl, v[k]);
             }
-            // d_bias: sum over the wave's 2 x 16 tokens (lanes L of one q).  Transposing
-            // butterfly: at each step a lane keeps one half of its values, adds its partner's
-            // copy of that half and hands over the other half; after 4 + 2 + 1 exchanges and a
-            // last pairwise sum, lanes L and L^1 hold the sum of value j = L >> 1 (fixed order).
+            // d_bias: sum over the wave's 16 tokens (lane bits 3-5).  Transposing butterfly:
+            // each step keeps one half of a lane's values and adds the partner's copy of that
+            // half; row_ror:8 for bit 3, then the row swaps for bits 4 and 5, whose two
+            // results sum to the even row's (half's) A value plus the odd one's in the even
+            // lanes and to the B values in the odd ones.  Lane (rw, cg) ends with channel
+            // 8 cg + 4 b3 + 2 b4 + b5, in a fixed order.
             {
-                const bool up = L & 8;
+                const bool up = lane & 8;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) vs[i] = (up ? vs[i + 4] : vs[i]) + lane_xor8(up ? vs[i] : vs[i + 4]);
             }
-            {
-                const bool up = L & 4;
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    vs[i] = (up ? vs[i + 2] : vs[i]) + lane_xor_swz<4>(up ? vs[i] : vs[i + 2]);
+            for (int i = 0; i < 2; ++i) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(vs[i]), __float_as_uint(vs[i + 2]),
+                                                                false, false);
+                vs[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
             }
             {
-                const bool up = L & 2;
-                vs[0] = (up ? vs[1] : vs[0]) + lane_xor2(up ? vs[0] : vs[1]);
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(vs[0]), __float_as_uint(vs[1]),
+                                                                false, false);
+                vs[0] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
             }
-            vs[0] += lane_xor1(vs[0]);
-            if ((L & 1) == 0) red[e][tw][cw + (L >> 1)] += vs[0];
+            bsum[e] = P == 0 ? vs[0] : bsum[e] + vs[0];
         }
 #pragma unroll
-        for (int P = 0; P < 2; ++P)
-            if (tv[P]) {
-                store8(dd_out + tok[P] * C + cl, dd[P]);
-                store8(ds_out + tok[P] * C + cl, ds[P]);
-            }
+        for (int k = 0; k < 2; ++k) {
+            store8(dd_out + tr[P][k] * C + cl, dd[k]);
+            store8(ds_out + tr[P][k] * C + cl, ds[k]);
+        }
+    }
+    {
+        const int ch = 8 * cg + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
+#pragma unroll
+        for (int e = 0; e < LORA_NE; ++e) red[e][wv][ch] = bsum[e];
     }
     __syncthreads();
     for (int j = threadIdx.x; j < LORA_NE * 64; j += LORA_THR) {
         const int e = j >> 6, c = j & 63;
-        part[(tb * LORA_NE + e) * C + cb * 64 + c] = red[e][0][c] + red[e][1][c];
+        part[(tb * LORA_NE + e) * C + c0 + c] = ((red[e][0][c] + red[e][1][c]) + red[e][2][c]) + red[e][3][c];
     }
 }
 
