@@ -21,9 +21,12 @@
 // Up-projection tile: a wave owns 16 tokens x 64 channels.  MFMA 16x16x32 with
 //   A = W_up^T rows (channels, k = rank), B = neck rows (tokens, k = rank),
 // so D[channel][token]; the A rows are permuted (tile_channel) so that lane (q, L) ends up
-// holding two runs of 8 channels, c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7), of token L:
-// every 16-byte load or store instruction of the epilogue covers 64 contiguous bytes of
-// each of the wave's 16 token rows.  Operands are staged in LDS once per block.
+// holding two runs of 8 channels, c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7), of token L.
+// That layout goes through a wave-private LDS tile (fp32) to the row layout of the global
+// loads and stores, lane (rw, cg) = (lane >> 3, lane & 7) holding channels c0 + 8 cg + (0..7)
+// of tokens rw and rw + 8, so every 16-byte access instruction covers 128 contiguous bytes of
+// 8 token rows (at 64 bytes of 16 rows, as the MFMA layout would store, the same loads and
+// stores stream 1.3-1.4x slower).  W_up^T is staged in LDS once per block.
 #include "common.h"
 #include "../../include/rwkv6_amd.h"
 
@@ -33,21 +36,10 @@
 #ifndef LORA_BWD_AHEAD
 #define LORA_BWD_AHEAD 2
 #endif
+#define LORA_MT_RS 68                  // row stride (floats) of a wave's m tile
 
 namespace {
 
-// A lane's 16 values are two runs of 8 channels: c0 + 8q + (0..7) and c0 + 32 + 8q + (0..7),
-// so each 16-byte access instruction of a wave covers 64 contiguous bytes of every token row.
-template <bool NT>
-__device__ __forceinline__ void store16(uint16_t* row_c0, int q, const float* f) {
-    if (NT) {
-        store8_nt(row_c0 + 8 * q, f);
-        store8_nt(row_c0 + 32 + 8 * q, f + 8);
-    } else {
-        store8(row_c0 + 8 * q, f);
-        store8(row_c0 + 32 + 8 * q, f + 8);
-    }
-}
 // channel (relative to c0) of MFMA tile tc, row 4q' + rr' = L': the run layout above
 __device__ __forceinline__ int tile_channel(int tc, int L) {
     const int qq = L >> 2, rr = L & 3;
@@ -85,55 +77,41 @@ __device__ __forceinline__ void lora_stage(uint16_t* sw, const uint16_t* __restr
     }
 }
 
-// m[j] = sum_r neck[tok][e*R + r] * W_up[e][r][c], c the lane's j-th channel (run layout).
-// KS = R / 32 when the launch knows it (0: from R at run time; a loop with a load inside makes
-// the compiler wait for every outstanding load and store where it merges).
-template <int KS>
-__device__ __forceinline__ void lora_up(const uint16_t* sw, const uint16_t* __restrict__ neck_row,
-                                        int R, int e, float* m) {
-    const int lane = threadIdx.x & 63, L = lane & 15, q = lane >> 4;
-    const int rs = lds_rs(R);
-    const uint16_t* swe = sw + e * 64 * rs;
-    f32x4 acc[4] = {};
-    auto step = [&](int ks) {
-        const int r0 = 32 * ks + 8 * q;
-        const bf16x8 b = ld_bf16x8(neck_row + e * R + r0);
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc)
-            acc[tc] = mfma32(ld_bf16x8(swe + tile_channel(tc, L) * rs + r0), b, acc[tc]);
-    };
-    if constexpr (KS > 0) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) step(ks);
-    } else {
-        for (int ks = 0; ks < R / 32; ++ks) step(ks);
-    }
-#pragma unroll
-    for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) m[4 * tc + rr] = acc[tc][rr];
-}
-
 }  // namespace
 
 // LERP: out_e = x + (shift(x) - x) * (m_e + bias_e)  (E = 5);  else out_e = m_e + bias_e.
 // Token n of output e starts at out.p[e] + n * ors (ors = C for separate [N,C] tensors, E * C
 // for one [N,E,C] tensor).  A block takes REP consecutive 128-token tiles of its channel block
 // (the single-mix decay output stages the block's W_up for four tiles instead of one).
-// Four waves per SIMD: without the bound the ddlerp form takes 124 + 16 registers (three waves
-// per SIMD) and runs ~3 % slower at the config-3 shape.
+// Wave wv takes the tokens 64 g + 16 wv + (0..15) of group g of the block (2 REP groups), all
+// 64 channels.  m comes out of the MFMA one token per lane column and goes through the wave's
+// LDS tile to the row layout of every global access, lane (rw, cg) = (lane >> 3, lane & 7)
+// holding channels 8 cg + (0..7) of tokens rw and rw + 8: a load or store instruction covers
+// 128 contiguous bytes of 8 token rows (16 rows at 64 bytes each stream ~1.3x slower).
+// The stages s = E g + e are one straight run; each issues the neck pieces of stage
+// s + AH (and, for LERP, x and x[t-B] of the group that stage opens) before its own
+// stores.  Loads and stores are unconditional: a token past the end works on the last token
+// and stores its values again (same values, same place).
+// KS = R / 32, or 0: from R at run time (ranks past the first 32 are then loaded in the stage).
 template <int E, bool LERP, int REP, int KS>
-__global__ void __launch_bounds__(LORA_THR) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(LORA_THR)
 rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
                      const void* __restrict__ bias, int pdt, const uint16_t* __restrict__ x,
                      OutPtrs<E> out, int64_t ors, int64_t N, int64_t B, int64_t C, int R,
                      int64_t per) {
+    constexpr int NG = 2 * REP, NS = NG * E, KP = KS > 0 ? KS : 1;
+    // prefetch depth: two stages for five mixes, one for the single decay output (measured
+    // best at the config-3 shape: 61.5 against 63.1 and 62.2 us at depths 1 and 3, and 19.5
+    // against 20.0 us)
+    constexpr int AH = E > 1 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) float mt[4][16 * LORA_MT_RS];   // per wave: m [token][channel]
+    __shared__ __attribute__((aligned(16))) float bsm[E][64];          // bias of the block's channels
     int64_t tb, cb;
     if (!lora_tile((N + LORA_TT * REP - 1) / (LORA_TT * REP), C / 64, per, tb, cb)) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, L = lane & 15, q = lane >> 4;
-    const int64_t c0 = cb * 64;
+    const int rw = lane >> 3, cg = lane & 7;
+    const int64_t c0 = cb * 64, cl = c0 + 8 * cg;
     extern __shared__ __attribute__((aligned(16))) uint16_t lora_sm[];
-    __shared__ __attribute__((aligned(16))) float bsm[E][64];          // bias of the block's channels
     lora_stage(lora_sm, wut, E, C, R, c0);
     if (threadIdx.x < E * 8) {
         const int e = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
@@ -142,65 +120,109 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
 #pragma unroll
         for (int j = 0; j < 8; ++j) bsm[e][c8 + j] = bb[j];
     }
-    __syncthreads();
-    // Loads and stores are unconditional: a token past the end works on the last token and
-    // stores its values again (same value, same place); a load under a branch makes the
-    // merge wait for every outstanding load.
-    static_assert(LORA_TT == 128, "two 64-token groups per block");
-    // both 64-token groups at a time (tokens g = 0, 1 of this lane): their neck loads of a
-    // mix are in flight together
-#pragma unroll 1
-    for (int rp = 0; rp < REP; ++rp) {
-        const int64_t tt = tb * REP + rp;            // 128-token tile
-        int64_t tc[2];
-        // x and x[t-B] of the lane's two channel runs stay packed bf16 (16 registers a token
-        // group instead of 32 as fp32: 124 registers in all, four waves per SIMD); delta is
-        // formed again for every mix
-        uint4 xr[2][2], pr[2][2];
-        float keep[2];
+    static_assert(LORA_TT == 128, "two 64-token groups per 128-token tile");
+    const int64_t tblk = tb * REP * LORA_TT + 16 * wv;
+    // group g: the MFMA column token (L) and the lane's row tokens (rw, rw + 8), clamped
+    auto tok_m = [&](int g) { const int64_t t = tblk + 64 * g + L; return t < N ? t : N - 1; };
+    auto tok_r = [&](int g, int k) { const int64_t t = tblk + 64 * g + rw + 8 * k; return t < N ? t : N - 1; };
+    uint4 xr[2], pr[2], nkb[AH][KP];
+    auto load_x = [&](int g) {
 #pragma unroll
-        for (int P = 0; P < 2; ++P) {
-            const int64_t tok = tt * LORA_TT + 64 * P + 16 * wv + L;
-            tc[P] = tok < N ? tok : N - 1;
-            if (LERP) {
-                keep[P] = tc[P] >= B ? 1.f : 0.f;
-                const uint16_t* x0 = x + tc[P] * C + c0;
-                const uint16_t* p0 = x + (tc[P] >= B ? tc[P] - B : tc[P]) * C + c0;
-                xr[P][0] = *reinterpret_cast<const uint4*>(x0 + 8 * q);
-                xr[P][1] = *reinterpret_cast<const uint4*>(x0 + 32 + 8 * q);
-                pr[P][0] = *reinterpret_cast<const uint4*>(p0 + 8 * q);
-                pr[P][1] = *reinterpret_cast<const uint4*>(p0 + 32 + 8 * q);
-            }
+        for (int k = 0; k < 2; ++k) {
+            const int64_t t = tok_r(g, k);
+            xr[k] = *reinterpret_cast<const uint4*>(x + t * C + cl);
+            pr[k] = *reinterpret_cast<const uint4*>(x + (t >= B ? t - B : t) * C + cl);
         }
-#pragma unroll 1
+    };
+    auto load_stage = [&](int st) {
+        const int g = st / E, e = st - g * E;
+        const uint16_t* nrow = neck + tok_m(g) * E * R + e * R + 8 * q;
+#pragma unroll
+        for (int ks = 0; ks < KP; ++ks)
+            nkb[st % AH][ks] = *reinterpret_cast<const uint4*>(nrow + 32 * ks);
+    };
+    if (LERP) load_x(0);
+#pragma unroll
+    for (int st = 0; st < AH; ++st) load_stage(st);
+    __syncthreads();
+    const int rs = lds_rs(R);
+    float* mtw = mt[wv];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        uint4 xc[2], pc[2];
+        if (LERP) {
+            xc[0] = xr[0]; xc[1] = xr[1]; pc[0] = pr[0]; pc[1] = pr[1];
+        }
+#pragma unroll
         for (int e = 0; e < E; ++e) {
-            float m[2][16];
+            const int st = E * g + e;
+            const uint16_t* swe = lora_sm + e * 64 * rs;
+            f32x4 acc[4] = {};
 #pragma unroll
-            for (int P = 0; P < 2; ++P) lora_up<KS>(lora_sm, neck + tc[P] * E * R, R, e, m[P]);
-            const float* bq = &bsm[e][0];
+            for (int ks = 0; ks < KP; ++ks) {
+                const bf16x8 bq = __builtin_bit_cast(bf16x8, nkb[st % AH][ks]);
 #pragma unroll
-            for (int P = 0; P < 2; ++P) {
-                float o[16], xv[16], xp[16];
+                for (int tcn = 0; tcn < 4; ++tcn)
+                    acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 32 * ks + 8 * q), bq,
+                                      acc[tcn]);
+            }
+            if (KS == 0) {
+                const uint16_t* nrow = neck + tok_m(g) * E * R + e * R + 8 * q;
+                for (int ks = 1; ks < R / 32; ++ks) {
+                    const bf16x8 bq = ld_bf16x8(nrow + 32 * ks);
+#pragma unroll
+                    for (int tcn = 0; tcn < 4; ++tcn)
+                        acc[tcn] = mfma32(ld_bf16x8(swe + tile_channel(tcn, L) * rs + 32 * ks + 8 * q), bq,
+                                          acc[tcn]);
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float* d = mtw + L * LORA_MT_RS + 32 * hh + 8 * q;
+                *reinterpret_cast<float4*>(d) = make_float4(acc[2 * hh][0], acc[2 * hh][1], acc[2 * hh][2], acc[2 * hh][3]);
+                *reinterpret_cast<float4*>(d + 4) =
+                    make_float4(acc[2 * hh + 1][0], acc[2 * hh + 1][1], acc[2 * hh + 1][2], acc[2 * hh + 1][3]);
+            }
+            // the wave's own LDS writes and reads run in issue order; the compiler must not
+            // move the reads above the writes
+            asm volatile("" ::: "memory");
+            float m[2][8];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const float* sp = mtw + (rw + 8 * k) * LORA_MT_RS + 8 * cg;
+                const float4 m0 = *reinterpret_cast<const float4*>(sp);
+                const float4 m1 = *reinterpret_cast<const float4*>(sp + 4);
+                m[k][0] = m0.x; m[k][1] = m0.y; m[k][2] = m0.z; m[k][3] = m0.w;
+                m[k][4] = m1.x; m[k][5] = m1.y; m[k][6] = m1.z; m[k][7] = m1.w;
+            }
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + AH < NS) {
+                if (LERP && (st + AH) % E == 0) load_x((st + AH) / E);
+                load_stage(st + AH);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const float4 b0 = *reinterpret_cast<const float4*>(&bsm[e][8 * cg]);
+            const float4 b1 = *reinterpret_cast<const float4*>(&bsm[e][8 * cg + 4]);
+            const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t t = tok_r(g, k);
+                float o[8];
                 if (LERP) {
-                    // opaque copies in every mix: the unpacked values are not hoisted out of
-                    // the mix loop (they would hold 64 registers through it)
-                    asm volatile("" : "+v"(xr[P][0].x), "+v"(xr[P][0].y), "+v"(xr[P][0].z), "+v"(xr[P][0].w),
-                                      "+v"(xr[P][1].x), "+v"(xr[P][1].y), "+v"(xr[P][1].z), "+v"(xr[P][1].w));
-                    asm volatile("" : "+v"(pr[P][0].x), "+v"(pr[P][0].y), "+v"(pr[P][0].z), "+v"(pr[P][0].w),
-                                      "+v"(pr[P][1].x), "+v"(pr[P][1].y), "+v"(pr[P][1].z), "+v"(pr[P][1].w));
-                    unpack8(xr[P][0], xv);
-                    unpack8(xr[P][1], xv + 8);
-                    unpack8(pr[P][0], xp);
-                    unpack8(pr[P][1], xp + 8);
-                }
+                    float xv[8], xp[8];
+                    unpack8(xc[k], xv);
+                    unpack8(pc[k], xp);
+                    const float keep = t >= B ? 1.f : 0.f;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float bb = bq[j < 8 ? 8 * q + j : 32 + 8 * q + (j - 8)];
-                    o[j] = LERP ? xv[j] + (xp[j] * keep[P] - xv[j]) * (m[P][j] + bb) : m[P][j] + bb;
+                    for (int j = 0; j < 8; ++j) o[j] = xv[j] + (xp[j] * keep - xv[j]) * (m[k][j] + bb[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = m[k][j] + bb[j];
                 }
-                // nontemporal for the five mixes (config 3: 133 -> 98 us for the ddlerp form,
-                // 138 -> 86 us for the bias form); the single decay output measured slower so
-                store16<(E > 1)>(out.p[e] + tc[P] * ors + c0, q, o);
+                // nontemporal for the five mixes (the single decay output measured slower so)
+                if (E > 1) store8_nt(out.p[e] + t * ors + cl, o);
+                else store8(out.p[e] + t * ors + cl, o);
             }
         }
     }
@@ -223,7 +245,6 @@ rwkv6_lora_up_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restri
 // past the end works on the last token and stores its values again (same values, same
 // place), and only its d_bias contribution is masked.
 // KS = R / 32 (1 or 2; the launch picks it).
-#define LORA_MT_RS 68                  // row stride (floats) of the wave's m tile
 template <int KS>
 __global__ void __launch_bounds__(LORA_THR)
 rwkv6_ddlerp_lora_bwd_kernel(const uint16_t* __restrict__ neck, const uint16_t* __restrict__ wut,
@@ -599,9 +620,9 @@ int rwkv6_ddlerp_lora_fwd(const void* x, const void* neck, const void* w_up_t, c
                        {bias, (size_t)(LORA_NE * C) * param_bytes(param_dtype)}}))
             return RWKV6_ERR_INVALID_ARG;
     }
-    // the rank count from R at run time: the compile-time form measured 7 % slower here (136
-    // against 127 us at the config-3 shape, R = 32), while it is faster for the bias forms
-    hipLaunchKernelGGL((rwkv6_lora_up_kernel<LORA_NE, true, 1, 0>), up_grid(T * B, C), dim3(LORA_THR),
+    // five mixes admit R = 32 and 64 (the LDS bound)
+    auto kern = R == 64 ? rwkv6_lora_up_kernel<LORA_NE, true, 1, 2> : rwkv6_lora_up_kernel<LORA_NE, true, 1, 1>;
+    hipLaunchKernelGGL(kern, up_grid(T * B, C), dim3(LORA_THR),
                        lora_lds_bytes(LORA_NE, (int)R),
                        reinterpret_cast<hipStream_t>(stream), (const uint16_t*)neck,
                        (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)x, out, C,
@@ -625,8 +646,9 @@ int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, 
     if (E == 1) {
         OutPtrs<1> o;
         o.p[0] = (uint16_t*)out;
-        // the decay LoRA's rank 64 with a compile-time count, any other rank from R
-        auto kern = R == 64 ? rwkv6_lora_up_kernel<1, false, 4, 2> : rwkv6_lora_up_kernel<1, false, 4, 0>;
+        // ranks 32 and 64 (the decay LoRA's) with a compile-time count, any other from R
+        auto kern = R == 64 ? rwkv6_lora_up_kernel<1, false, 4, 2>
+                            : R == 32 ? rwkv6_lora_up_kernel<1, false, 4, 1> : rwkv6_lora_up_kernel<1, false, 4, 0>;
         hipLaunchKernelGGL(kern, up_grid(N, C, 4), dim3(LORA_THR),
                            lora_lds_bytes(1, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
@@ -634,7 +656,7 @@ int rwkv6_lora_bias_fwd(const void* neck, const void* w_up_t, const void* bias, 
     } else {
         OutPtrs<LORA_NE> o;
         for (int e = 0; e < LORA_NE; ++e) o.p[e] = (uint16_t*)out + (int64_t)e * C;
-        auto kern = R == 64 ? rwkv6_lora_up_kernel<LORA_NE, false, 1, 2> : rwkv6_lora_up_kernel<LORA_NE, false, 1, 0>;
+        auto kern = R == 64 ? rwkv6_lora_up_kernel<LORA_NE, false, 1, 2> : rwkv6_lora_up_kernel<LORA_NE, false, 1, 1>;
         hipLaunchKernelGGL(kern, up_grid(N, C), dim3(LORA_THR),
                            lora_lds_bytes(LORA_NE, (int)R), s, (const uint16_t*)neck,
                            (const uint16_t*)w_up_t, bias, param_dtype, (const uint16_t*)nullptr, o,
