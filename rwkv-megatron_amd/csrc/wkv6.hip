@@ -723,18 +723,120 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 // ---------------------------------------------------------------------------
 // Segment p of the output walk starts from the state entering its first chunk.  Each of the
 // segments 0..P-2 is cut into SUB pieces of at most NCS chunks; one workgroup per (b,h, piece)
-// walks its chunks from a zero state,
-//   S = diag(e^{G_63}) S + sum_tau (k_tau e^{G_63 - G_tau}) v_tau^T        [MFMA]
-// and writes the piece's end state S_q (fp32 [64][64]) and total log2-decay A_q ([64]).  Only
-// k, v and w are read.  Per chunk, thread (part, i) scans the log-decay of channel i over the
-// tokens 8 part .. 8 part + 7 and forms those tokens' k e^{G_63 - G} itself, written
-// channel-major (one 16-byte store) as the MFMA's A operand: no cumulative-decay tile, four
-// barriers a chunk, ~30 KB of LDS.
+// walks its chunks from a zero state, two chunks (PSPAN = 128 tokens) per step,
+//   S = diag(e^{G_end}) S + sum_tau (k_tau e^{G_end - G_tau}) v_tau^T        [MFMA]
+// with G the cumulative log-decay over the step, and writes the piece's end state S_q (fp32
+// [64][64]) and total log2-decay A_q ([64]).  Only k, v and w are read.  Per step, thread
+// (part, i) scans the log-decay of channel i over the tokens 16 part .. 16 part + 15 and forms
+// those tokens' k e^{G_end - G} itself, written channel-major (two 16-byte stores) as the
+// MFMA's A operand: no cumulative-decay tile, four barriers a step.  The exponents
+// G_end - G_tau are never positive, whatever the step's length, so the end state needs none of
+// the walk's 64-token references; 128-token steps halve the barriers per token (86.7 against
+// 89.2 us at config 5 with one 64-token chunk per step: with one workgroup per CU the pieces
+// stream k, v, w at ~18 GB/s per CU, near what one CU's loads sustain, so fewer barriers,
+// or loads two steps ahead, move them little).
+#define PSPAN (2 * CL)     // tokens per step of the pre-pass pieces
+#define PETS (PSPAN + 8)   // row stride of the channel-major operand tile (elements)
+typedef uint16_t ptile_t[PSPAN][TS];
 struct PieceSmem {
-    float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
+    float dec[2][KD];                 // e^{G_end} of step m in dec[m & 1]
     float tot[NTHR_W];                // per-part log2-decay sums
-    tile_t Km, Wt, Vm;                // raw k; raw w, then (k e^{G_63 - G})^T channel-major; v
+    ptile_t Xm, Wt, Ym;               // the step's raw tiles (token-major): k, w, v forward;
+                                      // r, w, dO backward
+    uint16_t Et[KD][PETS];            // the A operand, channel-major: k e^{G_end - G}
+                                      // forward, r e^{G_{t-1}} backward
 };
+static_assert(sizeof(PieceSmem) <= 80 * 1024, "two piece workgroups per CU");
+
+// One step of a pre-pass piece on the raw tiles already in LDS (nvalid tokens; the rows past
+// them zeroed): the decay scan, the A operand and the state (gradient) update
+//   acc = diag(e^{G_end}) acc + E^T Y   (E = A operand, Y = v forward, dO backward).
+// BWD: the operand is x e^{G_{t-1}} (exclusive prefix) instead of x e^{G_end - G_t}.
+template <bool SEQ, bool BWD>
+__device__ __forceinline__ void piece_step(PieceSmem& sm, int nvalid, int par, f32x4* acc,
+                                           float& gsum) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;   // state rows [16W, +16) x columns [32hh, +32)
+    const int lr = lane & 15, lq = lane >> 4;
+    const int i = lane, part = wv;        // decay scan: channel i, tokens 16 part .. +15
+    float loc[16], run = 0.f;
+#pragma unroll
+    for (int s4 = 0; s4 < 16; s4 += 4) {
+        const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 16 * part + s4);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int s = s4 + jj;
+            const float x = (float)x4[jj];
+            const float wn = SEQ ? ((16 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
+            run += fmaxf(wn, W_MIN) * RW_L2E;
+            loc[s] = run;
+        }
+    }
+    bf16x4 xa[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) xa[s4] = ld_col4(&sm.Xm[0][0], 16 * part + 4 * s4);
+    sm.tot[part * 64 + i] = run;
+    __syncthreads();
+    {
+        // G_t = loc + (sum of the earlier parts); G_end = run_7 + sum of parts 0..6
+        float off = 0.f, o7 = 0.f;
+#pragma unroll
+        for (int p = 0; p < 7; ++p) {
+            const float t = sm.tot[p * 64 + i];
+            off += p < part ? t : 0.f;
+            o7 += t;
+        }
+        const float gend = sm.tot[7 * 64 + i] + o7;
+        float e[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float xf = (float)xa[s >> 2][s & 3];
+            e[s] = BWD ? xf * ex2(s == 0 ? off : loc[s - 1] + off) : xf * ex2(gend - (loc[s] + off));
+        }
+        *reinterpret_cast<uint4*>(&sm.Et[i][16 * part]) = pack8(e);
+        *reinterpret_cast<uint4*>(&sm.Et[i][16 * part + 8]) = pack8(e + 8);
+        if (part == 7) {
+            sm.dec[par][i] = ex2(gend);
+            gsum += gend;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const float d = sm.dec[par][16 * W + 4 * lq + rr];
+        acc[0][rr] *= d;
+        acc[1][rr] *= d;
+    }
+#pragma unroll
+    for (int ks = 0; ks < PSPAN / 32; ++ks) {
+        // A: row 16W + lr of Et in the slot order of ld_tr8 (tokens 32ks + 4lq + (0..3) and
+        // 32ks + 16 + 4lq + (0..3)), B: the same tokens of Y
+        const uint2 a0 = *reinterpret_cast<const uint2*>(&sm.Et[16 * W + lr][32 * ks + 4 * lq]);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(&sm.Et[16 * W + lr][32 * ks + 16 + 4 * lq]);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+            acc[tp] = mfma32(a, ld_tr8(&sm.Ym[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+    }
+    __syncthreads();
+}
+
+// The raw 16-byte pieces a thread stores per step: rows (tid >> 3) and (tid >> 3) + 64 of each
+// of three tensors (rows past the valid ones read the last valid token and are zeroed before
+// the store: unconditional loads).
+struct PieceLoads {
+    uint4 x[2], w[2], y[2];
+};
+__device__ __forceinline__ void piece_store(PieceSmem& sm, PieceLoads& f, int nvalid) {
+    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (row + 64 * h >= nvalid) f.x[h] = f.w[h] = f.y[h] = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(&sm.Ym[row + 64 * h][c8]) = f.y[h];
+        *reinterpret_cast<uint4*>(&sm.Wt[row + 64 * h][c8]) = f.w[h];
+        *reinterpret_cast<uint4*>(&sm.Xm[row + 64 * h][c8]) = f.x[h];
+    }
+}
 
 template <bool SEQ>
 __global__ void __launch_bounds__(NTHR_W)
@@ -748,79 +850,34 @@ wkv6_fwd_pieces(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     // and segments 0..P-2 hold NC chunks each
     const int c_begin = sg * NC + j * NCS;
     const int c_end = min(min(c_begin + NCS, (sg + 1) * NC), NT);
+    const int t_end = min(c_end * CL, T);
+    const int nsteps = (c_end - c_begin + 1) / 2;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int W = wv >> 1, hh = wv & 1;   // state rows [16W, +16) x columns [32hh, +32)
+    const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
-    const int i = lane, part = wv;        // decay scan: channel i, tokens 8 part .. +7
-
-    WalkPrefetch nx;
-    walk_issue<SEQ, false>(nx, nullptr, k, v, w, bh, c_begin, B, H, T);
+    const size_t rs = tok_rs<SEQ>(B, H);
+    PieceLoads nx;
+    auto issue = [&](int m) {
+        const int t0 = (c_begin + 2 * m) * CL, nv = min(PSPAN, t_end - t0);
+        const size_t base = tok_base<SEQ>(bh, t0, B, H, T);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const size_t off = base + (size_t)min(row + 64 * h, nv - 1) * rs + c8;
+            nx.x[h] = *reinterpret_cast<const uint4*>(k + off);
+            nx.y[h] = *reinterpret_cast<const uint4*>(v + off);
+            nx.w[h] = *reinterpret_cast<const uint4*>(w + off);
+        }
+    };
+    issue(0);
     f32x4 acc[2] = {};
-    float gsum = 0.f;                      // total log2-decay of channel i (part 7)
-    for (int c = c_begin; c < c_end; ++c) {
-        const int nvalid = min(CL, T - c * CL);
-        if (nvalid < CL && row >= nvalid) nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
-        sstore16(sm.Vm, row, c8, nx.v);
-        sstore16(sm.Wt, row, c8, nx.w);
-        sstore16(sm.Km, row, c8, nx.k);
-        // unconditional (the last iteration reloads its own chunk)
-        walk_issue<SEQ, false>(nx, nullptr, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
+    float gsum = 0.f;                      // total log2-decay of channel lane (wave 7)
+    for (int m = 0; m < nsteps; ++m) {
+        const int nvalid = min(PSPAN, t_end - (c_begin + 2 * m) * CL);
+        piece_store(sm, nx, nvalid);
+        issue(min(m + 1, nsteps - 1));     // unconditional (the last step reloads its own)
         __syncthreads();
-        // the part's running log2-decay (as build_G) and its raw k
-        float loc[8], run = 0.f;
-#pragma unroll
-        for (int s4 = 0; s4 < 8; s4 += 4) {
-            const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 8 * part + s4);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int s = s4 + jj;
-                const float x = (float)x4[jj];
-                const float wn = SEQ ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
-                run += fmaxf(wn, W_MIN) * RW_L2E;
-                loc[s] = run;
-            }
-        }
-        const bf16x4 ka = ld_col4(&sm.Km[0][0], 8 * part), kb = ld_col4(&sm.Km[0][0], 8 * part + 4);
-        sm.tot[part * 64 + i] = run;
-        __syncthreads();
-        {
-            // G_t = loc + (sum of the earlier parts), G_63 = run_7 + sum of parts 0..6, in the
-            // order build_G adds them
-            float off = 0.f, o7 = 0.f;
-#pragma unroll
-            for (int p = 0; p < 7; ++p) {
-                const float t = sm.tot[p * 64 + i];
-                off += p < part ? t : 0.f;
-                o7 += t;
-            }
-            const float g63 = sm.tot[7 * 64 + i] + o7;
-            const float kf[8] = {(float)ka[0], (float)ka[1], (float)ka[2], (float)ka[3],
-                                 (float)kb[0], (float)kb[1], (float)kb[2], (float)kb[3]};
-            float e[8];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) e[s] = kf[s] * ex2(g63 - (loc[s] + off));
-            *reinterpret_cast<uint4*>(&sm.Wt[i][8 * part]) = pack8(e);
-            if (part == 7) {
-                sm.dec[c & 1][i] = ex2(g63);
-                gsum += g63;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
-            acc[0][rr] *= d;
-            acc[1][rr] *= d;
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_dir8(&sm.Wt[0][0], 16 * W + lr, 32 * ks);
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                acc[tp] = mfma32(a, ld_tr8(&sm.Vm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
-        }
-        __syncthreads();
+        piece_step<SEQ, false>(sm, nvalid, m & 1, acc, gsum);
     }
     const size_t sq = (size_t)bh * npieces + q;
 #pragma unroll
@@ -828,7 +885,7 @@ wkv6_fwd_pieces(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
             Sseg[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = acc[tp][rr];
-    if (part == 7) Aseg[sq * KD + i] = gsum;
+    if (wv == 7) Aseg[sq * KD + lane] = gsum;
 }
 
 // Start states of the output walk's segments 1..P-1: the pieces folded in order onto h0 (or
@@ -871,107 +928,50 @@ wkv6_fwd_fold(const float* __restrict__ Sseg, const float* __restrict__ Aseg,
 // state gradient dS_end(p) the later segments hand it.  Each of the segments 1..P-1 is cut into
 // SUB pieces of at most NCS chunks (trailing pieces of a short last segment are empty); one
 // workgroup per (b,h, piece) walks its chunks from the last to the first from a zero state
-// gradient,
-//   dS = diag(e^{G_63}) dS + s sum_t (r_t e^{G_{t-1}}) dO_t^T                  [MFMA]
-// and writes the piece's dS_q (fp32 [64][64]) and total log2-decay A_q ([64]).  Reads r, w
-// (sequence-first for SEQ) and dO (head-first); the per-thread decay scan of wkv6_fwd_pieces
-// writes r e^{G_{t-1}} channel-major as the MFMA's A operand.
-struct BwdPieceSmem {
-    float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
-    float tot[NTHR_W];                // per-part log2-decay sums
-    tile_t Rm, Wt, Dm;                // raw r; raw w, then (r e^{G_{t-1}})^T channel-major; dO
-};
-
+// gradient, two chunks (PSPAN = 128 tokens) per step, aligned on the piece's first chunk,
+//   dS = diag(e^{G_end}) dS + s sum_t (r_t e^{G_{t-1}}) dO_t^T                  [MFMA]
+// (G from the step's start; the exponents are never positive) and writes the piece's dS_q
+// (fp32 [64][64]) and total log2-decay A_q ([64]).  Reads r, w (sequence-first for SEQ) and
+// dO (head-first); the step body is wkv6_fwd_pieces' with r e^{G_{t-1}} as the A operand.
 template <bool SEQ>
 __global__ void __launch_bounds__(NTHR_W)
 wkv6_bwd_pieces(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
                 const uint16_t* __restrict__ dO, float* __restrict__ dSp, float* __restrict__ Ap,
                 float scale, int B, int H, int T, int NT, int NC, int SUB, int NCS, int npieces) {
-    __shared__ __attribute__((aligned(16))) BwdPieceSmem sm;
+    __shared__ __attribute__((aligned(16))) PieceSmem sm;
     const int bh = blockIdx.x / npieces, q = blockIdx.x - bh * npieces;
     const int sg = 1 + q / SUB, j = q - (sg - 1) * SUB;            // segments 1..P-1
     const int c_begin = sg * NC + j * NCS;
     const int c_end = min(min(c_begin + NCS, (sg + 1) * NC), NT);
+    const int t_end = min(c_end * CL, T);
+    const int nsteps = (c_end - c_begin + 1) / 2;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int W = wv >> 1, hh = wv & 1;   // dS rows [16W, +16) x columns [32hh, +32)
+    const int W = wv >> 1, hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
-    const int i = lane, part = wv;        // decay scan: channel i, tokens 8 part .. +7
-
-    // the 16-byte pieces of r, w, dO this thread stores (rows past a ragged end read the last
-    // token; they are zeroed before the store)
-    uint4 xr = make_uint4(0u, 0u, 0u, 0u), xw = xr, xd = xr;
-    auto issue = [&](int c) {
-        const int t0 = c * CL, nv = min(CL, T - t0), rrow = min(row, nv - 1);
-        const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+    const size_t rs = tok_rs<SEQ>(B, H);
+    PieceLoads nx;
+    auto issue = [&](int m) {
+        const int t0 = (c_begin + 2 * m) * CL, nv = min(PSPAN, t_end - t0);
+        const size_t base = tok_base<SEQ>(bh, t0, B, H, T);
         const size_t dbase = tok_base<false>(bh, t0, B, H, T);
-        xr = *reinterpret_cast<const uint4*>(r + base + (size_t)rrow * rs + c8);
-        xw = *reinterpret_cast<const uint4*>(w + base + (size_t)rrow * rs + c8);
-        xd = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)rrow * KD + c8);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int rrow = min(row + 64 * h, nv - 1);
+            nx.x[h] = *reinterpret_cast<const uint4*>(r + base + (size_t)rrow * rs + c8);
+            nx.w[h] = *reinterpret_cast<const uint4*>(w + base + (size_t)rrow * rs + c8);
+            nx.y[h] = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)rrow * KD + c8);
+        }
     };
     f32x4 acc[2] = {};
-    float gsum = 0.f;                      // total log2-decay of channel i (part 7)
-    if (c_begin < c_end) issue(c_end - 1);
-    for (int c = c_end - 1; c >= c_begin; --c) {
-        const int nvalid = min(CL, T - c * CL);
-        if (nvalid < CL && row >= nvalid) xr = xw = xd = make_uint4(0u, 0u, 0u, 0u);
-        sstore16(sm.Dm, row, c8, xd);
-        sstore16(sm.Wt, row, c8, xw);
-        sstore16(sm.Rm, row, c8, xr);
-        issue(max(c - 1, c_begin));        // unconditional: the first chunk reloads itself
+    float gsum = 0.f;                      // total log2-decay of channel lane (wave 7)
+    if (nsteps > 0) issue(nsteps - 1);
+    for (int m = nsteps - 1; m >= 0; --m) {
+        const int nvalid = min(PSPAN, t_end - (c_begin + 2 * m) * CL);
+        piece_store(sm, nx, nvalid);
+        issue(max(m - 1, 0));              // unconditional: the first step reloads itself
         __syncthreads();
-        float loc[8], run = 0.f;
-#pragma unroll
-        for (int s4 = 0; s4 < 8; s4 += 4) {
-            const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 8 * part + s4);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int s = s4 + jj;
-                const float x = (float)x4[jj];
-                const float wn = SEQ ? ((8 * part + s < nvalid) ? -ex2(x * RW_L2E) : 0.f) : x;
-                run += fmaxf(wn, W_MIN) * RW_L2E;
-                loc[s] = run;
-            }
-        }
-        const bf16x4 ra = ld_col4(&sm.Rm[0][0], 8 * part), rb = ld_col4(&sm.Rm[0][0], 8 * part + 4);
-        sm.tot[part * 64 + i] = run;
-        __syncthreads();
-        {
-            // G_{t-1} = off (first token of the part) or loc[s-1] + off; G_63 = run_7 + parts 0..6
-            float off = 0.f, o7 = 0.f;
-#pragma unroll
-            for (int p = 0; p < 7; ++p) {
-                const float t = sm.tot[p * 64 + i];
-                off += p < part ? t : 0.f;
-                o7 += t;
-            }
-            const float g63 = sm.tot[7 * 64 + i] + o7;
-            const float rf[8] = {(float)ra[0], (float)ra[1], (float)ra[2], (float)ra[3],
-                                 (float)rb[0], (float)rb[1], (float)rb[2], (float)rb[3]};
-            float e[8];
-#pragma unroll
-            for (int s = 0; s < 8; ++s) e[s] = rf[s] * ex2(s == 0 ? off : loc[s - 1] + off);
-            *reinterpret_cast<uint4*>(&sm.Wt[i][8 * part]) = pack8(e);
-            if (part == 7) {
-                sm.dec[c & 1][i] = ex2(g63);
-                gsum += g63;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const float d = sm.dec[c & 1][16 * W + 4 * lq + rr];
-            acc[0][rr] *= d;
-            acc[1][rr] *= d;
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = ld_dir8(&sm.Wt[0][0], 16 * W + lr, 32 * ks);
-#pragma unroll
-            for (int tp = 0; tp < 2; ++tp)
-                acc[tp] = mfma32(a, ld_tr8(&sm.Dm[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
-        }
-        __syncthreads();
+        piece_step<SEQ, true>(sm, nvalid, m & 1, acc, gsum);
     }
     const size_t sq = (size_t)bh * npieces + q;
 #pragma unroll
@@ -979,7 +979,7 @@ wkv6_bwd_pieces(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
             dSp[sq * KD * KD + (16 * W + 4 * lq + rr) * KD + 32 * hh + 16 * tp + lr] = scale * acc[tp][rr];
-    if (part == 7) Ap[sq * KD + i] = gsum;
+    if (wv == 7) Ap[sq * KD + lane] = gsum;
 }
 
 // dS_end[b,h][p], p = 0..P-2: the state gradient segment p starts from, the pieces folded from
