@@ -732,9 +732,8 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 // MFMA's A operand: no cumulative-decay tile, four barriers a step.  The exponents
 // G_end - G_tau are never positive, whatever the step's length, so the end state needs none of
 // the walk's 64-token references; 128-token steps halve the barriers per token (86.7 against
-// 89.2 us at config 5 with one 64-token chunk per step: with one workgroup per CU the pieces
-// stream k, v, w at ~18 GB/s per CU, near what one CU's loads sustain, so fewer barriers,
-// or loads two steps ahead, move them little).
+// 89.2 us at config 5 with one 64-token chunk per step; loads two steps ahead measured no
+// faster, and a plain read stream of the same shape, one workgroup per CU, takes 59 us).
 #define PSPAN (2 * CL)     // tokens per step of the pre-pass pieces
 #define PETS (PSPAN + 8)   // row stride of the channel-major operand tile (elements)
 typedef uint16_t ptile_t[PSPAN][TS];
