@@ -120,10 +120,10 @@ def test_wkv_extreme_decay_is_floored(pkg):
     _compare(got, ref, ["o", "hT", "dr", "dk", "dv", "dw", "du", "dh0"])
 
 
-@pytest.mark.parametrize("shape", [(2, 2, 200), (2, 64, 64 * 17 + 5)])
+@pytest.mark.parametrize("shape", [(2, 2, 200), (4, 6, 64 * 24 + 3), (2, 64, 64 * 17 + 5)])
 def test_wkv_deterministic(pkg, shape):
-    """Bit-identical reruns: the chunk-parallel backward and, at B*H = 128, the segmented
-    forward and reverse walks (their pieces and folds sum in a fixed order)."""
+    """Bit-identical reruns: the chunk-parallel backward (B*H = 4 and 24) and, at B*H = 128,
+    the segmented forward and reverse walks (their pieces and folds sum in a fixed order)."""
     x = _inputs(*shape, seed=3)
     a = run_gpu(pkg, x, 1.0, True, True)
     b = run_gpu(pkg, x, 1.0, True, True)
@@ -144,16 +144,18 @@ def test_wkv_empty_sequence(pkg):
 
 
 @pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17), (2, 24, 64 * 32 + 11),
-                                   (3, 32, 64 * 20), (2, 64, 64 * 17 + 5), (1, 128, 64 * 30 + 9)])
+                                   (3, 32, 64 * 20), (2, 8, 64 * 64), (1, 32, 64 * 15 + 40),
+                                   (2, 64, 64 * 17 + 5), (1, 128, 64 * 30 + 9)])
 def test_wkv_parity_segmented(pkg, shape):
     """Few sequences of many chunks: the forward cuts each sequence into segments (pre-pass
     pieces folded into each segment's start state, then output walks), here 2 segments of 9
-    chunks, 5 of 9 with a ragged last chunk, 4 of 9 (48 sequences) and 2 of 10 (96
-    sequences).  The backward runs chunk-parallel for those four (the (b,h, segment) walks
-    would fill less than 7/8 of the device: 2, 5, 192 and 192 of 256) and as a segmented
-    reverse walk (backward pieces folded into each segment's starting state gradient) for the
-    128-sequence shapes: 2 segments of 9 chunks, and of 16 + 15 chunks with a ragged last
-    one."""
+    chunks, 5 of 9 with a ragged last chunk, 4 of 9 (48 sequences), 2 of 10 (96 sequences),
+    8 of 8 (16 sequences) and 2 of 8 with a ragged last chunk (32 sequences).  The backward
+    runs chunk-parallel for those six (the (b,h, segment) walks would fill less than 7/8 of the
+    device: 2, 5, 192, 192, 128 and 64 of 256) and as a segmented reverse walk (backward pieces
+    folded into each segment's starting state gradient) for the 128-sequence shapes: 2
+    segments of 9 chunks, and of 16 + 15 chunks with a ragged last one.  The pieces step two
+    chunks at a time, so segments of an odd chunk count (9, 15) end on a one-chunk step."""
     B, H, T = shape
     x = _inputs(B, H, T, seed=T)
     got = run_gpu(pkg, x, 0.5, True, True)
