@@ -1702,7 +1702,7 @@ struct LoopSmem {
     tile_t KqT, RiT;                // Kq^T; (s r e^{G_{t-1}})^T, the state-gradient step's operand
     tile_t RpT[2];                  // (s Rm_I p_IW)^T of the six cross pairs I > W (dv)
     tile_t Sin;                     // S_in (bf16 [i][j])
-    tile_t Out[4];                  // dr, dk, dv, dw staged channel-major
+    tile_t Out[4];                  // dr, dk, dv, dw staged channel-major (token-major for SEQ)
 };
 static_assert(sizeof(LoopSmem) <= 160 * 1024, "one loop workgroup per CU");
 
@@ -2016,23 +2016,39 @@ __device__ __forceinline__ void loop_issue(LoopPrefetch& f, const uint16_t* __re
 }
 
 // The staged gradients of chunk c to HBM: the waves of token block N (N = W of wave 4W + col)
-// write tensor N (dr, dk, dv, dw); wave col writes tokens 16 col + lr, channels 8 lq .. +7 and
-// 32 + 8 lq .. +7.
+// write tensor N (dr, dk, dv, dw), wave col the tokens 16 col .. 16 col + 15.
+//   head-first (Out channel-major): lane (lq, lr) writes token 16 col + lr, channels 8 lq .. +7
+//     and 32 + 8 lq .. +7 (the token rows are contiguous: each store covers 1 KB);
+//   sequence-first (Out token-major): lane (rw, cg) = (lane >> 3, lane & 7) writes tokens
+//     16 col + rw and + 8, channels 8 cg .. +7, so a store covers 128 contiguous bytes of 8
+//     token rows B*H*128 bytes apart (16 rows of 64 bytes there stream ~1.3x slower); rows
+//     past the end store the last token's values again (no branch around the stores).
 template <bool SEQ, int N>
 __device__ __forceinline__ void loop_store(const LoopSmem& sm, uint16_t* __restrict__ dr,
                                            uint16_t* __restrict__ dk, uint16_t* __restrict__ dv,
                                            uint16_t* __restrict__ dw, int bh, int c, int B, int H,
                                            int T, int col, int lane, const LaneOfs& o,
                                            const GlobOfs& g) {
-    const int tk = 16 * col + (lane & 15);
     const int t0 = c * CL, nvalid = min(CL, T - t0);
     uint16_t* dst = (N == 0 ? dr : N == 1 ? dk : N == 2 ? dv : dw) + tok_base<SEQ>(bh, t0, B, H, T);
-    const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 0, 0));   // o.g8 holds c0
-    const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 32, 0));
-    if (tk < nvalid) {
-        char* p = reinterpret_cast<char*>(dst) + (unsigned)g.st;
-        *reinterpret_cast<uint4*>(p) = x0;
-        *reinterpret_cast<uint4*>(p + 64) = x1;
+    if constexpr (SEQ) {
+        const int rw = lane >> 3, c8 = 8 * (lane & 7);
+        const size_t rs = tok_rs<SEQ>(B, H);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int tk = min(16 * col + rw + 8 * kk, nvalid - 1);
+            const uint4 x = *reinterpret_cast<const uint4*>(&sm.Out[N][tk][c8]);
+            *reinterpret_cast<uint4*>(dst + (size_t)tk * rs + c8) = x;
+        }
+    } else {
+        const int tk = 16 * col + (lane & 15);
+        const uint4 x0 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 0, 0));   // o.g8 holds c0
+        const uint4 x1 = __builtin_bit_cast(uint4, g8o(&sm.Out[N][0][0], o, 32, 0));
+        if (tk < nvalid) {
+            char* p = reinterpret_cast<char*>(dst) + (unsigned)g.st;
+            *reinterpret_cast<uint4*>(p) = x0;
+            *reinterpret_cast<uint4*>(p + 64) = x1;
+        }
     }
 }
 
@@ -2260,7 +2276,7 @@ __device__ __forceinline__ void bwd_loop_walk(
         }
         __syncthreads();                   // all products done; red, Pk in
 
-        // ---- S5: dw; dr, dk, dv, dw staged channel-major (stored during the next step) ----
+        // ---- S5: dw; dr, dk, dv, dw staged (stored during the next step) ----
         {
             later += lds_ld<float>(&sm.Dv[0], o.tab) +
                      ((lds_ld<float>(&sm.Pk[0][0], o.tab) + lds_ld<float>(&sm.Pk[1][0], o.tab)) +
@@ -2278,11 +2294,25 @@ __device__ __forceinline__ void bwd_loop_walk(
                 }
                 if (!SEQ && go.fl[rr]) g[rr] = 0.f;
             }
-            lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(0, TW), go.drb[0]);
-            lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(0, TW), go.dkb[0]);
-            const float avf[4] = {go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]};
-            st_ch4o(&sm.Out[2][0][0], o, 0, TW, avf);
-            st_ch4o(&sm.Out[3][0][0], o, 0, TW, g);
+            if constexpr (SEQ) {
+                // token-major (the store's row layout): X[TW + 4 lq + rr][c0 + lr], 2 bytes each
+                const int tm = o.q16 * TS / 2 + (o.tab >> 1) + tb(TW, 0);   // X[TW + 4 lq][c0 + lr]
+                auto st_tok = [&](uint16_t* X, bf16x4 x) {
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr)
+                        lds_st<__bf16>(X, tm + tb(rr, 0), x[rr]);
+                };
+                st_tok(&sm.Out[0][0][0], go.drb[0]);
+                st_tok(&sm.Out[1][0][0], go.dkb[0]);
+                st_tok(&sm.Out[2][0][0], cvt4(go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]));
+                st_tok(&sm.Out[3][0][0], cvt4(g[0], g[1], g[2], g[3]));
+            } else {
+                lds_st<bf16x4>(&sm.Out[0][0][0], o.ch + tb(0, TW), go.drb[0]);
+                lds_st<bf16x4>(&sm.Out[1][0][0], o.ch + tb(0, TW), go.dkb[0]);
+                const float avf[4] = {go.av[0][0], go.av[0][1], go.av[0][2], go.av[0][3]};
+                st_ch4o(&sm.Out[2][0][0], o, 0, TW, avf);
+                st_ch4o(&sm.Out[3][0][0], o, 0, TW, g);
+            }
         }
         // no barrier here: the next step's S1 touches nothing S5 reads or writes, and its B1
         // orders S5 before the next writes of Dv, red (S2) and Pk, Out (S4)
