@@ -279,7 +279,7 @@ struct WalkSmem {
     float c3[4][KD];                  // e^{G_63 - mu_J}
     float c6[6][KD];                  // e^{b_{I-1} - mu_J}, pair (I, J), J < I
     float dec[2][KD];                 // e^{G_63} of chunk c in dec[c & 1]
-    float tot[NTHR_W];                // build_G scratch
+    float tot[2][NTHR_W];             // per-part log2-decay sums of chunk c in tot[c & 1]
     float bonus[CL];
     float uh[KD];                     // u of this head
     float G[(CL + 1) * GSG];          // row 0 zero (G before the chunk), row t + 1 = G_t:
@@ -289,22 +289,27 @@ struct WalkSmem {
     tile_t Kt, Vm, Ot;                // state-update operand k e^{G_63 - G}, v, o staging
     tile_t Sin[2];                    // bf16 S_in of chunk c in Sin[c & 1]
     uint16_t Kc[6 * 16][TS];          // cross-block sources k e^{b_{I-1} - G}, rows 16 pair(I, J)
+    tile_t Wr;                        // raw w of chunk c + 2 (scanned during chunk c)
 };
 static_assert(sizeof(WalkSmem) <= 160 * 1024, "walk block LDS");
 
-// build_G for the output walk (512 threads, part = 8-token run): also fills the per-channel
-// tables, all from the part-end values ge[p] = G[8p + 7] (mu_I = ge[2I], b_{I-1} =
-// ge[2I - 1], G_63 = ge[7]).  `part` is wave-uniform, so the table branches are scalar.
+// The decay scan of the output walk runs two chunks ahead, in two halves, so that it shares the
+// products' phase of an earlier chunk instead of adding barriers of its own:
+//   walk_scan1(c')  (512 threads, part = 8-token run): thread (part, i) scans channel i over
+//                   tokens 8 part .. 8 part + 7 of the raw w in Wr, keeps the running sums in
+//                   loc and writes the part's total to tot[c' & 1];
+//   walk_scan2(c')  one barrier later: the part-end values ge[p] = G[8p + 7] from tot[c' & 1],
+//                   the cumulative-decay view G of chunk c' and its per-channel tables (mu_I =
+//                   ge[2I], b_{I-1} = ge[2I - 1], G_63 = ge[7]).
+// `part` is wave-uniform, so the table branches are scalar.
 template <bool DEC, int PB>
-__device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar) {
+__device__ __forceinline__ void walk_scan1(WalkSmem& sm, int nvalid, int tpar, float* loc) {
     // the wave's 8-token part is 2 PB + hh (PB the wave pair, compile-time; hh wave-uniform)
-    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G + GSG);
     const int i = threadIdx.x & 63, hh = (threadIdx.x >> 6) & 1, part = 2 * PB + hh;
-    float loc[8];
     float run = 0.f;
 #pragma unroll
     for (int s4 = 0; s4 < 8; s4 += 4) {
-        const bf16x4 x4 = ld_col4(&sm.Kt[0][0], 8 * part + s4);   // w scratch, column i = lane
+        const bf16x4 x4 = ld_col4(&sm.Wr[0][0], 8 * part + s4);   // column i = lane
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int s = s4 + j;
@@ -314,12 +319,16 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
             loc[s] = run;
         }
     }
-    sm.tot[part * 64 + i] = run;
-    __syncthreads();
+    sm.tot[tpar][part * 64 + i] = run;
+}
+template <int PB>
+__device__ __forceinline__ void walk_scan2(WalkSmem& sm, const float* loc, int tpar, int cpar) {
+    float (*Gm)[GSG] = reinterpret_cast<float (*)[GSG]>(sm.G + GSG);
+    const int i = threadIdx.x & 63, hh = (threadIdx.x >> 6) & 1, part = 2 * PB + hh;
     float ge[8], a = 0.f;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
-        a += sm.tot[p * 64 + i];
+        a += sm.tot[tpar][p * 64 + i];
         ge[p] = a;
     }
     // G before the part: the sum of parts 0 .. part-1
@@ -348,7 +357,6 @@ __device__ __forceinline__ void walk_build_G(WalkSmem& sm, int nvalid, int cpar)
             sm.dec[cpar][i] = ex2(ge[7]);
         }
     }
-    __syncthreads();
 }
 
 // Segments per sequence (shared by the workspace query and the launch): as many (b,h, segment)
@@ -407,22 +415,36 @@ __device__ __forceinline__ uint4 gload16c(const uint16_t* __restrict__ src, int 
     return row < nvalid ? x : make_uint4(0u, 0u, 0u, 0u);
 }
 
-template <bool SEQ, bool OUT>
+// Raw w of chunk cw for the thread's piece (token row tid >> 3, channels 8 (tid & 7) ..).
+template <bool SEQ>
+__device__ __forceinline__ uint4 walk_load_w(const uint16_t* __restrict__ w, int bh, int cw, int B,
+                                             int H, int T) {
+    const int t0 = cw * CL, nvalid = min(CL, T - t0);
+    const int row = min((int)(threadIdx.x >> 3), nvalid - 1), c8 = (threadIdx.x & 7) * 8;
+    return *reinterpret_cast<const uint4*>(w + tok_base<SEQ>(bh, t0, B, H, T) +
+                                           (size_t)row * tok_rs<SEQ>(B, H) + c8);
+}
+
+// r, k, v of chunk c and w of chunk cw (the decay scan runs two chunks ahead of the rest).
+template <bool SEQ>
 __device__ __forceinline__ void walk_issue(WalkPrefetch& f, const uint16_t* __restrict__ r,
                                            const uint16_t* __restrict__ k,
                                            const uint16_t* __restrict__ v,
-                                           const uint16_t* __restrict__ w, int bh, int c, int B,
-                                           int H, int T) {
-    const int t0 = c * CL, nvalid = min(CL, T - t0);
-    const size_t base = tok_base<SEQ>(bh, t0, B, H, T), rs = tok_rs<SEQ>(B, H);
+                                           const uint16_t* __restrict__ w, int bh, int c, int cw,
+                                           int B, int H, int T) {
+    const size_t rs = tok_rs<SEQ>(B, H);
     // unconditional loads (rows past the end read the last token; the walk zeroes those
-    // rows in LDS): a load under a branch makes the next wait a full one
-    const int row = min((int)(threadIdx.x >> 3), nvalid - 1), c8 = (threadIdx.x & 7) * 8;
-    const size_t off = base + (size_t)row * rs + c8;
-    if (OUT) f.r = *reinterpret_cast<const uint4*>(r + off);
-    f.k = *reinterpret_cast<const uint4*>(k + off);
-    f.v = *reinterpret_cast<const uint4*>(v + off);
-    f.w = *reinterpret_cast<const uint4*>(w + off);
+    // rows before they reach LDS): a load under a branch makes the next wait a full one
+    const int c8 = (threadIdx.x & 7) * 8;
+    {
+        const int t0 = c * CL, nvalid = min(CL, T - t0);
+        const int row = min((int)(threadIdx.x >> 3), nvalid - 1);
+        const size_t off = tok_base<SEQ>(bh, t0, B, H, T) + (size_t)row * rs + c8;
+        f.r = *reinterpret_cast<const uint4*>(r + off);
+        f.k = *reinterpret_cast<const uint4*>(k + off);
+        f.v = *reinterpret_cast<const uint4*>(v + off);
+    }
+    f.w = walk_load_w<SEQ>(w, bh, cw, B, H, T);
 }
 
 // Global stores of chunk c (o from Ot, S_in from Sin[c & 1]).  Issued one
@@ -468,17 +490,43 @@ __device__ __forceinline__ void fwd_walk_chunks(
         uf[0] = ua.x; uf[1] = ua.y; uf[2] = ua.z; uf[3] = ua.w;
         uf[4] = ub.x; uf[5] = ub.y; uf[6] = ub.z; uf[7] = ub.w;
     }
+    if (c_begin >= c_end) return;                      // (uniform over the workgroup)
+    // The decay scans of the first two chunks (the loop scans chunk c + 2 during chunk c):
+    // G and the tables of c_begin, the part sums of c_begin + 1 (tot, loc).  nx holds w of
+    // c_begin on entry and w of c_begin + 2 on leaving.
+    float loc[8];
+    {
+        const uint4 w1 = walk_load_w<SEQ>(w, bh, min(c_begin + 1, c_end - 1), B, H, T);
+        const uint4 w2 = walk_load_w<SEQ>(w, bh, min(c_begin + 2, c_end - 1), B, H, T);
+        int nv = min(CL, T - c_begin * CL);
+        sstore16(sm.Wr, row, c8, row < nv ? nx.w : make_uint4(0u, 0u, 0u, 0u));
+        __syncthreads();
+        walk_scan1<SEQ, PB>(sm, nv, c_begin & 1, loc);
+        __syncthreads();
+        walk_scan2<PB>(sm, loc, c_begin & 1, c_begin & 1);
+        nv = min(CL, T - min(c_begin + 1, c_end - 1) * CL);
+        sstore16(sm.Wr, row, c8, row < nv ? w1 : make_uint4(0u, 0u, 0u, 0u));
+        __syncthreads();
+        walk_scan1<SEQ, PB>(sm, nv, (c_begin + 1) & 1, loc);
+        __syncthreads();
+        nx.w = w2;
+    }
     // first chunk's loads complete here (vmcnt(0)), so the wait at the loop top is set by the
     // loop's own order (the next chunk's loads, then this chunk's two stores) alone
     __builtin_amdgcn_s_waitcnt(0x0F70);
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(CL, T - c * CL);
+        // nx holds r, k, v of chunk c and w of chunk cw = c + 2 (the last chunk of the segment
+        // past its end: that scan is never used)
+        const int nvw = min(CL, T - min(c + 2, c_end - 1) * CL);
         // Every tile written here was last read before the previous chunk's final barrier
-        // (Sin[c & 1] two chunks ago).  The thread's raw r and k stay in registers (rq, kq)
-        // for its own operand tiles below.
-        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = nx.w = make_uint4(0u, 0u, 0u, 0u);
+        // (Sin[c & 1] two chunks ago); G and the tables of chunk c were written in the previous
+        // chunk's second phase.  The thread's raw r and k stay in registers (rq, kq) for its
+        // own operand tiles below.
+        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = make_uint4(0u, 0u, 0u, 0u);
+        if (nvw < CL && row >= nvw) nx.w = make_uint4(0u, 0u, 0u, 0u);
         sstore16(sm.Vm, row, c8, nx.v);
-        sstore16(sm.Kt, row, c8, nx.w);                       // w scratch for build_G
+        sstore16(sm.Wr, row, c8, nx.w);                       // scanned after the barrier
         const uint4 rq = nx.r, kq = nx.k;
         {
             float rf[8], kf[8], bsum = 0.f;
@@ -495,12 +543,10 @@ __device__ __forceinline__ void fwd_walk_chunks(
                 *reinterpret_cast<uint2*>(&sm.Sin[c & 1][16 * W + lr][32 * hh + 16 * tp + 4 * lq]) =
                     make_uint2(pk2(acc[tp][0], acc[tp][1]), pk2(acc[tp][2], acc[tp][3]));
         }
-        // unconditional (the last iteration reloads its own chunk): loads under a branch
-        // would cost the loop a full wait
-        walk_issue<SEQ, true>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), B, H, T);
-        __syncthreads();
+        // unconditional (the last iterations reload the segment's last chunk): loads under a
+        // branch would cost the loop a full wait
+        walk_issue<SEQ>(nx, r, k, v, w, bh, min(c + 1, c_end - 1), min(c + 3, c_end - 1), B, H, T);
         {
-            walk_build_G<SEQ, PB>(sm, nvalid, c & 1);
             // Operand tiles of this thread's piece (token t = row in block I; I is
             // wave-uniform).  Two exponentials per element; every other factor is a
             // per-(block, channel) table entry <= 1 applied to the fp32 value:
@@ -628,6 +674,10 @@ __device__ __forceinline__ void fwd_walk_chunks(
                 acc[tp] = mfma32(__builtin_shufflevector(vt[2 * ks][tp], vt[2 * ks + 1][tp], 0, 1, 2, 3, 4, 5, 6, 7),
                                  b, acc[tp]);
         }
+        // the decay scans ahead: G and the tables of chunk c + 1 from the part sums made during
+        // chunk c - 1, then the part sums of chunk c + 2 (in Wr since this chunk's first phase)
+        walk_scan2<PB>(sm, loc, (c + 1) & 1, (c + 1) & 1);
+        walk_scan1<SEQ, PB>(sm, nvw, c & 1, loc);
         __syncthreads();
         // o and S_in of this chunk, stored after the next chunk's loads were issued: the wait
         // for those at the top of the next iteration leaves these stores in flight (vmcnt
@@ -658,11 +708,10 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
     // work (W products each) sums to the same 3
     const int W = wv < 4 ? (wv >> 1) : 5 - (wv >> 1), hh = wv & 1;
     const int lr = lane & 15, lq = lane >> 4;
-    const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
     const size_t sbase = (size_t)bh * KD * KD;
 
     WalkPrefetch nx;
-    if (c_begin < c_end) walk_issue<SEQ, true>(nx, r, k, v, w, bh, c_begin, B, H, T);
+    if (c_begin < c_end) walk_issue<SEQ>(nx, r, k, v, w, bh, c_begin, c_begin, B, H, T);
 
     // ---- starting state ----
     f32x4 acc[2];
