@@ -787,30 +787,32 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 #define PETS (PSPAN + 8)   // row stride of the channel-major operand tile (elements)
 typedef uint16_t ptile_t[PSPAN][TS];
 struct PieceSmem {
-    float dec[2][KD];                 // e^{G_end} of step m in dec[m & 1]
-    float tot[NTHR_W];                // per-part log2-decay sums
-    ptile_t Xm, Wt, Ym;               // the step's raw tiles (token-major): k, w, v forward;
-                                      // r, w, dO backward
+    float dec[KD];                    // e^{G_end} of the step
+    float tot[2][NTHR_W];             // per-part log2-decay sums of step s in tot[s & 1]
+    ptile_t Xm[2], Wt[2], Ym[2];      // the raw tiles of step s in [s & 1] (token-major): k, w,
+                                      // v forward; r, w, dO backward
     uint16_t Et[KD][PETS];            // the A operand, channel-major: k e^{G_end - G}
                                       // forward, r e^{G_{t-1}} backward
 };
-static_assert(sizeof(PieceSmem) <= 80 * 1024, "two piece workgroups per CU");
+static_assert(sizeof(PieceSmem) <= 160 * 1024, "piece block LDS");
 
-// One step of a pre-pass piece on the raw tiles already in LDS (nvalid tokens; the rows past
-// them zeroed): the decay scan, the A operand and the state (gradient) update
-//   acc = diag(e^{G_end}) acc + E^T Y   (E = A operand, Y = v forward, dO backward).
-// BWD: the operand is x e^{G_{t-1}} (exclusive prefix) instead of x e^{G_end - G_t}.
-template <bool SEQ, bool BWD>
-__device__ __forceinline__ void piece_step(PieceSmem& sm, int nvalid, int par, f32x4* acc,
-                                           float& gsum) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int W = wv >> 1, hh = wv & 1;   // state rows [16W, +16) x columns [32hh, +32)
-    const int lr = lane & 15, lq = lane >> 4;
-    const int i = lane, part = wv;        // decay scan: channel i, tokens 16 part .. +15
-    float loc[16], run = 0.f;
+// A step of a pre-pass piece is three parts on raw tiles in LDS (nvalid tokens; the rows past
+// them zeroed), spread over two barriers so that the decay scan of the next step shares the
+// state update's phase:
+//   piece_scan   thread (part, i) scans the log-decay of channel i over the tokens 16 part ..
+//                16 part + 15 (running sums kept in loc, the part's total in tot);
+//   piece_ebuild one barrier later: G = loc + the earlier parts' totals, the A operand
+//                k e^{G_end - G} (forward) or r e^{G_{t-1}} (backward, the exclusive prefix),
+//                written channel-major, and the step's decay e^{G_end};
+//   piece_update one barrier later: acc = diag(e^{G_end}) acc + E^T Y   (Y = v forward, dO
+//                backward).
+template <bool SEQ>
+__device__ __forceinline__ void piece_scan(PieceSmem& sm, int b, int nvalid, float* loc) {
+    const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
+    float run = 0.f;
 #pragma unroll
     for (int s4 = 0; s4 < 16; s4 += 4) {
-        const bf16x4 x4 = ld_col4(&sm.Wt[0][0], 16 * part + s4);
+        const bf16x4 x4 = ld_col4(&sm.Wt[b][0][0], 16 * part + s4);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int s = s4 + jj;
@@ -820,38 +822,43 @@ __device__ __forceinline__ void piece_step(PieceSmem& sm, int nvalid, int par, f
             loc[s] = run;
         }
     }
+    sm.tot[b][part * 64 + i] = run;
+}
+template <bool BWD>
+__device__ __forceinline__ void piece_ebuild(PieceSmem& sm, int b, const float* loc, float& gsum) {
+    const int i = threadIdx.x & 63, part = threadIdx.x >> 6;
     bf16x4 xa[4];
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) xa[s4] = ld_col4(&sm.Xm[0][0], 16 * part + 4 * s4);
-    sm.tot[part * 64 + i] = run;
-    __syncthreads();
-    {
-        // G_t = loc + (sum of the earlier parts); G_end = run_7 + sum of parts 0..6
-        float off = 0.f, o7 = 0.f;
+    for (int s4 = 0; s4 < 4; ++s4) xa[s4] = ld_col4(&sm.Xm[b][0][0], 16 * part + 4 * s4);
+    // G_t = loc + (sum of the earlier parts); G_end = run_7 + sum of parts 0..6
+    float off = 0.f, o7 = 0.f;
 #pragma unroll
-        for (int p = 0; p < 7; ++p) {
-            const float t = sm.tot[p * 64 + i];
-            off += p < part ? t : 0.f;
-            o7 += t;
-        }
-        const float gend = sm.tot[7 * 64 + i] + o7;
-        float e[16];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const float xf = (float)xa[s >> 2][s & 3];
-            e[s] = BWD ? xf * ex2(s == 0 ? off : loc[s - 1] + off) : xf * ex2(gend - (loc[s] + off));
-        }
-        *reinterpret_cast<uint4*>(&sm.Et[i][16 * part]) = pack8(e);
-        *reinterpret_cast<uint4*>(&sm.Et[i][16 * part + 8]) = pack8(e + 8);
-        if (part == 7) {
-            sm.dec[par][i] = ex2(gend);
-            gsum += gend;
-        }
+    for (int p = 0; p < 7; ++p) {
+        const float t = sm.tot[b][p * 64 + i];
+        off += p < part ? t : 0.f;
+        o7 += t;
     }
-    __syncthreads();
+    const float gend = sm.tot[b][7 * 64 + i] + o7;
+    float e[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const float xf = (float)xa[s >> 2][s & 3];
+        e[s] = BWD ? xf * ex2(s == 0 ? off : loc[s - 1] + off) : xf * ex2(gend - (loc[s] + off));
+    }
+    *reinterpret_cast<uint4*>(&sm.Et[i][16 * part]) = pack8(e);
+    *reinterpret_cast<uint4*>(&sm.Et[i][16 * part + 8]) = pack8(e + 8);
+    if (part == 7) {
+        sm.dec[i] = ex2(gend);
+        gsum += gend;
+    }
+}
+__device__ __forceinline__ void piece_update(PieceSmem& sm, int b, f32x4* acc) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int W = wv >> 1, hh = wv & 1;   // state rows [16W, +16) x columns [32hh, +32)
+    const int lr = lane & 15, lq = lane >> 4;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-        const float d = sm.dec[par][16 * W + 4 * lq + rr];
+        const float d = sm.dec[16 * W + 4 * lq + rr];
         acc[0][rr] *= d;
         acc[1][rr] *= d;
     }
@@ -864,9 +871,8 @@ __device__ __forceinline__ void piece_step(PieceSmem& sm, int nvalid, int par, f
         const bf16x8 a = __builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp)
-            acc[tp] = mfma32(a, ld_tr8(&sm.Ym[0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
+            acc[tp] = mfma32(a, ld_tr8(&sm.Ym[b][0][0], 32 * ks, 32 * hh + 16 * tp), acc[tp]);
     }
-    __syncthreads();
 }
 
 // The raw 16-byte pieces a thread stores per step: rows (tid >> 3) and (tid >> 3) + 64 of each
@@ -875,14 +881,43 @@ __device__ __forceinline__ void piece_step(PieceSmem& sm, int nvalid, int par, f
 struct PieceLoads {
     uint4 x[2], w[2], y[2];
 };
-__device__ __forceinline__ void piece_store(PieceSmem& sm, PieceLoads& f, int nvalid) {
+__device__ __forceinline__ void piece_store(PieceSmem& sm, int b, PieceLoads& f, int nvalid) {
     const int row = threadIdx.x >> 3, c8 = (threadIdx.x & 7) * 8;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         if (row + 64 * h >= nvalid) f.x[h] = f.w[h] = f.y[h] = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&sm.Ym[row + 64 * h][c8]) = f.y[h];
-        *reinterpret_cast<uint4*>(&sm.Wt[row + 64 * h][c8]) = f.w[h];
-        *reinterpret_cast<uint4*>(&sm.Xm[row + 64 * h][c8]) = f.x[h];
+        *reinterpret_cast<uint4*>(&sm.Ym[b][row + 64 * h][c8]) = f.y[h];
+        *reinterpret_cast<uint4*>(&sm.Wt[b][row + 64 * h][c8]) = f.w[h];
+        *reinterpret_cast<uint4*>(&sm.Xm[b][row + 64 * h][c8]) = f.x[h];
+    }
+}
+
+// The steps of a piece in the order `step(s)` gives (s = 0 .. nsteps-1; the backward walks its
+// steps from the last), two barriers a step: the raw tiles of step s + 1 go into the other
+// buffer and the A operand of step s is built (its scan done during step s - 1); then the
+// state update of step s and the scan of step s + 1.  `issue(m)` loads step m into nx and
+// `nvalid(m)` counts its tokens.  Past the last step the indices stay on it (unconditional
+// loads and stores; the extra scan is never used).
+template <bool SEQ, bool BWD, class Issue, class Nvalid>
+__device__ __forceinline__ void piece_steps(PieceSmem& sm, PieceLoads& nx, int nsteps, Issue issue,
+                                            Nvalid nvalid, f32x4* acc, float& gsum) {
+    auto step = [&](int s) { return BWD ? nsteps - 1 - min(s, nsteps - 1) : min(s, nsteps - 1); };
+    float loc[16];
+    issue(step(0));
+    piece_store(sm, 0, nx, nvalid(step(0)));
+    issue(step(1));
+    __syncthreads();
+    piece_scan<SEQ>(sm, 0, nvalid(step(0)), loc);
+    __syncthreads();
+    for (int s = 0; s < nsteps; ++s) {
+        const int b = s & 1, nv1 = nvalid(step(s + 1));
+        piece_store(sm, b ^ 1, nx, nv1);
+        issue(step(s + 2));
+        piece_ebuild<BWD>(sm, b, loc, gsum);
+        __syncthreads();
+        piece_update(sm, b, acc);
+        piece_scan<SEQ>(sm, b ^ 1, nv1, loc);
+        __syncthreads();
     }
 }
 
@@ -917,16 +952,10 @@ wkv6_fwd_pieces(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
             nx.w[h] = *reinterpret_cast<const uint4*>(w + off);
         }
     };
-    issue(0);
+    auto nvalid = [&](int m) { return min(PSPAN, t_end - (c_begin + 2 * m) * CL); };
     f32x4 acc[2] = {};
     float gsum = 0.f;                      // total log2-decay of channel lane (wave 7)
-    for (int m = 0; m < nsteps; ++m) {
-        const int nvalid = min(PSPAN, t_end - (c_begin + 2 * m) * CL);
-        piece_store(sm, nx, nvalid);
-        issue(min(m + 1, nsteps - 1));     // unconditional (the last step reloads its own)
-        __syncthreads();
-        piece_step<SEQ, false>(sm, nvalid, m & 1, acc, gsum);
-    }
+    if (nsteps > 0) piece_steps<SEQ, false>(sm, nx, nsteps, issue, nvalid, acc, gsum);
     const size_t sq = (size_t)bh * npieces + q;
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp)
@@ -1011,16 +1040,10 @@ wkv6_bwd_pieces(const uint16_t* __restrict__ r, const uint16_t* __restrict__ w,
             nx.y[h] = *reinterpret_cast<const uint4*>(dO + dbase + (size_t)rrow * KD + c8);
         }
     };
+    auto nvalid = [&](int m) { return min(PSPAN, t_end - (c_begin + 2 * m) * CL); };
     f32x4 acc[2] = {};
     float gsum = 0.f;                      // total log2-decay of channel lane (wave 7)
-    if (nsteps > 0) issue(nsteps - 1);
-    for (int m = nsteps - 1; m >= 0; --m) {
-        const int nvalid = min(PSPAN, t_end - (c_begin + 2 * m) * CL);
-        piece_store(sm, nx, nvalid);
-        issue(max(m - 1, 0));              // unconditional: the first step reloads itself
-        __syncthreads();
-        piece_step<SEQ, true>(sm, nvalid, m & 1, acc, gsum);
-    }
+    if (nsteps > 0) piece_steps<SEQ, true>(sm, nx, nsteps, issue, nvalid, acc, gsum);
     const size_t sq = (size_t)bh * npieces + q;
 #pragma unroll
     for (int tp = 0; tp < 2; ++tp)
