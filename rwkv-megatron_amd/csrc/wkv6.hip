@@ -778,11 +778,14 @@ wkv6_fwd_walk(const uint16_t* __restrict__ r, const uint16_t* __restrict__ k,
 // [64][64]) and total log2-decay A_q ([64]).  Only k, v and w are read.  Per step, thread
 // (part, i) scans the log-decay of channel i over the tokens 16 part .. 16 part + 15 and forms
 // those tokens' k e^{G_end - G} itself, written channel-major (two 16-byte stores) as the
-// MFMA's A operand: no cumulative-decay tile, four barriers a step.  The exponents
-// G_end - G_tau are never positive, whatever the step's length, so the end state needs none of
-// the walk's 64-token references; 128-token steps halve the barriers per token (86.7 against
-// 89.2 us at config 5 with one 64-token chunk per step; loads two steps ahead measured no
-// faster, and a plain read stream of the same shape, one workgroup per CU, takes 59 us).
+// MFMA's A operand: no cumulative-decay tile.  The raw tiles are double-buffered, so a step
+// takes two barriers (piece_steps: the next step's scan runs beside this step's state
+// update; four before, 78.4 -> 76.8 us at config 5).  The exponents G_end - G_tau are never
+// positive, whatever the step's length, so the end state needs none of the walk's 64-token
+// references; 128-token steps halve the barriers per token (86.7 against 89.2 us at config 5
+// with one 64-token chunk per step; loads two steps ahead measured no faster, and a plain
+// read stream of the same shape, one workgroup per CU, takes 59 us).  With 132 KB of LDS a
+// piece takes a CU to itself; prepass_pieces caps the pieces at one per CU.
 #define PSPAN (2 * CL)     // tokens per step of the pre-pass pieces
 #define PETS (PSPAN + 8)   // row stride of the channel-major operand tile (elements)
 typedef uint16_t ptile_t[PSPAN][TS];

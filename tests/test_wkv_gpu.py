@@ -257,9 +257,11 @@ def test_wkv_seqfirst_entry(pkg, shape):
     """The time-mix module's entry: r, k, v, decay in [T,B,H*64], w = -exp(decay) inside,
     o head-first; d_decay = dw * w.  Checked against the oracle on the rearranged inputs.
     (2, 24, 2059): B*H = 48, 4 forward segments of 9 chunks and the chunk-parallel backward;
-    (2, 64, 1093): B*H = 128, the segmented walks (2 segments of 9 chunks, ragged end)."""
+    (2, 64, 1093): B*H = 128, the segmented walks (2 segments of 9 chunks, ragged end), with
+    scale 0.5 (the other shapes take RWKV-6's unit scale)."""
     B, H, T = shape
     K = 64
+    scale = 0.5 if H == 64 else 1.0
     g = torch.Generator().manual_seed(T + B)
     bf = lambda t: t.to(torch.bfloat16)
     r, k, v = (bf(torch.randn(T, B, H * K, generator=g)) for _ in range(3))
@@ -268,14 +270,14 @@ def test_wkv_seqfirst_entry(pkg, shape):
     do = bf(torch.randn(B, H, T, K, generator=g))
     dev = torch.device("cuda:0")
     leaves = [t.to(dev).requires_grad_(True) for t in (r, k, v, decay, u)]
-    o, _ = pkg.wkv6_seqfirst(*leaves, H, scale=1.0)
+    o, _ = pkg.wkv6_seqfirst(*leaves, H, scale=scale)
     (o.float() * do.to(dev).float()).sum().backward()
     torch.cuda.synchronize()
     hf = lambda t: t.float().view(T, B, H, K).permute(1, 2, 0, 3).numpy()
     w_hf = -np.exp(hf(decay).astype(np.float64))
     a = lambda t: t.detach().float().cpu()
-    o_ref, _ = orc.wkv6_fwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), None, 1.0)
-    gr = orc.wkv6_bwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), _n(do), None, None, 1.0)
+    o_ref, _ = orc.wkv6_fwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), None, scale)
+    gr = orc.wkv6_bwd(hf(r), hf(k), hf(v), w_hf, u.numpy(), _n(do), None, None, scale)
     got = dict(o=_n(o), du=_n(leaves[4].grad))
     for name, leaf in zip(("dr", "dk", "dv"), leaves[:3]):
         got[name] = hf(a(leaf.grad))
