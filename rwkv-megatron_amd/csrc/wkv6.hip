@@ -523,8 +523,16 @@ __device__ __forceinline__ void fwd_walk_chunks(
         // (Sin[c & 1] two chunks ago); G and the tables of chunk c were written in the previous
         // chunk's second phase.  The thread's raw r and k stay in registers (rq, kq) for its
         // own operand tiles below.
-        if (nvalid < CL && row >= nvalid) nx.r = nx.k = nx.v = make_uint4(0u, 0u, 0u, 0u);
-        if (nvw < CL && row >= nvw) nx.w = make_uint4(0u, 0u, 0u, 0u);
+        // Only a sequence's last chunk can be ragged: a wave-uniform branch around the per-lane
+        // zeroing (the empty asm keeps the compiler from turning it into selects on every chunk)
+        if (nvalid < CL) {
+            asm volatile("");
+            if (row >= nvalid) nx.r = nx.k = nx.v = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (nvw < CL) {
+            asm volatile("");
+            if (row >= nvw) nx.w = make_uint4(0u, 0u, 0u, 0u);
+        }
         sstore16(sm.Vm, row, c8, nx.v);
         sstore16(sm.Wr, row, c8, nx.w);                       // scanned after the barrier
         const uint4 rq = nx.r, kq = nx.k;
@@ -2163,9 +2171,12 @@ __device__ __forceinline__ void bwd_loop_walk(
         // ---- S1: the raw pieces into LDS, the bonus, dd, dS_out(c) as a bf16 tile ----
         {
             LoopPrefetch x = pf;
-            if (nvalid < CL && row >= nvalid) {
-                const uint2 z = make_uint2(0u, 0u);
-                x.r = x.k = x.v = x.w = x.d = z;
+            if (nvalid < CL) {             // the ragged last chunk only: a wave-uniform branch
+                asm volatile("");          // (no per-chunk selects)
+                if (row >= nvalid) {
+                    const uint2 z = make_uint2(0u, 0u);
+                    x.r = x.k = x.v = x.w = x.d = z;
+                }
             }
             lds_st<uint2>(&sm.Vt[0][0], o.th, x.v);
             lds_st<uint2>(&sm.Dt[0][0], o.th, x.d);
