@@ -145,7 +145,8 @@ def test_wkv_empty_sequence(pkg):
 
 @pytest.mark.parametrize("shape", [(1, 2, 1100), (1, 1, 64 * 40 + 17), (2, 24, 64 * 32 + 11),
                                    (3, 32, 64 * 20), (2, 8, 64 * 64), (1, 32, 64 * 15 + 40),
-                                   (2, 64, 64 * 17 + 5), (1, 128, 64 * 30 + 9)])
+                                   (2, 64, 64 * 17 + 5), (1, 128, 64 * 30 + 9),
+                                   (1, 1, 64 * 72 + 10), (1, 1, 64 * 64 + 30)])
 def test_wkv_parity_segmented(pkg, shape):
     """Few sequences of many chunks: the forward cuts each sequence into segments (pre-pass
     pieces folded into each segment's start state, then output walks), here 2 segments of 9
@@ -155,7 +156,10 @@ def test_wkv_parity_segmented(pkg, shape):
     device: 2, 5, 192, 192, 128 and 64 of 256) and as a segmented reverse walk (backward pieces
     folded into each segment's starting state gradient) for the 128-sequence shapes: 2
     segments of 9 chunks, and of 16 + 15 chunks with a ragged last one.  The pieces step two
-    chunks at a time, so segments of an odd chunk count (9, 15) end on a one-chunk step."""
+    chunks at a time, so segments of an odd chunk count (9, 15) end on a one-chunk step.
+    The last two shapes end the forward on a one-chunk (ragged, 10 tokens) and a two-chunk
+    segment (9 and 8 segments of 9 chunks): the walk's decay scan runs two chunks ahead, so
+    there its look-ahead stays on the segment's last chunk from the start."""
     B, H, T = shape
     x = _inputs(B, H, T, seed=T)
     got = run_gpu(pkg, x, 0.5, True, True)
