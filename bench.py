@@ -512,6 +512,15 @@ def slice_7b_bench(pkg, steps, warmup):
     return out
 
 
+def _extra(fn, *a):
+    """One of the extra configurations; an exception there is recorded in its own field
+    instead of costing the run its JSON line."""
+    try:
+        return fn(*a)
+    except Exception as e:  # noqa: BLE001 -- reported, the headline line still prints
+        return {"error": f"{type(e).__name__}: {e}"}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -576,10 +585,10 @@ def main():
                      "traffic": measured_traffic(B, H, T)},
     }
     if not args.no_extra_configs:
-        out["config5"] = config5_bench(pkg, L, args)
-        if not args.no_cpu_baseline:
-            out["config5"]["cpu_baseline"] = cpu_baseline(1, 32, 32768, 0, with_state=True)
-        out["slice_7b"] = slice_7b_bench(pkg, args.train_steps, args.train_warmup)
+        out["config5"] = _extra(config5_bench, pkg, L, args)
+        if not args.no_cpu_baseline and "error" not in out["config5"]:
+            out["config5"]["cpu_baseline"] = _extra(cpu_baseline, 1, 32, 32768, 0, True)
+        out["slice_7b"] = _extra(slice_7b_bench, pkg, args.train_steps, args.train_warmup)
     if args.copy_calibration_mb > 0:
         n = args.copy_calibration_mb * (1 << 20) // 2
         src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
@@ -590,12 +599,12 @@ def main():
         torch.cuda.synchronize()
         out["copy_calibration_bytes"] = 2 * n
     if not args.no_train:
-        out["train_step"] = train_step_bench(pkg, args.train_steps, args.train_warmup)
+        out["train_step"] = _extra(train_step_bench, pkg, args.train_steps, args.train_warmup)
     if not args.no_extra_configs:
-        out["config1"] = config1_bench(pkg, max(5, args.steps // 2), not args.no_cpu_baseline)
+        out["config1"] = _extra(config1_bench, pkg, max(5, args.steps // 2), not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(B, H, T, args.cpu_sample_heads)
-        out["cpu_host"] = cpu_info()
+        out["cpu_baseline"] = _extra(cpu_baseline, B, H, T, args.cpu_sample_heads)
+        out["cpu_host"] = _extra(cpu_info)
     print(json.dumps(out), flush=True)
 
 
