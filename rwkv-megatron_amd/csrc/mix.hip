@@ -122,28 +122,59 @@ rwkv6_cmix_lerp_bwd_kernel(const uint16_t* __restrict__ x, const void* __restric
         float xprev[8];
         if (t_lo > 0) load8(x + ((t_lo - 1) * B + b) * C + 8 * cg, xprev);
         else for (int s = 0; s < 8; ++s) xprev[s] = 0.f;
-        for (int64_t t = t_lo; t < t_hi; ++t) {
-            const int64_t off = (t * B + b) * C + 8 * cg;
-            float xv[8], dd[8], dsum[8], g[CMIX_NE][8], out[8];
-            load8(x + off, xv);
-            cmix_token(mv, dmix, off, dd, dsum, g);
+        // The thread's MIX_SS tokens in a fixed, unrolled walk: x and d_mixed of the token two
+        // ahead are loaded (clamped to the last token, unconditionally) before this token's
+        // arithmetic, so a load's latency overlaps two tokens of work instead of stalling each
+        // one (58.5 -> 54.6 us at the config-3 shape; one ahead 56.0, all eight up front 55.2).
+        const int n = (int)(t_hi - t_lo);
+        auto ld = [&](int j, uint4* r) {
+            const int64_t off = ((t_lo + min(j, n - 1)) * B + b) * C + 8 * cg;
+            r[0] = *reinterpret_cast<const uint4*>(x + off);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float delta = xprev[s] - xv[s];
+            for (int e = 0; e < CMIX_NE; ++e) r[1 + e] = *reinterpret_cast<const uint4*>(dmix.p[e] + off);
+        };
+        uint4 nxt[1 + CMIX_NE], nx2[1 + CMIX_NE];
+        ld(0, nxt);
+        ld(1, nx2);
 #pragma unroll
-                for (int e = 0; e < CMIX_NE; ++e) acc[e][s] += g[e][s] * delta;
-                xprev[s] = xv[s];
+        for (int j = 0; j < MIX_SS; ++j) {
+            uint4 cur[1 + CMIX_NE];
+#pragma unroll
+            for (int q = 0; q <= CMIX_NE; ++q) { cur[q] = nxt[q]; nxt[q] = nx2[q]; }
+            if (j + 2 < MIX_SS) ld(j + 2, nx2);
+            if (j < n) {
+                const int64_t off = ((t_lo + j) * B + b) * C + 8 * cg;
+                float xv[8], dd[8], dsum[8], g[CMIX_NE][8], out[8];
+                unpack8(cur[0], xv);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) dd[s] = dsum[s] = 0.f;
+#pragma unroll
+                for (int e = 0; e < CMIX_NE; ++e) {
+                    unpack8(cur[1 + e], g[e]);
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) {
+                        dd[s] += g[e][s] * mv[e * 8 + s];
+                        dsum[s] += g[e][s];
+                    }
+                }
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const float delta = xprev[s] - xv[s];
+#pragma unroll
+                    for (int e = 0; e < CMIX_NE; ++e) acc[e][s] += g[e][s] * delta;
+                    xprev[s] = xv[s];
+                }
+                if (j > 0) {
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) out[s] = pend[s] + dd[s];
+                    store8(dx + off - B * C, out);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 8; ++s) first_dd[ss][cgl][s] = dd[s];
+                }
+#pragma unroll
+                for (int s = 0; s < 8; ++s) pend[s] = dsum[s] - dd[s];
             }
-            if (t > t_lo) {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) out[s] = pend[s] + dd[s];
-                store8(dx + off - B * C, out);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) first_dd[ss][cgl][s] = dd[s];
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) pend[s] = dsum[s] - dd[s];
         }
     }
     __syncthreads();
